@@ -1,0 +1,194 @@
+"""Benchmark of the int8 (W8A8) inference path on one MI355X.
+
+``python bench.py [--gpus 1] [--steps K] [--warmup W]`` prints ONE JSON line.
+
+Headline (``value``): the 4096³ dynamic-quant GEMM of config C2 — a step is one pass of
+the hot path over one batch: per-row quantization of A (f32 [4096,4096] → int8) plus the
+int8 MFMA GEMM with the fused dequant+bias epilogue (f32 out), inputs resident in HBM.
+``value`` = 2·M·N·K / step time, in TOPS (int8 ops).
+
+``roofline`` is the dominant kernel (the GEMM) timed alone with HIP events on the stream
+it runs on: achieved = 2·M·N·K ops ÷ average kernel duration vs. the dense int8 peak.
+Beside it: the GEMV (M = 1, 16) and M = 256 rows of the same sweep, cache-cold (the
+weight rotates over > 256 MB of copies so the 256 MB Infinity Cache cannot hold it), and
+the CPU baseline (the oracle's int8 arithmetic on the host cores, a bounded sample).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_INT8_TOPS = 5000.0  # MI355X dense int8 MFMA, 5.0 POP/s
+PEAK_HBM_GBS = 8000.0    # MI355X HBM3E, 8 TB/s
+METRIC = "int8 GEMM TOPS (% MFMA peak) at 4096³; ResNet-18 int8 b16 fwd ms; GEMV GB/s"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def time_events(fn, reps, stream):
+    """Average ms per call of ``fn`` over ``reps`` back-to-back calls, HIP events on ``stream``."""
+    import torch
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(reps):
+        fn(i)
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) / reps
+
+
+def cpu_baseline(M_sample=256):
+    """The oracle's int8 arithmetic (per-row quantize + exact GEMM + epilogue) on the host,
+    on a bounded sample: M_sample rows of the 4096³ workload, scaled to TOPS."""
+    from oracle import quant as O
+    from borch_amd import workloads as WL
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
+    except Exception:  # pragma: no cover
+        threads = os.cpu_count() or 1
+    a, w, b = WL.c2_gemm(M_sample, 0)
+    qw, sw = O.quantize_weight_per_channel(w)
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        qa, sa = O.quantize_rows(a)
+        acc = O.gemm_i8_i32(qa, qw)
+        O.dequant(acc, sa, sw, b)
+        times.append(time.perf_counter() - t0)
+    t = min(times)
+    ops = 2 * M_sample * 4096 * 4096
+    return {"value": round(ops / t / 1e12, 4), "unit": "TOPS", "cores": int(threads), "kind": "port",
+            "sample": f"oracle int8 Linear (per-row quantize + float64-BLAS exact GEMM + f32 epilogue), "
+                      f"{M_sample}x4096x4096 rows of the 4096³ workload, min of 3, {t * 1e3:.1f} ms"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(json.dumps({"error": "this build runs on one GPU only: the int8 path is measured on 1 MI355X "
+                                   "(the multi-GPU sharding is a design note, not a benchmark)"}))
+        sys.exit(2)
+
+    import torch
+    from borch_amd import int8 as I
+    from borch_amd import workloads as WL
+
+    dev = torch.device("cuda:0")
+    from borch_amd._lib import require_device
+    require_device(dev)
+    stream = torch.cuda.current_stream(dev)
+    M = N = K = 4096
+
+    # ---- headline: 4096³ dynamic-quant GEMM (quantize + GEMM)
+    a, w, b = WL.c2_gemm(M, 0)
+    A = torch.from_numpy(a).to(dev)
+    W = torch.from_numpy(w).to(dev)
+    B = torch.from_numpy(b).to(dev)
+    qw, sw = I.quantize_weight_per_channel(W)
+    del W
+    qa, sa = I.quantize_rows(A)
+    out = I.gemm_i8(qa, qw, sa, sw, B)
+
+    def step(_i):
+        q, s = I.quantize_rows(A)
+        I.gemm_i8(q, qw, s, sw, B)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ms_events = time_events(step, args.steps, stream)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / args.steps
+    ops = WL.gemm_ops(M)
+    value = ops / (ms_events * 1e-3) / 1e12
+
+    # kernels alone
+    gemm_ms = time_events(lambda i: I.gemm_i8(qa, qw, sa, sw, B), max(args.steps, 20), stream)
+    quant_ms = time_events(lambda i: I.quantize_rows(A), max(args.steps, 20), stream)
+    gemm_tops = ops / (gemm_ms * 1e-3) / 1e12
+    quant_bytes = 5 * M * K + 4 * M
+    del A, out
+
+    # ---- sweep rows (cache-cold weight rotation for the HBM-bound ones)
+    sweep = {}
+    for m in (1, 16, 256):
+        a_m, w_m, b_m = WL.c2_gemm(m, 0)
+        Am = torch.from_numpy(a_m).to(dev)
+        qw_m, sw_m = I.quantize_weight_per_channel(torch.from_numpy(w_m).to(dev))
+        Bm = torch.from_numpy(b_m).to(dev)
+        copies = 24  # 24 x 16 MiB = 384 MiB > 256 MiB Infinity Cache
+        qws = [qw_m.clone() for _ in range(copies)]
+        qa_m, sa_m = I.quantize_rows(Am)
+        for i in range(copies):
+            I.gemm_i8(qa_m, qws[i], sa_m, sw_m, Bm)
+        reps = copies * 8
+        t_k = time_events(lambda i: I.gemm_i8(qa_m, qws[i % copies], sa_m, sw_m, Bm), reps, stream)
+        t_e2e = time_events(lambda i: (lambda q_s: I.gemm_i8(q_s[0], qws[i % copies], q_s[1], sw_m, Bm))(
+            I.quantize_rows(Am)), reps, stream)
+        byts = WL.gemm_bytes(m)
+        sweep[f"M{m}"] = {"kernel_us": round(t_k * 1e3, 3), "GBps": round(byts / (t_k * 1e-3) / 1e9, 1),
+                          "hbm_frac": round(byts / (t_k * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                          "TOPS": round(WL.gemm_ops(m) / (t_k * 1e-3) / 1e12, 2),
+                          "e2e_us_with_quantize": round(t_e2e * 1e3, 3), "bytes": byts}
+        del qws, Am
+        log(f"M={m}: {sweep[f'M{m}']}")
+    sweep["M4096"] = {"kernel_us": round(gemm_ms * 1e3, 3), "TOPS": round(gemm_tops, 1),
+                      "mfma_frac": round(gemm_tops / PEAK_INT8_TOPS, 4),
+                      "quantize_us": round(quant_ms * 1e3, 3),
+                      "quantize_GBps": round(quant_bytes / (quant_ms * 1e-3) / 1e9, 1)}
+
+    traffic = None
+    tf = ROOT / "profiles" / "gemm_4096_traffic.json"
+    if tf.exists():
+        try:
+            traffic = json.loads(tf.read_text()).get("hbm_bytes_per_launch")
+        except Exception:
+            traffic = None
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_events, 5),
+        "wall_ms_per_step": round(wall, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded numpy default_rng(0): A ~ N(0,1), W ~ N(0,1/4096), b ~ N(0,0.01))",
+        "config": {"workload": "C2 dynamic-quant GEMM M=N=K=4096: per-row int8 quantize of A + int8 MFMA GEMM "
+                               "+ fused dequant/bias epilogue, f32 out", "M": M, "N": N, "K": K},
+        "roofline": {"bound": "mfma", "achieved": round(gemm_tops, 2), "peak": PEAK_INT8_TOPS, "unit": "TOPS",
+                     "frac": round(gemm_tops / PEAK_INT8_TOPS, 4), "traffic": traffic,
+                     "kernel": "gemm_i8_kernel 256x256 (bq_gemm_i8)", "kernel_ms": round(gemm_ms, 5)},
+        "sweep": sweep,
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

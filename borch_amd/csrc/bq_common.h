@@ -1,0 +1,62 @@
+// Shared helpers of the int8 inference library (libbq): error state, vector types and
+// the exact rounding rule every quantizer uses.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/bq.h"
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+namespace bq {
+
+// Records the message for bq_last_error() and returns `code`.
+int set_error(int code, const char* fmt, ...);
+
+// Maps the launch status (hipGetLastError) onto the return codes.
+int check_launch(const char* what);
+
+// Wave64 max of a non-negative float.
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// The scale rule: float32(peak / 127), correctly rounded. The quotient is taken in
+// float64 and rounded once to float32; for a single division that equals the correctly
+// rounded float32 quotient (53 >= 2*24 + 2).
+__device__ __forceinline__ float scale_of(float peak) {
+  return (float)((double)peak / 127.0);
+}
+
+// q = clip(rint(f64(v) / f64(s)), -127, 127); s == 0 gives 0. The float64 quotient of
+// two float32 values is never moved onto or off a .5 tie by its own rounding, so rint
+// (round half to even) of it is the exact-quotient rounding.
+__device__ __forceinline__ int quant_one(float v, double s) {
+  if (s == 0.0) return 0;
+  double r = rint((double)v / s);
+  r = r > 127.0 ? 127.0 : (r < -127.0 ? -127.0 : r);
+  return (int)r;
+}
+
+__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
+  return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
+         ((uint32_t)(d & 0xff) << 24);
+}
+
+// The f32 epilogue, one rounding per operation (no contraction into FMA):
+// y = ((f32(acc) * sa) * sw) + b, then + residual, then relu.
+__device__ __forceinline__ float dequant_one(int acc, float sa, float sw, float b, bool has_b,
+                                             float r, bool has_r, int act) {
+  float v = __fmul_rn(__fmul_rn((float)acc, sa), sw);
+  if (has_b) v = __fadd_rn(v, b);
+  if (has_r) v = __fadd_rn(v, r);
+  if (act == BQ_ACT_RELU) v = v > 0.f ? v : 0.f;
+  else if (act == BQ_ACT_SILU) v = __fdiv_rn(v, __fadd_rn(1.0f, expf(-v)));
+  return v;
+}
+
+}  // namespace bq

@@ -1,0 +1,457 @@
+// W8A8 GEMM and implicit-GEMM convolution on gfx950 int8 MFMA, with the dequant epilogue.
+//
+// One kernel template serves both: C[M, N] = A[M, K] · W[N, K]^T where W is the int8
+// weight (K-contiguous rows) and A is either a dense int8 matrix (Linear) or the implicit
+// im2col of an NHWC int8 activation (conv: M = N·OH·OW pixels, K = KH·KW·C, tap-major then
+// channel). Both operands are K-contiguous, so each MFMA lane reads 16 contiguous bytes
+// of one row of each — no transposes anywhere.
+//
+// Tiles: BM x BN output per workgroup, K walked in 128-byte steps (one 128 B cache line
+// per row per step), double-buffered in LDS with an XOR swizzle of the 16-byte chunks.
+// Each wave owns a (BM/WAVES_M) x (BN/WAVES_N) sub-tile of 32x32 v_mfma_i32_32x32x32_i8
+// results; the next K step's global loads are in flight while the current one computes.
+//
+// Skinny path (M <= 64): the weight is streamed once at HBM rate. A workgroup owns 16
+// output channels; its waves split K; each lane loads 64 contiguous weight bytes per step
+// and v_mfma_i32_16x16x64_i8 multiplies them against up to four 16-row activation tiles.
+#include "bq_common.h"
+
+namespace bq {
+
+struct GemmP {
+  const int8_t* A;  // dense [M, K]; conv: NHWC [Nimg, H, W, C]
+  const int8_t* W;  // [N, K]
+  int M, N, K;
+  const float* sA;  // [M] per row, or [1] per tensor
+  int sa_per_row;
+  const float* sW;  // [N]
+  const float* bias;
+  const float* res;  // [M, N] or null
+  int act;
+  float* out;    // [M, N]
+  int32_t* acc;  // [M, N] or null
+  // conv geometry (CONV only)
+  int H, Wd, C, OH, OW, KWd, stride, pad;
+};
+
+constexpr int BK = 128;  // bytes of K per LDS stage: one cache line per row
+
+// Byte offset of 16-byte chunk `c` (0..7) of LDS row `r`, XOR-swizzled so that the
+// 16 lanes of an MFMA fragment read (16 consecutive rows, one chunk) hit distinct banks.
+template <int SWZ>
+__device__ __forceinline__ int lds_off(int r, int c) {
+  return r * BK + ((c ^ ((r >> SWZ) & 7)) << 4);
+}
+
+template <int BM, int BN, int WAVES_M, int WAVES_N, int SWZ, bool CONV>
+__global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const GemmP p) {
+  constexpr int T = WAVES_M * WAVES_N * 64;
+  constexpr int WTM = BM / WAVES_M;  // wave tile rows
+  constexpr int WTN = BN / WAVES_N;
+  constexpr int TM = WTM / 32;
+  constexpr int TN = WTN / 32;
+  constexpr int ROWS_PER_PASS = T / 8;  // rows a pass of all threads loads (8 chunks a row)
+  constexpr int A_LD = BM / ROWS_PER_PASS;
+  constexpr int B_LD = BN / ROWS_PER_PASS;
+  static_assert(BM % ROWS_PER_PASS == 0 && BN % ROWS_PER_PASS == 0, "tile/threads");
+  static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile");
+
+  __shared__ __attribute__((aligned(16))) int8_t lds[2 * (BM + BN) * BK];
+  int8_t* As = lds;                 // [2][BM][BK]
+  int8_t* Bs = lds + 2 * BM * BK;   // [2][BN][BK]
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave / WAVES_N;
+  const int wn = wave % WAVES_N;
+
+  // Grid swizzle: consecutive workgroups walk down M within a column band of 8 tiles so
+  // the W tiles they share stay in L2.
+  const int tiles_m = (p.M + BM - 1) / BM;
+  int bm, bn;
+  {
+    const int id = blockIdx.x;
+    constexpr int GROUP = 8;
+    const int tiles_n = (p.N + BN - 1) / BN;
+    const int per_group = GROUP * tiles_m;
+    const int g = id / per_group;
+    const int first_n = g * GROUP;
+    const int gsize = min(tiles_n - first_n, GROUP);
+    const int in = id - g * per_group;
+    bm = in / gsize;
+    bn = first_n + in % gsize;
+  }
+  const int m0 = bm * BM;
+  const int n0 = bn * BN;
+
+  // Each thread loads chunk `kc` of rows (tid >> 3) + i * ROWS_PER_PASS.
+  const int kc = tid & 7;
+  const int lr = tid >> 3;
+
+  // Per-row source bases for A.
+  const int8_t* a_row[A_LD];
+  int a_ih0[A_LD], a_iw0[A_LD];
+  bool a_ok[A_LD];
+#pragma unroll
+  for (int i = 0; i < A_LD; ++i) {
+    const int m = m0 + lr + i * ROWS_PER_PASS;
+    a_ok[i] = m < p.M;
+    if constexpr (CONV) {
+      const int mm = a_ok[i] ? m : 0;
+      const int plane = p.OH * p.OW;
+      const int n = mm / plane;
+      const int r = mm - n * plane;
+      const int oh = r / p.OW;
+      const int ow = r - oh * p.OW;
+      a_ih0[i] = oh * p.stride - p.pad;
+      a_iw0[i] = ow * p.stride - p.pad;
+      a_row[i] = p.A + (size_t)n * p.H * p.Wd * p.C;
+    } else {
+      a_row[i] = p.A + (size_t)(a_ok[i] ? m : 0) * p.K;
+      a_ih0[i] = a_iw0[i] = 0;
+    }
+  }
+  const int8_t* b_row[B_LD];
+  bool b_ok[B_LD];
+#pragma unroll
+  for (int i = 0; i < B_LD; ++i) {
+    const int n = n0 + lr + i * ROWS_PER_PASS;
+    b_ok[i] = n < p.N;
+    b_row[i] = p.W + (size_t)(b_ok[i] ? n : 0) * p.K;
+  }
+
+  v4i ra[A_LD], rb[B_LD];
+  auto load_tile = [&](int kt) {
+    const int k0 = kt * BK + kc * 16;
+    const bool kin = k0 < p.K;
+    if constexpr (CONV) {
+      const int tap = k0 / p.C;
+      const int c0 = k0 - tap * p.C;
+      const int kh = tap / p.KWd;
+      const int kw = tap - kh * p.KWd;
+#pragma unroll
+      for (int i = 0; i < A_LD; ++i) {
+        const int ih = a_ih0[i] + kh, iw = a_iw0[i] + kw;
+        const bool ok = kin && a_ok[i] && ih >= 0 && ih < p.H && iw >= 0 && iw < p.Wd;
+        ra[i] = ok ? *reinterpret_cast<const v4i*>(a_row[i] + ((size_t)ih * p.Wd + iw) * p.C + c0) : v4i{0, 0, 0, 0};
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < A_LD; ++i)
+        ra[i] = (kin && a_ok[i]) ? *reinterpret_cast<const v4i*>(a_row[i] + k0) : v4i{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int i = 0; i < B_LD; ++i)
+      rb[i] = (kin && b_ok[i]) ? *reinterpret_cast<const v4i*>(b_row[i] + k0) : v4i{0, 0, 0, 0};
+  };
+  auto store_tile = [&](int buf) {
+    int8_t* as = As + buf * BM * BK;
+    int8_t* bs = Bs + buf * BN * BK;
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i) *reinterpret_cast<v4i*>(as + lds_off<SWZ>(lr + i * ROWS_PER_PASS, kc)) = ra[i];
+#pragma unroll
+    for (int i = 0; i < B_LD; ++i) *reinterpret_cast<v4i*>(bs + lds_off<SWZ>(lr + i * ROWS_PER_PASS, kc)) = rb[i];
+  };
+
+  v16i c[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) c[i][j] = v16i{};
+
+  const int KT = (p.K + BK - 1) / BK;
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+
+  const int fr = lane & 31;   // fragment row within a 32-row block
+  const int fh = lane >> 5;   // which 16-byte half of the 32-byte K slice
+  for (int kt = 0; kt < KT; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < KT) load_tile(kt + 1);
+    const int8_t* as = As + cur * BM * BK;
+    const int8_t* bs = Bs + cur * BN * BK;
+#pragma unroll
+    for (int ks = 0; ks < BK / 32; ++ks) {
+      v4i af[TM], bf[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        af[i] = *reinterpret_cast<const v4i*>(as + lds_off<SWZ>(wm * WTM + i * 32 + fr, ks * 2 + fh));
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        bf[j] = *reinterpret_cast<const v4i*>(bs + lds_off<SWZ>(wn * WTN + j * 32 + fr, ks * 2 + fh));
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) c[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], c[i][j], 0, 0, 0);
+    }
+    if (kt + 1 < KT) store_tile(cur ^ 1);
+    __syncthreads();
+  }
+
+  // Epilogue. 32x32 result layout: lane l, register r holds
+  // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+  const float sa_t = p.sa_per_row ? 0.f : p.sA[0];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int n = n0 + wn * WTN + j * 32 + (lane & 31);
+    const bool nok = n < p.N;
+    const float sw = nok ? p.sW[n] : 0.f;
+    const float b = (nok && p.bias) ? p.bias[n] : 0.f;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + wm * WTM + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+        if (nok && m < p.M) {
+          const size_t idx = (size_t)m * p.N + n;
+          const int a = c[i][j][r];
+          const float sa = p.sa_per_row ? p.sA[m] : sa_t;
+          const float rv = p.res ? p.res[idx] : 0.f;
+          p.out[idx] = dequant_one(a, sa, sw, b, p.bias != nullptr, rv, p.res != nullptr, p.act);
+          if (p.acc) p.acc[idx] = a;
+        }
+      }
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------- skinny
+
+constexpr int SK_WAVES = 4;
+constexpr int SK_COLS = 16;  // output channels a workgroup
+
+template <int MT>
+__global__ __launch_bounds__(SK_WAVES * 64) void skinny_i8_kernel(const GemmP p) {
+  __shared__ int red[SK_WAVES][MT][64][4];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int n0 = blockIdx.x * SK_COLS;
+  const int col = lane & 15;     // weight row within the 16 (B operand column)
+  const int kg = lane >> 4;      // which 64-byte group of the 256-byte step
+  const int n = n0 + col;
+  const bool nok = n < p.N;
+  const int8_t* wrow = p.W + (size_t)(nok ? n : 0) * p.K;
+
+  v4i c[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) c[t] = v4i{};
+
+  const int steps = (p.K + 255) / 256;
+  for (int s = wave; s < steps; s += SK_WAVES) {
+    const int kb = s * 256 + kg * 64;
+    v4i w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int k = kb + j * 16;
+      w[j] = (nok && k < p.K) ? __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wrow + k)) : v4i{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const int m = t * 16 + (lane & 15);
+      const bool mok = m < p.M;
+      const int8_t* arow = p.A + (size_t)(mok ? m : 0) * p.K;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int k = kb + j * 16;
+        const v4i a = (mok && k < p.K) ? *reinterpret_cast<const v4i*>(arow + k) : v4i{0, 0, 0, 0};
+        c[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, w[j], c[t], 0, 0, 0);
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[wave][t][lane][r] = c[t][r];
+  __syncthreads();
+  // 16x16 result layout: lane l, register r holds row 4*(l/16) + r, column l%16.
+  const int e = threadIdx.x;  // one output of a 16x16 tile per thread
+  const int ml = e >> 4, nl = e & 15;
+  const int src_lane = (ml >> 2) * 16 + nl, src_r = ml & 3;
+  const int nn = n0 + nl;
+  if (nn < p.N) {
+    const float sw = p.sW[nn];
+    const float b = p.bias ? p.bias[nn] : 0.f;
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const int m = t * 16 + ml;
+      if (m < p.M) {
+        int a = 0;
+#pragma unroll
+        for (int w = 0; w < SK_WAVES; ++w) a += red[w][t][src_lane][src_r];
+        const size_t idx = (size_t)m * p.N + nn;
+        const float sa = p.sa_per_row ? p.sA[m] : p.sA[0];
+        const float rv = p.res ? p.res[idx] : 0.f;
+        p.out[idx] = dequant_one(a, sa, sw, b, p.bias != nullptr, rv, p.res != nullptr, p.act);
+        if (p.acc) p.acc[idx] = a;
+      }
+    }
+  }
+}
+
+// -------------------------------------------------------------------------- depthwise
+
+// One thread: 4 channels of one output pixel. x NHWC int8, w [KH*KW, C] int8.
+__global__ __launch_bounds__(256) void dwconv_i8_kernel(const int8_t* __restrict__ x, int Nimg, int H, int Wd,
+                                                        int C, const int8_t* __restrict__ w, int KH, int KW,
+                                                        int stride, int pad, int OH, int OW,
+                                                        const float* __restrict__ sA, const float* __restrict__ sW,
+                                                        const float* __restrict__ bias, int act,
+                                                        float* __restrict__ out, int32_t* __restrict__ acc) {
+  const int C4 = C >> 2;
+  const int64_t total = (int64_t)Nimg * OH * OW * C4;
+  const float sa = sA[0];
+  for (int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; g < total; g += (int64_t)gridDim.x * blockDim.x) {
+    const int c4 = (int)(g % C4);
+    const int64_t pix = g / C4;
+    const int ow = (int)(pix % OW);
+    const int64_t t = pix / OW;
+    const int oh = (int)(t % OH);
+    const int n = (int)(t / OH);
+    int a0 = 0, a1 = 0, a2 = 0, a3 = 0;
+    for (int kh = 0; kh < KH; ++kh) {
+      const int ih = oh * stride - pad + kh;
+      if (ih < 0 || ih >= H) continue;
+      for (int kw = 0; kw < KW; ++kw) {
+        const int iw = ow * stride - pad + kw;
+        if (iw < 0 || iw >= Wd) continue;
+        const uint32_t xv = *reinterpret_cast<const uint32_t*>(x + (((size_t)n * H + ih) * Wd + iw) * C + c4 * 4);
+        const uint32_t wv = *reinterpret_cast<const uint32_t*>(w + (size_t)(kh * KW + kw) * C + c4 * 4);
+        a0 += (int)(int8_t)(xv & 0xff) * (int)(int8_t)(wv & 0xff);
+        a1 += (int)(int8_t)((xv >> 8) & 0xff) * (int)(int8_t)((wv >> 8) & 0xff);
+        a2 += (int)(int8_t)((xv >> 16) & 0xff) * (int)(int8_t)((wv >> 16) & 0xff);
+        a3 += (int)(int8_t)(xv >> 24) * (int)(int8_t)(wv >> 24);
+      }
+    }
+    const int c = c4 * 4;
+    const int av[4] = {a0, a1, a2, a3};
+    float o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      o[j] = dequant_one(av[j], sa, sW[c + j], bias ? bias[c + j] : 0.f, bias != nullptr, 0.f, false, act);
+    const size_t idx = (size_t)pix * C + c;
+    *reinterpret_cast<float4*>(out + idx) = make_float4(o[0], o[1], o[2], o[3]);
+    if (acc) *reinterpret_cast<int4*>(acc + idx) = make_int4(a0, a1, a2, a3);
+  }
+}
+
+// ---------------------------------------------------------------------------- dispatch
+
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool CONV>
+static void launch_tiled(const GemmP& p, hipStream_t st) {
+  const int tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
+  gemm_i8_kernel<BM, BN, WAVES_M, WAVES_N, 1, CONV><<<tiles, WAVES_M * WAVES_N * 64, 0, st>>>(p);
+}
+
+template <bool CONV>
+static void launch_gemm(const GemmP& p, hipStream_t st) {
+  const long long t256 = (long long)((p.M + 255) / 256) * ((p.N + 255) / 256);
+  const long long t128 = (long long)((p.M + 127) / 128) * ((p.N + 127) / 128);
+  if (t256 >= 192)
+    launch_tiled<256, 256, 2, 4, CONV>(p, st);
+  else if (t128 >= 128)
+    launch_tiled<128, 128, 2, 2, CONV>(p, st);
+  else
+    launch_tiled<64, 64, 2, 2, CONV>(p, st);
+}
+
+static bool aligned16(const void* q) { return ((uintptr_t)q & 15) == 0; }
+
+}  // namespace bq
+
+using namespace bq;
+
+extern "C" {
+
+int bq_gemm_i8(const int8_t* A, const int8_t* W, int64_t M, int64_t N, int64_t K, const float* sA,
+               const float* sW, const float* bias, int act, float* out, int32_t* acc, bq_stream_t stream) {
+  const char* what = "bq_gemm_i8";
+  if (M < 0 || N < 0 || K < 0) return set_error(BQ_ERR_ARG, "%s: negative size", what);
+  if (M > 0x7fffffff || N > 0x7fffffff || K > 0x7fffffff || M * N > ((int64_t)1 << 40))
+    return set_error(BQ_ERR_ARG, "%s: size too large", what);
+  if (M == 0 || N == 0) return BQ_OK;
+  if (K % 16) return set_error(BQ_ERR_UNSUPPORTED, "%s: K=%lld is not a multiple of 16", what, (long long)K);
+  if (!A || !W || !sA || !sW || !out) return set_error(BQ_ERR_ARG, "%s: null pointer", what);
+  if (!aligned16(A) || !aligned16(W)) return set_error(BQ_ERR_ARG, "%s: A and W must be 16-byte aligned", what);
+  if (act < BQ_ACT_NONE || act > BQ_ACT_SILU) return set_error(BQ_ERR_ARG, "%s: bad activation %d", what, act);
+  GemmP p{};
+  p.A = A; p.W = W; p.M = (int)M; p.N = (int)N; p.K = (int)K;
+  p.sA = sA; p.sa_per_row = 1; p.sW = sW; p.bias = bias; p.res = nullptr; p.act = act;
+  p.out = out; p.acc = acc;
+  hipStream_t st = (hipStream_t)stream;
+  if (M <= 64) {
+    const unsigned grid = (unsigned)((N + SK_COLS - 1) / SK_COLS);
+    switch ((M + 15) / 16) {
+      case 1: skinny_i8_kernel<1><<<grid, SK_WAVES * 64, 0, st>>>(p); break;
+      case 2: skinny_i8_kernel<2><<<grid, SK_WAVES * 64, 0, st>>>(p); break;
+      case 3: skinny_i8_kernel<3><<<grid, SK_WAVES * 64, 0, st>>>(p); break;
+      default: skinny_i8_kernel<4><<<grid, SK_WAVES * 64, 0, st>>>(p); break;
+    }
+  } else {
+    launch_gemm<false>(p, st);
+  }
+  return check_launch(what);
+}
+
+int bq_conv2d_i8_nhwc(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t C, const int8_t* w,
+                      int64_t O, int64_t KH, int64_t KW, int64_t stride, int64_t pad, const float* sA,
+                      const float* sW, const float* bias, const float* residual, int act, float* out,
+                      int32_t* acc, bq_stream_t stream) {
+  const char* what = "bq_conv2d_i8_nhwc";
+  if (N < 0 || H < 1 || W < 1 || C < 1 || O < 1 || KH < 1 || KW < 1 || stride < 1 || pad < 0)
+    return set_error(BQ_ERR_ARG, "%s: bad geometry", what);
+  if (C % 16) return set_error(BQ_ERR_UNSUPPORTED, "%s: C=%lld is not a multiple of 16 (pad it)", what, (long long)C);
+  const int64_t OH = (H + 2 * pad - KH) / stride + 1;
+  const int64_t OW = (W + 2 * pad - KW) / stride + 1;
+  if (H + 2 * pad < KH || W + 2 * pad < KW || OH < 1 || OW < 1)
+    return set_error(BQ_ERR_ARG, "%s: the filter is larger than the input.", what);
+  const int64_t M = N * OH * OW, K = KH * KW * C;
+  if (M > 0x7fffffff || K > 0x7fffffff || O > 0x7fffffff || N * H * W * C > ((int64_t)1 << 40))
+    return set_error(BQ_ERR_ARG, "%s: size too large", what);
+  if (M == 0) return BQ_OK;
+  if (!x || !w || !sA || !sW || !out) return set_error(BQ_ERR_ARG, "%s: null pointer", what);
+  if (!aligned16(x) || !aligned16(w)) return set_error(BQ_ERR_ARG, "%s: x and w must be 16-byte aligned", what);
+  if (act < BQ_ACT_NONE || act > BQ_ACT_SILU) return set_error(BQ_ERR_ARG, "%s: bad activation %d", what, act);
+  GemmP p{};
+  p.A = x; p.W = w; p.M = (int)M; p.N = (int)O; p.K = (int)K;
+  p.sA = sA; p.sa_per_row = 0; p.sW = sW; p.bias = bias; p.res = residual; p.act = act;
+  p.out = out; p.acc = acc;
+  p.H = (int)H; p.Wd = (int)W; p.C = (int)C; p.OH = (int)OH; p.OW = (int)OW; p.KWd = (int)KW;
+  p.stride = (int)stride; p.pad = (int)pad;
+  hipStream_t st = (hipStream_t)stream;
+  if (KH == 1 && KW == 1 && stride == 1 && pad == 0)
+    launch_gemm<false>(p, st);  // a 1x1 conv is the dense GEMM on [N*H*W, C]
+  else
+    launch_gemm<true>(p, st);
+  return check_launch(what);
+}
+
+int bq_dwconv_i8_nhwc(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t C, const int8_t* w, int64_t KH,
+                      int64_t KW, int64_t stride, int64_t pad, const float* sA, const float* sW, const float* bias,
+                      int act, float* out, int32_t* acc, bq_stream_t stream) {
+  const char* what = "bq_dwconv_i8_nhwc";
+  if (N < 0 || H < 1 || W < 1 || C < 1 || KH < 1 || KW < 1 || stride < 1 || pad < 0)
+    return set_error(BQ_ERR_ARG, "%s: bad geometry", what);
+  if (C % 4) return set_error(BQ_ERR_UNSUPPORTED, "%s: C=%lld is not a multiple of 4", what, (long long)C);
+  const int64_t OH = (H + 2 * pad - KH) / stride + 1;
+  const int64_t OW = (W + 2 * pad - KW) / stride + 1;
+  if (H + 2 * pad < KH || W + 2 * pad < KW || OH < 1 || OW < 1)
+    return set_error(BQ_ERR_ARG, "%s: the filter is larger than the input.", what);
+  if (N * H * W * C > ((int64_t)1 << 40) || H > 0x7fffffff || W > 0x7fffffff || C > 0x7fffffff)
+    return set_error(BQ_ERR_ARG, "%s: size too large", what);
+  if (N == 0) return BQ_OK;
+  if (!x || !w || !sA || !sW || !out) return set_error(BQ_ERR_ARG, "%s: null pointer", what);
+  if (((uintptr_t)x & 3) || ((uintptr_t)w & 3) || ((uintptr_t)out & 15) || ((uintptr_t)acc & 15))
+    return set_error(BQ_ERR_ARG, "%s: misaligned pointer", what);
+  if (act < BQ_ACT_NONE || act > BQ_ACT_SILU) return set_error(BQ_ERR_ARG, "%s: bad activation %d", what, act);
+  const int64_t total = N * OH * OW * (C / 4);
+  int64_t blocks = (total + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  dwconv_i8_kernel<<<(unsigned)blocks, 256, 0, (hipStream_t)stream>>>(
+      x, (int)N, (int)H, (int)W, (int)C, w, (int)KH, (int)KW, (int)stride, (int)pad, (int)OH, (int)OW, sA, sW, bias,
+      act, out, acc);
+  return check_launch(what);
+}
+
+}  // extern "C"

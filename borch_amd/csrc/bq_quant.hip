@@ -1,0 +1,251 @@
+// Quantizers: per-row (activations, Linear weights) and per-tensor (conv activations).
+//
+// Per-row: one 256-thread block a row, the row held in registers between the max and the
+// quantize, so x is read from HBM once (read 4 B + write 1 B per element: HBM-bound).
+// Per-tensor: partial maxima (one per block) into a workspace, then every block of the
+// quantize kernel reduces the partials itself — no atomics, no zeroing, deterministic.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "bq_common.h"
+
+namespace bq {
+
+static thread_local char g_err[512];
+
+int set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(BQ_ERR_LAUNCH, "%s: launch failed: %s", what, hipGetErrorString(e));
+  return BQ_OK;
+}
+
+constexpr int QR_THREADS = 256;
+
+__device__ __forceinline__ float block_max(float v, float* red) {
+  v = wave_max(v);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  float m = red[0];
+#pragma unroll
+  for (int i = 1; i < QR_THREADS / 64; ++i) m = fmaxf(m, red[i]);
+  return m;
+}
+
+// NV float4 per thread kept in registers (K <= NV * 1024); NV == 0: any K, two reads.
+template <int NV>
+__global__ __launch_bounds__(QR_THREADS) void quantize_rows_kernel(const float* __restrict__ x,
+                                                                  int K, int8_t* __restrict__ q,
+                                                                  float* __restrict__ s) {
+  __shared__ float red[QR_THREADS / 64];
+  const size_t row = blockIdx.x;
+  const float* xr = x + row * (size_t)K;
+  int8_t* qr = q + row * (size_t)K;
+  const int t = threadIdx.x;
+  if constexpr (NV > 0) {
+    float4 v[NV];
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int k = (t + i * QR_THREADS) * 4;
+      if (k < K) {
+        v[i] = *reinterpret_cast<const float4*>(xr + k);
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+      } else {
+        v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+    const float sc = scale_of(block_max(m, red));
+    if (t == 0) s[row] = sc;
+    const double sd = sc;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int k = (t + i * QR_THREADS) * 4;
+      if (k < K)
+        *reinterpret_cast<uint32_t*>(qr + k) =
+            pack4(quant_one(v[i].x, sd), quant_one(v[i].y, sd), quant_one(v[i].z, sd), quant_one(v[i].w, sd));
+    }
+  } else {
+    float m = 0.f;
+    for (int k = t; k < K; k += QR_THREADS) m = fmaxf(m, fabsf(xr[k]));
+    const float sc = scale_of(block_max(m, red));
+    if (t == 0) s[row] = sc;
+    const double sd = sc;
+    for (int k = t; k < K; k += QR_THREADS) qr[k] = (int8_t)quant_one(xr[k], sd);
+  }
+}
+
+constexpr int QT_THREADS = 256;
+constexpr int QT_MAX_PARTS = 1024;
+
+// Partial maxima: block b covers elements [b*chunk, (b+1)*chunk).
+__global__ __launch_bounds__(QT_THREADS) void absmax_parts_kernel(const float* __restrict__ x, int64_t n,
+                                                                  int64_t chunk, float* __restrict__ parts) {
+  __shared__ float red[QT_THREADS / 64];
+  const int64_t lo = (int64_t)blockIdx.x * chunk;
+  const int64_t hi = max(lo, min(lo + chunk, n));
+  float m = 0.f;
+  if (((uintptr_t)x & 15) == 0 && (lo & 3) == 0) {
+    const int64_t hi4 = lo + ((hi - lo) & ~(int64_t)3);
+    for (int64_t i = lo + threadIdx.x * 4; i < hi4; i += QT_THREADS * 4) {
+      const float4 v = *reinterpret_cast<const float4*>(x + i);
+      m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+    for (int64_t i = hi4 + threadIdx.x; i < hi; i += QT_THREADS) m = fmaxf(m, fabsf(x[i]));
+  } else {
+    for (int64_t i = lo + threadIdx.x; i < hi; i += QT_THREADS) m = fmaxf(m, fabsf(x[i]));
+  }
+  m = wave_max(m);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float r = red[0];
+    for (int i = 1; i < QT_THREADS / 64; ++i) r = fmaxf(r, red[i]);
+    parts[blockIdx.x] = r;
+  }
+}
+
+// Quantize with the scale from the partial maxima. Output element e of [P, Cpad]:
+// channel c = e % Cpad reads x[p*C + c] when c < C, else 0. Four output bytes a thread.
+__global__ __launch_bounds__(QT_THREADS) void quantize_tensor_kernel(const float* __restrict__ x, int64_t P,
+                                                                     int C, int Cpad,
+                                                                     const float* __restrict__ parts,
+                                                                     int nparts, int8_t* __restrict__ q,
+                                                                     float* __restrict__ s) {
+  __shared__ float red[QT_THREADS / 64];
+  float m = 0.f;
+  for (int i = threadIdx.x; i < nparts; i += QT_THREADS) m = fmaxf(m, parts[i]);
+  m = wave_max(m);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  float peak = red[0];
+  for (int i = 1; i < QT_THREADS / 64; ++i) peak = fmaxf(peak, red[i]);
+  const float sc = scale_of(peak);
+  if (blockIdx.x == 0 && threadIdx.x == 0) s[0] = sc;
+  const double sd = sc;
+  const int64_t total = P * (int64_t)Cpad;
+  const int64_t words = (total + 3) / 4;
+  const bool flat = (C == Cpad) && ((uintptr_t)x & 15) == 0 && ((uintptr_t)q & 3) == 0 && (total & 3) == 0;
+  for (int64_t wi = (int64_t)blockIdx.x * QT_THREADS + threadIdx.x; wi < words;
+       wi += (int64_t)gridDim.x * QT_THREADS) {
+    const int64_t e0 = wi * 4;
+    if (flat) {
+      const float4 v = *reinterpret_cast<const float4*>(x + e0);
+      *reinterpret_cast<uint32_t*>(q + e0) =
+          pack4(quant_one(v.x, sd), quant_one(v.y, sd), quant_one(v.z, sd), quant_one(v.w, sd));
+    } else {
+      for (int j = 0; j < 4; ++j) {
+        const int64_t e = e0 + j;
+        if (e >= total) break;
+        const int64_t p = e / Cpad;
+        const int c = (int)(e - p * Cpad);
+        q[e] = c < C ? (int8_t)quant_one(x[p * C + c], sd) : (int8_t)0;
+      }
+    }
+  }
+}
+
+static int nparts_for(int64_t n) {
+  int64_t p = (n + QT_THREADS * 16 - 1) / (QT_THREADS * 16);
+  if (p < 1) p = 1;
+  if (p > QT_MAX_PARTS) p = QT_MAX_PARTS;
+  return (int)p;
+}
+
+static int launch_rows(const float* x, int64_t M, int64_t K, int8_t* q, float* s, hipStream_t st,
+                       const char* what) {
+  if (M < 0 || K < 0) return set_error(BQ_ERR_ARG, "%s: negative size (%lld x %lld)", what, (long long)M, (long long)K);
+  if (M == 0) return BQ_OK;
+  if (!x || !q || !s) return set_error(BQ_ERR_ARG, "%s: null pointer", what);
+  if (M > 0x7fffffff || K > 0x7fffffff) return set_error(BQ_ERR_ARG, "%s: size too large", what);
+  const bool vec = (K % 4 == 0) && (((uintptr_t)x | (uintptr_t)q) & 15) == 0;
+  const int nv = vec ? (int)((K + 1023) / 1024) : 0;
+  dim3 grid((unsigned)M), block(QR_THREADS);
+  switch (vec ? nv : 0) {
+    case 1: quantize_rows_kernel<1><<<grid, block, 0, st>>>(x, (int)K, q, s); break;
+    case 2: quantize_rows_kernel<2><<<grid, block, 0, st>>>(x, (int)K, q, s); break;
+    case 3: quantize_rows_kernel<3><<<grid, block, 0, st>>>(x, (int)K, q, s); break;
+    case 4: quantize_rows_kernel<4><<<grid, block, 0, st>>>(x, (int)K, q, s); break;
+    case 5:
+    case 6: quantize_rows_kernel<6><<<grid, block, 0, st>>>(x, (int)K, q, s); break;
+    case 7:
+    case 8: quantize_rows_kernel<8><<<grid, block, 0, st>>>(x, (int)K, q, s); break;
+    default: quantize_rows_kernel<0><<<grid, block, 0, st>>>(x, (int)K, q, s); break;
+  }
+  return check_launch(what);
+}
+
+}  // namespace bq
+
+using namespace bq;
+
+extern "C" {
+
+int bq_version(void) { return (0 << 16) | 1; }
+
+const char* bq_last_error(void) { return g_err; }
+
+int bq_device_ok(int device) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n == 0) return (set_error(BQ_ERR_DEVICE, "int8: no HIP device"), 0);
+  if (device < 0 || device >= n) return (set_error(BQ_ERR_DEVICE, "int8: no device %d (%d present)", device, n), 0);
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) != hipSuccess)
+    return (set_error(BQ_ERR_DEVICE, "int8: cannot query device %d", device), 0);
+  if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return (set_error(BQ_ERR_DEVICE,
+                      "int8: device %d is %s; the int8 kernels are built for gfx950 (MI350/MI355X) only",
+                      device, prop.gcnArchName),
+            0);
+  return 1;
+}
+
+int bq_quantize_rows(const float* x, int64_t M, int64_t K, int8_t* q, float* s, bq_stream_t stream) {
+  return launch_rows(x, M, K, q, s, (hipStream_t)stream, "bq_quantize_rows");
+}
+
+int bq_quantize_weight_per_channel(const float* w, int64_t N, int64_t K, int8_t* q, float* s,
+                                   bq_stream_t stream) {
+  return launch_rows(w, N, K, q, s, (hipStream_t)stream, "bq_quantize_weight_per_channel");
+}
+
+size_t bq_quantize_tensor_ws_bytes(int64_t n) { return (size_t)nparts_for(n < 0 ? 0 : n) * sizeof(float); }
+
+int bq_quantize_nhwc(const float* x, int64_t P, int64_t C, int64_t Cpad, int8_t* q, float* s, void* ws,
+                     size_t ws_bytes, bq_stream_t stream) {
+  const char* what = "bq_quantize_nhwc";
+  if (P < 0 || C < 0 || Cpad < C) return set_error(BQ_ERR_ARG, "%s: bad sizes P=%lld C=%lld Cpad=%lld", what, (long long)P, (long long)C, (long long)Cpad);
+  if (!x || !q || !s || !ws) return set_error(BQ_ERR_ARG, "%s: null pointer", what);
+  if (Cpad > 0x7fffffff) return set_error(BQ_ERR_ARG, "%s: too many channels", what);
+  const int64_t n = P * C;
+  const int np = nparts_for(n);
+  if (ws_bytes < (size_t)np * sizeof(float))
+    return set_error(BQ_ERR_ARG, "%s: workspace %zu bytes, need %zu", what, ws_bytes, (size_t)np * sizeof(float));
+  hipStream_t st = (hipStream_t)stream;
+  float* parts = (float*)ws;
+  const int64_t chunk = n == 0 ? 1 : (n + np - 1) / np;
+  absmax_parts_kernel<<<np, QT_THREADS, 0, st>>>(x, n, ((chunk + 3) / 4) * 4, parts);
+  if (int r = check_launch(what)) return r;
+  const int64_t words = (P * Cpad + 3) / 4;
+  int64_t blocks = (words + QT_THREADS - 1) / QT_THREADS;
+  if (blocks > 4096) blocks = 4096;
+  if (blocks < 1) blocks = 1;
+  quantize_tensor_kernel<<<(unsigned)blocks, QT_THREADS, 0, st>>>(x, P, (int)C, (int)Cpad, parts, np, q, s);
+  return check_launch(what);
+}
+
+int bq_quantize_tensor(const float* x, int64_t n, int8_t* q, float* s, void* ws, size_t ws_bytes,
+                       bq_stream_t stream) {
+  return bq_quantize_nhwc(x, n, 1, 1, q, s, ws, ws_bytes, stream);
+}
+
+}  // extern "C"

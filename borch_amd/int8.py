@@ -1,0 +1,297 @@
+"""Tensor-level int8 operations over the HIP library (``include/bq.h``).
+
+Everything here takes and returns PyTorch-ROCm device tensors and enqueues on torch's
+current stream. Weights are packed once (``pack_*``, the prepare step of
+borch-ts/src/nn.ts:967-980 and quant.ts:23-103); activations are quantized per call
+(per row for Linear, per tensor for conv, as borch-ts/src/tensor.ts:11909-11921 does for
+its conv input). There is no CPU path: a tensor that is not on a gfx950 device raises.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from ._lib import ACT_NONE, ACT_RELU, ACT_SILU, check, lib, require_device
+
+__all__ = [
+    "ACT_NONE", "ACT_RELU", "ACT_SILU", "Int8Weight", "Int8ConvWeight", "Int8DwWeight",
+    "quantize_rows", "quantize_weight_per_channel", "quantize_tensor", "quantize_nhwc",
+    "gemm_i8", "conv2d_i8_nhwc", "dwconv_i8_nhwc", "pack_linear_weight", "pack_conv_weight",
+    "pack_dw_weight", "linear", "conv2d", "depthwise_conv2d", "round_up",
+]
+
+
+def round_up(v: int, m: int) -> int:
+    return (v + m - 1) // m * m
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _stream(t: torch.Tensor):
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _need(t: torch.Tensor, name: str, dtype: torch.dtype) -> None:
+    if t.dtype != dtype:
+        raise TypeError(f"{name}: expected {dtype}, got {t.dtype}")
+    require_device(t.device)
+
+
+def _f32c(x: torch.Tensor) -> torch.Tensor:
+    if x.dtype != torch.float32:
+        raise TypeError(f"int8 path takes float32 activations, got {x.dtype}")
+    return x.contiguous()
+
+
+# --------------------------------------------------------------------------- quantizers
+
+def quantize_rows(x: torch.Tensor):
+    """Per-row int8 of f32 ``[M, K]`` → ``(q int8 [M, K], s f32 [M])`` (bq_quantize_rows)."""
+    x = _f32c(x)
+    require_device(x.device)
+    if x.dim() != 2:
+        raise ValueError("quantize_rows wants a 2-D tensor")
+    M, K = x.shape
+    q = torch.empty((M, K), dtype=torch.int8, device=x.device)
+    s = torch.empty((M,), dtype=torch.float32, device=x.device)
+    check(lib().bq_quantize_rows(x.data_ptr(), M, K, q.data_ptr(), s.data_ptr(), _stream(x)))
+    return q, s
+
+
+def quantize_weight_per_channel(w: torch.Tensor):
+    """Per-output-channel int8 of a Linear weight ``[N, K]`` (quant.ts:23-53)."""
+    w = _f32c(w)
+    require_device(w.device)
+    N, K = w.shape
+    q = torch.empty((N, K), dtype=torch.int8, device=w.device)
+    s = torch.empty((N,), dtype=torch.float32, device=w.device)
+    check(lib().bq_quantize_weight_per_channel(w.data_ptr(), N, K, q.data_ptr(), s.data_ptr(), _stream(w)))
+    return q, s
+
+
+def _ws(n: int, device) -> torch.Tensor:
+    return torch.empty((max(int(lib().bq_quantize_tensor_ws_bytes(n)), 4),), dtype=torch.uint8, device=device)
+
+
+def quantize_tensor(x: torch.Tensor):
+    """Per-tensor int8 of any f32 tensor → ``(q int8 same shape, s f32 [1])``."""
+    x = _f32c(x)
+    require_device(x.device)
+    q = torch.empty(x.shape, dtype=torch.int8, device=x.device)
+    s = torch.empty((1,), dtype=torch.float32, device=x.device)
+    ws = _ws(x.numel(), x.device)
+    check(lib().bq_quantize_tensor(x.data_ptr(), x.numel(), q.data_ptr(), s.data_ptr(), ws.data_ptr(),
+                                   ws.numel(), _stream(x)))
+    return q, s
+
+
+def quantize_nhwc(x: torch.Tensor, cpad: int | None = None):
+    """Per-tensor int8 of an NCHW f32 activation into NHWC int8 with channels padded to
+    ``cpad`` (zeros) → ``(q int8 [N, H, W, cpad], s f32 [1])``. A channels-last input is
+    read in place; a contiguous NCHW input is converted first."""
+    if x.dtype != torch.float32:
+        raise TypeError(f"int8 path takes float32 activations, got {x.dtype}")
+    require_device(x.device)
+    N, C, H, W = x.shape
+    cpad = C if cpad is None else int(cpad)
+    xl = x.contiguous(memory_format=torch.channels_last)
+    q = torch.empty((N, H, W, cpad), dtype=torch.int8, device=x.device)
+    s = torch.empty((1,), dtype=torch.float32, device=x.device)
+    P = N * H * W
+    ws = _ws(P * C, x.device)
+    check(lib().bq_quantize_nhwc(xl.data_ptr(), P, C, cpad, q.data_ptr(), s.data_ptr(), ws.data_ptr(),
+                                 ws.numel(), _stream(x)))
+    return q, s
+
+
+# ------------------------------------------------------------------------ packed weights
+
+@dataclass
+class Int8Weight:
+    """A Linear weight packed for ``bq_gemm_i8``: ``q int8 [N, Kpad]``, ``s f32 [N]``."""
+    q: torch.Tensor
+    s: torch.Tensor
+    in_features: int
+    out_features: int
+
+    @property
+    def kpad(self) -> int:
+        return self.q.shape[1]
+
+
+@dataclass
+class Int8ConvWeight:
+    """A conv weight packed for ``bq_conv2d_i8_nhwc``: ``q int8 [O, KH*KW*Cpad]``
+    (tap-major then channel), ``s f32 [O]``."""
+    q: torch.Tensor
+    s: torch.Tensor
+    O: int
+    C: int
+    cpad: int
+    KH: int
+    KW: int
+
+
+@dataclass
+class Int8DwWeight:
+    """A depthwise weight packed for ``bq_dwconv_i8_nhwc``: ``q int8 [KH*KW, Cpad]``,
+    ``s f32 [Cpad]``."""
+    q: torch.Tensor
+    s: torch.Tensor
+    C: int
+    cpad: int
+    KH: int
+    KW: int
+
+
+def pack_linear_weight(w: torch.Tensor) -> Int8Weight:
+    """Quantize once (quant.ts:23-53); K padded to a multiple of 16 with zeros (exact)."""
+    N, K = w.shape
+    kp = round_up(max(K, 16), 16)
+    wp = w if kp == K else torch.nn.functional.pad(w, (0, kp - K))
+    q, s = quantize_weight_per_channel(wp.float())
+    return Int8Weight(q, s, K, N)
+
+
+def pack_conv_weight(w: torch.Tensor) -> Int8ConvWeight:
+    """Quantize a conv weight ``[O, C, KH, KW]`` once (quant.ts:80-103's scale rule) into
+    ``[O, KH, KW, Cpad]`` with Cpad a multiple of 16 (zero channels: exact)."""
+    O, C, KH, KW = w.shape
+    cpad = round_up(C, 16)
+    t = w.float().permute(0, 2, 3, 1)
+    if cpad != C:
+        t = torch.nn.functional.pad(t, (0, cpad - C))
+    q, s = quantize_weight_per_channel(t.reshape(O, KH * KW * cpad))
+    return Int8ConvWeight(q, s, O, C, cpad, KH, KW)
+
+
+def pack_dw_weight(w: torch.Tensor) -> Int8DwWeight:
+    """Quantize a depthwise weight ``[C, 1, KH, KW]`` once, one scale per channel over its
+    taps, into tap-major ``[KH*KW, Cpad]`` (Cpad a multiple of 4)."""
+    C, one, KH, KW = w.shape
+    if one != 1:
+        raise ValueError("depthwise weight must be [C, 1, KH, KW]")
+    cpad = round_up(C, 4)
+    t = w.float().reshape(C, KH * KW)
+    if cpad != C:
+        t = torch.nn.functional.pad(t, (0, 0, 0, cpad - C))
+    q, s = quantize_weight_per_channel(t)
+    return Int8DwWeight(q.t().contiguous(), s, C, cpad, KH, KW)
+
+
+# --------------------------------------------------------------------------- int8 ops
+
+def gemm_i8(qa, qw, sa, sw, bias=None, act=ACT_NONE, want_acc=False):
+    """``out = ((f32(qa @ qw.T) * sa[m]) * sw[n]) + bias[n]`` then act (bq_gemm_i8).
+    Returns ``out`` or ``(out, acc int32)``."""
+    _need(qa, "A", torch.int8)
+    _need(qw, "W", torch.int8)
+    M, K = qa.shape
+    N, K2 = qw.shape
+    if K != K2:
+        raise RuntimeError(f"mat1 and mat2 shapes cannot be multiplied ({M}x{K} and {K2}x{N})")
+    qa, qw = qa.contiguous(), qw.contiguous()
+    sa, sw = sa.contiguous().float(), sw.contiguous().float()
+    if sa.numel() != M or sw.numel() != N:
+        raise ValueError("scale sizes do not match the operands")
+    b = None if bias is None else bias.contiguous().float()
+    out = torch.empty((M, N), dtype=torch.float32, device=qa.device)
+    acc = torch.empty((M, N), dtype=torch.int32, device=qa.device) if want_acc else None
+    check(lib().bq_gemm_i8(qa.data_ptr(), qw.data_ptr(), M, N, K, sa.data_ptr(), sw.data_ptr(), _ptr(b), act,
+                           out.data_ptr(), _ptr(acc), _stream(qa)))
+    return (out, acc) if want_acc else out
+
+
+def conv2d_i8_nhwc(qx, sa, wq: Int8ConvWeight, stride=1, pad=0, bias=None, residual=None, act=ACT_NONE,
+                   want_acc=False):
+    """Implicit-GEMM int8 conv on NHWC int8 ``qx [N, H, W, Cpad]`` (bq_conv2d_i8_nhwc).
+    Returns f32 NCHW-shaped output in channels-last memory (NHWC bytes), optionally with
+    the int32 accumulators ``[N*OH*OW, O]``. ``residual`` is NCHW-shaped (any layout)."""
+    _need(qx, "x", torch.int8)
+    N, H, W, C = qx.shape
+    if C != wq.cpad:
+        raise RuntimeError(f"channels do not match: input {C}, filter {wq.cpad}")
+    OH = (H + 2 * pad - wq.KH) // stride + 1
+    OW = (W + 2 * pad - wq.KW) // stride + 1
+    if OH < 1 or OW < 1:
+        raise RuntimeError("the filter is larger than the input.")
+    out = torch.empty((N, wq.O, OH, OW), dtype=torch.float32, device=qx.device, memory_format=torch.channels_last)
+    res = None
+    if residual is not None:
+        if tuple(residual.shape) != (N, wq.O, OH, OW):
+            raise RuntimeError(f"residual shape {tuple(residual.shape)} != output {(N, wq.O, OH, OW)}")
+        res = residual.float().contiguous(memory_format=torch.channels_last)
+    acc = torch.empty((N * OH * OW, wq.O), dtype=torch.int32, device=qx.device) if want_acc else None
+    b = None if bias is None else bias.contiguous().float()
+    check(lib().bq_conv2d_i8_nhwc(qx.contiguous().data_ptr(), N, H, W, C, wq.q.data_ptr(), wq.O, wq.KH, wq.KW,
+                                  stride, pad, sa.data_ptr(), wq.s.data_ptr(), _ptr(b), _ptr(res), act,
+                                  out.data_ptr(), _ptr(acc), _stream(qx)))
+    return (out, acc) if want_acc else out
+
+
+def dwconv_i8_nhwc(qx, sa, wq: Int8DwWeight, stride=1, pad=0, bias=None, act=ACT_NONE, want_acc=False):
+    """Depthwise int8 conv on NHWC int8 ``qx [N, H, W, Cpad]`` (bq_dwconv_i8_nhwc).
+    Returns f32 ``[N, Cpad, OH, OW]`` in channels-last memory (and int32 NHWC acc)."""
+    _need(qx, "x", torch.int8)
+    N, H, W, C = qx.shape
+    if C != wq.cpad:
+        raise RuntimeError(f"channels do not match: input {C}, filter {wq.cpad}")
+    OH = (H + 2 * pad - wq.KH) // stride + 1
+    OW = (W + 2 * pad - wq.KW) // stride + 1
+    if OH < 1 or OW < 1:
+        raise RuntimeError("the filter is larger than the input.")
+    out = torch.empty((N, C, OH, OW), dtype=torch.float32, device=qx.device, memory_format=torch.channels_last)
+    acc = torch.empty((N, OH, OW, C), dtype=torch.int32, device=qx.device) if want_acc else None
+    b = None
+    if bias is not None:
+        b = bias.contiguous().float()
+        if b.numel() != C:
+            b = torch.nn.functional.pad(b, (0, C - b.numel()))
+    check(lib().bq_dwconv_i8_nhwc(qx.contiguous().data_ptr(), N, H, W, C, wq.q.data_ptr(), wq.KH, wq.KW, stride,
+                                  pad, sa.data_ptr(), wq.s.data_ptr(), _ptr(b), act, out.data_ptr(), _ptr(acc),
+                                  _stream(qx)))
+    return (out, acc) if want_acc else out
+
+
+# ----------------------------------------------------------------- float-in, float-out
+
+def linear(x: torch.Tensor, w8: Int8Weight, bias=None, act=ACT_NONE) -> torch.Tensor:
+    """Dynamic-quant int8 Linear: per-row activations, per-channel weights, f32 out
+    ``[..., N]`` (the numpy core's ``x @ W.T + b``, borch/_nn.py:413-415, in W8A8)."""
+    if x.shape[-1] != w8.in_features:
+        a = "x".join(str(n) for n in (x.reshape(-1, x.shape[-1]).shape if x.dim() else ()))
+        raise RuntimeError(
+            f"mat1 and mat2 shapes cannot be multiplied ({a} and {w8.in_features}x{w8.out_features})")
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, x.shape[-1])
+    if w8.kpad != w8.in_features:
+        x2 = torch.nn.functional.pad(x2, (0, w8.kpad - w8.in_features))
+    qa, sa = quantize_rows(x2)
+    out = gemm_i8(qa, w8.q, sa, w8.s, bias, act)
+    return out.reshape(*lead, w8.out_features)
+
+
+def conv2d(x: torch.Tensor, w8: Int8ConvWeight, bias=None, stride=1, padding=0, act=ACT_NONE,
+           residual=None) -> torch.Tensor:
+    """Dynamic-quant int8 conv (per-tensor activation scale, tensor.ts:11915-11920):
+    quantize into NHWC, implicit GEMM, fused epilogue; NCHW-shaped channels-last out."""
+    if x.dim() != 4:
+        raise RuntimeError(f"conv2d expects a 4-D input, got {x.dim()}-D")
+    if x.shape[1] != w8.C:
+        raise RuntimeError(f"channels do not match: input {x.shape[1]}, filter {w8.C}")
+    qx, sa = quantize_nhwc(x, w8.cpad)
+    return conv2d_i8_nhwc(qx, sa, w8, stride, padding, bias, residual, act)
+
+
+def depthwise_conv2d(x: torch.Tensor, w8: Int8DwWeight, bias=None, stride=1, padding=0,
+                     act=ACT_NONE) -> torch.Tensor:
+    """Dynamic-quant int8 depthwise conv; NCHW-shaped channels-last f32 out."""
+    if x.dim() != 4 or x.shape[1] != w8.C:
+        raise RuntimeError(f"channels do not match: input {x.shape[1]}, filter {w8.C}")
+    qx, sa = quantize_nhwc(x, w8.cpad)
+    out = dwconv_i8_nhwc(qx, sa, w8, stride, padding, bias, act)
+    return out if w8.cpad == w8.C else out[:, : w8.C]

@@ -1,0 +1,68 @@
+"""Fused modules in the place of ``torch.ao.nn.intrinsic`` (borch-ts/src/nn.ts:6698-6750).
+
+Each wraps a (BN-folded) conv or linear and fuses the ReLU and/or the residual add into
+its kernel's epilogue: ``y = ((f32(acc)·sA)·sW) + b (+ residual)``, then ReLU
+(kernels.ts:4230-4244's ``ConvEpilogue`` order). On the f32 path the same arithmetic
+runs as separate torch ops.
+"""
+from __future__ import annotations
+
+import torch.nn as _tnn
+
+from .. import int8 as _i8
+
+
+class ConvReLU2d(_tnn.Module):
+    """``relu(conv(x))`` in one kernel (nn.ts:6698-6711)."""
+
+    def __init__(self, conv, relu=None):
+        super().__init__()
+        self.conv = conv
+        self.conv.act = _i8.ACT_RELU
+        self.training = False
+
+    def forward(self, x):
+        return self.conv(x)
+
+
+class ConvAdd2d(_tnn.Module):
+    """``conv(x1) + x2`` in one kernel (nn.ts:6717-6731)."""
+
+    def __init__(self, conv):
+        super().__init__()
+        self.conv = conv
+        self.conv.act = _i8.ACT_NONE
+        self.training = False
+
+    def forward(self, x, residual=None):
+        if residual is None:
+            raise TypeError("ConvAdd2d.forward takes (x1, x2)")
+        return self.conv(x, residual)
+
+
+class ConvAddReLU2d(_tnn.Module):
+    """``relu(conv(x1) + x2)`` in one kernel (nn.ts:6736-6750)."""
+
+    def __init__(self, conv):
+        super().__init__()
+        self.conv = conv
+        self.conv.act = _i8.ACT_RELU
+        self.training = False
+
+    def forward(self, x, residual=None):
+        if residual is None:
+            raise TypeError("ConvAddReLU2d.forward takes (x1, x2)")
+        return self.conv(x, residual)
+
+
+class LinearReLU(_tnn.Module):
+    """``relu(linear(x))`` in one kernel (torch.ao.nn.intrinsic.LinearReLU)."""
+
+    def __init__(self, linear, relu=None):
+        super().__init__()
+        self.linear = linear
+        self.linear.act = _i8.ACT_RELU
+        self.training = False
+
+    def forward(self, x):
+        return self.linear(x)

@@ -1,0 +1,127 @@
+/*
+ * libbq — int8 (W8A8) inference kernels for AMD Instinct MI355X (gfx950).
+ *
+ * The C ABI of the drop-in boundary. Every pointer argument except `ws` is caller-owned
+ * device memory (for example `torch.Tensor.data_ptr()`); the library allocates nothing
+ * (scratch memory is the caller's `ws`). Every call enqueues on `stream` (a hipStream_t
+ * handle; NULL = the null stream) and returns without a host synchronisation.
+ *
+ * Return value: BQ_OK (0) or a negative BQ_ERR_*; the message of the last failure on
+ * the calling thread is bq_last_error(). No C++ exception crosses this boundary.
+ *
+ * Arithmetic (one rule for weights and activations):
+ *   s = float32(max|v| / 127)                 correctly rounded
+ *   q = clip(rint(f64(v) / f64(s)), -127, 127) exact quotient, round half to even
+ *   s == 0 (all-zero row / tensor)  ->  q = 0
+ *   acc = sum_k qa * qw                        exact int32
+ *   y = ((f32(acc) * sA) * sW[n]) + bias[n], then + residual, then the activation,
+ *       one float32 rounding per operation.
+ *
+ * Reference interfaces replaced (paths into playidea-lab/borch):
+ *   quantizers   borch-ts/src/quant.ts:23-103, kernels.ts:2024-2081
+ *   GEMM         borch-ts/src/kernels.ts:1782-1857 (matmulInt8), called where the numpy
+ *                core runs nn.Linear / F.linear (borch/_nn.py:397-415, 4675-4677)
+ *   conv         borch-ts/src/kernels.ts:2084-2302 (convForwardInt8) + 5834-5914
+ *                (sumSplitsConv), called from Tensor.convNDFusedInt8 (tensor.ts:11869-11958)
+ *   depthwise    borch-ts/src/kernels.ts:5932-5968 (depthwiseForward, f32 in the
+ *                reference) and borch-ts/wasm/src/lib.rs:598-641 (dwconv_rows)
+ */
+#ifndef BQ_H
+#define BQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* bq_stream_t; /* a hipStream_t; NULL = the null stream */
+
+#define BQ_OK 0
+#define BQ_ERR_ARG (-1)         /* bad pointer, size, alignment or shape */
+#define BQ_ERR_DEVICE (-2)      /* no device, or not gfx950 */
+#define BQ_ERR_LAUNCH (-3)      /* the kernel launch failed */
+#define BQ_ERR_UNSUPPORTED (-4) /* a shape this library does not take */
+
+#define BQ_ACT_NONE 0
+#define BQ_ACT_RELU 1
+#define BQ_ACT_SILU 2
+
+/* Library version, (major << 16) | minor. */
+int bq_version(void);
+
+/* The message of the last failing call on this thread ("" if none). */
+const char* bq_last_error(void);
+
+/* 1 if `device` is a gfx950 (MI350/MI355X) the kernels were built for, else 0 with the
+ * reason in bq_last_error(). Replaces the capability gate Device.subgroupInt8
+ * (borch-ts/src/device.ts:466-482, refused by name at nn.ts:6771-6773). */
+int bq_device_ok(int device);
+
+/* Per-row dynamic activation quantization: x f32 [M, K] row-major -> q int8 [M, K],
+ * s f32 [M]. One pass over x. Replaces absMaxAtomic + quantizeActivationInt8
+ * (borch-ts/src/kernels.ts:2024-2081) with per-row scales. x, q: 16-byte aligned. */
+int bq_quantize_rows(const float* x, int64_t M, int64_t K, int8_t* q, float* s,
+                     bq_stream_t stream);
+
+/* Per-output-channel weight quantization of a Linear weight W f32 [N, K] -> q int8
+ * [N, K], s f32 [N]. Replaces quantizeInt8PerChannel (borch-ts/src/quant.ts:23-53); the
+ * same kernel and rule as bq_quantize_rows. */
+int bq_quantize_weight_per_channel(const float* w, int64_t N, int64_t K, int8_t* q,
+                                   float* s, bq_stream_t stream);
+
+/* Bytes of `ws` that bq_quantize_tensor / bq_quantize_nhwc need for n elements. */
+size_t bq_quantize_tensor_ws_bytes(int64_t n);
+
+/* Per-tensor quantization of x f32 [n] -> q int8 [n], s f32 [1]. Two kernels: partial
+ * maxima into ws, then quantize. Replaces absMaxAtomic + quantizeActivationInt8
+ * (borch-ts/src/kernels.ts:2024-2081). */
+int bq_quantize_tensor(const float* x, int64_t n, int8_t* q, float* s, void* ws,
+                       size_t ws_bytes, bq_stream_t stream);
+
+/* Per-tensor quantization of a channels-last activation x f32 [P, C] (P = N*H*W pixels)
+ * into q int8 [P, Cpad], channels C..Cpad-1 zero, s f32 [1]. The conv input
+ * (tensor.ts:11909-11921; kernels.ts:2057-2081 packs NC/4HW4, this packs NHWC). */
+int bq_quantize_nhwc(const float* x, int64_t P, int64_t C, int64_t Cpad, int8_t* q, float* s,
+                     void* ws, size_t ws_bytes, bq_stream_t stream);
+
+/* W8A8 GEMM with the fused dequant epilogue, Linear layout (x @ W.T):
+ *   A int8 [M, K] (per-row scales sA f32 [M]), W int8 [N, K] (per-channel sW f32 [N]),
+ *   out f32 [M, N] = ((f32(A @ W.T) * sA[m]) * sW[n]) + bias[n] (bias nullable), then
+ *   the activation `act` (BQ_ACT_*). `acc` (nullable) receives the exact int32 [M, N].
+ * K % 16 == 0; A, W 16-byte aligned. Replaces matmulInt8(M,K,N,scaled)
+ * (borch-ts/src/kernels.ts:1808-1852), which took only whole 32s. */
+int bq_gemm_i8(const int8_t* A, const int8_t* W, int64_t M, int64_t N, int64_t K,
+               const float* sA, const float* sW, const float* bias, int act, float* out,
+               int32_t* acc, bq_stream_t stream);
+
+/* Implicit-GEMM int8 convolution, NHWC, groups 1, dilation 1:
+ *   x int8 [N, H, W, C] (C % 16 == 0, per-tensor scale sA f32 [1]),
+ *   w int8 [O, KH, KW, C] (per-channel scale sW f32 [O]),
+ *   out f32 [N, OH, OW, O] = ((f32(acc) * sA) * sW[o]) + bias[o] + residual, then act.
+ * bias, residual (f32 [N, OH, OW, O]) and acc (int32 [N*OH*OW, O]) are nullable.
+ * Replaces convForwardInt8 (+ sumSplitsConv) and its ConvEpilogue
+ * (borch-ts/src/kernels.ts:2156-2302, 4230-4244, 5860-5914), which took stride 1, k <= 3,
+ * C % 32 and O % 16 only. */
+int bq_conv2d_i8_nhwc(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t C,
+                      const int8_t* w, int64_t O, int64_t KH, int64_t KW, int64_t stride,
+                      int64_t pad, const float* sA, const float* sW, const float* bias,
+                      const float* residual, int act, float* out, int32_t* acc,
+                      bq_stream_t stream);
+
+/* Depthwise int8 convolution, NHWC (groups = C, channel multiplier 1):
+ *   x int8 [N, H, W, C] (C % 4 == 0, per-tensor sA f32 [1]), w int8 [KH*KW, C]
+ *   (per-channel sW f32 [C]), out f32 [N, OH, OW, C] with the same epilogue.
+ * Replaces depthwiseForward (borch-ts/src/kernels.ts:5932-5968, f32 there) and
+ * dwconv_rows (borch-ts/wasm/src/lib.rs:598-641). */
+int bq_dwconv_i8_nhwc(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t C,
+                      const int8_t* w, int64_t KH, int64_t KW, int64_t stride, int64_t pad,
+                      const float* sA, const float* sW, const float* bias, int act,
+                      float* out, int32_t* acc, bq_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BQ_H */

@@ -1,0 +1,80 @@
+"""The C ABI library loads (no GPU needed) and exports exactly what include/bq.h declares;
+host-side argument checks run without touching a device."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "bq.h"
+
+
+def declared():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(bq_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_path():
+    names = declared()
+    for n in ("bq_quantize_rows", "bq_quantize_weight_per_channel", "bq_quantize_tensor", "bq_quantize_nhwc",
+              "bq_gemm_i8", "bq_conv2d_i8_nhwc", "bq_dwconv_i8_nhwc", "bq_device_ok", "bq_last_error"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    from borch_amd import _lib
+    lib = _lib.lib()
+    for name in declared():
+        assert hasattr(lib, name), name
+    assert sorted(_lib.SIGNATURES) == declared()
+
+
+def test_version_and_error_without_gpu():
+    from borch_amd import _lib
+    lib = _lib.lib()
+    assert lib.bq_version() >= 1
+    import torch
+    if not torch.cuda.is_available():
+        assert lib.bq_device_ok(0) == 0
+        assert "device" in _lib.last_error()
+
+
+def test_argument_checks_run_on_host():
+    """Bad sizes are refused before any launch (no device memory is touched)."""
+    from borch_amd import _lib
+    lib = _lib.lib()
+    assert lib.bq_gemm_i8(None, None, 4, 4, 20, None, None, None, 0, None, None, None) == _lib.BQ_ERR_UNSUPPORTED
+    assert "multiple of 16" in _lib.last_error()
+    assert lib.bq_gemm_i8(None, None, -1, 4, 16, None, None, None, 0, None, None, None) == _lib.BQ_ERR_ARG
+    assert lib.bq_gemm_i8(None, None, 4, 4, 16, None, None, None, 0, None, None, None) == _lib.BQ_ERR_ARG
+    assert lib.bq_conv2d_i8_nhwc(None, 1, 4, 4, 8, None, 8, 3, 3, 1, 1, None, None, None, None, 0, None, None,
+                                 None) == _lib.BQ_ERR_UNSUPPORTED
+    assert lib.bq_conv2d_i8_nhwc(None, 1, 2, 2, 16, None, 8, 5, 5, 1, 0, None, None, None, None, 0, None, None,
+                                 None) == _lib.BQ_ERR_ARG
+    assert "larger than the input" in _lib.last_error()
+    assert lib.bq_dwconv_i8_nhwc(None, 1, 4, 4, 6, None, 3, 3, 1, 1, None, None, None, 0, None, None,
+                                 None) == _lib.BQ_ERR_UNSUPPORTED
+    assert lib.bq_quantize_nhwc(None, 4, 3, 2, None, None, None, 0, None) == _lib.BQ_ERR_ARG
+    # zero-size work is a no-op success
+    assert lib.bq_gemm_i8(None, None, 0, 4, 16, None, None, None, 0, None, None, None) == 0
+
+
+def test_cpu_tensors_are_refused_by_name():
+    import torch
+    from borch_amd import int8
+    from borch_amd._lib import Int8Unavailable
+    with pytest.raises(Int8Unavailable, match="gfx950"):
+        int8.quantize_rows(torch.zeros(2, 16))
+
+
+def test_quantize_for_int8_refuses_without_device():
+    import torch
+    import borch_amd as bt
+    from borch_amd._lib import Int8Unavailable
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    m = bt.nn.Sequential(bt.nn.Linear(16, 8), bt.nn.ReLU())
+    with pytest.raises(Int8Unavailable, match="int8"):
+        bt.quantize_for_int8(m)

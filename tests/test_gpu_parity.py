@@ -1,0 +1,247 @@
+"""GPU parity: the HIP kernels through the C ABI against the CPU oracle on seeded inputs.
+
+Integer results (int8 packings, int32 accumulators) must be bit-exact. f32 outputs are
+held to the task's tolerance (1e-5 relative / 1e-6 absolute) and, since the epilogue does
+one float32 rounding per operation in the oracle's order, are also checked bit-exact.
+"""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from borch_amd import int8 as I
+from borch_amd import workloads as WL
+from oracle import quant as O
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-5, 1e-6
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def t(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def n(x):
+    return x.detach().cpu().numpy()
+
+
+def assert_f32(got, want):
+    np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
+    assert np.array_equal(got, want), f"max |diff| {np.abs(got - want).max()}"
+
+
+# ------------------------------------------------------------------------ quantizers
+
+@pytest.mark.parametrize("M,K", [(1, 16), (16, 512), (7, 1000), (3, 4096), (6304 // 16, 768), (5, 10000),
+                                 (4, 13), (2, 8192), (1, 3072)])
+def test_quantize_rows(dev, M, K):
+    say(f"quantize_rows M={M} K={K}")
+    rng = np.random.default_rng(M * 131 + K)
+    x = rng.normal(size=(M, K)).astype(np.float32) * np.float32(rng.uniform(0.1, 10))
+    if M > 2:
+        x[1] = 0.0
+    q, s = I.quantize_rows(t(x, dev))
+    qo, so = O.quantize_rows(x)
+    assert np.array_equal(n(s), so)
+    assert np.array_equal(n(q), qo)
+
+
+def test_quantize_rows_exact_ties(dev):
+    say("quantize_rows ties")
+    # peak 127 -> s = 1 exactly; k + 0.5 ties and their neighbours
+    ks = np.arange(-126, 126, dtype=np.float32)
+    row = np.concatenate([[127.0], ks + 0.5, np.nextafter(ks + 0.5, np.float32(200)),
+                          np.nextafter(ks + 0.5, np.float32(-200))]).astype(np.float32)
+    row = np.pad(row, (0, (-row.size) % 4))
+    x = np.stack([row, row * np.float32(0.5), -row]).astype(np.float32)
+    q, s = I.quantize_rows(t(x, dev))
+    qo, so = O.quantize_rows(x)
+    assert np.array_equal(n(s), so)
+    assert np.array_equal(n(q), qo)
+
+
+@pytest.mark.parametrize("shape,cpad,cl", [((2, 3, 8, 8), 16, False), ((2, 64, 16, 16), 64, True),
+                                          ((3, 24, 5, 7), 32, True), ((1, 5, 3, 3), 8, False)])
+def test_quantize_nhwc(dev, shape, cpad, cl):
+    say(f"quantize_nhwc {shape} cpad={cpad} channels_last={cl}")
+    rng = np.random.default_rng(sum(shape))
+    x = rng.normal(size=shape).astype(np.float32)
+    xt = t(x, dev)
+    if cl:
+        xt = xt.contiguous(memory_format=torch.channels_last)
+    q, s = I.quantize_nhwc(xt, cpad)
+    qo, so = O.quantize_act_nhwc(x, cpad)
+    assert np.array_equal(n(s), so)
+    assert np.array_equal(n(q), qo)
+
+
+def test_quantize_tensor(dev):
+    say("quantize_tensor")
+    rng = np.random.default_rng(11)
+    for size in (1, 7, 1000, 1 << 20, (1 << 20) + 3):
+        x = rng.normal(size=size).astype(np.float32)
+        q, s = I.quantize_tensor(t(x, dev))
+        qo, so = O.quantize_tensor(x)
+        assert np.array_equal(n(s), so) and np.array_equal(n(q), qo), size
+
+
+# ------------------------------------------------------------------------------ GEMM
+
+def test_c1_linear(dev):
+    """C1: the 16x512x512 int8 Linear, every stage against the oracle."""
+    say("C1 linear 16x512x512")
+    x, w, b = WL.c1_linear(0)
+    y_o, acc_o, (qx_o, sx_o), (qw_o, sw_o) = O.linear_int8(x, w, b)
+    qw, sw = I.quantize_weight_per_channel(t(w, dev))
+    assert np.array_equal(n(qw), qw_o) and np.array_equal(n(sw), sw_o)
+    qx, sx = I.quantize_rows(t(x, dev))
+    assert np.array_equal(n(qx), qx_o) and np.array_equal(n(sx), sx_o)
+    y, acc = I.gemm_i8(qx, qw, sx, sw, t(b, dev), want_acc=True)
+    assert np.array_equal(n(acc), acc_o)
+    assert_f32(n(y), y_o)
+
+
+@pytest.mark.parametrize("M", [1, 16, 256])
+def test_c2_gemm_full(dev, M):
+    say(f"C2 gemm M={M} K=N=4096 (full oracle)")
+    a, w, b = WL.c2_gemm(M, 0)
+    qa_o, sa_o = O.quantize_rows(a)
+    qw_o, sw_o = O.quantize_weight_per_channel(w)
+    acc_o = O.gemm_i8_i32(qa_o, qw_o)
+    y_o = O.dequant(acc_o, sa_o, sw_o, b)
+    qa, sa = I.quantize_rows(t(a, dev))
+    qw, sw = I.quantize_weight_per_channel(t(w, dev))
+    assert np.array_equal(n(qa), qa_o) and np.array_equal(n(qw), qw_o)
+    y, acc = I.gemm_i8(qa, qw, sa, sw, t(b, dev), want_acc=True)
+    assert np.array_equal(n(acc), acc_o)
+    assert_f32(n(y), y_o)
+
+
+def test_c2_gemm_4096(dev):
+    """C2 M=4096: exact on 256 sampled rows, and column/row checksums of every entry."""
+    say("C2 gemm M=4096 K=N=4096 (sampled rows + checksums)")
+    a, w, b = WL.c2_gemm(4096, 0)
+    qa, sa = I.quantize_rows(t(a, dev))
+    qw, sw = I.quantize_weight_per_channel(t(w, dev))
+    y, acc = I.gemm_i8(qa, qw, sa, sw, t(b, dev), want_acc=True)
+    qa_n, qw_n, acc_n, y_n = n(qa), n(qw), n(acc), n(y)
+    rows = np.random.default_rng(0).choice(4096, 256, replace=False)
+    qa_o, sa_o = O.quantize_rows(a[rows])
+    assert np.array_equal(qa_n[rows], qa_o)
+    qw_o, sw_o = O.quantize_weight_per_channel(w)
+    assert np.array_equal(qw_n, qw_o)
+    acc_o = O.gemm_i8_i32(qa_o, qw_o)
+    assert np.array_equal(acc_n[rows], acc_o)
+    assert_f32(y_n[rows], O.dequant(acc_o, sa_o, sw_o, b))
+    # checksums over all rows/cols (exact in int64)
+    A64, W64 = qa_n.astype(np.int64), qw_n.astype(np.int64)
+    assert np.array_equal(acc_n.astype(np.int64).sum(0), A64.sum(0) @ W64.T)
+    assert np.array_equal(acc_n.astype(np.int64).sum(1), A64 @ W64.sum(0))
+    # the f32 epilogue of every entry from the device's own accumulators
+    assert_f32(y_n, O.dequant(acc_n, n(sa), n(sw), b))
+
+
+@pytest.mark.parametrize("M,N,K", [(17, 33, 16), (65, 100, 48), (100, 1, 272), (300, 130, 4096 + 16),
+                                   (64, 64, 128), (129, 257, 1152), (6304, 768, 768), (2, 4100, 64)])
+@pytest.mark.parametrize("act", [0, 1])
+def test_gemm_shapes(dev, M, N, K, act):
+    say(f"gemm shape M={M} N={N} K={K} act={act}")
+    rng = np.random.default_rng(M + N + K)
+    qa = rng.integers(-127, 128, size=(M, K)).astype(np.int8)
+    qw = rng.integers(-127, 128, size=(N, K)).astype(np.int8)
+    sa = rng.uniform(1e-3, 1e-2, M).astype(np.float32)
+    sw = rng.uniform(1e-3, 1e-2, N).astype(np.float32)
+    b = rng.normal(size=N).astype(np.float32)
+    y, acc = I.gemm_i8(t(qa, dev), t(qw, dev), t(sa, dev), t(sw, dev), t(b, dev), act=act, want_acc=True)
+    acc_o = O.gemm_i8_i32(qa, qw)
+    assert np.array_equal(n(acc), acc_o)
+    assert_f32(n(y), O.dequant(acc_o, sa, sw, b, relu=bool(act)))
+
+
+def test_gemm_no_bias_extremes(dev):
+    say("gemm extremes (all +-127, K=4096)")
+    K = 4096
+    qa = np.full((80, K), 127, np.int8)
+    qa[1::2] = -127
+    qw = np.full((48, K), -127, np.int8)
+    sa = np.ones(80, np.float32)
+    sw = np.ones(48, np.float32)
+    y, acc = I.gemm_i8(t(qa, dev), t(qw, dev), t(sa, dev), t(sw, dev), None, want_acc=True)
+    assert np.array_equal(n(acc), O.gemm_i8_i32(qa, qw))
+
+
+# ------------------------------------------------------------------------------ conv
+
+CONV_CASES = [
+    # N, C, H, O, k, stride, pad
+    (2, 3, 32, 64, 3, 1, 1),     # ResNet stem (C padded to 16)
+    (2, 64, 32, 64, 3, 1, 1),
+    (2, 64, 32, 128, 3, 2, 1),
+    (2, 64, 32, 128, 1, 2, 0),   # downsample 1x1 stride 2
+    (2, 128, 16, 128, 3, 1, 1),
+    (2, 256, 8, 512, 3, 2, 1),
+    (2, 512, 4, 512, 3, 1, 1),
+    (1, 16, 9, 24, 5, 2, 2),
+    (2, 40, 7, 48, 1, 1, 0),     # 1x1 stride 1 (dense path), C padded to 48
+    (16, 64, 32, 64, 3, 1, 1),   # C3 full batch
+]
+
+
+@pytest.mark.parametrize("N,C,H,O_,k,stride,pad", CONV_CASES)
+def test_conv2d(dev, N, C, H, O_, k, stride, pad):
+    say(f"conv N={N} C={C} H={H} O={O_} k={k} s={stride} p={pad}")
+    rng = np.random.default_rng(N * C + H + O_ + k)
+    x = rng.normal(size=(N, C, H, H)).astype(np.float32)
+    w = (rng.normal(size=(O_, C, k, k)) * np.sqrt(2.0 / (C * k * k))).astype(np.float32)
+    b = rng.normal(size=O_).astype(np.float32) * np.float32(0.1)
+    OH = (H + 2 * pad - k) // stride + 1
+    res = rng.normal(size=(N, O_, OH, OH)).astype(np.float32)
+    cpad = I.round_up(C, 16)
+    w8 = I.pack_conv_weight(t(w, dev))
+    qw_o, sw_o = O.quantize_conv_weight(w, cpad)
+    assert np.array_equal(n(w8.q), qw_o) and np.array_equal(n(w8.s), sw_o)
+    for relu, residual in ((False, None), (True, res)):
+        y_o, acc_o, sa_o, _ = O.conv2d_int8(x, w, b, stride, pad, relu, residual, cpad)
+        qx, sa = I.quantize_nhwc(t(x, dev), cpad)
+        assert np.array_equal(n(sa), sa_o)
+        y, acc = I.conv2d_i8_nhwc(qx, sa, w8, stride, pad, t(b, dev), None if residual is None else t(residual, dev),
+                                  I.ACT_RELU if relu else I.ACT_NONE, want_acc=True)
+        assert np.array_equal(n(acc), acc_o)
+        assert_f32(n(y), y_o)
+
+
+DW_CASES = [(2, 32, 16, 3, 1, 1), (2, 96, 15, 3, 2, 1), (2, 144, 14, 5, 1, 2), (2, 240, 13, 5, 2, 2),
+            (1, 6, 7, 3, 1, 1), (4, 1152, 7, 5, 1, 2)]
+
+
+@pytest.mark.parametrize("N,C,H,k,stride,pad", DW_CASES)
+def test_dwconv(dev, N, C, H, k, stride, pad):
+    say(f"dwconv N={N} C={C} H={H} k={k} s={stride} p={pad}")
+    rng = np.random.default_rng(N + C + H + k)
+    x = rng.normal(size=(N, C, H, H)).astype(np.float32)
+    w = rng.normal(size=(C, 1, k, k)).astype(np.float32)
+    b = rng.normal(size=C).astype(np.float32)
+    cpad = I.round_up(C, 4)
+    w8 = I.pack_dw_weight(t(w, dev))
+    qw_o, sw_o = O.quantize_dw_weight(np.pad(w, ((0, cpad - C), (0, 0), (0, 0), (0, 0))))
+    assert np.array_equal(n(w8.q), qw_o) and np.array_equal(n(w8.s), sw_o)
+    qx_o, sa_o = O.quantize_act_nhwc(x, cpad)
+    acc_o = O.dwconv_i8_nhwc(qx_o, qw_o, k, k, stride, pad)
+    bp = np.pad(b, (0, cpad - C))
+    for act in (I.ACT_NONE, I.ACT_RELU, I.ACT_SILU):
+        qx, sa = I.quantize_nhwc(t(x, dev), cpad)
+        y, acc = I.dwconv_i8_nhwc(qx, sa, w8, stride, pad, t(b, dev), act, want_acc=True)
+        assert np.array_equal(n(acc), acc_o)
+        y_o = O.dequant(acc_o.reshape(-1, cpad), sa_o[0], sw_o, bp, relu=(act == I.ACT_RELU))
+        if act == I.ACT_SILU:
+            y_o = O.silu(y_o)
+            np.testing.assert_allclose(n(y).transpose(0, 2, 3, 1).reshape(-1, cpad), y_o, rtol=RTOL, atol=ATOL)
+        else:
+            assert_f32(n(y).transpose(0, 2, 3, 1).reshape(-1, cpad), y_o)

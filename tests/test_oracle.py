@@ -1,0 +1,303 @@
+"""Pins the CPU oracle (oracle/quant.py) against the reference's golden values, exact
+rational arithmetic, brute force on tiny inputs and closed forms — never against a
+retyped copy of its own formula."""
+import json
+import struct
+from fractions import Fraction
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import quant as O
+
+GOLD = json.loads((Path(__file__).parent / "golden" / "ref_fake_quantize.json").read_text())["cases"]
+
+
+def f32(v):
+    return struct.unpack("f", struct.pack("f", v))[0]
+
+
+# -------------------------------------------------------------- reference goldens
+
+def _fake_quant(x, scale, zp, qmin, qmax):
+    """round → +zp → clamp → dequant, built on the oracle's rounding core."""
+    r = O.round_quotient(np.asarray(x, np.float32), np.asarray(scale, np.float32))
+    q = np.clip(r + zp, qmin, qmax)
+    return ((q - zp) * np.asarray(scale, np.float64)).astype(np.float32)
+
+
+@pytest.mark.parametrize("key", ["top::fake_quantize(per_tensor)", "top::fake_quantize(zp=2)"])
+def test_reference_golden_per_tensor(key):
+    c = GOLD[key]
+    i = c["input"]
+    got = _fake_quant(i["x"], i["scale"], i["zero_point"], i["qmin"], i["qmax"])
+    assert got.tolist() == c["expected"]["values"]
+
+
+def test_reference_golden_per_channel():
+    c = GOLD["top::fake_quantize(per_channel)"]
+    i = c["input"]
+    x = np.asarray(i["x"], np.float32)
+    s = np.asarray(i["scale"], np.float32).reshape(-1, 1)
+    z = np.asarray(i["zero_point"], np.float64).reshape(-1, 1)
+    got = _fake_quant(x, s, z, i["qmin"], i["qmax"])
+    assert got.reshape(-1).tolist() == c["expected"]["values"]
+
+
+def test_reference_golden_grad_mask():
+    """The straight-through mask (1 inside the range) agrees with the oracle's rounding."""
+    c = GOLD["top::grad::fake_quantize"]
+    i = c["input"]
+    r = O.round_quotient(np.asarray(i["x"], np.float32), np.float32(i["scale"])) + i["zero_point"]
+    mask = ((r >= i["qmin"]) & (r <= i["qmax"])).astype(np.float32)
+    assert mask.tolist() == c["expected"]["values"]
+
+
+# ------------------------------------------------------------- exact rational checks
+
+def _exact_round(v, s):
+    """Round-half-even of the exact rational v/s (Fraction.__round__ is half-even)."""
+    if s == 0:
+        return 0
+    return max(-127, min(127, round(Fraction(v) / Fraction(s))))
+
+
+def test_round_quotient_matches_exact_rationals():
+    rng = np.random.default_rng(1)
+    v = rng.normal(size=4000).astype(np.float32) * np.float32(3)
+    s = rng.uniform(1e-3, 0.2, size=4000).astype(np.float32)
+    got = O.quantize_with_scale(v, s)
+    want = [_exact_round(float(a), float(b)) for a, b in zip(v, s)]
+    assert got.tolist() == want
+
+
+def test_exact_ties_round_half_even():
+    # s = 1/2, 1/4, 1 are exact; k + 0.5 ties must go to the even neighbour.
+    for s in (0.5, 0.25, 1.0, 2.0**-7):
+        ks = np.arange(-126, 126)
+        v = ((ks + 0.5) * s).astype(np.float32)
+        assert np.all((v.astype(np.float64) / s) == ks + 0.5)  # true ties
+        got = O.quantize_with_scale(v, np.float32(s)).astype(int)
+        want = [_exact_round(float(a), s) for a in v]
+        assert got.tolist() == want
+        assert np.all(got % 2 == 0)
+
+
+def test_near_ties_are_not_ties():
+    """One ulp either side of an exact tie rounds away from the tie's even choice."""
+    s = np.float32(0.5)
+    tie = np.float32(1.25)  # 2.5 * s
+    lo, hi = np.nextafter(tie, np.float32(0)), np.nextafter(tie, np.float32(10))
+    assert O.quantize_with_scale(np.array([lo, tie, hi], np.float32), s).tolist() == [2, 2, 3]
+
+
+def test_scale_is_correctly_rounded_f32():
+    rng = np.random.default_rng(2)
+    peaks = np.abs(rng.normal(size=2000)).astype(np.float32) * np.float32(10)
+    s = O.scale_of(peaks)
+    for p, sc in zip(peaks, s):
+        exact = Fraction(float(p)) / 127
+        err = abs(Fraction(float(sc)) - exact)
+        ulp = Fraction(float(np.spacing(sc)))
+        assert err <= ulp / 2
+
+
+def test_quantize_rows_invariants():
+    rng = np.random.default_rng(3)
+    x = rng.normal(size=(64, 300)).astype(np.float32)
+    x[5] = 0.0  # a zero row → s = 0, q = 0 (quant.ts:36)
+    q, s = O.quantize_rows(x)
+    assert s[5] == 0 and not q[5].any()
+    assert np.abs(q.astype(int)).max() <= 127
+    for m in range(64):
+        if m == 5:
+            continue
+        j = np.argmax(np.abs(x[m]))
+        assert abs(int(q[m, j])) == 127
+        err = np.abs(q[m].astype(np.float64) * s[m] - x[m].astype(np.float64))
+        assert np.all(err <= s[m] / 2 * (1 + 1e-6))
+
+
+def test_quantize_rows_hand_row():
+    x = np.array([[127.0, 2.5, 3.5, -0.5, -1.5, 0.49999997, -127.0, 126.5]], np.float32)
+    q, s = O.quantize_rows(x)
+    assert s.tolist() == [1.0]
+    assert q.tolist() == [[127, 2, 4, 0, -2, 0, -127, 126]]
+
+
+def test_pack_words_low_byte_first():
+    q = np.array([1, -1, 2, -128, 5], np.int8)
+    w = O.pack_words(q)
+    assert w.tolist() == [0x80_02_FF_01, 0x00_00_00_05]
+
+
+def test_quantize_tensor_and_nhwc_layout():
+    rng = np.random.default_rng(4)
+    x = rng.normal(size=(2, 3, 4, 5)).astype(np.float32)
+    q, s = O.quantize_act_nhwc(x, cpad=16)
+    assert q.shape == (2, 4, 5, 16) and not q[..., 3:].any()
+    qt, st = O.quantize_tensor(x)
+    assert s == st
+    assert np.array_equal(q[..., :3], qt.transpose(0, 2, 3, 1))
+    assert np.array_equal(qt, O.quantize_with_scale(x, np.float32(np.abs(x).max() / np.float32(127))))
+
+
+# -------------------------------------------------------------------- integer GEMM
+
+def _lcg_int8(n, seed):
+    """kernel_bench.html:300-301: st = st·1664525 + 1013904223 (u32), int8 = (st>>>28) − 8."""
+    out = np.empty(n, np.int8)
+    st = seed
+    for i in range(n):
+        st = (st * 1664525 + 1013904223) & 0xFFFFFFFF
+        out[i] = (st >> 28) - 8
+    return out
+
+
+def _brute_gemm(a, w):
+    M, K = a.shape
+    N = w.shape[0]
+    out = np.zeros((M, N), np.int64)
+    for m in range(M):
+        for n in range(N):
+            s = 0
+            for k in range(K):
+                s += int(a[m, k]) * int(w[n, k])
+            out[m, n] = s
+    return out
+
+
+@pytest.mark.parametrize("M,K,N", [(32, 32, 32), (5, 48, 7), (1, 64, 3)])
+def test_gemm_matches_brute_force_lcg(M, K, N):
+    a = _lcg_int8(M * K, 7).reshape(M, K)
+    w = _lcg_int8(K * N, 11).reshape(N, K)
+    assert np.array_equal(O.gemm_i8_i32(a, w), _brute_gemm(a, w))
+
+
+def test_gemm_closed_forms():
+    K = 4096
+    a = np.full((2, K), 127, np.int8)
+    a[1] = -127
+    w = np.full((3, K), -127, np.int8)
+    acc = O.gemm_i8_i32(a, w)
+    assert acc[0].tolist() == [-K * 16129] * 3 and acc[1].tolist() == [K * 16129] * 3
+    eye = np.eye(16, dtype=np.int8)
+    x = np.arange(-8, 8, dtype=np.int8).reshape(1, 16).repeat(4, 0)
+    assert np.array_equal(O.gemm_i8_i32(x, eye), x.astype(np.int32))
+
+
+# ----------------------------------------------------------------------- epilogue
+
+def test_dequant_order_and_rounding():
+    rng = np.random.default_rng(5)
+    acc = rng.integers(-2**26, 2**26, size=(7, 9)).astype(np.int32)
+    sA = rng.uniform(0.001, 0.1, 7).astype(np.float32)
+    sW = rng.uniform(0.001, 0.1, 9).astype(np.float32)
+    b = rng.normal(size=9).astype(np.float32)
+    res = rng.normal(size=(7, 9)).astype(np.float32)
+    y = O.dequant(acc, sA, sW, b, relu=True, residual=res)
+    for m in range(7):
+        for n in range(9):
+            v = f32(f32(f32(float(acc[m, n])) * float(sA[m])) * float(sW[n]))
+            v = f32(f32(v + float(b[n])) + float(res[m, n]))
+            v = v if v > 0 else 0.0
+            assert y[m, n] == np.float32(v)
+    # hand value: 1000 * 0.5 * 0.25 + 1 = 126
+    assert O.dequant(np.array([[1000]]), np.float32(0.5), np.array([0.25], np.float32),
+                     np.array([1.0], np.float32))[0, 0] == 126.0
+
+
+# ---------------------------------------------------------------------------- conv
+
+def _brute_conv(xq, wq, KH, KW, stride, pad):
+    """Direct loops as kernel_bench.html:406-413, NHWC x, [O][KH][KW][C] w."""
+    N, H, W, C = xq.shape
+    O_ = wq.shape[0]
+    w4 = wq.reshape(O_, KH, KW, C).astype(np.int64)
+    OH = (H + 2 * pad - KH) // stride + 1
+    OW = (W + 2 * pad - KW) // stride + 1
+    out = np.zeros((N, OH, OW, O_), np.int64)
+    for n in range(N):
+        for oy in range(OH):
+            for ox in range(OW):
+                for kh in range(KH):
+                    iy = oy * stride - pad + kh
+                    if iy < 0 or iy >= H:
+                        continue
+                    for kw in range(KW):
+                        ix = ox * stride - pad + kw
+                        if ix < 0 or ix >= W:
+                            continue
+                        out[n, oy, ox] += w4[:, kh, kw, :] @ xq[n, iy, ix].astype(np.int64)
+    return out.reshape(-1, O_)
+
+
+@pytest.mark.parametrize("KH,stride,pad", [(3, 1, 1), (3, 2, 1), (1, 2, 0), (5, 1, 2), (1, 1, 0)])
+def test_conv_matches_brute_force(KH, stride, pad):
+    rng = np.random.default_rng(6)
+    xq = rng.integers(-127, 128, size=(2, 7, 6, 5)).astype(np.int8)
+    wq = rng.integers(-127, 128, size=(4, KH * KH * 5)).astype(np.int8)
+    acc, OH, OW = O.conv2d_i8_nhwc(xq, wq, KH, KH, stride, pad)
+    assert np.array_equal(acc, _brute_conv(xq, wq, KH, KH, stride, pad))
+
+
+@pytest.mark.parametrize("KH,stride,pad", [(3, 1, 1), (3, 2, 1), (5, 1, 2), (5, 2, 2)])
+def test_dwconv_matches_brute_force(KH, stride, pad):
+    rng = np.random.default_rng(7)
+    N, H, W, C = 2, 9, 8, 6
+    xq = rng.integers(-127, 128, size=(N, H, W, C)).astype(np.int8)
+    wq = rng.integers(-127, 128, size=(KH * KH, C)).astype(np.int8)
+    got = O.dwconv_i8_nhwc(xq, wq, KH, KH, stride, pad)
+    # brute force: each channel is a single-channel conv
+    for c in range(C):
+        one = _brute_conv(xq[..., c:c + 1], wq[:, c].reshape(1, -1), KH, KH, stride, pad)
+        assert np.array_equal(got[..., c].reshape(-1), one[:, 0])
+
+
+def test_conv_f32_matches_torch():
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(8)
+    x = rng.normal(size=(2, 3, 9, 9)).astype(np.float32)
+    w = rng.normal(size=(4, 3, 3, 3)).astype(np.float32)
+    b = rng.normal(size=4).astype(np.float32)
+    for stride, pad in ((1, 1), (2, 1), (2, 0)):
+        got = O.conv2d_f32(x, w, b, stride, pad)
+        want = torch.nn.functional.conv2d(torch.from_numpy(x), torch.from_numpy(w), torch.from_numpy(b),
+                                          stride, pad).numpy()
+        np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5)
+
+
+def test_conv_weight_layout_matches_f32_conv():
+    """The [O][KH][KW][C] packing with im2col reproduces the f32 conv on exact values."""
+    rng = np.random.default_rng(9)
+    x = rng.integers(-3, 4, size=(1, 5, 6, 6)).astype(np.float32)
+    w = rng.integers(-3, 4, size=(3, 5, 3, 3)).astype(np.float32)
+    xq = x.transpose(0, 2, 3, 1).astype(np.int8)
+    wq = w.transpose(0, 2, 3, 1).reshape(3, -1).astype(np.int8)
+    acc, OH, OW = O.conv2d_i8_nhwc(xq, wq, 3, 3, 1, 1)
+    ref = O.conv2d_f32(x, w, None, 1, 1)
+    assert np.array_equal(acc.reshape(1, OH, OW, 3).transpose(0, 3, 1, 2), ref.astype(np.int32))
+
+
+def test_bn_fold_equals_conv_then_bn():
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(10)
+    w = rng.normal(size=(4, 3, 3, 3)).astype(np.float32)
+    rm, rv = rng.normal(size=4).astype(np.float32) * 0.1, rng.uniform(0.5, 1.5, 4).astype(np.float32)
+    g, be = (1 + 0.1 * rng.normal(size=4)).astype(np.float32), (0.1 * rng.normal(size=4)).astype(np.float32)
+    x = rng.normal(size=(2, 3, 8, 8)).astype(np.float32)
+    fw, fb = O.fuse_conv_bn_weights(w, None, rm, rv, 1e-5, g, be)
+    y = torch.nn.functional.conv2d(torch.from_numpy(x), torch.from_numpy(w), None, 1, 1)
+    y = torch.nn.functional.batch_norm(y, torch.from_numpy(rm), torch.from_numpy(rv), torch.from_numpy(g),
+                                       torch.from_numpy(be), False, 0.0, 1e-5)
+    np.testing.assert_allclose(O.conv2d_f32(x, fw, fb, 1, 1), y.numpy(), rtol=1e-4, atol=1e-5)
+
+
+def test_linear_int8_close_to_f32():
+    """The quantized Linear stays near the f32 one (accuracy sanity, not parity)."""
+    from borch_amd import workloads as WL
+    x, w, b = WL.c1_linear(0)
+    y, acc, _, _ = O.linear_int8(x, w, b)
+    ref = O.linear_f32(x, w, b)
+    assert np.abs(y - ref).max() < 0.05 * np.abs(ref).max()
