@@ -23,7 +23,7 @@ LIB = LIBDIR / "libbq.so"
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
-    "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
+    "-O3", "-std=c++20", "-fPIC", f"--offload-arch={ARCH}",
     "-mcode-object-version=5",
     "-ffp-contract=off",
     # packed-fp32 instructions are kept out of the generated code

@@ -47,6 +47,8 @@ __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
          ((uint32_t)(d & 0xff) << 24);
 }
 
+__device__ __forceinline__ float silu(float v) { return __fdiv_rn(v, __fadd_rn(1.0f, expf(-v))); }
+
 // The f32 epilogue, one rounding per operation (no contraction into FMA):
 // y = ((f32(acc) * sa) * sw) + b, then + residual, then relu.
 __device__ __forceinline__ float dequant_one(int acc, float sa, float sw, float b, bool has_b,
@@ -55,7 +57,7 @@ __device__ __forceinline__ float dequant_one(int acc, float sa, float sw, float 
   if (has_b) v = __fadd_rn(v, b);
   if (has_r) v = __fadd_rn(v, r);
   if (act == BQ_ACT_RELU) v = v > 0.f ? v : 0.f;
-  else if (act == BQ_ACT_SILU) v = __fdiv_rn(v, __fadd_rn(1.0f, expf(-v)));
+  else if (act == BQ_ACT_SILU) v = silu(v);
   return v;
 }
 

@@ -14,6 +14,10 @@
 // Skinny path (M <= 64): the weight is streamed once at HBM rate. A workgroup owns 16
 // output channels; its waves split K; each lane loads 64 contiguous weight bytes per step
 // and v_mfma_i32_16x16x64_i8 multiplies them against up to four 16-row activation tiles.
+#include <stdlib.h>
+
+#include <utility>
+
 #include "bq_common.h"
 
 namespace bq {
@@ -32,33 +36,68 @@ struct GemmP {
   int32_t* acc;  // [M, N] or null
   // conv geometry (CONV only)
   int H, Wd, C, OH, OW, KWd, stride, pad;
+  int64_t Nimg_HWC;  // conv: bytes of the NHWC activation
+  int vec_ok;        // N % 4 == 0 and out/res/acc 16-byte aligned: float4 epilogue
 };
 
 constexpr int BK = 128;  // bytes of K per LDS stage: one cache line per row
 
-// Byte offset of 16-byte chunk `c` (0..7) of LDS row `r`, XOR-swizzled so that the
-// 16 lanes of an MFMA fragment read (16 consecutive rows, one chunk) hit distinct banks.
-template <int SWZ>
-__device__ __forceinline__ int lds_off(int r, int c) {
-  return r * BK + ((c ^ ((r >> SWZ) & 7)) << 4);
+// Buffer resources: raw (stride 0) descriptors whose range check returns zero for any
+// 16-byte load at or past `bytes` — the tile edges (rows past M or N, the K tail, conv
+// padding) become zeros without a branch. OOB is the offset that is always out of range.
+constexpr uint32_t OOB = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, int SWZ, bool CONV>
+__device__ __forceinline__ v4i buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+// Byte offset of 16-byte chunk `c` (0..7) of LDS row `r`. The chunk index is XORed with
+// bits 1..3 of the row: the 16 lanes that read one MFMA fragment (16 consecutive rows,
+// one chunk) then cover all 64 four-byte banks exactly once (rows 2j and 2j+1 sit in the
+// two 128-byte halves of the 256-byte bank line). Measured: zero LDS bank conflicts.
+__device__ __forceinline__ int lds_off(int r, int c) { return r * BK + ((c ^ ((r >> 1) & 7)) << 4); }
+
+// Workgroup -> output tile. Workgroups are dispatched round-robin over the 8 XCDs (each
+// with its own L2), so workgroup id is first regrouped by XCD, then tiles are handed out
+// in bands of 8 tile columns walking down M: the 32 workgroups of one XCD at a 4096^2
+// problem cover a 4 x 8 block of tiles, and each K step's A and W slabs are fetched into
+// that XCD's L2 once and then shared.
+__device__ __forceinline__ void tile_of(int id, int G, int tiles_m, int tiles_n, int& bm, int& bn) {
+  constexpr int XCDS = 8;
+  if (G % XCDS == 0) id = (id % XCDS) * (G / XCDS) + id / XCDS;
+  constexpr int GROUP = 8;
+  const int per_group = GROUP * tiles_m;
+  const int g = id / per_group;
+  const int first_n = g * GROUP;
+  const int gsize = min(tiles_n - first_n, GROUP);
+  const int in = id - g * per_group;
+  bm = in / gsize;
+  bn = first_n + in % gsize;
+}
+
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool CONV>
 __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const GemmP p) {
   constexpr int T = WAVES_M * WAVES_N * 64;
   constexpr int WTM = BM / WAVES_M;  // wave tile rows
   constexpr int WTN = BN / WAVES_N;
   constexpr int TM = WTM / 32;
   constexpr int TN = WTN / 32;
-  constexpr int ROWS_PER_PASS = T / 8;  // rows a pass of all threads loads (8 chunks a row)
+  constexpr int ROWS_PER_PASS = T / 8;  // rows one pass of all threads loads (8 chunks a row)
   constexpr int A_LD = BM / ROWS_PER_PASS;
   constexpr int B_LD = BN / ROWS_PER_PASS;
   static_assert(BM % ROWS_PER_PASS == 0 && BN % ROWS_PER_PASS == 0, "tile/threads");
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile");
 
   __shared__ __attribute__((aligned(16))) int8_t lds[2 * (BM + BN) * BK];
-  int8_t* As = lds;                 // [2][BM][BK]
-  int8_t* Bs = lds + 2 * BM * BK;   // [2][BN][BK]
+  // Per-tile scales and bias, staged once so the epilogue reads no global memory: on
+  // gfx9 stores and loads share one counter, and a load between stores waits for them.
+  __shared__ __attribute__((aligned(16))) float s_sa[BM];
+  __shared__ __attribute__((aligned(16))) float s_sw[BN];
+  __shared__ __attribute__((aligned(16))) float s_b[BN];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -66,63 +105,58 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
   const int wm = wave / WAVES_N;
   const int wn = wave % WAVES_N;
 
-  // Grid swizzle: consecutive workgroups walk down M within a column band of 8 tiles so
-  // the W tiles they share stay in L2.
   const int tiles_m = (p.M + BM - 1) / BM;
+  const int tiles_n = (p.N + BN - 1) / BN;
   int bm, bn;
-  {
-    const int id = blockIdx.x;
-    constexpr int GROUP = 8;
-    const int tiles_n = (p.N + BN - 1) / BN;
-    const int per_group = GROUP * tiles_m;
-    const int g = id / per_group;
-    const int first_n = g * GROUP;
-    const int gsize = min(tiles_n - first_n, GROUP);
-    const int in = id - g * per_group;
-    bm = in / gsize;
-    bn = first_n + in % gsize;
-  }
+  tile_of(blockIdx.x, gridDim.x, tiles_m, tiles_n, bm, bn);
   const int m0 = bm * BM;
   const int n0 = bn * BN;
 
-  // Each thread loads chunk `kc` of rows (tid >> 3) + i * ROWS_PER_PASS.
+  for (int i = tid; i < BM; i += T) {
+    const int m = m0 + i;
+    s_sa[i] = m < p.M ? p.sA[p.sa_per_row ? m : 0] : 0.f;
+  }
+  for (int i = tid; i < BN; i += T) {
+    const int n = n0 + i;
+    s_sw[i] = n < p.N ? p.sW[n] : 0.f;
+    s_b[i] = (n < p.N && p.bias) ? p.bias[n] : 0.f;
+  }
+
+  // Each thread loads 16-byte chunk `kc` of rows lr + i * ROWS_PER_PASS.
   const int kc = tid & 7;
   const int lr = tid >> 3;
 
-  // Per-row source bases for A.
-  const int8_t* a_row[A_LD];
+  // B (weights): rows n0.., range-checked at the last valid row.
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.W + (size_t)n0 * p.K, (uint32_t)(min(BN, p.N - n0) * p.K));
+  // A: dense rows m0.., or the whole NHWC activation for the implicit im2col.
+  __amdgpu_buffer_rsrc_t ra;
+  uint32_t a_pix[A_LD];  // conv: byte offset of image n's pixel (0, 0); dense: row offset
   int a_ih0[A_LD], a_iw0[A_LD];
-  bool a_ok[A_LD];
+  if constexpr (CONV) {
+    ra = make_rsrc(p.A, (uint32_t)((size_t)p.Nimg_HWC));
+    const int plane = p.OH * p.OW;
 #pragma unroll
-  for (int i = 0; i < A_LD; ++i) {
-    const int m = m0 + lr + i * ROWS_PER_PASS;
-    a_ok[i] = m < p.M;
-    if constexpr (CONV) {
-      const int mm = a_ok[i] ? m : 0;
-      const int plane = p.OH * p.OW;
-      const int n = mm / plane;
-      const int r = mm - n * plane;
+    for (int i = 0; i < A_LD; ++i) {
+      const int m = m0 + lr + i * ROWS_PER_PASS;
+      const int n = m / plane;
+      const int r = m - n * plane;
       const int oh = r / p.OW;
       const int ow = r - oh * p.OW;
-      a_ih0[i] = oh * p.stride - p.pad;
+      const bool ok = m < p.M;
+      a_ih0[i] = ok ? oh * p.stride - p.pad : -(1 << 20);  // an invalid row never passes the bounds test
       a_iw0[i] = ow * p.stride - p.pad;
-      a_row[i] = p.A + (size_t)n * p.H * p.Wd * p.C;
-    } else {
-      a_row[i] = p.A + (size_t)(a_ok[i] ? m : 0) * p.K;
+      a_pix[i] = (uint32_t)(n * p.H * p.Wd * p.C);
+    }
+  } else {
+    ra = make_rsrc(p.A + (size_t)m0 * p.K, (uint32_t)(min(BM, p.M - m0) * p.K));
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i) {
+      a_pix[i] = (uint32_t)((lr + i * ROWS_PER_PASS) * p.K);
       a_ih0[i] = a_iw0[i] = 0;
     }
   }
-  const int8_t* b_row[B_LD];
-  bool b_ok[B_LD];
-#pragma unroll
-  for (int i = 0; i < B_LD; ++i) {
-    const int n = n0 + lr + i * ROWS_PER_PASS;
-    b_ok[i] = n < p.N;
-    b_row[i] = p.W + (size_t)(b_ok[i] ? n : 0) * p.K;
-  }
 
-  v4i ra[A_LD], rb[B_LD];
-  auto load_tile = [&](int kt) {
+  auto load = [&](int kt, v4i (&ga)[A_LD], v4i (&gb)[B_LD]) {
     const int k0 = kt * BK + kc * 16;
     const bool kin = k0 < p.K;
     if constexpr (CONV) {
@@ -133,25 +167,34 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
 #pragma unroll
       for (int i = 0; i < A_LD; ++i) {
         const int ih = a_ih0[i] + kh, iw = a_iw0[i] + kw;
-        const bool ok = kin && a_ok[i] && ih >= 0 && ih < p.H && iw >= 0 && iw < p.Wd;
-        ra[i] = ok ? *reinterpret_cast<const v4i*>(a_row[i] + ((size_t)ih * p.Wd + iw) * p.C + c0) : v4i{0, 0, 0, 0};
+        const bool ok = kin && (unsigned)ih < (unsigned)p.H && (unsigned)iw < (unsigned)p.Wd;
+        ga[i] = buf_load16(ra, ok ? a_pix[i] + (uint32_t)((ih * p.Wd + iw) * p.C + c0) : OOB);
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < A_LD; ++i)
-        ra[i] = (kin && a_ok[i]) ? *reinterpret_cast<const v4i*>(a_row[i] + k0) : v4i{0, 0, 0, 0};
+      for (int i = 0; i < A_LD; ++i) ga[i] = buf_load16(ra, kin ? a_pix[i] + (uint32_t)k0 : OOB);
     }
 #pragma unroll
     for (int i = 0; i < B_LD; ++i)
-      rb[i] = (kin && b_ok[i]) ? *reinterpret_cast<const v4i*>(b_row[i] + k0) : v4i{0, 0, 0, 0};
+      gb[i] = buf_load16(rb, kin ? (uint32_t)((lr + i * ROWS_PER_PASS) * p.K + k0) : OOB);
   };
-  auto store_tile = [&](int buf) {
-    int8_t* as = As + buf * BM * BK;
-    int8_t* bs = Bs + buf * BN * BK;
+  auto store = [&](int buf, const v4i (&ga)[A_LD], const v4i (&gb)[B_LD]) {
+    int8_t* as = lds + buf * (BM + BN) * BK;
+    int8_t* bs = as + BM * BK;
 #pragma unroll
-    for (int i = 0; i < A_LD; ++i) *reinterpret_cast<v4i*>(as + lds_off<SWZ>(lr + i * ROWS_PER_PASS, kc)) = ra[i];
+    for (int i = 0; i < A_LD; ++i) *reinterpret_cast<v4i*>(as + lds_off(lr + i * ROWS_PER_PASS, kc)) = ga[i];
 #pragma unroll
-    for (int i = 0; i < B_LD; ++i) *reinterpret_cast<v4i*>(bs + lds_off<SWZ>(lr + i * ROWS_PER_PASS, kc)) = rb[i];
+    for (int i = 0; i < B_LD; ++i) *reinterpret_cast<v4i*>(bs + lds_off(lr + i * ROWS_PER_PASS, kc)) = gb[i];
+  };
+  const int fr = lane & 31;  // fragment row within a 32-row block
+  const int fh = lane >> 5;  // which 16-byte half of the 32-byte K slice
+  auto frags = [&](int buf, int ks, v4i (&af)[TM], v4i (&bf)[TN]) {
+    const int8_t* as = lds + buf * (BM + BN) * BK;
+    const int8_t* bs = as + BM * BK;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const v4i*>(as + lds_off(wm * WTM + i * 32 + fr, ks * 2 + fh));
+#pragma unroll
+    for (int j = 0; j < TN; ++j) bf[j] = *reinterpret_cast<const v4i*>(bs + lds_off(wn * WTN + j * 32 + fr, ks * 2 + fh));
   };
 
   v16i c[TM][TN];
@@ -160,61 +203,119 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
 #pragma unroll
     for (int j = 0; j < TN; ++j) c[i][j] = v16i{};
 
+  // Pipeline: the global loads of tile kt+2 are in flight while tile kt computes; tile
+  // kt+1 is written to the other LDS buffer in the middle of tile kt; the fragments of the
+  // next 32-byte K slice are read while the current slice's MFMAs run.
   const int KT = (p.K + BK - 1) / BK;
-  load_tile(0);
-  store_tile(0);
+  v4i ga[A_LD], gb[B_LD];
+  load(0, ga, gb);
+  store(0, ga, gb);
+  if (KT > 1) load(1, ga, gb);
   __syncthreads();
-
-  const int fr = lane & 31;   // fragment row within a 32-row block
-  const int fh = lane >> 5;   // which 16-byte half of the 32-byte K slice
+  v4i af[2][TM], bf[2][TN];
+  frags(0, 0, af[0], bf[0]);
   for (int kt = 0; kt < KT; ++kt) {
     const int cur = kt & 1;
-    if (kt + 1 < KT) load_tile(kt + 1);
-    const int8_t* as = As + cur * BM * BK;
-    const int8_t* bs = Bs + cur * BN * BK;
 #pragma unroll
     for (int ks = 0; ks < BK / 32; ++ks) {
-      v4i af[TM], bf[TN];
+      if (ks + 1 < BK / 32) frags(cur, ks + 1, af[(ks + 1) & 1], bf[(ks + 1) & 1]);
+      if (ks == 1 && kt + 1 < KT) {
+        store(cur ^ 1, ga, gb);
+        if (kt + 2 < KT) load(kt + 2, ga, gb);
+      }
 #pragma unroll
       for (int i = 0; i < TM; ++i)
-        af[i] = *reinterpret_cast<const v4i*>(as + lds_off<SWZ>(wm * WTM + i * 32 + fr, ks * 2 + fh));
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
-        bf[j] = *reinterpret_cast<const v4i*>(bs + lds_off<SWZ>(wn * WTN + j * 32 + fr, ks * 2 + fh));
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) c[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], c[i][j], 0, 0, 0);
+        for (int j = 0; j < TN; ++j)
+          c[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[ks & 1][i], bf[ks & 1][j], c[i][j], 0, 0, 0);
     }
-    if (kt + 1 < KT) store_tile(cur ^ 1);
     __syncthreads();
+    if (kt + 1 < KT) frags(cur ^ 1, 0, af[0], bf[0]);
   }
 
-  // Epilogue. 32x32 result layout: lane l, register r holds
-  // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
-  const float sa_t = p.sa_per_row ? 0.f : p.sA[0];
+  // Epilogue, one 32-row slice of the wave tile at a time: the int32 results go through a
+  // per-wave LDS patch (exact), come back as four consecutive columns of one row per lane,
+  // and leave as 16-byte stores of whole 256-byte row segments. 32x32 result layout:
+  // lane l, register r holds row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+  constexpr int PITCH = WTN + 8;  // ints; 4*PITCH % 64 == 32 keeps both half-waves' rows apart
+  static_assert(WAVES_M * WAVES_N * 32 * PITCH * 4 <= 2 * (BM + BN) * BK, "epilogue patch");
+  static_assert((PITCH * 4) % 16 == 0 && (4 * PITCH) % 64 == 32, "patch pitch");
+  int* patch = reinterpret_cast<int*>(lds) + wave * 32 * PITCH;
+  constexpr int C4 = WTN / 4;                 // float4 columns per row
+  constexpr int ROWS_PER_STORE = 64 / C4;     // rows one 64-lane store covers
+  const bool has_r = p.res != nullptr;
+  // One slice per compile-time i (a run-time i would index the accumulators dynamically
+  // and send them to scratch memory).
+  auto slice = [&](auto ic) {
+    constexpr int i = decltype(ic)::value;
 #pragma unroll
-  for (int j = 0; j < TN; ++j) {
-    const int n = n0 + wn * WTN + j * 32 + (lane & 31);
-    const bool nok = n < p.N;
-    const float sw = nok ? p.sW[n] : 0.f;
-    const float b = (nok && p.bias) ? p.bias[n] : 0.f;
+    for (int j = 0; j < TN; ++j)
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int m = m0 + wm * WTM + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-        if (nok && m < p.M) {
+      for (int r = 0; r < 16; ++r)
+        patch[((r >> 2) * 8 + (lane >> 5) * 4 + (r & 3)) * PITCH + j * 32 + (lane & 31)] = c[i][j][r];
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's patch is written
+    __builtin_amdgcn_wave_barrier();
+    const int col4 = lane % C4;
+    const int ncol = wn * WTN + col4 * 4;  // tile-local column of this lane's 4 values
+    const int n = n0 + ncol;
+    const float4 sw4 = *reinterpret_cast<const float4*>(&s_sw[ncol]);
+    const float4 b4 = *reinterpret_cast<const float4*>(&s_b[ncol]);
+    if (p.vec_ok && n < p.N) {
+      // Rolled on purpose: an unrolled copy per row and slice overflows the instruction
+      // cache. Bias 0 when absent: y + 0.0f == y for every y this produces (no -0.0).
+#pragma unroll 1
+      for (int rr = 0; rr < 32; rr += ROWS_PER_STORE) {
+        const int row = rr + lane / C4;
+        const int mloc = wm * WTM + i * 32 + row;
+        const int m = m0 + mloc;
+        if (m < p.M) {
+          const int4 a = *reinterpret_cast<const int4*>(&patch[row * PITCH + col4 * 4]);
+          const float sa = s_sa[mloc];
           const size_t idx = (size_t)m * p.N + n;
-          const int a = c[i][j][r];
-          const float sa = p.sa_per_row ? p.sA[m] : sa_t;
-          const float rv = p.res ? p.res[idx] : 0.f;
-          p.out[idx] = dequant_one(a, sa, sw, b, p.bias != nullptr, rv, p.res != nullptr, p.act);
-          if (p.acc) p.acc[idx] = a;
+          float4 o;
+          o.x = __fadd_rn(__fmul_rn(__fmul_rn((float)a.x, sa), sw4.x), b4.x);
+          o.y = __fadd_rn(__fmul_rn(__fmul_rn((float)a.y, sa), sw4.y), b4.y);
+          o.z = __fadd_rn(__fmul_rn(__fmul_rn((float)a.z, sa), sw4.z), b4.z);
+          o.w = __fadd_rn(__fmul_rn(__fmul_rn((float)a.w, sa), sw4.w), b4.w);
+          if (has_r) {
+            const float4 rv = *reinterpret_cast<const float4*>(p.res + idx);
+            o.x = __fadd_rn(o.x, rv.x); o.y = __fadd_rn(o.y, rv.y);
+            o.z = __fadd_rn(o.z, rv.z); o.w = __fadd_rn(o.w, rv.w);
+          }
+          if (p.act == BQ_ACT_RELU) {
+            o.x = o.x > 0.f ? o.x : 0.f; o.y = o.y > 0.f ? o.y : 0.f;
+            o.z = o.z > 0.f ? o.z : 0.f; o.w = o.w > 0.f ? o.w : 0.f;
+          } else if (p.act == BQ_ACT_SILU) {
+            o.x = silu(o.x); o.y = silu(o.y); o.z = silu(o.z); o.w = silu(o.w);
+          }
+          *reinterpret_cast<float4*>(p.out + idx) = o;
+          if (p.acc) *reinterpret_cast<int4*>(p.acc + idx) = a;
+        }
+      }
+    } else if (!p.vec_ok) {
+#pragma unroll 1
+      for (int rr = 0; rr < 32; rr += ROWS_PER_STORE) {
+        const int row = rr + lane / C4;
+        const int mloc = wm * WTM + i * 32 + row;
+        const int m = m0 + mloc;
+#pragma unroll 1
+        for (int q = 0; q < 4; ++q) {
+          if (m < p.M && n + q < p.N) {
+            const int a = patch[row * PITCH + col4 * 4 + q];
+            const size_t idx = (size_t)m * p.N + n + q;
+            const float rv = has_r ? p.res[idx] : 0.f;
+            p.out[idx] = dequant_one(a, s_sa[mloc], s_sw[ncol + q], s_b[ncol + q], true, rv, has_r, p.act);
+            if (p.acc) p.acc[idx] = a;
+          }
         }
       }
     }
-  }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // this slice's patch reads are done before the next writes
+    __builtin_amdgcn_wave_barrier();
+  };
+  [&]<int... Is>(std::integer_sequence<int, Is...>) {
+    (slice(std::integral_constant<int, Is>{}), ...);
+  }(std::make_integer_sequence<int, TM>{});
 }
 
 // ----------------------------------------------------------------------------- skinny
@@ -341,11 +442,29 @@ __global__ __launch_bounds__(256) void dwconv_i8_kernel(const int8_t* __restrict
 template <int BM, int BN, int WAVES_M, int WAVES_N, bool CONV>
 static void launch_tiled(const GemmP& p, hipStream_t st) {
   const int tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
-  gemm_i8_kernel<BM, BN, WAVES_M, WAVES_N, 1, CONV><<<tiles, WAVES_M * WAVES_N * 64, 0, st>>>(p);
+  gemm_i8_kernel<BM, BN, WAVES_M, WAVES_N, CONV><<<tiles, WAVES_M * WAVES_N * 64, 0, st>>>(p);
+}
+
+// BQ_GEMM_CFG forces one tile configuration (tuning sweeps); unset = the shape rule.
+static int forced_cfg() {
+  static int cfg = [] {
+    const char* e = getenv("BQ_GEMM_CFG");
+    return e ? atoi(e) : 0;
+  }();
+  return cfg;
 }
 
 template <bool CONV>
 static void launch_gemm(const GemmP& p, hipStream_t st) {
+  switch (forced_cfg()) {
+    case 1: return launch_tiled<256, 256, 2, 4, CONV>(p, st);
+    case 3: return launch_tiled<256, 256, 2, 2, CONV>(p, st);
+    case 4: return launch_tiled<128, 128, 2, 2, CONV>(p, st);
+    case 5: return launch_tiled<256, 128, 2, 2, CONV>(p, st);
+    case 6: return launch_tiled<128, 256, 2, 2, CONV>(p, st);
+    case 7: return launch_tiled<64, 64, 2, 2, CONV>(p, st);
+    default: break;
+  }
   const long long t256 = (long long)((p.M + 255) / 256) * ((p.N + 255) / 256);
   const long long t128 = (long long)((p.M + 127) / 128) * ((p.N + 127) / 128);
   if (t256 >= 192)
@@ -368,8 +487,8 @@ int bq_gemm_i8(const int8_t* A, const int8_t* W, int64_t M, int64_t N, int64_t K
                const float* sW, const float* bias, int act, float* out, int32_t* acc, bq_stream_t stream) {
   const char* what = "bq_gemm_i8";
   if (M < 0 || N < 0 || K < 0) return set_error(BQ_ERR_ARG, "%s: negative size", what);
-  if (M > 0x7fffffff || N > 0x7fffffff || K > 0x7fffffff || M * N > ((int64_t)1 << 40))
-    return set_error(BQ_ERR_ARG, "%s: size too large", what);
+  if (M > 0x7fffffff || N > 0x7fffffff || K >= (1 << 23) || M * N > ((int64_t)1 << 40))
+    return set_error(BQ_ERR_ARG, "%s: size too large (K must be < 2^23)", what);
   if (M == 0 || N == 0) return BQ_OK;
   if (K % 16) return set_error(BQ_ERR_UNSUPPORTED, "%s: K=%lld is not a multiple of 16", what, (long long)K);
   if (!A || !W || !sA || !sW || !out) return set_error(BQ_ERR_ARG, "%s: null pointer", what);
@@ -379,6 +498,7 @@ int bq_gemm_i8(const int8_t* A, const int8_t* W, int64_t M, int64_t N, int64_t K
   p.A = A; p.W = W; p.M = (int)M; p.N = (int)N; p.K = (int)K;
   p.sA = sA; p.sa_per_row = 1; p.sW = sW; p.bias = bias; p.res = nullptr; p.act = act;
   p.out = out; p.acc = acc;
+  p.vec_ok = (N % 4 == 0) && aligned16(out) && aligned16(acc);
   hipStream_t st = (hipStream_t)stream;
   if (M <= 64) {
     const unsigned grid = (unsigned)((N + SK_COLS - 1) / SK_COLS);
@@ -407,8 +527,9 @@ int bq_conv2d_i8_nhwc(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t 
   if (H + 2 * pad < KH || W + 2 * pad < KW || OH < 1 || OW < 1)
     return set_error(BQ_ERR_ARG, "%s: the filter is larger than the input.", what);
   const int64_t M = N * OH * OW, K = KH * KW * C;
-  if (M > 0x7fffffff || K > 0x7fffffff || O > 0x7fffffff || N * H * W * C > ((int64_t)1 << 40))
-    return set_error(BQ_ERR_ARG, "%s: size too large", what);
+  if (M > 0x7fffffff || K >= (1 << 23) || O > 0x7fffffff || N * H * W * C >= ((int64_t)1 << 31) ||
+      O * K >= ((int64_t)1 << 31))
+    return set_error(BQ_ERR_ARG, "%s: size too large (activation and weight must each be < 2 GiB)", what);
   if (M == 0) return BQ_OK;
   if (!x || !w || !sA || !sW || !out) return set_error(BQ_ERR_ARG, "%s: null pointer", what);
   if (!aligned16(x) || !aligned16(w)) return set_error(BQ_ERR_ARG, "%s: x and w must be 16-byte aligned", what);
@@ -419,6 +540,8 @@ int bq_conv2d_i8_nhwc(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t 
   p.out = out; p.acc = acc;
   p.H = (int)H; p.Wd = (int)W; p.C = (int)C; p.OH = (int)OH; p.OW = (int)OW; p.KWd = (int)KW;
   p.stride = (int)stride; p.pad = (int)pad;
+  p.Nimg_HWC = N * H * W * C;
+  p.vec_ok = (O % 4 == 0) && aligned16(out) && aligned16(acc) && aligned16(residual);
   hipStream_t st = (hipStream_t)stream;
   if (KH == 1 && KW == 1 && stride == 1 && pad == 0)
     launch_gemm<false>(p, st);  // a 1x1 conv is the dense GEMM on [N*H*W, C]
