@@ -320,46 +320,56 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
 
 // ----------------------------------------------------------------------------- skinny
 
-constexpr int SK_WAVES = 4;
 constexpr int SK_COLS = 16;  // output channels a workgroup
 
-template <int MT>
-__global__ __launch_bounds__(SK_WAVES * 64) void skinny_i8_kernel(const GemmP p) {
-  __shared__ int red[SK_WAVES][MT][64][4];
+// Weight-streaming GEMM for M <= 64: W is read once, at HBM rate. A workgroup owns 16
+// weight rows (output channels); its WAVES waves split K; each lane owns 64 contiguous
+// bytes of one weight row per 256-byte step, and every weight load of a wave's share
+// (U steps) is issued before the first MFMA, so a whole 16-row slab is in flight at once.
+// The activation rows (tiny, L2-resident) are loaded first. v_mfma_i32_16x16x64_i8
+// multiplies the weight bytes against up to four 16-row activation tiles; the waves'
+// partial sums meet in LDS.
+template <int MT, int WAVES, int U>
+__global__ __launch_bounds__(WAVES * 64) void skinny_i8_kernel(const GemmP p) {
+  __shared__ int red[WAVES][MT][64][4];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int n0 = blockIdx.x * SK_COLS;
-  const int col = lane & 15;     // weight row within the 16 (B operand column)
-  const int kg = lane >> 4;      // which 64-byte group of the 256-byte step
-  const int n = n0 + col;
-  const bool nok = n < p.N;
-  const int8_t* wrow = p.W + (size_t)(nok ? n : 0) * p.K;
+  const int col = lane & 15;  // weight row within the 16 (the B operand's column)
+  const int kg = lane >> 4;   // which 64-byte group of a 256-byte step
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.W + (size_t)n0 * p.K, (uint32_t)(min(SK_COLS, p.N - n0) * p.K));
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, (uint32_t)(p.M * p.K));
 
   v4i c[MT];
 #pragma unroll
   for (int t = 0; t < MT; ++t) c[t] = v4i{};
 
   const int steps = (p.K + 255) / 256;
-  for (int s = wave; s < steps; s += SK_WAVES) {
-    const int kb = s * 256 + kg * 64;
-    v4i w[4];
+  for (int s0 = wave * U; s0 < steps; s0 += WAVES * U) {
+    v4i a[U][MT][4], w[U][4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int k = kb + j * 16;
-      w[j] = (nok && k < p.K) ? __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wrow + k)) : v4i{0, 0, 0, 0};
-    }
+    for (int u = 0; u < U; ++u)
 #pragma unroll
-    for (int t = 0; t < MT; ++t) {
-      const int m = t * 16 + (lane & 15);
-      const bool mok = m < p.M;
-      const int8_t* arow = p.A + (size_t)(mok ? m : 0) * p.K;
+      for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int k = (s0 + u) * 256 + kg * 64 + j * 16;
+          a[u][t][j] = buf_load16(ra, k < p.K ? (uint32_t)((t * 16 + col) * p.K + k) : OOB);
+        }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int k = kb + j * 16;
-        const v4i a = (mok && k < p.K) ? *reinterpret_cast<const v4i*>(arow + k) : v4i{0, 0, 0, 0};
-        c[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, w[j], c[t], 0, 0, 0);
+        const int k = (s0 + u) * 256 + kg * 64 + j * 16;
+        w[u][j] = buf_load16(rw, k < p.K ? (uint32_t)(col * p.K + k) : OOB);
       }
-    }
+    __builtin_amdgcn_sched_barrier(0);  // keep every load of the share ahead of the MFMAs
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) c[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[u][t][j], w[u][j], c[t], 0, 0, 0);
   }
 #pragma unroll
   for (int t = 0; t < MT; ++t)
@@ -368,6 +378,7 @@ __global__ __launch_bounds__(SK_WAVES * 64) void skinny_i8_kernel(const GemmP p)
   __syncthreads();
   // 16x16 result layout: lane l, register r holds row 4*(l/16) + r, column l%16.
   const int e = threadIdx.x;  // one output of a 16x16 tile per thread
+  if (e >= 256) return;
   const int ml = e >> 4, nl = e & 15;
   const int src_lane = (ml >> 2) * 16 + nl, src_r = ml & 3;
   const int nn = n0 + nl;
@@ -378,17 +389,96 @@ __global__ __launch_bounds__(SK_WAVES * 64) void skinny_i8_kernel(const GemmP p)
     for (int t = 0; t < MT; ++t) {
       const int m = t * 16 + ml;
       if (m < p.M) {
-        int a = 0;
+        int acc = 0;
 #pragma unroll
-        for (int w = 0; w < SK_WAVES; ++w) a += red[w][t][src_lane][src_r];
+        for (int w = 0; w < WAVES; ++w) acc += red[w][t][src_lane][src_r];
         const size_t idx = (size_t)m * p.N + nn;
         const float sa = p.sa_per_row ? p.sA[m] : p.sA[0];
         const float rv = p.res ? p.res[idx] : 0.f;
-        p.out[idx] = dequant_one(a, sa, sw, b, p.bias != nullptr, rv, p.res != nullptr, p.act);
-        if (p.acc) p.acc[idx] = a;
+        p.out[idx] = dequant_one(acc, sa, sw, b, p.bias != nullptr, rv, p.res != nullptr, p.act);
+        if (p.acc) p.acc[idx] = acc;
       }
     }
   }
+}
+
+// GEMV for M <= 4 (the HBM-bound decode shape): no MFMA. A weight row is read as
+// contiguous 1 KB wave-loads (64 lanes x 16 bytes); each lane dots its 16 weight bytes
+// (v_dot4_i32_i8) against the same 16 bytes of every activation row, which sit in
+// registers for the whole kernel (K <= KC * 1024); one wave reduction per (row, m).
+// Each wave keeps RPW rows (RPW * KC loads) in flight.
+constexpr int GV_WAVES = 8;
+
+__device__ __forceinline__ int wave_sum(int v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+template <int MR, int KC, int RPW>
+__global__ __launch_bounds__(GV_WAVES * 64) void gemv_i8_kernel(const GemmP p) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int row0 = (blockIdx.x * GV_WAVES + wave) * RPW;
+  if (row0 >= p.N) return;
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.W + (size_t)row0 * p.K, (uint32_t)(min(RPW, p.N - row0) * p.K));
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, (uint32_t)(p.M * p.K));
+  v4i x[MR][KC];
+#pragma unroll
+  for (int m = 0; m < MR; ++m)
+#pragma unroll
+    for (int c = 0; c < KC; ++c) {
+      const int k = c * 1024 + lane * 16;
+      x[m][c] = buf_load16(ra, (m < p.M && k < p.K) ? (uint32_t)(m * p.K + k) : OOB);
+    }
+  v4i w[RPW][KC];
+#pragma unroll
+  for (int j = 0; j < RPW; ++j)
+#pragma unroll
+    for (int c = 0; c < KC; ++c) {
+      const int k = c * 1024 + lane * 16;
+      w[j][c] = buf_load16(rw, k < p.K ? (uint32_t)(j * p.K + k) : OOB);
+    }
+  __builtin_amdgcn_sched_barrier(0);
+  int acc[RPW][MR];
+#pragma unroll
+  for (int j = 0; j < RPW; ++j)
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      int a = 0;
+#pragma unroll
+      for (int c = 0; c < KC; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) a = __builtin_amdgcn_sdot4(w[j][c][q], x[m][c][q], a, false);
+      acc[j][m] = wave_sum(a);
+    }
+  // lane j*MR + m writes output (m, row0 + j)
+#pragma unroll
+  for (int j = 0; j < RPW; ++j)
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      const int n = row0 + j;
+      if (lane == j * MR + m && n < p.N && m < p.M) {
+        const size_t idx = (size_t)m * p.N + n;
+        const float sa = p.sa_per_row ? p.sA[m] : p.sA[0];
+        const float rv = p.res ? p.res[idx] : 0.f;
+        p.out[idx] = dequant_one(acc[j][m], sa, p.sW[n], p.bias ? p.bias[n] : 0.f, p.bias != nullptr, rv,
+                                 p.res != nullptr, p.act);
+        if (p.acc) p.acc[idx] = acc[j][m];
+      }
+    }
+}
+
+template <int MR>
+static bool launch_gemv(const GemmP& p, hipStream_t st) {
+  constexpr int RPW = 2;
+  const unsigned grid = (unsigned)((p.N + GV_WAVES * RPW - 1) / (GV_WAVES * RPW));
+  if (p.K <= 1024) gemv_i8_kernel<MR, 1, RPW><<<grid, GV_WAVES * 64, 0, st>>>(p);
+  else if (p.K <= 2048) gemv_i8_kernel<MR, 2, RPW><<<grid, GV_WAVES * 64, 0, st>>>(p);
+  else if (p.K <= 4096) gemv_i8_kernel<MR, 4, RPW><<<grid, GV_WAVES * 64, 0, st>>>(p);
+  else if (p.K <= 8192) gemv_i8_kernel<MR, 8, RPW><<<grid, GV_WAVES * 64, 0, st>>>(p);
+  else return false;
+  return true;
 }
 
 // -------------------------------------------------------------------------- depthwise
@@ -500,13 +590,23 @@ int bq_gemm_i8(const int8_t* A, const int8_t* W, int64_t M, int64_t N, int64_t K
   p.out = out; p.acc = acc;
   p.vec_ok = (N % 4 == 0) && aligned16(out) && aligned16(acc);
   hipStream_t st = (hipStream_t)stream;
-  if (M <= 64) {
+  bool done = false;
+  if (M <= 4) {
+    switch (M) {
+      case 1: done = launch_gemv<1>(p, st); break;
+      case 2: done = launch_gemv<2>(p, st); break;
+      case 3: done = launch_gemv<3>(p, st); break;
+      default: done = launch_gemv<4>(p, st); break;
+    }
+  }
+  if (done) {
+  } else if (M <= 64) {
     const unsigned grid = (unsigned)((N + SK_COLS - 1) / SK_COLS);
     switch ((M + 15) / 16) {
-      case 1: skinny_i8_kernel<1><<<grid, SK_WAVES * 64, 0, st>>>(p); break;
-      case 2: skinny_i8_kernel<2><<<grid, SK_WAVES * 64, 0, st>>>(p); break;
-      case 3: skinny_i8_kernel<3><<<grid, SK_WAVES * 64, 0, st>>>(p); break;
-      default: skinny_i8_kernel<4><<<grid, SK_WAVES * 64, 0, st>>>(p); break;
+      case 1: skinny_i8_kernel<1, 8, 2><<<grid, 8 * 64, 0, st>>>(p); break;
+      case 2: skinny_i8_kernel<2, 8, 2><<<grid, 8 * 64, 0, st>>>(p); break;
+      case 3: skinny_i8_kernel<3, 8, 1><<<grid, 8 * 64, 0, st>>>(p); break;
+      default: skinny_i8_kernel<4, 8, 1><<<grid, 8 * 64, 0, st>>>(p); break;
     }
   } else {
     launch_gemm<false>(p, st);
