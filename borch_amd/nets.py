@@ -1,0 +1,274 @@
+"""The model workloads of the task configurations, built on ``borch_amd.nn``.
+
+* ``ResNet18`` — the CIFAR variant of tests/browser/export_resnet18.py:27-60 in the
+  reference (3x3 stem, no max-pool, 8 BasicBlocks with the reference's attribute names,
+  mean pool, 10-way Linear). ``fuse()`` folds every BN (borch/_nn.py:4916-4955) and wraps
+  the convs into the fused modules the reference's ``fuse()`` builds (borch-ts
+  test/bench.ts:63-75, nn.ts:6698-6750): stem and conv1 -> ConvReLU2d, conv2 ->
+  ConvAddReLU2d with the shortcut as residual, the 1x1 downsample a plain conv.
+* ``EfficientNetB0`` — the published B0 (Tan & Le 2019; torchvision's layout): MBConv
+  blocks with int8 1x1 expand/project convs and int8 depthwise 3x3/5x5; squeeze-excite and
+  the classifier stay f32 (SE uses torch's own layers); SiLU runs in f32 in the epilogue.
+  The reference holds no B0 definition (it comes from an npm package not vendored), so
+  this one follows the paper.
+* ``ViTEncoder`` — ViT-B/16's encoder (Dosovitskiy et al. 2021; torchvision's pre-norm
+  layout, LayerNorm eps 1e-6): QKV / proj / MLP Linears are int8 dynamic-quant;
+  LayerNorm, softmax attention and GELU stay f32.
+
+Weights are random, from a seeded ``torch.Generator`` on the host: Kaiming-normal
+(fan_out, ReLU gain) convs, BN running statistics as export_resnet18.py:84-91 (mean
+N(0, 0.1²), var U(0.5, 1.5), gamma N(1, 0.1²), beta N(0, 0.1²)).
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn as tnn
+
+from . import nn
+from .nn import intrinsic as I
+from .nn.utils.fusion import fuse_conv_bn_eval
+
+
+def _bn_stats(bn: tnn.BatchNorm2d, g: torch.Generator) -> None:
+    with torch.no_grad():
+        c = bn.num_features
+        bn.running_mean.copy_(torch.randn(c, generator=g) * 0.1)
+        bn.running_var.copy_(torch.rand(c, generator=g) + 0.5)
+        bn.weight.copy_(1.0 + torch.randn(c, generator=g) * 0.1)
+        bn.bias.copy_(torch.randn(c, generator=g) * 0.1)
+
+
+def _kaiming(conv, g: torch.Generator) -> None:
+    with torch.no_grad():
+        o, ci, kh, kw = conv.weight.shape
+        conv.weight.copy_(torch.randn(conv.weight.shape, generator=g) * math.sqrt(2.0 / (o * kh * kw)))
+        if conv.bias is not None:
+            conv.bias.zero_()
+
+
+def init_weights(model: tnn.Module, seed: int = 0) -> tnn.Module:
+    """Seeded random weights for every conv, BN and Linear (host generator)."""
+    g = torch.Generator().manual_seed(seed)
+    for m in model.modules():
+        if isinstance(m, (nn.Conv2d, tnn.Conv2d)):
+            _kaiming(m, g)
+        elif isinstance(m, tnn.BatchNorm2d):
+            _bn_stats(m, g)
+        elif isinstance(m, (nn.Linear, tnn.Linear)):
+            with torch.no_grad():
+                bound = 1.0 / math.sqrt(m.in_features)
+                m.weight.copy_((torch.rand(m.weight.shape, generator=g) * 2 - 1) * bound)
+                if m.bias is not None:
+                    m.bias.copy_((torch.rand(m.bias.shape, generator=g) * 2 - 1) * bound)
+        elif isinstance(m, tnn.LayerNorm):
+            with torch.no_grad():
+                m.weight.copy_(1.0 + torch.randn(m.weight.shape, generator=g) * 0.1)
+                m.bias.copy_(torch.randn(m.bias.shape, generator=g) * 0.1)
+    return model
+
+
+# ------------------------------------------------------------------------ ResNet-18
+
+class Block(tnn.Module):
+    """BasicBlock with the reference's attribute names (export_resnet18.py:27-43)."""
+
+    def __init__(self, cin, cout, stride):
+        super().__init__()
+        self.conv1 = nn.Conv2d(cin, cout, 3, stride, 1, bias=False)
+        self.bn1 = tnn.BatchNorm2d(cout)
+        self.conv2 = nn.Conv2d(cout, cout, 3, 1, 1, bias=False)
+        self.bn2 = tnn.BatchNorm2d(cout)
+        shrinks = stride != 1 or cin != cout
+        self.downConv = nn.Conv2d(cin, cout, 1, stride, 0, bias=False) if shrinks else None
+        self.downBn = tnn.BatchNorm2d(cout) if shrinks else None
+        self.c1 = self.c2 = self.down = None
+
+    def forward(self, x):
+        if self.c1 is not None:
+            side = self.down(x) if self.down is not None else x
+            return self.c2(self.c1(x), side)
+        out = torch.relu(self.bn1(self.conv1(x)))
+        out = self.bn2(self.conv2(out))
+        side = self.downBn(self.downConv(x)) if self.downConv is not None else x
+        return torch.relu(out + side)
+
+    def fuse(self):
+        self.c1 = I.ConvReLU2d(fuse_conv_bn_eval(self.conv1, self.bn1))
+        self.c2 = I.ConvAddReLU2d(fuse_conv_bn_eval(self.conv2, self.bn2))
+        self.down = fuse_conv_bn_eval(self.downConv, self.downBn) if self.downConv is not None else None
+        self.conv1 = self.bn1 = self.conv2 = self.bn2 = self.downConv = self.downBn = None
+
+
+class ResNet18(tnn.Module):
+    """CIFAR ResNet-18 (export_resnet18.py:46-60)."""
+
+    def __init__(self, classes=10):
+        super().__init__()
+        self.stem = nn.Conv2d(3, 64, 3, 1, 1, bias=False)
+        self.bn = tnn.BatchNorm2d(64)
+        self.body = tnn.Sequential(
+            Block(64, 64, 1), Block(64, 64, 1), Block(64, 128, 2), Block(128, 128, 1),
+            Block(128, 256, 2), Block(256, 256, 1), Block(256, 512, 2), Block(512, 512, 1))
+        self.fc = nn.Linear(512, classes)
+        self.fc.int8_exempt = True  # the f32 head of the configuration
+        self.stem_f = None
+
+    def features(self, x):
+        if self.stem_f is not None:
+            h = self.stem_f(x)
+        else:
+            h = torch.relu(self.bn(self.stem(x)))
+        return self.body(h)
+
+    def forward(self, x):
+        return self.fc(self.features(x).mean(dim=(2, 3)))
+
+    def fuse(self):
+        self.eval()
+        self.stem_f = I.ConvReLU2d(fuse_conv_bn_eval(self.stem, self.bn))
+        self.stem = self.bn = None
+        for b in self.body:
+            b.fuse()
+        return self
+
+
+# ------------------------------------------------------------------ EfficientNet-B0
+
+# (expand ratio, kernel, stride, in, out, repeats) — Tan & Le 2019, Table 1.
+B0_STAGES = [(1, 3, 1, 32, 16, 1), (6, 3, 2, 16, 24, 2), (6, 5, 2, 24, 40, 2), (6, 3, 2, 40, 80, 3),
+             (6, 5, 1, 80, 112, 3), (6, 5, 2, 112, 192, 4), (6, 3, 1, 192, 320, 1)]
+
+
+class MBConv(tnn.Module):
+    def __init__(self, cin, cout, k, stride, expand):
+        super().__init__()
+        mid = cin * expand
+        self.has_expand = expand != 1
+        self.expand = nn.Conv2d(cin, mid, 1, bias=False) if self.has_expand else None
+        self.bn0 = tnn.BatchNorm2d(mid) if self.has_expand else None
+        self.dw = nn.Conv2d(mid, mid, k, stride, k // 2, groups=mid, bias=False)
+        self.bn1 = tnn.BatchNorm2d(mid)
+        sq = max(1, cin // 4)
+        self.se_reduce = tnn.Conv2d(mid, sq, 1)  # squeeze-excite stays f32 (torch's layer)
+        self.se_expand = tnn.Conv2d(sq, mid, 1)
+        self.project = nn.Conv2d(mid, cout, 1, bias=False)
+        self.bn2 = tnn.BatchNorm2d(cout)
+        self.residual = stride == 1 and cin == cout
+        self.fused = False
+
+    def _se(self, h):
+        s = h.mean(dim=(2, 3), keepdim=True)
+        s = torch.sigmoid(self.se_expand(torch.nn.functional.silu(self.se_reduce(s))))
+        return h * s
+
+    def forward(self, x):
+        if self.fused:
+            h = self.expand(x) if self.expand is not None else x
+            h = self._se(self.dw(h))
+            return self.project(h, x) if self.residual else self.project(h)
+        h = torch.nn.functional.silu(self.bn0(self.expand(x))) if self.has_expand else x
+        h = torch.nn.functional.silu(self.bn1(self.dw(h)))
+        h = self.bn2(self.project(self._se(h)))
+        return h + x if self.residual else h
+
+    def fuse(self):
+        if self.has_expand:
+            self.expand = I.ConvSiLU2d(fuse_conv_bn_eval(self.expand, self.bn0))
+        self.dw = I.ConvSiLU2d(fuse_conv_bn_eval(self.dw, self.bn1))
+        p = fuse_conv_bn_eval(self.project, self.bn2)
+        self.project = I.ConvAdd2d(p) if self.residual else p
+        self.bn0 = self.bn1 = self.bn2 = None
+        self.fused = True
+
+
+class EfficientNetB0(tnn.Module):
+    def __init__(self, classes=1000):
+        super().__init__()
+        self.stem = nn.Conv2d(3, 32, 3, 2, 1, bias=False)
+        self.bn = tnn.BatchNorm2d(32)
+        blocks = []
+        for e, k, s, cin, cout, n in B0_STAGES:
+            for i in range(n):
+                blocks.append(MBConv(cin if i == 0 else cout, cout, k, s if i == 0 else 1, e))
+        self.blocks = tnn.Sequential(*blocks)
+        self.head = nn.Conv2d(320, 1280, 1, bias=False)
+        self.bn_head = tnn.BatchNorm2d(1280)
+        self.fc = nn.Linear(1280, classes)
+        self.fc.int8_exempt = True
+        self.fused = False
+
+    def forward(self, x):
+        if self.fused:
+            h = self.head(self.blocks(self.stem(x)))
+        else:
+            h = torch.nn.functional.silu(self.bn(self.stem(x)))
+            h = torch.nn.functional.silu(self.bn_head(self.head(self.blocks(h))))
+        return self.fc(h.mean(dim=(2, 3)))
+
+    def fuse(self):
+        self.eval()
+        self.stem = I.ConvSiLU2d(fuse_conv_bn_eval(self.stem, self.bn))
+        self.head = I.ConvSiLU2d(fuse_conv_bn_eval(self.head, self.bn_head))
+        self.bn = self.bn_head = None
+        for b in self.blocks:
+            b.fuse()
+        self.fused = True
+        return self
+
+
+# ---------------------------------------------------------------- ViT-B/16 encoder
+
+class EncoderLayer(tnn.Module):
+    def __init__(self, d=768, heads=12, mlp=3072):
+        super().__init__()
+        self.heads = heads
+        self.ln1 = tnn.LayerNorm(d, eps=1e-6)
+        self.qkv = nn.Linear(d, 3 * d)
+        self.proj = nn.Linear(d, d)
+        self.ln2 = tnn.LayerNorm(d, eps=1e-6)
+        self.fc1 = nn.Linear(d, mlp)
+        self.fc2 = nn.Linear(mlp, d)
+
+    def attention(self, h):
+        B, T, D = h.shape
+        H, dh = self.heads, D // self.heads
+        qkv = self.qkv(h).reshape(B, T, 3, H, dh).permute(2, 0, 3, 1, 4)
+        q, k, v = qkv[0].contiguous(), qkv[1].contiguous(), qkv[2].contiguous()
+        # f32 attention; the transposed operand is made contiguous before the batched product
+        att = torch.matmul(q, k.transpose(-2, -1).contiguous()) * (dh ** -0.5)
+        o = torch.matmul(torch.softmax(att, dim=-1), v)
+        return self.proj(o.transpose(1, 2).reshape(B, T, D))
+
+    def forward(self, x):
+        x = x + self.attention(self.ln1(x))
+        return x + self.fc2(torch.nn.functional.gelu(self.fc1(self.ln2(x))))
+
+
+class ViTEncoder(tnn.Module):
+    """ViT-B/16 encoder on already patch-embedded tokens [B, 197, 768]."""
+
+    def __init__(self, layers=12, d=768, heads=12, mlp=3072):
+        super().__init__()
+        self.layers = tnn.Sequential(*[EncoderLayer(d, heads, mlp) for _ in range(layers)])
+        self.ln = tnn.LayerNorm(d, eps=1e-6)
+
+    def forward(self, x):
+        return self.ln(self.layers(x))
+
+
+def build(name: str, seed: int = 0, device="cuda"):
+    """A seeded model of configuration C3 / C4 / C5, folded for inference (not yet int8)."""
+    if name == "resnet18":
+        m = init_weights(ResNet18(), seed)
+    elif name == "efficientnet_b0":
+        m = init_weights(EfficientNetB0(), seed)
+    elif name == "vit_b16":
+        m = init_weights(ViTEncoder(), seed)
+    else:
+        raise ValueError(f"unknown model {name!r}")
+    m = m.to(device).eval()
+    if hasattr(m, "fuse"):
+        m.fuse()
+    return m

@@ -167,8 +167,10 @@ class Conv2d(_tnn.Module):
 
 
 def _int8_layers(model):
+    """Every Linear / Conv2d of this package in ``model`` that is not marked
+    ``int8_exempt`` (a layer the configuration keeps in f32, e.g. a classifier head)."""
     for name, mod in model.named_modules():
-        if isinstance(mod, (Linear, Conv2d)):
+        if isinstance(mod, (Linear, Conv2d)) and not getattr(mod, "int8_exempt", False):
             yield name, mod
 
 

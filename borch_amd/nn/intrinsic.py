@@ -66,3 +66,18 @@ class LinearReLU(_tnn.Module):
 
     def forward(self, x):
         return self.linear(x)
+
+
+class ConvSiLU2d(_tnn.Module):
+    """``silu(conv(x))`` in one kernel: the SiLU is evaluated in f32 in the epilogue
+    (EfficientNet's conv-BN-SiLU after the BN fold). Not a torch.ao name; the same shape
+    as ``ConvReLU2d``."""
+
+    def __init__(self, conv):
+        super().__init__()
+        self.conv = conv
+        self.conv.act = _i8.ACT_SILU
+        self.training = False
+
+    def forward(self, x):
+        return self.conv(x)

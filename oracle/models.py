@@ -1,0 +1,102 @@
+"""Model-level oracle: the int8 layers of the configurations restated in numpy — TEST
+INFRASTRUCTURE ONLY (imported by tests/ and the CPU-baseline leg of bench.py).
+
+Each function takes the layer's float32 parameters as numpy arrays (read from the model
+under test after the BN fold) and applies oracle.quant's arithmetic:
+
+* ``conv_layer`` — per-tensor activation quantization into NHWC (tensor.ts:11915-11920),
+  per-channel weights (quant.ts:80-103's scale rule), exact int32 implicit GEMM
+  (kernels.ts:2156-2302 restated as im2col + GEMM), epilogue
+  ``((acc·sA)·sW)+b (+residual)`` then the activation (kernels.ts:4230-4244);
+* ``dwconv_layer`` — the same for a depthwise conv (lib.rs:598-641's tap sum, integers);
+* ``linear_layer`` — per-row activations, per-channel weights (quant.ts:23-53);
+* ``resnet18_features`` — the CIFAR ResNet-18 conv stack of export_resnet18.py:27-60
+  chained layer by layer (pinned by the per-layer checks and the brute-force conv tests).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from . import quant as Q
+
+ACT_NONE, ACT_RELU, ACT_SILU = 0, 1, 2
+
+
+def _act(y, act):
+    if act == ACT_RELU:
+        return np.where(y > 0, y, np.float32(0)).astype(np.float32)
+    if act == ACT_SILU:
+        return Q.silu(y)
+    return y
+
+
+def conv_layer(x_nchw, w, b, stride, pad, act=ACT_NONE, residual_nchw=None):
+    """Returns ``(y_nchw, acc [N·OH·OW, O], sA, sW, qw)``."""
+    x_nchw = np.asarray(x_nchw, np.float32)
+    O_, C, KH, KW = w.shape
+    cpad = (C + 15) // 16 * 16
+    xq, sA = Q.quantize_act_nhwc(x_nchw, cpad)
+    qw, sW = Q.quantize_conv_weight(w, cpad)
+    acc, OH, OW = Q.conv2d_i8_nhwc(xq, qw, KH, KW, stride, pad)
+    res = None
+    if residual_nchw is not None:
+        res = np.asarray(residual_nchw, np.float32).transpose(0, 2, 3, 1).reshape(-1, O_)
+    y = Q.dequant(acc, sA[0], sW, b, False, res)
+    y = _act(y, act)
+    N = x_nchw.shape[0]
+    return y.reshape(N, OH, OW, O_).transpose(0, 3, 1, 2), acc, sA, sW, qw
+
+
+def dwconv_layer(x_nchw, w, b, stride, pad, act=ACT_NONE):
+    """Depthwise; returns ``(y_nchw, acc [N, OH, OW, C], sA, sW, qw [KH·KW, C])``."""
+    x_nchw = np.asarray(x_nchw, np.float32)
+    C, _, KH, KW = w.shape
+    cpad = (C + 3) // 4 * 4
+    wp = np.zeros((cpad, 1, KH, KW), np.float32)
+    wp[:C] = w
+    xq, sA = Q.quantize_act_nhwc(x_nchw, cpad)
+    qw, sW = Q.quantize_dw_weight(wp)
+    acc = Q.dwconv_i8_nhwc(xq, qw, KH, KW, stride, pad)
+    N, OH, OW, _ = acc.shape
+    bp = np.zeros(cpad, np.float32)
+    if b is not None:
+        bp[:C] = b
+    y = Q.dequant(acc.reshape(-1, cpad), sA[0], sW, bp)
+    y = _act(y, act).reshape(N, OH, OW, cpad)[..., :C]
+    return y.transpose(0, 3, 1, 2), acc[..., :C], sA, sW, qw
+
+
+def linear_layer(x, w, b, act=ACT_NONE):
+    """Returns ``(y [..., N], acc [M, N], sA [M], sW, qw)``."""
+    x = np.asarray(x, np.float32)
+    lead = x.shape[:-1]
+    K = x.shape[-1]
+    kp = (max(K, 16) + 15) // 16 * 16
+    x2 = np.zeros((int(np.prod(lead)) if lead else 1, kp), np.float32)
+    x2[:, :K] = x.reshape(-1, K)
+    wp = np.zeros((w.shape[0], kp), np.float32)
+    wp[:, :K] = w
+    qa, sA = Q.quantize_rows(x2)
+    qw, sW = Q.quantize_weight_per_channel(wp)
+    acc = Q.gemm_i8_i32(qa, qw)
+    y = _act(Q.dequant(acc, sA, sW, b), act)
+    return y.reshape(*lead, w.shape[0]), acc, sA, sW, qw
+
+
+def resnet18_features(params, x):
+    """The folded CIFAR ResNet-18 conv stack, int8 layer by layer. ``params`` maps
+    ``stem``, ``body.{i}.c1|c2|down`` to ``(w, b, stride, pad)``. Returns the features
+    before the mean pool, NCHW f32."""
+    w, b, s, p = params["stem"]
+    h = conv_layer(x, w, b, s, p, ACT_RELU)[0]
+    for i in range(8):
+        w1, b1, s1, p1 = params[f"body.{i}.c1"]
+        out = conv_layer(h, w1, b1, s1, p1, ACT_RELU)[0]
+        if f"body.{i}.down" in params:
+            wd, bd, sd, pd = params[f"body.{i}.down"]
+            side = conv_layer(h, wd, bd, sd, pd, ACT_NONE)[0]
+        else:
+            side = h
+        w2, b2, s2, p2 = params[f"body.{i}.c2"]
+        h = conv_layer(out, w2, b2, s2, p2, ACT_RELU, side)[0]
+    return h

@@ -1,0 +1,188 @@
+"""GPU parity of the model configurations C3–C5, layer by layer, through the module surface.
+
+Every int8 layer's input is captured during the real forward; the oracle recomputes that
+layer from the captured input and the layer's folded f32 parameters. Per layer: int8
+weight packing and int32 accumulators bit-exact (accumulators re-read through the C ABI
+with the layer's input), f32 output bit-exact (SiLU layers: within 1e-5 rel / 1e-6 abs,
+since the device's expf and numpy's exp differ in the last bit). ResNet-18's whole conv
+stack is additionally chained in the oracle from the network input and matches bit for
+bit; logits after the f32 pool + head are held to 1e-5 (rel and abs).
+"""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import borch_amd as bt
+from borch_amd import int8 as I
+from borch_amd import nets, workloads as WL
+from oracle import models as OM
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-5, 1e-6
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def n(x):
+    return x.detach().float().cpu().numpy()
+
+
+def int8_modules(model):
+    return [(name, m) for name, m in model.named_modules()
+            if isinstance(m, (bt.nn.Linear, bt.nn.Conv2d)) and m.int8 is not None]
+
+
+def capture(model, rows=None):
+    """Hooks recording (name, module, x, residual, y) for every int8 layer. ``rows(name)``
+    may return row indices to keep (Linear inputs flattened to [M, K])."""
+    recs, hooks = [], []
+    for name, m in int8_modules(model):
+        def hook(mod, args, out, name=name):
+            x = args[0].detach()
+            res = args[1].detach() if len(args) > 1 and args[1] is not None else None
+            if isinstance(mod, bt.nn.Linear):
+                x2, y2 = x.reshape(-1, x.shape[-1]), out.detach().reshape(-1, out.shape[-1])
+                sel = rows(name, x2.shape[0]) if rows else None
+                if sel is not None:
+                    x2, y2 = x2[sel], y2[sel]
+                recs.append((name, mod, n(x2), None, n(y2)))
+            else:
+                recs.append((name, mod, n(x), None if res is None else n(res), n(out)))
+        hooks.append(m.register_forward_hook(hook))
+    return recs, hooks
+
+
+def check_layer(name, mod, x, res, y):
+    dev = mod.weight.device
+    w = n(mod.weight)
+    b = None if mod.bias is None else n(mod.bias)
+    if isinstance(mod, bt.nn.Linear):
+        y_o, acc_o, sa_o, sw_o, qw_o = OM.linear_layer(x, w, b, mod.act)
+        assert np.array_equal(n(mod.int8.q), qw_o), name
+        xt = torch.from_numpy(x).to(dev)
+        if mod.int8.kpad != mod.int8.in_features:
+            xt = torch.nn.functional.pad(xt, (0, mod.int8.kpad - mod.int8.in_features))
+        qa, sa = I.quantize_rows(xt)
+        _, acc = I.gemm_i8(qa, mod.int8.q, sa, mod.int8.s, mod.bias, mod.act, want_acc=True)
+    elif isinstance(mod.int8, I.Int8DwWeight):
+        stride, pad = mod._geometry()
+        y_o, acc_o, sa_o, sw_o, qw_o = OM.dwconv_layer(x, w, b, stride, pad, mod.act)
+        assert np.array_equal(n(mod.int8.q), qw_o), name
+        qx, sa = I.quantize_nhwc(torch.from_numpy(x).to(dev), mod.int8.cpad)
+        _, acc = I.dwconv_i8_nhwc(qx, sa, mod.int8, stride, pad, mod.bias, mod.act, want_acc=True)
+        acc = acc[..., : mod.int8.C]
+    else:
+        stride, pad = mod._geometry()
+        y_o, acc_o, sa_o, sw_o, qw_o = OM.conv_layer(x, w, b, stride, pad, mod.act, res)
+        assert np.array_equal(n(mod.int8.q), qw_o), name
+        qx, sa = I.quantize_nhwc(torch.from_numpy(x).to(dev), mod.int8.cpad)
+        r = None if res is None else torch.from_numpy(res).to(dev)
+        _, acc = I.conv2d_i8_nhwc(qx, sa, mod.int8, stride, pad, mod.bias, r, mod.act, want_acc=True)
+    assert np.array_equal(n(acc).astype(np.int32), acc_o), f"{name}: int32 accumulators differ"
+    np.testing.assert_allclose(y, y_o, rtol=RTOL, atol=ATOL, err_msg=name)
+    if mod.act != I.ACT_SILU:
+        assert np.array_equal(y, y_o), f"{name}: f32 output not bit-exact"
+
+
+def _conv_params(conv):
+    s, p = conv._geometry()
+    return (n(conv.weight), None if conv.bias is None else n(conv.bias), s, p)
+
+
+# --------------------------------------------------------------------------- C3
+
+def test_c3_resnet18(dev):
+    say("C3 ResNet-18 CIFAR b16")
+    model = nets.build("resnet18", seed=0, device=dev)
+    x = WL.c3_input(16, 0)
+    xt = torch.from_numpy(x).to(dev)
+    with torch.no_grad():
+        f32_logits = n(model(xt))
+    assert bt.quantize_for_int8(model) == 20  # every conv; the fc head stays f32
+    recs, hooks = capture(model)
+    with torch.no_grad():
+        feats = model.features(xt)
+        logits = model(xt)
+    for h in hooks:
+        h.remove()
+    assert len(recs) == 40  # 20 layers, two forwards
+    for rec in recs[:20]:
+        check_layer(*rec)
+    # the whole conv stack, chained in the oracle from the network input
+    params = {"stem": _conv_params(model.stem_f.conv)}
+    for i, blk in enumerate(model.body):
+        params[f"body.{i}.c1"] = _conv_params(blk.c1.conv)
+        params[f"body.{i}.c2"] = _conv_params(blk.c2.conv)
+        if blk.down is not None:
+            params[f"body.{i}.down"] = _conv_params(blk.down)
+    feats_o = OM.resnet18_features(params, x)
+    assert np.array_equal(n(feats), feats_o), "conv stack not bit-exact"
+    logits_o = feats_o.mean(axis=(2, 3)) @ n(model.fc.weight).T + n(model.fc.bias)
+    np.testing.assert_allclose(n(logits), logits_o, rtol=1e-5, atol=1e-5)
+    gap = np.abs(n(logits) - f32_logits).max() / np.abs(f32_logits).max()
+    say(f"  int8 vs f32 logits: max |diff| / max |logit| = {gap:.3g}")
+    assert gap < 0.05
+
+
+# --------------------------------------------------------------------------- C4
+
+def test_c4_efficientnet_b0_layers(dev):
+    say("C4 EfficientNet-B0 per-layer parity (batch 2 at 224)")
+    model = nets.build("efficientnet_b0", seed=0, device=dev)
+    assert bt.quantize_for_int8(model) == 49  # 1x1 + depthwise + stem + head; SE and fc f32
+    x = torch.from_numpy(WL.c4_input(2, 0)).to(dev)
+    recs, hooks = capture(model)
+    with torch.no_grad():
+        model(x)
+    for h in hooks:
+        h.remove()
+    assert len(recs) == 49
+    for rec in recs:
+        check_layer(*rec)
+
+
+def test_c4_efficientnet_b0_batch64(dev):
+    say("C4 EfficientNet-B0 b64 forward")
+    model = nets.build("efficientnet_b0", seed=0, device=dev)
+    x = torch.from_numpy(WL.c4_input(64, 0)).to(dev)
+    with torch.no_grad():
+        ref = n(model(x))
+        assert bt.quantize_for_int8(model) == 49
+        y = n(model(x))
+    assert y.shape == (64, 1000) and np.isfinite(y).all()
+    gap = np.abs(y - ref).max() / np.abs(ref).max()
+    say(f"  int8 vs f32 logits: max |diff| / max |logit| = {gap:.3g}")
+    assert gap < 0.1
+
+
+# --------------------------------------------------------------------------- C5
+
+def test_c5_vit_b16(dev):
+    say("C5 ViT-B/16 encoder b32 (layer 0 full, every other Linear on 256 sampled rows)")
+    model = nets.build("vit_b16", seed=0, device=dev)
+    x = torch.from_numpy(WL.c5_input(32, 197, 768, 0)).to(dev)
+    with torch.no_grad():
+        ref = n(model(x))
+    assert bt.quantize_for_int8(model) == 48
+    sample = np.random.default_rng(0).choice(32 * 197, 256, replace=False)
+
+    def rows(name, m):
+        return None if name.startswith("layers.0.") else sample
+
+    recs, hooks = capture(model, rows)
+    with torch.no_grad():
+        y = n(model(x))
+    for h in hooks:
+        h.remove()
+    assert len(recs) == 48
+    for rec in recs:
+        check_layer(*rec)
+    gap = np.abs(y - ref).max() / np.abs(ref).max()
+    say(f"  int8 vs f32 encoder output: max |diff| / max |out| = {gap:.3g}")
+    assert np.isfinite(y).all() and gap < 0.1
