@@ -99,12 +99,47 @@ def cpu_baseline(M_sample=256):
                       f"{M_sample}x4096x4096 rows of the 4096³ workload, min of 3, {t * 1e3:.1f} ms"}
 
 
+def bench_models(dev, stream, steps):
+    """Forward ms of the model configurations: int8 (HIP-graph replay of the compiled
+    model, and eager) beside the same folded model in f32 (torch-ROCm ops)."""
+    import torch
+    import borch_amd as bt
+    from borch_amd import nets, workloads as WL
+    out = {}
+    cases = [("resnet18_b16", "resnet18", lambda: WL.c3_input(16, 0)),
+             ("efficientnet_b0_b64", "efficientnet_b0", lambda: WL.c4_input(64, 0)),
+             ("vit_b16_b32", "vit_b16", lambda: WL.c5_input(32, 197, 768, 0))]
+    for key, name, make in cases:
+        model = nets.build(name, seed=0, device=dev)
+        x = torch.from_numpy(make()).to(dev)
+        with torch.no_grad():
+            f32_ms = time_events(lambda i: model(x), 3, stream)
+            f32_ms = time_events(lambda i: model(x), steps, stream)
+            ref = model(x)
+        c = bt.compiled(model, int8=True, graph=True, fuse=False)
+        with torch.no_grad():
+            y = c(x)
+            eager_ms = time_events(lambda i: model(x), steps, stream)
+            g_ms = time_events(lambda i: c(x), steps, stream)
+        gap = float((y - ref).abs().max() / ref.abs().max())
+        out[key] = {"int8_graph_ms": round(g_ms, 4), "int8_eager_ms": round(eager_ms, 4),
+                    "f32_ms": round(f32_ms, 4), "int8_layers": c.int8_layers,
+                    "max_abs_diff_vs_f32_rel": round(gap, 5)}
+        log(f"{key}: {out[key]}")
+        del model, c, x, y, ref
+        torch.cuda.empty_cache()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--kernels-only", action="store_true",
+                    help="for counter runs: 5 launches of the 4096^3 GEMM and 5 of a 64 MiB device copy "
+                         "(the copy calibrates FETCH_SIZE / WRITE_SIZE), nothing else")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this build runs on one GPU only: the int8 path is measured on 1 MI355X "
@@ -120,6 +155,23 @@ def main():
     require_device(dev)
     stream = torch.cuda.current_stream(dev)
     M = N = K = 4096
+
+    if args.kernels_only:
+        from borch_amd import workloads as WL2
+        a, w, b = WL2.c2_gemm(M, 0)
+        qa, sa = I.quantize_rows(torch.from_numpy(a).to(dev))
+        qw, sw = I.quantize_weight_per_channel(torch.from_numpy(w).to(dev))
+        B = torch.from_numpy(b).to(dev)
+        src = torch.randn(16 << 20, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(5):
+            I.gemm_i8(qa, qw, sa, sw, B)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"kernels_only": True, "gemm_launches": 5, "copy_launches": 5, "copy_bytes": 64 << 20}))
+        return
 
     # ---- headline: 4096³ dynamic-quant GEMM (quantize + GEMM)
     a, w, b = WL.c2_gemm(M, 0)
@@ -184,6 +236,8 @@ def main():
                       "quantize_us": round(quant_ms * 1e3, 3),
                       "quantize_GBps": round(quant_bytes / (quant_ms * 1e-3) / 1e9, 1)}
 
+    models = bench_models(dev, stream, steps=max(args.steps // 2, 10))
+
     traffic = None
     tf = ROOT / "profiles" / "gemm_4096_traffic.json"
     if tf.exists():
@@ -213,6 +267,7 @@ def main():
                      "kernel": "gemm_i8_kernel 256x256 (bq_gemm_i8)", "kernel_ms": round(gemm_ms, 5),
                      "timing": "HIP events around HIP-graph replays on the launch stream"},
         "sweep": sweep,
+        "models": models,
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline()

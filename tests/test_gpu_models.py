@@ -186,3 +186,22 @@ def test_c5_vit_b16(dev):
     gap = np.abs(y - ref).max() / np.abs(ref).max()
     say(f"  int8 vs f32 encoder output: max |diff| / max |out| = {gap:.3g}")
     assert np.isfinite(y).all() and gap < 0.1
+
+
+def test_graph_replay_matches_eager(dev):
+    """The compiled (HIP graph) int8 forward equals the eager int8 forward bit for bit, on
+    every replay, with eager work and synchronizations between replays."""
+    say("graph replay vs eager (ResNet-18 b4, EfficientNet-B0 b2)")
+    for name, x in (("resnet18", WL.c3_input(4, 1)), ("efficientnet_b0", WL.c4_input(2, 1))):
+        model = nets.build(name, seed=1, device=dev)
+        c = bt.compiled(model, int8=True, graph=True, fuse=False)
+        xt = torch.from_numpy(x).to(dev)
+        with torch.no_grad():
+            eager = n(model(xt))
+            for i in range(4):
+                got = n(c(xt))
+                assert np.array_equal(got, eager), f"{name} replay {i}"
+                model(torch.randn_like(xt))  # eager work in between
+                torch.cuda.synchronize()
+            other = torch.from_numpy(WL.c3_input(4, 2) if name == "resnet18" else WL.c4_input(2, 2)).to(dev)
+            assert np.array_equal(n(c(other)), n(model(other))), f"{name} new input"
