@@ -423,6 +423,17 @@ __global__ __launch_bounds__(GV_WAVES * 64) void gemv_i8_kernel(const GemmP p) {
   if (row0 >= p.N) return;
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.W + (size_t)row0 * p.K, (uint32_t)(min(RPW, p.N - row0) * p.K));
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, (uint32_t)(p.M * p.K));
+  // Lane j*MR + m stores output (m, row0 + j); its scales and bias are fetched now, ahead
+  // of the weight stream, so the tail does not wait on another memory round trip.
+  const int my_j = lane / MR, my_m = lane % MR;
+  const int my_n = row0 + my_j;
+  const bool writer = lane < RPW * MR && my_n < p.N && my_m < p.M;
+  float e_sa = 0.f, e_sw = 0.f, e_b = 0.f;
+  if (writer) {
+    e_sa = p.sa_per_row ? p.sA[my_m] : p.sA[0];
+    e_sw = p.sW[my_n];
+    e_b = p.bias ? p.bias[my_n] : 0.f;
+  }
   v4i x[MR][KC];
 #pragma unroll
   for (int m = 0; m < MR; ++m)
@@ -452,21 +463,18 @@ __global__ __launch_bounds__(GV_WAVES * 64) void gemv_i8_kernel(const GemmP p) {
         for (int q = 0; q < 4; ++q) a = __builtin_amdgcn_sdot4(w[j][c][q], x[m][c][q], a, false);
       acc[j][m] = wave_sum(a);
     }
-  // lane j*MR + m writes output (m, row0 + j)
+  int mine = 0;
 #pragma unroll
   for (int j = 0; j < RPW; ++j)
 #pragma unroll
-    for (int m = 0; m < MR; ++m) {
-      const int n = row0 + j;
-      if (lane == j * MR + m && n < p.N && m < p.M) {
-        const size_t idx = (size_t)m * p.N + n;
-        const float sa = p.sa_per_row ? p.sA[m] : p.sA[0];
-        const float rv = p.res ? p.res[idx] : 0.f;
-        p.out[idx] = dequant_one(acc[j][m], sa, p.sW[n], p.bias ? p.bias[n] : 0.f, p.bias != nullptr, rv,
-                                 p.res != nullptr, p.act);
-        if (p.acc) p.acc[idx] = acc[j][m];
-      }
-    }
+    for (int m = 0; m < MR; ++m)
+      if (lane == j * MR + m) mine = acc[j][m];
+  if (writer) {
+    const size_t idx = (size_t)my_m * p.N + my_n;
+    const float rv = p.res ? p.res[idx] : 0.f;
+    p.out[idx] = dequant_one(mine, e_sa, e_sw, e_b, p.bias != nullptr, rv, p.res != nullptr, p.act);
+    if (p.acc) p.acc[idx] = mine;
+  }
 }
 
 template <int MR>
@@ -483,47 +491,63 @@ static bool launch_gemv(const GemmP& p, hipStream_t st) {
 
 // -------------------------------------------------------------------------- depthwise
 
-// One thread: 4 channels of one output pixel. x NHWC int8, w [KH*KW, C] int8.
+// One thread: CPT (4 or 8) consecutive channels of one output pixel; consecutive threads
+// take consecutive channel groups of the same pixel, so each tap load and the output
+// store are contiguous across the wave. x NHWC int8, w [KH*KW, C] int8; no MFMA
+// (bandwidth-bound: the f32 output write dominates).
+template <int CPT>
 __global__ __launch_bounds__(256) void dwconv_i8_kernel(const int8_t* __restrict__ x, int Nimg, int H, int Wd,
                                                         int C, const int8_t* __restrict__ w, int KH, int KW,
                                                         int stride, int pad, int OH, int OW,
                                                         const float* __restrict__ sA, const float* __restrict__ sW,
                                                         const float* __restrict__ bias, int act,
                                                         float* __restrict__ out, int32_t* __restrict__ acc) {
-  const int C4 = C >> 2;
-  const int64_t total = (int64_t)Nimg * OH * OW * C4;
+  typedef int vw __attribute__((ext_vector_type(CPT / 4)));
+  const int CG = C / CPT;
+  const int64_t total = (int64_t)Nimg * OH * OW * CG;
   const float sa = sA[0];
   for (int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; g < total; g += (int64_t)gridDim.x * blockDim.x) {
-    const int c4 = (int)(g % C4);
-    const int64_t pix = g / C4;
+    const int cg = (int)(g % CG);
+    const int64_t pix = g / CG;
     const int ow = (int)(pix % OW);
     const int64_t t = pix / OW;
     const int oh = (int)(t % OH);
     const int n = (int)(t / OH);
-    int a0 = 0, a1 = 0, a2 = 0, a3 = 0;
+    const int c = cg * CPT;
+    int a[CPT];
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) a[j] = 0;
     for (int kh = 0; kh < KH; ++kh) {
       const int ih = oh * stride - pad + kh;
       if (ih < 0 || ih >= H) continue;
+      const int8_t* xrow = x + (((size_t)n * H + ih) * Wd) * C + c;
+      const int8_t* wrow = w + (size_t)(kh * KW) * C + c;
       for (int kw = 0; kw < KW; ++kw) {
         const int iw = ow * stride - pad + kw;
         if (iw < 0 || iw >= Wd) continue;
-        const uint32_t xv = *reinterpret_cast<const uint32_t*>(x + (((size_t)n * H + ih) * Wd + iw) * C + c4 * 4);
-        const uint32_t wv = *reinterpret_cast<const uint32_t*>(w + (size_t)(kh * KW + kw) * C + c4 * 4);
-        a0 += (int)(int8_t)(xv & 0xff) * (int)(int8_t)(wv & 0xff);
-        a1 += (int)(int8_t)((xv >> 8) & 0xff) * (int)(int8_t)((wv >> 8) & 0xff);
-        a2 += (int)(int8_t)((xv >> 16) & 0xff) * (int)(int8_t)((wv >> 16) & 0xff);
-        a3 += (int)(int8_t)(xv >> 24) * (int)(int8_t)(wv >> 24);
+        const vw xv = *reinterpret_cast<const vw*>(xrow + (size_t)iw * C);
+        const vw wv = *reinterpret_cast<const vw*>(wrow + (size_t)kw * C);
+#pragma unroll
+        for (int q = 0; q < CPT / 4; ++q) {
+          const uint32_t xq = (uint32_t)xv[q], wq = (uint32_t)wv[q];
+#pragma unroll
+          for (int b = 0; b < 4; ++b)
+            a[q * 4 + b] += (int)(int8_t)((xq >> (8 * b)) & 0xff) * (int)(int8_t)((wq >> (8 * b)) & 0xff);
+        }
       }
     }
-    const int c = c4 * 4;
-    const int av[4] = {a0, a1, a2, a3};
-    float o[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      o[j] = dequant_one(av[j], sa, sW[c + j], bias ? bias[c + j] : 0.f, bias != nullptr, 0.f, false, act);
     const size_t idx = (size_t)pix * C + c;
-    *reinterpret_cast<float4*>(out + idx) = make_float4(o[0], o[1], o[2], o[3]);
-    if (acc) *reinterpret_cast<int4*>(acc + idx) = make_int4(a0, a1, a2, a3);
+#pragma unroll
+    for (int q = 0; q < CPT / 4; ++q) {
+      float o[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int cc = c + q * 4 + j;
+        o[j] = dequant_one(a[q * 4 + j], sa, sW[cc], bias ? bias[cc] : 0.f, bias != nullptr, 0.f, false, act);
+      }
+      *reinterpret_cast<float4*>(out + idx + q * 4) = make_float4(o[0], o[1], o[2], o[3]);
+      if (acc) *reinterpret_cast<int4*>(acc + idx + q * 4) = make_int4(a[q * 4], a[q * 4 + 1], a[q * 4 + 2], a[q * 4 + 3]);
+    }
   }
 }
 
@@ -553,13 +577,19 @@ static void launch_gemm(const GemmP& p, hipStream_t st) {
     case 5: return launch_tiled<256, 128, 2, 2, CONV>(p, st);
     case 6: return launch_tiled<128, 256, 2, 2, CONV>(p, st);
     case 7: return launch_tiled<64, 64, 2, 2, CONV>(p, st);
+    case 8: return launch_tiled<256, 64, 4, 1, CONV>(p, st);
     default: break;
   }
+  // The largest tile that still fills the chip (>= 192 / 128 workgroups) without wasting
+  // most of its columns; narrow outputs (N <= 64) take a tall 256x64 tile.
   const long long t256 = (long long)((p.M + 255) / 256) * ((p.N + 255) / 256);
   const long long t128 = (long long)((p.M + 127) / 128) * ((p.N + 127) / 128);
-  if (t256 >= 192)
+  const long long t256x64 = (long long)((p.M + 255) / 256) * ((p.N + 63) / 64);
+  if (p.N <= 64 && t256x64 >= 128)
+    launch_tiled<256, 64, 4, 1, CONV>(p, st);
+  else if (t256 >= 192 && p.N >= 192)
     launch_tiled<256, 256, 2, 4, CONV>(p, st);
-  else if (t128 >= 128)
+  else if (t128 >= 128 && p.N >= 96)
     launch_tiled<128, 128, 2, 2, CONV>(p, st);
   else
     launch_tiled<64, 64, 2, 2, CONV>(p, st);
@@ -668,12 +698,18 @@ int bq_dwconv_i8_nhwc(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t 
   if (((uintptr_t)x & 3) || ((uintptr_t)w & 3) || ((uintptr_t)out & 15) || ((uintptr_t)acc & 15))
     return set_error(BQ_ERR_ARG, "%s: misaligned pointer", what);
   if (act < BQ_ACT_NONE || act > BQ_ACT_SILU) return set_error(BQ_ERR_ARG, "%s: bad activation %d", what, act);
-  const int64_t total = N * OH * OW * (C / 4);
+  const bool wide = (C % 8 == 0) && ((uintptr_t)x & 7) == 0 && ((uintptr_t)w & 7) == 0;
+  const int64_t total = N * OH * OW * (C / (wide ? 8 : 4));
   int64_t blocks = (total + 255) / 256;
   if (blocks > 65536) blocks = 65536;
-  dwconv_i8_kernel<<<(unsigned)blocks, 256, 0, (hipStream_t)stream>>>(
-      x, (int)N, (int)H, (int)W, (int)C, w, (int)KH, (int)KW, (int)stride, (int)pad, (int)OH, (int)OW, sA, sW, bias,
-      act, out, acc);
+  if (wide)
+    dwconv_i8_kernel<8><<<(unsigned)blocks, 256, 0, (hipStream_t)stream>>>(
+        x, (int)N, (int)H, (int)W, (int)C, w, (int)KH, (int)KW, (int)stride, (int)pad, (int)OH, (int)OW, sA, sW,
+        bias, act, out, acc);
+  else
+    dwconv_i8_kernel<4><<<(unsigned)blocks, 256, 0, (hipStream_t)stream>>>(
+        x, (int)N, (int)H, (int)W, (int)C, w, (int)KH, (int)KW, (int)stride, (int)pad, (int)OH, (int)OW, sA, sW,
+        bias, act, out, acc);
   return check_launch(what);
 }
 

@@ -154,6 +154,45 @@ __global__ __launch_bounds__(QT_THREADS) void quantize_tensor_kernel(const float
   }
 }
 
+// Padded-channel variant (C < Cpad, Cpad % 16 == 0): one thread per 16-byte chunk of a
+// pixel's Cpad output bytes; it reads that chunk's (up to 16) input channels, which are
+// contiguous, and stores one 16-byte word. No per-element division.
+__global__ __launch_bounds__(QT_THREADS) void quantize_pad16_kernel(const float* __restrict__ x, int64_t P,
+                                                                    int C, int Cpad,
+                                                                    const float* __restrict__ parts, int nparts,
+                                                                    int8_t* __restrict__ q, float* __restrict__ s) {
+  __shared__ float red[QT_THREADS / 64];
+  float m = 0.f;
+  for (int i = threadIdx.x; i < nparts; i += QT_THREADS) m = fmaxf(m, parts[i]);
+  m = wave_max(m);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  float peak = red[0];
+  for (int i = 1; i < QT_THREADS / 64; ++i) peak = fmaxf(peak, red[i]);
+  const float sc = scale_of(peak);
+  if (blockIdx.x == 0 && threadIdx.x == 0) s[0] = sc;
+  const double sd = sc;
+  const int chunks = Cpad / 16;
+  const int64_t total = P * chunks;
+  for (int64_t i = (int64_t)blockIdx.x * QT_THREADS + threadIdx.x; i < total; i += (int64_t)gridDim.x * QT_THREADS) {
+    const int64_t p = i / chunks;
+    const int c0 = (int)(i - p * chunks) * 16;
+    const float* xp = x + p * C + c0;
+    uint32_t wv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      int b[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int c = c0 + j * 4 + t;
+        b[t] = c < C ? quant_one(xp[j * 4 + t], sd) : 0;
+      }
+      wv[j] = pack4(b[0], b[1], b[2], b[3]);
+    }
+    *reinterpret_cast<uint4*>(q + i * 16) = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+  }
+}
+
 static int nparts_for(int64_t n) {
   int64_t p = (n + QT_THREADS * 16 - 1) / (QT_THREADS * 16);
   if (p < 1) p = 1;
@@ -235,6 +274,14 @@ int bq_quantize_nhwc(const float* x, int64_t P, int64_t C, int64_t Cpad, int8_t*
   const int64_t chunk = n == 0 ? 1 : (n + np - 1) / np;
   absmax_parts_kernel<<<np, QT_THREADS, 0, st>>>(x, n, ((chunk + 3) / 4) * 4, parts);
   if (int r = check_launch(what)) return r;
+  if (C != Cpad && Cpad % 16 == 0 && ((uintptr_t)q & 15) == 0) {
+    const int64_t chunks = P * (Cpad / 16);
+    int64_t blocks = (chunks + QT_THREADS - 1) / QT_THREADS;
+    if (blocks > 8192) blocks = 8192;
+    if (blocks < 1) blocks = 1;
+    quantize_pad16_kernel<<<(unsigned)blocks, QT_THREADS, 0, st>>>(x, P, (int)C, (int)Cpad, parts, np, q, s);
+    return check_launch(what);
+  }
   const int64_t words = (P * Cpad + 3) / 4;
   int64_t blocks = (words + QT_THREADS - 1) / QT_THREADS;
   if (blocks > 4096) blocks = 4096;

@@ -68,7 +68,9 @@ def test_quantize_rows_exact_ties(dev):
 
 
 @pytest.mark.parametrize("shape,cpad,cl", [((2, 3, 8, 8), 16, False), ((2, 64, 16, 16), 64, True),
-                                          ((3, 24, 5, 7), 32, True), ((1, 5, 3, 3), 8, False)])
+                                          ((3, 24, 5, 7), 32, True), ((1, 5, 3, 3), 8, False),
+                                          ((4, 3, 33, 31), 16, False), ((2, 40, 9, 9), 48, True),
+                                          ((1, 17, 4, 4), 32, True)])
 def test_quantize_nhwc(dev, shape, cpad, cl):
     say(f"quantize_nhwc {shape} cpad={cpad} channels_last={cl}")
     rng = np.random.default_rng(sum(shape))
@@ -193,6 +195,8 @@ CONV_CASES = [
     (1, 16, 9, 24, 5, 2, 2),
     (2, 40, 7, 48, 1, 1, 0),     # 1x1 stride 1 (dense path), C padded to 48
     (16, 64, 32, 64, 3, 1, 1),   # C3 full batch
+    (8, 3, 56, 32, 3, 2, 1),     # EfficientNet stem shape (N=32 outputs: the tall 256x64 tile)
+    (4, 24, 28, 40, 1, 1, 0),    # 1x1 with C padded 24 -> 32, N=40
 ]
 
 
