@@ -79,7 +79,26 @@ __device__ __forceinline__ void tile_of(int id, int G, int tiles_m, int tiles_n,
   bn = first_n + in % gsize;
 }
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, bool CONV>
+// Scheduling hints: NMMA MFMAs, each followed by up to ceil(COUNT/NMMA) instructions of
+// class MASK (0x008 MFMA, 0x020 VMEM read, 0x100 DS read, 0x200 DS write), so memory
+// instructions issue between MFMAs instead of in one block.
+template <int MASK, int N>
+__device__ __forceinline__ void sched_group() {
+  if constexpr (N > 0) __builtin_amdgcn_sched_group_barrier(MASK, N, 0);
+}
+template <int MASK, int COUNT, int NMMA, int... I>
+__device__ __forceinline__ void interleave_impl(std::integer_sequence<int, I...>) {
+  constexpr int per = (COUNT + NMMA - 1) / NMMA;
+  ((sched_group<0x008, 1>(),
+    sched_group<MASK, (COUNT - I * per >= per ? per : (COUNT - I * per > 0 ? COUNT - I * per : 0))>()),
+   ...);
+}
+template <bool ON, int MASK, int COUNT, int NMMA>
+__device__ __forceinline__ void interleave() {
+  if constexpr (ON) interleave_impl<MASK, COUNT, NMMA>(std::make_integer_sequence<int, NMMA>{});
+}
+
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool CONV, bool SCHED = true>
 __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const GemmP p) {
   constexpr int T = WAVES_M * WAVES_N * 64;
   constexpr int WTM = BM / WAVES_M;  // wave tile rows
@@ -203,35 +222,53 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
 #pragma unroll
     for (int j = 0; j < TN; ++j) c[i][j] = v16i{};
 
-  // Pipeline: the global loads of tile kt+2 are in flight while tile kt computes; tile
-  // kt+1 is written to the other LDS buffer in the middle of tile kt; the fragments of the
-  // next 32-byte K slice are read while the current slice's MFMAs run.
+  // Pipeline over the four 32-byte K slices (ks) of a 128-byte stage:
+  //   ks0: MFMAs of slice 0  | LDS reads of slice 1
+  //   ks1: MFMAs of slice 1  | LDS reads of slice 2, LDS writes of stage kt+1 (other buffer)
+  //   ks2: MFMAs of slice 2  | LDS reads of slice 3, global loads of stage kt+2
+  //   barrier (stage kt+1 written by every wave; every read of stage kt issued and done)
+  //   ks3: MFMAs of slice 3  | LDS reads of slice 0 of stage kt+1
+  // One barrier per stage, placed so the next stage's first fragments load under the last
+  // slice's MFMAs; the MFMAs of each slice are interleaved with its memory instructions.
   const int KT = (p.K + BK - 1) / BK;
   v4i ga[A_LD], gb[B_LD];
   load(0, ga, gb);
   store(0, ga, gb);
-  if (KT > 1) load(1, ga, gb);
+  load(1, ga, gb);
   __syncthreads();
   v4i af[2][TM], bf[2][TN];
   frags(0, 0, af[0], bf[0]);
+  auto mma = [&](const v4i (&a)[TM], const v4i (&b)[TN]) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) c[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], c[i][j], 0, 0, 0);
+  };
+  constexpr int NMMA = TM * TN, NRD = TM + TN;
+  constexpr int NLD = A_LD + B_LD;
   for (int kt = 0; kt < KT; ++kt) {
     const int cur = kt & 1;
-#pragma unroll
-    for (int ks = 0; ks < BK / 32; ++ks) {
-      if (ks + 1 < BK / 32) frags(cur, ks + 1, af[(ks + 1) & 1], bf[(ks + 1) & 1]);
-      if (ks == 1 && kt + 1 < KT) {
-        store(cur ^ 1, ga, gb);
-        if (kt + 2 < KT) load(kt + 2, ga, gb);
-      }
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-          c[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[ks & 1][i], bf[ks & 1][j], c[i][j], 0, 0, 0);
-    }
+    frags(cur, 1, af[1], bf[1]);
+    mma(af[0], bf[0]);
+    interleave<SCHED, 0x100, NRD, NMMA>();
+    __builtin_amdgcn_sched_barrier(0);
+    frags(cur, 2, af[0], bf[0]);
+    store(cur ^ 1, ga, gb);  // unconditional: past the last stage it writes a buffer no one reads
+    mma(af[1], bf[1]);
+    interleave<SCHED, 0x100 | 0x200, NRD + NLD, NMMA>();
+    __builtin_amdgcn_sched_barrier(0);
+    frags(cur, 3, af[1], bf[1]);
+    load(kt + 2, ga, gb);  // past K every offset is out of range: zeros, no memory access
+    mma(af[0], bf[0]);
+    interleave<SCHED, 0x100 | 0x020, NRD + NLD, NMMA>();
+    __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
-    if (kt + 1 < KT) frags(cur ^ 1, 0, af[0], bf[0]);
+    frags(cur ^ 1, 0, af[0], bf[0]);
+    mma(af[1], bf[1]);
+    interleave<SCHED, 0x100, NRD, NMMA>();
+    __builtin_amdgcn_sched_barrier(0);
   }
+  __syncthreads();
 
   // Epilogue, one 32-row slice of the wave tile at a time: the int32 results go through a
   // per-wave LDS patch (exact), come back as four consecutive columns of one row per lane,
@@ -553,10 +590,10 @@ __global__ __launch_bounds__(256) void dwconv_i8_kernel(const int8_t* __restrict
 
 // ---------------------------------------------------------------------------- dispatch
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, bool CONV>
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool CONV, bool SCHED = true>
 static void launch_tiled(const GemmP& p, hipStream_t st) {
   const int tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
-  gemm_i8_kernel<BM, BN, WAVES_M, WAVES_N, CONV><<<tiles, WAVES_M * WAVES_N * 64, 0, st>>>(p);
+  gemm_i8_kernel<BM, BN, WAVES_M, WAVES_N, CONV, SCHED><<<tiles, WAVES_M * WAVES_N * 64, 0, st>>>(p);
 }
 
 // BQ_GEMM_CFG forces one tile configuration (tuning sweeps); unset = the shape rule.
@@ -578,6 +615,8 @@ static void launch_gemm(const GemmP& p, hipStream_t st) {
     case 6: return launch_tiled<128, 256, 2, 2, CONV>(p, st);
     case 7: return launch_tiled<64, 64, 2, 2, CONV>(p, st);
     case 8: return launch_tiled<256, 64, 4, 1, CONV>(p, st);
+    case 9: return launch_tiled<256, 256, 2, 4, CONV, false>(p, st);
+    case 10: return launch_tiled<256, 256, 2, 2, CONV, false>(p, st);
     default: break;
   }
   // The largest tile that still fills the chip (>= 192 / 128 workgroups) without wasting
