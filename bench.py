@@ -73,30 +73,63 @@ def time_graph(g, calls, replays, stream):
     return time_events(lambda i: g.replay(), replays, stream) / calls
 
 
-def cpu_baseline(M_sample=256):
-    """The oracle's int8 arithmetic (per-row quantize + exact GEMM + epilogue) on the host,
-    on a bounded sample: M_sample rows of the 4096³ workload, scaled to TOPS."""
+def cpu_baseline(M_sample=512):
+    """The reference's CPU path on the host cores, on a bounded sample of the same workload.
+
+    ``value``: borch_cpu's f32 ``gemm_bias_act`` (4x16 register-blocked, row-sliced over
+    threads; restated in C from borch-ts/wasm/src/lib.rs:508-584 in oracle/cpu_ref.c) on
+    M_sample rows of the 4096^3 Linear, min of 3 — "kind": "port" (the Rust/wasm original
+    cannot be built or run here). Beside it: the numpy int8 oracle on 256 rows, and one
+    ResNet-18 CIFAR b16 f32 forward through the same C kernels (im2col_rows +
+    gemm_bias_act per conv, as the reference CPU runner does)."""
+    from oracle import cpu_ref as R
     from oracle import quant as O
     from borch_amd import workloads as WL
-    try:
-        from threadpoolctl import threadpool_info
-        threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
-    except Exception:  # pragma: no cover
-        threads = os.cpu_count() or 1
+    nthreads = R.threads()
     a, w, b = WL.c2_gemm(M_sample, 0)
-    qw, sw = O.quantize_weight_per_channel(w)
+    wt = np.ascontiguousarray(w.T)
+    R.gemm(a[:16], wt, b, 0, nthreads)
     times = []
     for _ in range(3):
         t0 = time.perf_counter()
-        qa, sa = O.quantize_rows(a)
-        acc = O.gemm_i8_i32(qa, qw)
-        O.dequant(acc, sa, sw, b)
+        R.gemm(a, wt, b, 0, nthreads)
         times.append(time.perf_counter() - t0)
     t = min(times)
-    ops = 2 * M_sample * 4096 * 4096
-    return {"value": round(ops / t / 1e12, 4), "unit": "TOPS", "cores": int(threads), "kind": "port",
-            "sample": f"oracle int8 Linear (per-row quantize + float64-BLAS exact GEMM + f32 epilogue), "
-                      f"{M_sample}x4096x4096 rows of the 4096³ workload, min of 3, {t * 1e3:.1f} ms"}
+    out = {"value": round(2 * M_sample * 4096 * 4096 / t / 1e12, 5), "unit": "TOPS", "cores": int(nthreads),
+           "kind": "port",
+           "sample": f"borch_cpu gemm_bias_act (f32, C restatement of lib.rs:508-584, {nthreads} threads) on "
+                     f"{M_sample}x4096x4096 rows of the 4096^3 workload, min of 3: {t * 1e3:.1f} ms"}
+    # int8 oracle (numpy: per-row quantize + float64-BLAS exact GEMM + f32 epilogue)
+    a2, w2, b2 = WL.c2_gemm(256, 0)
+    qw, sw = O.quantize_weight_per_channel(w2)
+    t0 = time.perf_counter()
+    qa, sa = O.quantize_rows(a2)
+    O.dequant(O.gemm_i8_i32(qa, qw), sa, sw, b2)
+    out["int8_oracle_TOPS"] = round(2 * 256 * 4096 * 4096 / (time.perf_counter() - t0) / 1e12, 5)
+    # ResNet-18 CIFAR b16 f32 through the C kernels
+    try:
+        import torch
+        from borch_amd import nets
+        model = nets.build("resnet18", seed=0, device="cpu")
+
+        def cp(conv):
+            s, p = conv._geometry()
+            return (conv.weight.detach().numpy(), conv.bias.detach().numpy(), s, p)
+        params = {"stem": cp(model.stem_f.conv),
+                  "fc": (model.fc.weight.detach().numpy(), model.fc.bias.detach().numpy())}
+        for i, blk in enumerate(model.body):
+            params[f"body.{i}.c1"] = cp(blk.c1.conv)
+            params[f"body.{i}.c2"] = cp(blk.c2.conv)
+            if blk.down is not None:
+                params[f"body.{i}.down"] = cp(blk.down)
+        x = WL.c3_input(16, 0)
+        R.resnet18_forward(params, x[:2], nthreads)
+        t0 = time.perf_counter()
+        R.resnet18_forward(params, x, nthreads)
+        out["resnet18_b16_f32_ms"] = round((time.perf_counter() - t0) * 1e3, 2)
+    except Exception as e:  # pragma: no cover - reported, not fatal
+        out["resnet18_b16_f32_ms"] = f"failed: {e}"
+    return out
 
 
 def bench_models(dev, stream, steps):
