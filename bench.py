@@ -158,6 +158,17 @@ def bench_models(dev, stream, steps):
         out[key] = {"int8_graph_ms": round(g_ms, 4), "int8_eager_ms": round(eager_ms, 4),
                     "f32_ms": round(f32_ms, 4), "int8_layers": c.int8_layers,
                     "max_abs_diff_vs_f32_rel": round(gap, 5)}
+        if name == "resnet18":
+            # calibrated static scales + int8 twins (calibrate_int8): one quantize pass a forward
+            calib = [torch.from_numpy(WL.c3_input(16, s)).to(dev) for s in (11, 12)]
+            bt.calibrate_int8(model, calib)
+            c2 = bt.compiled(model, int8=False, graph=True, fuse=False)
+            with torch.no_grad():
+                ys = c2(x)
+                s_ms = time_events(lambda i: c2(x), steps, stream)
+            out[key]["int8_static_graph_ms"] = round(s_ms, 4)
+            out[key]["static_max_abs_diff_vs_f32_rel"] = round(float((ys - ref).abs().max() / ref.abs().max()), 5)
+            del c2, ys
         log(f"{key}: {out[key]}")
         del model, c, x, y, ref
         torch.cuda.empty_cache()

@@ -38,6 +38,8 @@ struct GemmP {
   int H, Wd, C, OH, OW, KWd, stride, pad;
   int64_t Nimg_HWC;  // conv: bytes of the NHWC activation
   int vec_ok;        // N % 4 == 0 and out/res/acc 16-byte aligned: float4 epilogue
+  const float* s_out;  // static output scale [1] (nullable): the int8 twin of the output
+  int8_t* q_out;       // [M, N] int8 = clip(rint(y / s_out)) (nullable)
 };
 
 constexpr int BK = 128;  // bytes of K per LDS stage: one cache line per row
@@ -140,6 +142,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
     s_sw[i] = n < p.N ? p.sW[n] : 0.f;
     s_b[i] = (n < p.N && p.bias) ? p.bias[n] : 0.f;
   }
+  const double s_out = p.q_out ? (double)p.s_out[0] : 0.0;
 
   // Each thread loads 16-byte chunk `kc` of rows lr + i * ROWS_PER_PASS.
   const int kc = tid & 7;
@@ -327,6 +330,9 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
           }
           *reinterpret_cast<float4*>(p.out + idx) = o;
           if (p.acc) *reinterpret_cast<int4*>(p.acc + idx) = a;
+          if (p.q_out)
+            *reinterpret_cast<uint32_t*>(p.q_out + idx) =
+                pack4(quant_one(o.x, s_out), quant_one(o.y, s_out), quant_one(o.z, s_out), quant_one(o.w, s_out));
         }
       }
     } else if (!p.vec_ok) {
@@ -341,8 +347,10 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
             const int a = patch[row * PITCH + col4 * 4 + q];
             const size_t idx = (size_t)m * p.N + n + q;
             const float rv = has_r ? p.res[idx] : 0.f;
-            p.out[idx] = dequant_one(a, s_sa[mloc], s_sw[ncol + q], s_b[ncol + q], true, rv, has_r, p.act);
+            const float o = dequant_one(a, s_sa[mloc], s_sw[ncol + q], s_b[ncol + q], true, rv, has_r, p.act);
+            p.out[idx] = o;
             if (p.acc) p.acc[idx] = a;
+            if (p.q_out) p.q_out[idx] = (int8_t)quant_one(o, s_out);
           }
         }
       }
@@ -683,11 +691,10 @@ int bq_gemm_i8(const int8_t* A, const int8_t* W, int64_t M, int64_t N, int64_t K
   return check_launch(what);
 }
 
-int bq_conv2d_i8_nhwc(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t C, const int8_t* w,
-                      int64_t O, int64_t KH, int64_t KW, int64_t stride, int64_t pad, const float* sA,
-                      const float* sW, const float* bias, const float* residual, int act, float* out,
-                      int32_t* acc, bq_stream_t stream) {
-  const char* what = "bq_conv2d_i8_nhwc";
+static int conv_impl(const char* what, const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t C,
+                     const int8_t* w, int64_t O, int64_t KH, int64_t KW, int64_t stride, int64_t pad,
+                     const float* sA, const float* sW, const float* bias, const float* residual, int act,
+                     float* out, int32_t* acc, const float* s_out, int8_t* q_out, bq_stream_t stream) {
   if (N < 0 || H < 1 || W < 1 || C < 1 || O < 1 || KH < 1 || KW < 1 || stride < 1 || pad < 0)
     return set_error(BQ_ERR_ARG, "%s: bad geometry", what);
   if (C % 16) return set_error(BQ_ERR_UNSUPPORTED, "%s: C=%lld is not a multiple of 16 (pad it)", what, (long long)C);
@@ -710,13 +717,33 @@ int bq_conv2d_i8_nhwc(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t 
   p.H = (int)H; p.Wd = (int)W; p.C = (int)C; p.OH = (int)OH; p.OW = (int)OW; p.KWd = (int)KW;
   p.stride = (int)stride; p.pad = (int)pad;
   p.Nimg_HWC = N * H * W * C;
-  p.vec_ok = (O % 4 == 0) && aligned16(out) && aligned16(acc) && aligned16(residual);
+  p.vec_ok = (O % 4 == 0) && aligned16(out) && aligned16(acc) && aligned16(residual) && ((uintptr_t)q_out & 3) == 0;
+  p.s_out = s_out;
+  p.q_out = q_out;
   hipStream_t st = (hipStream_t)stream;
   if (KH == 1 && KW == 1 && stride == 1 && pad == 0)
     launch_gemm<false>(p, st);  // a 1x1 conv is the dense GEMM on [N*H*W, C]
   else
     launch_gemm<true>(p, st);
   return check_launch(what);
+}
+
+int bq_conv2d_i8_nhwc(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t C, const int8_t* w,
+                      int64_t O, int64_t KH, int64_t KW, int64_t stride, int64_t pad, const float* sA,
+                      const float* sW, const float* bias, const float* residual, int act, float* out,
+                      int32_t* acc, bq_stream_t stream) {
+  return conv_impl("bq_conv2d_i8_nhwc", x, N, H, W, C, w, O, KH, KW, stride, pad, sA, sW, bias, residual, act, out,
+                   acc, nullptr, nullptr, stream);
+}
+
+int bq_conv2d_i8_nhwc_q(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t C, const int8_t* w,
+                        int64_t O, int64_t KH, int64_t KW, int64_t stride, int64_t pad, const float* sA,
+                        const float* sW, const float* bias, const float* residual, int act, float* out,
+                        int32_t* acc, const float* s_out, int8_t* q_out, bq_stream_t stream) {
+  if (!s_out || !q_out) return set_error(BQ_ERR_ARG, "bq_conv2d_i8_nhwc_q: null s_out or q_out");
+  if (O % 16) return set_error(BQ_ERR_UNSUPPORTED, "bq_conv2d_i8_nhwc_q: O=%lld is not a multiple of 16", (long long)O);
+  return conv_impl("bq_conv2d_i8_nhwc_q", x, N, H, W, C, w, O, KH, KW, stride, pad, sA, sW, bias, residual, act,
+                   out, acc, s_out, q_out, stream);
 }
 
 int bq_dwconv_i8_nhwc(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t C, const int8_t* w, int64_t KH,

@@ -120,7 +120,8 @@ __global__ __launch_bounds__(QT_THREADS) void quantize_tensor_kernel(const float
                                                                      int C, int Cpad,
                                                                      const float* __restrict__ parts,
                                                                      int nparts, int8_t* __restrict__ q,
-                                                                     float* __restrict__ s) {
+                                                                     float* __restrict__ s,
+                                                                     const float* __restrict__ s_given) {
   __shared__ float red[QT_THREADS / 64];
   float m = 0.f;
   for (int i = threadIdx.x; i < nparts; i += QT_THREADS) m = fmaxf(m, parts[i]);
@@ -129,8 +130,8 @@ __global__ __launch_bounds__(QT_THREADS) void quantize_tensor_kernel(const float
   __syncthreads();
   float peak = red[0];
   for (int i = 1; i < QT_THREADS / 64; ++i) peak = fmaxf(peak, red[i]);
-  const float sc = scale_of(peak);
-  if (blockIdx.x == 0 && threadIdx.x == 0) s[0] = sc;
+  const float sc = s_given ? s_given[0] : scale_of(peak);
+  if (!s_given && blockIdx.x == 0 && threadIdx.x == 0) s[0] = sc;
   const double sd = sc;
   const int64_t total = P * (int64_t)Cpad;
   const int64_t words = (total + 3) / 4;
@@ -160,7 +161,8 @@ __global__ __launch_bounds__(QT_THREADS) void quantize_tensor_kernel(const float
 __global__ __launch_bounds__(QT_THREADS) void quantize_pad16_kernel(const float* __restrict__ x, int64_t P,
                                                                     int C, int Cpad,
                                                                     const float* __restrict__ parts, int nparts,
-                                                                    int8_t* __restrict__ q, float* __restrict__ s) {
+                                                                    int8_t* __restrict__ q, float* __restrict__ s,
+                                                                    const float* __restrict__ s_given) {
   __shared__ float red[QT_THREADS / 64];
   float m = 0.f;
   for (int i = threadIdx.x; i < nparts; i += QT_THREADS) m = fmaxf(m, parts[i]);
@@ -169,8 +171,8 @@ __global__ __launch_bounds__(QT_THREADS) void quantize_pad16_kernel(const float*
   __syncthreads();
   float peak = red[0];
   for (int i = 1; i < QT_THREADS / 64; ++i) peak = fmaxf(peak, red[i]);
-  const float sc = scale_of(peak);
-  if (blockIdx.x == 0 && threadIdx.x == 0) s[0] = sc;
+  const float sc = s_given ? s_given[0] : scale_of(peak);
+  if (!s_given && blockIdx.x == 0 && threadIdx.x == 0) s[0] = sc;
   const double sd = sc;
   const int chunks = Cpad / 16;
   const int64_t total = P * chunks;
@@ -259,35 +261,48 @@ int bq_quantize_weight_per_channel(const float* w, int64_t N, int64_t K, int8_t*
 
 size_t bq_quantize_tensor_ws_bytes(int64_t n) { return (size_t)nparts_for(n < 0 ? 0 : n) * sizeof(float); }
 
-int bq_quantize_nhwc(const float* x, int64_t P, int64_t C, int64_t Cpad, int8_t* q, float* s, void* ws,
-                     size_t ws_bytes, bq_stream_t stream) {
-  const char* what = "bq_quantize_nhwc";
+static int quantize_nhwc_impl(const char* what, const float* x, int64_t P, int64_t C, int64_t Cpad, int8_t* q,
+                              float* s, const float* s_given, void* ws, size_t ws_bytes, hipStream_t st) {
   if (P < 0 || C < 0 || Cpad < C) return set_error(BQ_ERR_ARG, "%s: bad sizes P=%lld C=%lld Cpad=%lld", what, (long long)P, (long long)C, (long long)Cpad);
-  if (!x || !q || !s || !ws) return set_error(BQ_ERR_ARG, "%s: null pointer", what);
+  if (!x || !q || (!s && !s_given) || (!ws && !s_given)) return set_error(BQ_ERR_ARG, "%s: null pointer", what);
   if (Cpad > 0x7fffffff) return set_error(BQ_ERR_ARG, "%s: too many channels", what);
   const int64_t n = P * C;
-  const int np = nparts_for(n);
-  if (ws_bytes < (size_t)np * sizeof(float))
-    return set_error(BQ_ERR_ARG, "%s: workspace %zu bytes, need %zu", what, ws_bytes, (size_t)np * sizeof(float));
-  hipStream_t st = (hipStream_t)stream;
-  float* parts = (float*)ws;
-  const int64_t chunk = n == 0 ? 1 : (n + np - 1) / np;
-  absmax_parts_kernel<<<np, QT_THREADS, 0, st>>>(x, n, ((chunk + 3) / 4) * 4, parts);
-  if (int r = check_launch(what)) return r;
+  int np = 0;
+  float* parts = nullptr;
+  if (!s_given) {
+    np = nparts_for(n);
+    if (ws_bytes < (size_t)np * sizeof(float))
+      return set_error(BQ_ERR_ARG, "%s: workspace %zu bytes, need %zu", what, ws_bytes, (size_t)np * sizeof(float));
+    parts = (float*)ws;
+    const int64_t chunk = n == 0 ? 1 : (n + np - 1) / np;
+    absmax_parts_kernel<<<np, QT_THREADS, 0, st>>>(x, n, ((chunk + 3) / 4) * 4, parts);
+    if (int r = check_launch(what)) return r;
+  }
   if (C != Cpad && Cpad % 16 == 0 && ((uintptr_t)q & 15) == 0) {
     const int64_t chunks = P * (Cpad / 16);
     int64_t blocks = (chunks + QT_THREADS - 1) / QT_THREADS;
     if (blocks > 8192) blocks = 8192;
     if (blocks < 1) blocks = 1;
-    quantize_pad16_kernel<<<(unsigned)blocks, QT_THREADS, 0, st>>>(x, P, (int)C, (int)Cpad, parts, np, q, s);
+    quantize_pad16_kernel<<<(unsigned)blocks, QT_THREADS, 0, st>>>(x, P, (int)C, (int)Cpad, parts, np, q, s, s_given);
     return check_launch(what);
   }
   const int64_t words = (P * Cpad + 3) / 4;
   int64_t blocks = (words + QT_THREADS - 1) / QT_THREADS;
   if (blocks > 4096) blocks = 4096;
   if (blocks < 1) blocks = 1;
-  quantize_tensor_kernel<<<(unsigned)blocks, QT_THREADS, 0, st>>>(x, P, (int)C, (int)Cpad, parts, np, q, s);
+  quantize_tensor_kernel<<<(unsigned)blocks, QT_THREADS, 0, st>>>(x, P, (int)C, (int)Cpad, parts, np, q, s, s_given);
   return check_launch(what);
+}
+
+int bq_quantize_nhwc(const float* x, int64_t P, int64_t C, int64_t Cpad, int8_t* q, float* s, void* ws,
+                     size_t ws_bytes, bq_stream_t stream) {
+  return quantize_nhwc_impl("bq_quantize_nhwc", x, P, C, Cpad, q, s, nullptr, ws, ws_bytes, (hipStream_t)stream);
+}
+
+int bq_quantize_nhwc_scaled(const float* x, int64_t P, int64_t C, int64_t Cpad, const float* s, int8_t* q,
+                            bq_stream_t stream) {
+  if (!s) return set_error(BQ_ERR_ARG, "bq_quantize_nhwc_scaled: null scale");
+  return quantize_nhwc_impl("bq_quantize_nhwc_scaled", x, P, C, Cpad, q, nullptr, s, nullptr, 0, (hipStream_t)stream);
 }
 
 int bq_quantize_tensor(const float* x, int64_t n, int8_t* q, float* s, void* ws, size_t ws_bytes,

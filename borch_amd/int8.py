@@ -18,7 +18,8 @@ from ._lib import ACT_NONE, ACT_RELU, ACT_SILU, check, lib, require_device
 __all__ = [
     "ACT_NONE", "ACT_RELU", "ACT_SILU", "Int8Weight", "Int8ConvWeight", "Int8DwWeight",
     "quantize_rows", "quantize_weight_per_channel", "quantize_tensor", "quantize_nhwc",
-    "gemm_i8", "conv2d_i8_nhwc", "dwconv_i8_nhwc", "pack_linear_weight", "pack_conv_weight",
+    "gemm_i8", "conv2d_i8_nhwc", "conv2d_i8_nhwc_q", "dwconv_i8_nhwc", "pack_linear_weight", "pack_conv_weight",
+    "quantize_nhwc_scaled",
     "pack_dw_weight", "linear", "conv2d", "depthwise_conv2d", "round_up",
 ]
 
@@ -106,6 +107,21 @@ def quantize_nhwc(x: torch.Tensor, cpad: int | None = None):
     check(lib().bq_quantize_nhwc(xl.data_ptr(), P, C, cpad, q.data_ptr(), s.data_ptr(), ws.data_ptr(),
                                  ws.numel(), _stream(x)))
     return q, s
+
+
+def quantize_nhwc_scaled(x: torch.Tensor, scale: torch.Tensor, cpad: int | None = None):
+    """Per-tensor int8 of an NCHW f32 activation with a given (calibrated) scale ``[1]``
+    into NHWC int8 ``[N, H, W, cpad]``: one pass (bq_quantize_nhwc_scaled)."""
+    if x.dtype != torch.float32:
+        raise TypeError(f"int8 path takes float32 activations, got {x.dtype}")
+    require_device(x.device)
+    N, C, H, W = x.shape
+    cpad = C if cpad is None else int(cpad)
+    xl = x.contiguous(memory_format=torch.channels_last)
+    q = torch.empty((N, H, W, cpad), dtype=torch.int8, device=x.device)
+    check(lib().bq_quantize_nhwc_scaled(xl.data_ptr(), N * H * W, C, cpad, scale.data_ptr(), q.data_ptr(),
+                                        _stream(x)))
+    return q
 
 
 # ------------------------------------------------------------------------ packed weights
@@ -231,6 +247,31 @@ def conv2d_i8_nhwc(qx, sa, wq: Int8ConvWeight, stride=1, pad=0, bias=None, resid
                                   stride, pad, sa.data_ptr(), wq.s.data_ptr(), _ptr(b), _ptr(res), act,
                                   out.data_ptr(), _ptr(acc), _stream(qx)))
     return (out, acc) if want_acc else out
+
+
+def conv2d_i8_nhwc_q(qx, sa, wq: Int8ConvWeight, s_out, stride=1, pad=0, bias=None, residual=None, act=ACT_NONE):
+    """``conv2d_i8_nhwc`` that also returns the output's int8 twin ``[N, OH, OW, O]``
+    quantized with the calibrated scale ``s_out [1]`` (bq_conv2d_i8_nhwc_q; O % 16 == 0)."""
+    _need(qx, "x", torch.int8)
+    N, H, W, C = qx.shape
+    if C != wq.cpad:
+        raise RuntimeError(f"channels do not match: input {C}, filter {wq.cpad}")
+    OH = (H + 2 * pad - wq.KH) // stride + 1
+    OW = (W + 2 * pad - wq.KW) // stride + 1
+    if OH < 1 or OW < 1:
+        raise RuntimeError("the filter is larger than the input.")
+    out = torch.empty((N, wq.O, OH, OW), dtype=torch.float32, device=qx.device, memory_format=torch.channels_last)
+    q = torch.empty((N, OH, OW, wq.O), dtype=torch.int8, device=qx.device)
+    res = None
+    if residual is not None:
+        if tuple(residual.shape) != (N, wq.O, OH, OW):
+            raise RuntimeError(f"residual shape {tuple(residual.shape)} != output {(N, wq.O, OH, OW)}")
+        res = residual.float().contiguous(memory_format=torch.channels_last)
+    b = None if bias is None else bias.contiguous().float()
+    check(lib().bq_conv2d_i8_nhwc_q(qx.contiguous().data_ptr(), N, H, W, C, wq.q.data_ptr(), wq.O, wq.KH, wq.KW,
+                                    stride, pad, sa.data_ptr(), wq.s.data_ptr(), _ptr(b), _ptr(res), act,
+                                    out.data_ptr(), None, s_out.data_ptr(), q.data_ptr(), _stream(qx)))
+    return out, q
 
 
 def dwconv_i8_nhwc(qx, sa, wq: Int8DwWeight, stride=1, pad=0, bias=None, act=ACT_NONE, want_acc=False):

@@ -8,6 +8,7 @@ and otherwise the float32 op. The model-level calls mirror borch-ts/src/nn.ts:67
 
 * ``quantize_for_int8(model) -> int`` — quantizes every layer the kernels take and
   returns the count; refuses by name on a device without the int8 kernels;
+* ``calibrate_int8(model, batches) -> int`` — static scales and the int8 output twin;
 * ``clear_int8(model)`` — back to float32 (the f32 weights never left);
 * ``int8_report(model)`` — which layers took the path and why the others did not.
 
@@ -18,6 +19,7 @@ from __future__ import annotations
 
 import math
 
+import numpy as np
 import torch
 import torch.nn as _tnn
 
@@ -29,6 +31,15 @@ from . import utils  # noqa: F401
 
 Module = _tnn.Module
 Parameter = _tnn.Parameter
+
+# Set by calibrate_int8: int8 convs run their f32 path and record max|input| / max|output|
+# (the reference's setInt8Calibrating, tensor.ts:11896-11901).
+_CALIBRATING = False
+
+
+def _scale_value(peak: float) -> float:
+    """float32(peak / 127), correctly rounded: the same value the device computes."""
+    return float(np.float32(peak) / np.float32(127.0))
 
 
 def _pair(v):
@@ -99,6 +110,10 @@ class Conv2d(_tnn.Module):
                               .uniform_(-bound, bound)) if bias else None
         self.int8 = None  # Int8ConvWeight / Int8DwWeight once quantize_int8() has run
         self.act = _i8.ACT_NONE
+        # calibrated static scales (calibrate_int8): device [1] tensors and their values
+        self.in_scale = self.out_scale = None
+        self.in_scale_v = self.out_scale_v = None
+        self._calib = None
 
     def _geometry(self):
         """(stride, pad) when square and zero-padded, else None."""
@@ -136,18 +151,60 @@ class Conv2d(_tnn.Module):
             self.int8 = _i8.pack_conv_weight(w) if self.groups == 1 else _i8.pack_dw_weight(w)
         return True
 
+    def _int8_input(self, x):
+        """(q NHWC int8, scale [1]) for the int8 kernels, cheapest first, as
+        tensor.ts:11909-11921: the producer's int8 twin when its scale is this layer's
+        calibrated input scale and ``x`` is unchanged since; else one pass with the static
+        scale; else the dynamic per-tensor quantization."""
+        cpad = self.int8.cpad
+        if self.in_scale is not None:
+            twin = getattr(x, "_int8_twin", None)
+            if (twin is not None and twin[2] == self.in_scale_v and twin[3] == x._version
+                    and twin[0].shape[-1] == cpad):
+                return twin[0], twin[1]
+            return _i8.quantize_nhwc_scaled(x, self.in_scale, cpad), self.in_scale
+        return _i8.quantize_nhwc(x, cpad)
+
+    def _f32_forward(self, x, residual):
+        out = functional._f32_conv2d(x, self.weight, self.bias, self.stride, self.padding, self.dilation,
+                                     self.groups, self.padding_mode)
+        if residual is not None:
+            out = out + residual
+        if self.act == _i8.ACT_RELU:
+            out = torch.relu(out)
+        elif self.act == _i8.ACT_SILU:
+            out = torch.nn.functional.silu(out)
+        return out
+
     def forward(self, x, residual=None):
+        if self.int8 is not None and _CALIBRATING:
+            out = self._f32_forward(x, residual)
+            cin, cout = x.detach().abs().amax(), out.detach().abs().amax()
+            self._calib = [cin, cout] if self._calib is None else [torch.maximum(self._calib[0], cin),
+                                                                   torch.maximum(self._calib[1], cout)]
+            return out
         if self.int8 is not None:
             stride, pad = self._geometry()
+            if x.dim() != 4 or x.shape[1] != self.in_channels:
+                raise RuntimeError(f"channels do not match: input {x.shape[1] if x.dim() > 1 else x.shape}, "
+                                   f"filter {self.in_channels}")
+            qx, sa = self._int8_input(x)
             if isinstance(self.int8, _i8.Int8DwWeight):
-                out = _i8.depthwise_conv2d(x, self.int8, self.bias, stride, pad,
-                                           self.act if residual is None else _i8.ACT_NONE)
+                out = _i8.dwconv_i8_nhwc(qx, sa, self.int8, stride, pad, self.bias,
+                                         self.act if residual is None else _i8.ACT_NONE)
+                if self.int8.cpad != self.int8.C:
+                    out = out[:, : self.int8.C]
                 if residual is not None:
                     out = out + residual
                     if self.act == _i8.ACT_RELU:
                         out = torch.relu(out)
                 return out
-            return _i8.conv2d(x, self.int8, self.bias, stride, pad, self.act, residual)
+            if self.out_scale is not None and self.int8.O % 16 == 0:
+                out, q = _i8.conv2d_i8_nhwc_q(qx, sa, self.int8, self.out_scale, stride, pad, self.bias, residual,
+                                              self.act)
+                out._int8_twin = (q, self.out_scale, self.out_scale_v, out._version)
+                return out
+            return _i8.conv2d_i8_nhwc(qx, sa, self.int8, stride, pad, self.bias, residual, self.act)
         out = functional._f32_conv2d(x, self.weight, self.bias, self.stride, self.padding, self.dilation,
                                      self.groups, self.padding_mode)
         if residual is not None:
@@ -196,10 +253,43 @@ def quantize_for_int8(model, linear: bool = True, conv: bool = True) -> int:
     return taken
 
 
+def calibrate_int8(model, batches) -> int:
+    """Static scales (borch-ts/src/nn.ts:6790-6824): every int8 conv runs f32 over the
+    calibration ``batches`` while ``max|input|`` and ``max|output|`` accumulate on the
+    device (no readback until the end); each layer then keeps both as scales. Its input is
+    then quantized in one pass with the first, and its output is packed at its own store
+    with the second (the int8 twin the next conv takes with no pass at all). Returns how
+    many layers were calibrated. After ``quantize_for_int8``; ``clear_int8`` undoes both."""
+    global _CALIBRATING
+    layers = [m for _, m in _int8_layers(model) if isinstance(m, Conv2d) and m.int8 is not None]
+    for m in layers:
+        m._calib = None
+    _CALIBRATING = True
+    try:
+        with torch.no_grad():
+            for xb in batches:
+                model(xb)
+    finally:
+        _CALIBRATING = False
+    for m in layers:
+        if m._calib is None:  # never reached by the calibration inputs
+            continue
+        in_max, out_max = (float(t) for t in m._calib)
+        dev = m.weight.device
+        m.in_scale_v, m.out_scale_v = _scale_value(in_max), _scale_value(out_max)
+        m.in_scale = torch.tensor([m.in_scale_v], dtype=torch.float32, device=dev)
+        m.out_scale = torch.tensor([m.out_scale_v], dtype=torch.float32, device=dev)
+        m._calib = None
+    return len(layers)
+
+
 def clear_int8(model) -> None:
-    """Back to f32: every layer's int8 weight dropped (nn.ts:6827-6829)."""
+    """Back to f32: every layer's int8 weight and calibrated scales dropped (nn.ts:6827-6829)."""
     for _, mod in _int8_layers(model):
         mod.int8 = None
+        if isinstance(mod, Conv2d):
+            mod.in_scale = mod.out_scale = None
+            mod.in_scale_v = mod.out_scale_v = None
 
 
 def int8_report(model):

@@ -86,6 +86,12 @@ int bq_quantize_tensor(const float* x, int64_t n, int8_t* q, float* s, void* ws,
 int bq_quantize_nhwc(const float* x, int64_t P, int64_t C, int64_t Cpad, int8_t* q, float* s,
                      void* ws, size_t ws_bytes, bq_stream_t stream);
 
+/* The same quantization with a given (calibrated) scale s f32 [1]: one pass, no maximum.
+ * The static-scale input of borch-ts (int8.inMax, tensor.ts:11912-11913; calibrateInt8
+ * nn.ts:6790-6824). Values beyond the calibrated range clamp to +-127. */
+int bq_quantize_nhwc_scaled(const float* x, int64_t P, int64_t C, int64_t Cpad, const float* s, int8_t* q,
+                            bq_stream_t stream);
+
 /* W8A8 GEMM with the fused dequant epilogue, Linear layout (x @ W.T):
  *   A int8 [M, K] (per-row scales sA f32 [M]), W int8 [N, K] (per-channel sW f32 [N]),
  *   out f32 [M, N] = ((f32(A @ W.T) * sA[m]) * sW[n]) + bias[n] (bias nullable), then
@@ -109,6 +115,17 @@ int bq_conv2d_i8_nhwc(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t 
                       int64_t pad, const float* sA, const float* sW, const float* bias,
                       const float* residual, int act, float* out, int32_t* acc,
                       bq_stream_t stream);
+
+/* bq_conv2d_i8_nhwc that also writes the output's int8 twin with a calibrated scale:
+ * q_out int8 [N, OH, OW, O] = clip(rint(f64(y) / f64(s_out[0])), +-127) of the final f32 y
+ * (after residual and activation), the next conv's input with no quantize pass.
+ * O % 16 == 0 (the twin is then the next layer's padded NHWC layout). Replaces the
+ * quantOut store of convForwardInt8 / sumSplitsConv (borch-ts/src/kernels.ts:2177-2190,
+ * 5866-5898) and the Int8Twin hand-off (tensor.ts:11909-11910, 11954-11955). */
+int bq_conv2d_i8_nhwc_q(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t C, const int8_t* w,
+                        int64_t O, int64_t KH, int64_t KW, int64_t stride, int64_t pad, const float* sA,
+                        const float* sW, const float* bias, const float* residual, int act, float* out,
+                        int32_t* acc, const float* s_out, int8_t* q_out, bq_stream_t stream);
 
 /* Depthwise int8 convolution, NHWC (groups = C, channel multiplier 1):
  *   x int8 [N, H, W, C] (C % 4 == 0, per-tensor sA f32 [1]), w int8 [KH*KW, C]

@@ -100,3 +100,41 @@ def resnet18_features(params, x):
         w2, b2, s2, p2 = params[f"body.{i}.c2"]
         h = conv_layer(out, w2, b2, s2, p2, ACT_RELU, side)[0]
     return h
+
+
+def conv_layer_static(x_nchw, w, b, stride, pad, act, residual_nchw, s_in, s_out):
+    """A conv with calibrated scales (nn.ts:6790-6824): the input quantized with ``s_in``
+    (clamped), the epilogue as ``conv_layer``, and the output's int8 twin
+    ``clip(rint(y / s_out))`` (kernels.ts:2177-2190 with this build's rounding rule).
+    Returns ``(y_nchw, twin NHWC int8, acc)``."""
+    x_nchw = np.asarray(x_nchw, np.float32)
+    O_, C, KH, KW = w.shape
+    cpad = (C + 15) // 16 * 16
+    xq = np.zeros(x_nchw.shape[:1] + x_nchw.shape[2:] + (cpad,), np.int8)
+    xq[..., :C] = Q.quantize_with_scale(x_nchw, np.float32(s_in)).transpose(0, 2, 3, 1)
+    qw, sW = Q.quantize_conv_weight(w, cpad)
+    acc, OH, OW = Q.conv2d_i8_nhwc(xq, qw, KH, KW, stride, pad)
+    res = None
+    if residual_nchw is not None:
+        res = np.asarray(residual_nchw, np.float32).transpose(0, 2, 3, 1).reshape(-1, O_)
+    y = _act(Q.dequant(acc, np.float32(s_in), sW, b, False, res), act)
+    twin = Q.quantize_with_scale(y, np.float32(s_out)).reshape(x_nchw.shape[0], OH, OW, O_)
+    N = x_nchw.shape[0]
+    return y.reshape(N, OH, OW, O_).transpose(0, 3, 1, 2), twin, acc
+
+
+def resnet18_features_static(params, scales, x):
+    """The calibrated ResNet-18 conv stack. ``scales[key] = (s_in, s_out)``. A layer whose
+    input is another layer's output uses that producer's twin when the scales agree (which
+    the calibration guarantees), i.e. exactly ``quantize_with_scale(y, s_in)``: the twin
+    and a fresh static quantization are the same bytes, so the chain is computed from the
+    f32 values."""
+    def run(key, h, act, res=None):
+        w, b, s, p = params[key]
+        return conv_layer_static(h, w, b, s, p, act, res, *scales[key])[0]
+    h = run("stem", x, ACT_RELU)
+    for i in range(8):
+        out = run(f"body.{i}.c1", h, ACT_RELU)
+        side = run(f"body.{i}.down", h, ACT_NONE) if f"body.{i}.down" in params else h
+        h = run(f"body.{i}.c2", out, ACT_RELU, side)
+    return h

@@ -205,3 +205,68 @@ def test_graph_replay_matches_eager(dev):
                 torch.cuda.synchronize()
             other = torch.from_numpy(WL.c3_input(4, 2) if name == "resnet18" else WL.c4_input(2, 2)).to(dev)
             assert np.array_equal(n(c(other)), n(model(other))), f"{name} new input"
+
+
+def test_c3_resnet18_static_calibrated(dev):
+    """Static scales + int8 twins (calibrate_int8): the calibrated conv stack equals the
+    oracle chain bit for bit; each producer's twin equals the oracle quantization of its
+    f32 output; the consumer really takes the twin (no quantize pass runs)."""
+    say("C3 ResNet-18 b16, calibrated static scales + int8 twins")
+    model = nets.build("resnet18", seed=0, device=dev)
+    x = WL.c3_input(16, 0)
+    xt = torch.from_numpy(x).to(dev)
+    with torch.no_grad():
+        f32_logits = n(model(xt))
+    assert bt.quantize_for_int8(model) == 20
+    calib = [torch.from_numpy(WL.c3_input(16, s)).to(dev) for s in (11, 12)]
+    assert bt.calibrate_int8(model, calib) == 20
+    twins = {}
+    hooks = []
+    for name, m in int8_modules(model):
+        def hook(mod, args, out, name=name):
+            twins[name] = (n(out), None if getattr(out, "_int8_twin", None) is None else n(out._int8_twin[0]),
+                           mod.out_scale_v)
+        hooks.append(m.register_forward_hook(hook))
+    calls = {"n": 0}
+    orig = I.quantize_nhwc_scaled
+
+    def counting(*a, **k):
+        calls["n"] += 1
+        return orig(*a, **k)
+    I.quantize_nhwc_scaled = counting
+    try:
+        with torch.no_grad():
+            feats = model.features(xt)
+    finally:
+        I.quantize_nhwc_scaled = orig
+        for h in hooks:
+            h.remove()
+    assert calls["n"] == 1, f"{calls['n']} static quantize passes: only the network input should need one"
+    for name, (y, twin, s_out) in twins.items():
+        assert twin is not None, name
+        assert np.array_equal(twin, O_quant().quantize_with_scale(y.transpose(0, 2, 3, 1), np.float32(s_out))), name
+    params, scales = {}, {}
+
+    def put(key, conv):
+        params[key] = _conv_params(conv)
+        scales[key] = (conv.in_scale_v, conv.out_scale_v)
+    put("stem", model.stem_f.conv)
+    for i, blk in enumerate(model.body):
+        put(f"body.{i}.c1", blk.c1.conv)
+        put(f"body.{i}.c2", blk.c2.conv)
+        if blk.down is not None:
+            put(f"body.{i}.down", blk.down)
+    feats_o = OM.resnet18_features_static(params, scales, x)
+    assert np.array_equal(n(feats), feats_o), "calibrated conv stack not bit-exact"
+    with torch.no_grad():
+        logits = n(model(xt))
+    gap = np.abs(logits - f32_logits).max() / np.abs(f32_logits).max()
+    say(f"  static int8 vs f32 logits: max |diff| / max |logit| = {gap:.3g}")
+    assert gap < 0.05
+    bt.clear_int8(model)
+    assert model.stem_f.conv.in_scale is None
+
+
+def O_quant():
+    from oracle import quant
+    return quant
