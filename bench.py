@@ -275,6 +275,20 @@ def main():
                           "e2e_us_with_quantize": round(t_e2e * 1e3, 3), "bytes": byts}
         del qws, Am
         log(f"M={m}: {sweep[f'M{m}']}")
+    # weight-only W8A32 decode GEMV (M = 1): f32 x against the int8 weight, cache-cold
+    a_1, w_1, b_1 = WL.c2_gemm(1, 0)
+    w8s = [I.pack_linear_weight(torch.from_numpy(w_1).to(dev), weight_only=True) for _ in range(1)]
+    qws = [w8s[0].q.clone() for _ in range(24)]
+    X1 = torch.from_numpy(a_1).to(dev)
+    B1 = torch.from_numpy(b_1).to(dev)
+    w8v = [I.Int8Weight(q, w8s[0].s, 4096, 4096, True) for q in qws]
+    g_w = capture(lambda i: I.linear_w8a32(X1, w8v[i], B1), 24)
+    t_w = time_graph(g_w, 24, 8, stream)
+    wbytes = 4096 * 4096 + 4 * 4096 * 3 + 4 * 4096
+    sweep["W8A32_M1"] = {"kernel_us": round(t_w * 1e3, 3), "GBps": round(wbytes / (t_w * 1e-3) / 1e9, 1),
+                         "hbm_frac": round(wbytes / (t_w * 1e-3) / 1e9 / PEAK_HBM_GBS, 4), "bytes": wbytes}
+    log(f"W8A32 M=1: {sweep['W8A32_M1']}")
+    del g_w, qws, w8v, w8s
     sweep["M4096"] = {"kernel_us": round(gemm_ms * 1e3, 3), "TOPS": round(gemm_tops, 1),
                       "mfma_frac": round(gemm_tops / PEAK_INT8_TOPS, 4),
                       "quantize_us": round(quant_ms * 1e3, 3),

@@ -49,6 +49,8 @@ SIGNATURES = {
                                    _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_int, _c_p, _c_p, _c_p]),
     "bq_dwconv_i8_nhwc": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i64,
                                    _c_i64, _c_p, _c_p, _c_p, _c_int, _c_p, _c_p, _c_p]),
+    "bq_gemv_w8a32": (_c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_int, _c_p, _c_p]),
+    "bq_dequant_i8": (_c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_p]),
 }
 
 _lock = threading.Lock()

@@ -1,0 +1,147 @@
+// Weight-only int8 (W8A32): f32 activations against an int8 weight with one f32 scale per
+// output channel; the effective weight is f32(q) * scale (one rounding), the products are
+// accumulated in f32 (FMA). The reference's `matmul(..., weightInt8)` (borch-ts/src/
+// kernels.ts:2695-2708) for streamed/windowed weights, and its `dequantInt8` unpack pass
+// (kernels.ts:1264-1274).
+//
+// gemv_w8a32_kernel (M <= 8, the decode shape): HBM-bound on the int8 weight — a quarter
+// of the f32 bytes. Each wave owns RPW weight rows; a row is read as contiguous 1 KB
+// wave-loads (64 lanes x 16 bytes) and every load of the wave's rows is issued before any
+// arithmetic; each lane multiplies its 16 weights against the matching 16 activations
+// (L1/L2-resident, reused across the wave's rows) and the wave reduces the lane sums.
+#include "bq_common.h"
+
+namespace bq {
+
+constexpr uint32_t W_OOB = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t w_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ float wave_fsum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = __fadd_rn(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+constexpr int WA_WAVES = 8;
+
+template <int KC, int RPW>
+__global__ __launch_bounds__(WA_WAVES * 64) void gemv_w8a32_kernel(const float* __restrict__ x, const int8_t* W,
+                                                                   int M, int N, int K, const float* __restrict__ sW,
+                                                                   const float* __restrict__ bias, int act,
+                                                                   float* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int row0 = (blockIdx.x * WA_WAVES + wave) * RPW;
+  if (row0 >= N) return;
+  const __amdgpu_buffer_rsrc_t rw = w_rsrc(W + (size_t)row0 * K, (uint32_t)(min(RPW, N - row0) * K));
+  v4i w[RPW][KC];
+#pragma unroll
+  for (int j = 0; j < RPW; ++j)
+#pragma unroll
+    for (int c = 0; c < KC; ++c) {
+      const int k = c * 1024 + lane * 16;
+      w[j][c] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rw, k < K ? (uint32_t)(j * K + k) : W_OOB, 0, 0));
+    }
+  float sc[RPW];
+#pragma unroll
+  for (int j = 0; j < RPW; ++j) sc[j] = row0 + j < N ? sW[row0 + j] : 0.f;
+  __builtin_amdgcn_sched_barrier(0);
+  for (int m = 0; m < M; ++m) {
+    float acc[RPW];
+#pragma unroll
+    for (int j = 0; j < RPW; ++j) acc[j] = 0.f;
+#pragma unroll
+    for (int c = 0; c < KC; ++c) {
+      const int k = c * 1024 + lane * 16;
+      if (k >= K) break;
+      const float4* xp = reinterpret_cast<const float4*>(x + (size_t)m * K + k);
+      float xv[16];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const float4 v = xp[t];
+        xv[t * 4] = v.x; xv[t * 4 + 1] = v.y; xv[t * 4 + 2] = v.z; xv[t * 4 + 3] = v.w;
+      }
+#pragma unroll
+      for (int j = 0; j < RPW; ++j)
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+          const int b = (int)(int8_t)((uint32_t)w[j][c][q >> 2] >> ((q & 3) * 8));
+          acc[j] = __fmaf_rn(xv[q], __fmul_rn((float)b, sc[j]), acc[j]);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < RPW; ++j) {
+      const float s = wave_fsum(acc[j]);
+      const int n = row0 + j;
+      if (lane == 0 && n < N) {
+        float v = bias ? __fadd_rn(s, bias[n]) : s;
+        if (act == BQ_ACT_RELU) v = v > 0.f ? v : 0.f;
+        else if (act == BQ_ACT_SILU) v = silu(v);
+        out[(size_t)m * N + n] = v;
+      }
+    }
+  }
+}
+
+// w[n, k] = f32(q[n, k]) * s[n] (one rounding), four elements a thread.
+__global__ __launch_bounds__(256) void dequant_i8_kernel(const int8_t* __restrict__ q, int64_t N, int64_t K,
+                                                         const float* __restrict__ s, float* __restrict__ w) {
+  const int64_t total = N * K;
+  for (int64_t e = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4; e < total; e += (int64_t)gridDim.x * 256 * 4) {
+    if (e + 3 < total && (K & 3) == 0) {
+      const uint32_t v = *reinterpret_cast<const uint32_t*>(q + e);
+      const float sc = s[e / K];
+      *reinterpret_cast<float4*>(w + e) =
+          make_float4(__fmul_rn((float)(int8_t)(v & 0xff), sc), __fmul_rn((float)(int8_t)((v >> 8) & 0xff), sc),
+                      __fmul_rn((float)(int8_t)((v >> 16) & 0xff), sc), __fmul_rn((float)(int8_t)(v >> 24), sc));
+    } else {
+      for (int64_t i = e; i < e + 4 && i < total; ++i) w[i] = __fmul_rn((float)q[i], s[i / K]);
+    }
+  }
+}
+
+}  // namespace bq
+
+using namespace bq;
+
+extern "C" {
+
+int bq_gemv_w8a32(const float* x, const int8_t* W, int64_t M, int64_t N, int64_t K, const float* sW,
+                  const float* bias, int act, float* out, bq_stream_t stream) {
+  const char* what = "bq_gemv_w8a32";
+  if (M < 0 || N < 0 || K < 0) return set_error(BQ_ERR_ARG, "%s: negative size", what);
+  if (M == 0 || N == 0) return BQ_OK;
+  if (M > 8) return set_error(BQ_ERR_UNSUPPORTED, "%s: M=%lld > 8 (dequantize and use an f32 GEMM)", what, (long long)M);
+  if (K % 16 || K > 8192) return set_error(BQ_ERR_UNSUPPORTED, "%s: K=%lld (needs K %% 16 == 0 and K <= 8192)", what, (long long)K);
+  if (N > 0x7fffffff || (int64_t)N * K >= ((int64_t)1 << 31)) return set_error(BQ_ERR_ARG, "%s: size too large", what);
+  if (!x || !W || !sW || !out) return set_error(BQ_ERR_ARG, "%s: null pointer", what);
+  if (((uintptr_t)x & 15) || ((uintptr_t)W & 15)) return set_error(BQ_ERR_ARG, "%s: x and W must be 16-byte aligned", what);
+  if (act < BQ_ACT_NONE || act > BQ_ACT_SILU) return set_error(BQ_ERR_ARG, "%s: bad activation %d", what, act);
+  constexpr int RPW = 2;
+  const unsigned grid = (unsigned)((N + WA_WAVES * RPW - 1) / (WA_WAVES * RPW));
+  hipStream_t st = (hipStream_t)stream;
+  const int m = (int)M, n = (int)N, k = (int)K;
+  if (K <= 1024) gemv_w8a32_kernel<1, RPW><<<grid, WA_WAVES * 64, 0, st>>>(x, W, m, n, k, sW, bias, act, out);
+  else if (K <= 2048) gemv_w8a32_kernel<2, RPW><<<grid, WA_WAVES * 64, 0, st>>>(x, W, m, n, k, sW, bias, act, out);
+  else if (K <= 4096) gemv_w8a32_kernel<4, RPW><<<grid, WA_WAVES * 64, 0, st>>>(x, W, m, n, k, sW, bias, act, out);
+  else gemv_w8a32_kernel<8, RPW><<<grid, WA_WAVES * 64, 0, st>>>(x, W, m, n, k, sW, bias, act, out);
+  return check_launch(what);
+}
+
+int bq_dequant_i8(const int8_t* q, int64_t N, int64_t K, const float* s, float* w, bq_stream_t stream) {
+  const char* what = "bq_dequant_i8";
+  if (N < 0 || K < 0) return set_error(BQ_ERR_ARG, "%s: negative size", what);
+  if (N == 0 || K == 0) return BQ_OK;
+  if (!q || !s || !w) return set_error(BQ_ERR_ARG, "%s: null pointer", what);
+  if (((uintptr_t)q & 3) || ((uintptr_t)w & 15)) return set_error(BQ_ERR_ARG, "%s: misaligned pointer", what);
+  int64_t blocks = (N * K / 4 + 255) / 256;
+  if (blocks > 16384) blocks = 16384;
+  if (blocks < 1) blocks = 1;
+  dequant_i8_kernel<<<(unsigned)blocks, 256, 0, (hipStream_t)stream>>>(q, N, K, s, w);
+  return check_launch(what);
+}
+
+}  // extern "C"

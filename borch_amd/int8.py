@@ -19,7 +19,7 @@ __all__ = [
     "ACT_NONE", "ACT_RELU", "ACT_SILU", "Int8Weight", "Int8ConvWeight", "Int8DwWeight",
     "quantize_rows", "quantize_weight_per_channel", "quantize_tensor", "quantize_nhwc",
     "gemm_i8", "conv2d_i8_nhwc", "conv2d_i8_nhwc_q", "dwconv_i8_nhwc", "pack_linear_weight", "pack_conv_weight",
-    "quantize_nhwc_scaled",
+    "quantize_nhwc_scaled", "linear_w8a32", "dequant_weight",
     "pack_dw_weight", "linear", "conv2d", "depthwise_conv2d", "round_up",
 ]
 
@@ -128,11 +128,14 @@ def quantize_nhwc_scaled(x: torch.Tensor, scale: torch.Tensor, cpad: int | None 
 
 @dataclass
 class Int8Weight:
-    """A Linear weight packed for ``bq_gemm_i8``: ``q int8 [N, Kpad]``, ``s f32 [N]``."""
+    """A Linear weight packed for ``bq_gemm_i8``: ``q int8 [N, Kpad]``, ``s f32 [N]``.
+    ``weight_only`` selects W8A32 (f32 activations, ``bq_gemv_w8a32`` / dequant + f32 GEMM)
+    instead of W8A8."""
     q: torch.Tensor
     s: torch.Tensor
     in_features: int
     out_features: int
+    weight_only: bool = False
 
     @property
     def kpad(self) -> int:
@@ -164,13 +167,51 @@ class Int8DwWeight:
     KW: int
 
 
-def pack_linear_weight(w: torch.Tensor) -> Int8Weight:
+def pack_linear_weight(w: torch.Tensor, weight_only: bool = False) -> Int8Weight:
     """Quantize once (quant.ts:23-53); K padded to a multiple of 16 with zeros (exact)."""
     N, K = w.shape
     kp = round_up(max(K, 16), 16)
     wp = w if kp == K else torch.nn.functional.pad(w, (0, kp - K))
     q, s = quantize_weight_per_channel(wp.float())
-    return Int8Weight(q, s, K, N)
+    return Int8Weight(q, s, K, N, weight_only)
+
+
+def dequant_weight(w8: Int8Weight) -> torch.Tensor:
+    """f32 ``[N, Kpad]`` = f32(q) * s[n] (bq_dequant_i8; dequantInt8, kernels.ts:1264-1274)."""
+    require_device(w8.q.device)
+    N, K = w8.q.shape
+    out = torch.empty((N, K), dtype=torch.float32, device=w8.q.device)
+    check(lib().bq_dequant_i8(w8.q.data_ptr(), N, K, w8.s.data_ptr(), out.data_ptr(), _stream(w8.q)))
+    return out
+
+
+def linear_w8a32(x: torch.Tensor, w8: Int8Weight, bias=None, act=ACT_NONE) -> torch.Tensor:
+    """Weight-only int8 Linear (W8A32, matmul(..., weightInt8), kernels.ts:2695-2708):
+    effective weight f32(q)·s, f32 accumulation. M <= 8: the streaming GEMV kernel; larger
+    M: the dequant pass, then torch-ROCm's f32 GEMM (the reference's fallback)."""
+    if x.shape[-1] != w8.in_features:
+        raise RuntimeError(f"mat1 and mat2 shapes cannot be multiplied "
+                           f"({'x'.join(str(n) for n in x.reshape(-1, x.shape[-1]).shape)} and "
+                           f"{w8.in_features}x{w8.out_features})")
+    require_device(x.device)
+    lead = x.shape[:-1]
+    x2 = _f32c(x.reshape(-1, x.shape[-1]))
+    if w8.kpad != w8.in_features:
+        x2 = torch.nn.functional.pad(x2, (0, w8.kpad - w8.in_features))
+    M, K = x2.shape
+    N = w8.out_features
+    if M <= 8 and K <= 8192:
+        out = torch.empty((M, N), dtype=torch.float32, device=x.device)
+        b = None if bias is None else bias.contiguous().float()
+        check(lib().bq_gemv_w8a32(x2.data_ptr(), w8.q.data_ptr(), M, N, K, w8.s.data_ptr(), _ptr(b), act,
+                                  out.data_ptr(), _stream(x2)))
+    else:
+        out = torch.nn.functional.linear(x2, dequant_weight(w8), bias)
+        if act == ACT_RELU:
+            out = torch.relu(out)
+        elif act == ACT_SILU:
+            out = torch.nn.functional.silu(out)
+    return out.reshape(*lead, N)
 
 
 def pack_conv_weight(w: torch.Tensor) -> Int8ConvWeight:
@@ -302,7 +343,10 @@ def dwconv_i8_nhwc(qx, sa, wq: Int8DwWeight, stride=1, pad=0, bias=None, act=ACT
 
 def linear(x: torch.Tensor, w8: Int8Weight, bias=None, act=ACT_NONE) -> torch.Tensor:
     """Dynamic-quant int8 Linear: per-row activations, per-channel weights, f32 out
-    ``[..., N]`` (the numpy core's ``x @ W.T + b``, borch/_nn.py:413-415, in W8A8)."""
+    ``[..., N]`` (the numpy core's ``x @ W.T + b``, borch/_nn.py:413-415, in W8A8). A
+    weight-only packing runs ``linear_w8a32`` instead."""
+    if w8.weight_only:
+        return linear_w8a32(x, w8, bias, act)
     if x.shape[-1] != w8.in_features:
         a = "x".join(str(n) for n in (x.reshape(-1, x.shape[-1]).shape if x.dim() else ()))
         raise RuntimeError(

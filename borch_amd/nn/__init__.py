@@ -66,12 +66,13 @@ class Linear(_tnn.Module):
         self.int8 = None  # Int8Weight once quantize_int8() has run
         self.act = _i8.ACT_NONE  # fused epilogue activation (LinearReLU sets RELU)
 
-    def quantize_int8(self) -> bool:
+    def quantize_int8(self, weight_only: bool = False) -> bool:
         """Packs the weight once per output channel (quant.ts:23-53). Any shape is taken
-        (K is zero-padded to a multiple of 16). Returns True."""
+        (K is zero-padded to a multiple of 16). ``weight_only`` keeps activations f32
+        (W8A32, the reference's int8 window weight, tensor.ts:1681-1705). Returns True."""
         require_device(self.weight.device)
         with torch.no_grad():
-            self.int8 = _i8.pack_linear_weight(self.weight.detach())
+            self.int8 = _i8.pack_linear_weight(self.weight.detach(), weight_only)
         return True
 
     def forward(self, x):
@@ -231,7 +232,7 @@ def _int8_layers(model):
             yield name, mod
 
 
-def quantize_for_int8(model, linear: bool = True, conv: bool = True) -> int:
+def quantize_for_int8(model, linear: bool = True, conv: bool = True, weight_only: bool = False) -> int:
     """Every Linear / Conv2d of ``model`` the int8 kernels take, quantized once; returns
     how many took it (borch-ts/src/nn.ts:6770-6780). Refused by name where the device has
     no int8 kernels (nn.ts:6771-6773): the path is an accuracy trade a caller asks for and
@@ -247,7 +248,7 @@ def quantize_for_int8(model, linear: bool = True, conv: bool = True) -> int:
     taken = 0
     for _, mod in layers:
         if isinstance(mod, Linear) and linear:
-            taken += bool(mod.quantize_int8())
+            taken += bool(mod.quantize_int8(weight_only))
         elif isinstance(mod, Conv2d) and conv:
             taken += bool(mod.quantize_int8())
     return taken

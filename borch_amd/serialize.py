@@ -29,7 +29,8 @@ FORMAT = "borch_amd-int8/1"
 
 def _record(w8) -> dict:
     if isinstance(w8, _i8.Int8Weight):
-        return {"kind": "linear", "in_features": w8.in_features, "out_features": w8.out_features}
+        return {"kind": "linear", "in_features": w8.in_features, "out_features": w8.out_features,
+                "weight_only": bool(w8.weight_only)}
     if isinstance(w8, _i8.Int8ConvWeight):
         return {"kind": "conv", "O": w8.O, "C": w8.C, "cpad": w8.cpad, "KH": w8.KH, "KW": w8.KW}
     if isinstance(w8, _i8.Int8DwWeight):
@@ -82,6 +83,8 @@ def load_int8(model, path, device=None) -> int:
             continue
         rec = json.loads(meta[name])
         want = _expected(mod)
+        if rec.get("kind") == "linear":
+            want["weight_only"] = bool(rec.get("weight_only", False))
         if rec != want:
             raise ValueError(f"{path}: layer {name!r} is {rec}, the model has {want}")
         dev = device if device is not None else mod.weight.device
@@ -91,7 +94,7 @@ def load_int8(model, path, device=None) -> int:
             raise ValueError(f"{path}: layer {name!r} has dtypes {q.dtype}/{s.dtype}")
         kind = rec["kind"]
         if kind == "linear":
-            mod.int8 = _i8.Int8Weight(q, s, rec["in_features"], rec["out_features"])
+            mod.int8 = _i8.Int8Weight(q, s, rec["in_features"], rec["out_features"], rec.get("weight_only", False))
         elif kind == "conv":
             mod.int8 = _i8.Int8ConvWeight(q, s, rec["O"], rec["C"], rec["cpad"], rec["KH"], rec["KW"])
         else:

@@ -137,6 +137,19 @@ int bq_dwconv_i8_nhwc(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t 
                       const float* sA, const float* sW, const float* bias, int act,
                       float* out, int32_t* acc, bq_stream_t stream);
 
+/* Weight-only int8 (W8A32) GEMV for the decode shape, M <= 8: f32 x [M, K] against int8
+ * W [N, K] with per-channel sW [N]; out f32 [M, N] = sum_k x * f32(f32(q) * sW[n]) (f32 FMA
+ * accumulation, wave-tree reduction) + bias, then act. K % 16 == 0, K <= 8192.
+ * Replaces matmul(..., weightInt8) (borch-ts/src/kernels.ts:2695-2708) for streamed weights
+ * (Tensor.inWindowInt8, tensor.ts:1681-1705; stream_sequential(int8=True),
+ * borch_webgpu/_stream.py:61-66). */
+int bq_gemv_w8a32(const float* x, const int8_t* W, int64_t M, int64_t N, int64_t K, const float* sW,
+                  const float* bias, int act, float* out, bq_stream_t stream);
+
+/* w f32 [N, K] = f32(q[n, k]) * s[n] (one rounding): the weight-only fallback's unpack pass
+ * for larger M. Replaces dequantInt8 (borch-ts/src/kernels.ts:1264-1274). */
+int bq_dequant_i8(const int8_t* q, int64_t N, int64_t K, const float* s, float* w, bq_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

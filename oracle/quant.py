@@ -318,3 +318,26 @@ def fuse_conv_bn_weights(w, b, rm, rv, eps, gamma, beta):
     fw = (w * scale.reshape([-1] + [1] * (w.ndim - 1))).astype(w.dtype)
     fb = ((b - rm) * scale + beta).astype(b.dtype)
     return fw, fb
+
+
+# ----------------------------------------------------------------- weight-only (W8A32)
+
+def dequant_weight(q, s):
+    """``f32(q) · s[n]`` with one float32 rounding: the effective weight of the reference's
+    int8 window matmul (kernels.ts:2695-2708, ``f32(q) * scale[bcol]``) and of
+    ``dequantInt8PerChannel`` (quant.ts:60-71). ``q [N, K]`` int8, ``s [N]``."""
+    return (np.asarray(q, np.int8).astype(np.float32) * np.asarray(s, np.float32).reshape(-1, 1)).astype(np.float32)
+
+
+def linear_w8a32(x, q, s, b=None):
+    """W8A32 Linear in float64 on the f32 effective weights, plus the bound an f32
+    accumulation of K products may differ by: ``(K + 2) · 2^-24 · Σ|x·w|`` per output
+    (Higham's γ_K for recursive/tree summation with one rounding per product)."""
+    w = dequant_weight(q, s).astype(np.float64)
+    x64 = np.asarray(x, np.float32).astype(np.float64)
+    y = x64 @ w.T
+    if b is not None:
+        y = y + np.asarray(b, np.float64)
+    K = w.shape[1]
+    bound = (K + 2) * 2.0 ** -24 * (np.abs(x64) @ np.abs(w).T) + 2.0 ** -24 * np.abs(y)
+    return y, bound

@@ -251,3 +251,35 @@ def test_dwconv(dev, N, C, H, k, stride, pad):
             np.testing.assert_allclose(n(y).transpose(0, 2, 3, 1).reshape(-1, cpad), y_o, rtol=RTOL, atol=ATOL)
         else:
             assert_f32(n(y).transpose(0, 2, 3, 1).reshape(-1, cpad), y_o)
+
+
+# ------------------------------------------------------------------- weight-only W8A32
+
+@pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (2, 17, 16), (5, 300, 1040), (8, 64, 8192), (1, 33, 2048),
+                                   (64, 96, 768), (3, 4100, 4096)])
+def test_w8a32_linear(dev, M, N, K):
+    say(f"w8a32 M={M} N={N} K={K}")
+    rng = np.random.default_rng(M * 7 + N + K)
+    x = rng.normal(size=(M, K)).astype(np.float32)
+    w = rng.normal(size=(N, K)).astype(np.float32) * np.float32(0.05)
+    b = rng.normal(size=N).astype(np.float32)
+    w8 = I.pack_linear_weight(t(w, dev), weight_only=True)
+    qw_o, sw_o = O.quantize_weight_per_channel(w)
+    assert np.array_equal(n(w8.q), qw_o) and np.array_equal(n(w8.s), sw_o)
+    assert np.array_equal(n(I.dequant_weight(w8)), O.dequant_weight(qw_o, sw_o))
+    y = n(I.linear_w8a32(t(x, dev), w8, t(b, dev)))
+    y_o, bound = O.linear_w8a32(x, qw_o, sw_o, b)
+    err = np.abs(y.astype(np.float64) - y_o)
+    assert np.all(err <= bound + 1e-30), f"max err {err.max()} vs bound {bound[err.argmax() // N, err.argmax() % N]}"
+
+
+def test_w8a32_module(dev):
+    say("w8a32 via quantize_for_int8(weight_only=True)")
+    import borch_amd as bt
+    torch.manual_seed(0)
+    lin = bt.nn.Linear(768, 3072).to(dev)
+    assert bt.quantize_for_int8(lin, weight_only=True) == 1
+    x = torch.randn(1, 768, device=dev)
+    y = n(lin(x))
+    y_o, bound = O.linear_w8a32(n(x), n(lin.int8.q), n(lin.int8.s), n(lin.bias))
+    assert np.all(np.abs(y - y_o) <= bound)

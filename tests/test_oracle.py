@@ -301,3 +301,30 @@ def test_linear_int8_close_to_f32():
     y, acc, _, _ = O.linear_int8(x, w, b)
     ref = O.linear_f32(x, w, b)
     assert np.abs(y - ref).max() < 0.05 * np.abs(ref).max()
+
+
+def test_dequant_weight_is_one_f32_rounding():
+    """f32(q)·s rounded once (quant.ts:60-71 stores the double product into a Float32Array)."""
+    rng = np.random.default_rng(12)
+    q = rng.integers(-127, 128, size=(7, 33)).astype(np.int8)
+    s = rng.uniform(1e-4, 1e-1, 7).astype(np.float32)
+    w = O.dequant_weight(q, s)
+    for n in range(7):
+        for k in range(33):
+            assert w[n, k] == np.float32(float(q[n, k]) * float(s[n]))
+
+
+def test_linear_w8a32_bound_holds_for_f32_accumulation():
+    """The bound admits a plain sequential f32 FMA accumulation (the kernel's kind)."""
+    rng = np.random.default_rng(13)
+    x = rng.normal(size=(3, 256)).astype(np.float32)
+    q = rng.integers(-127, 128, size=(5, 256)).astype(np.int8)
+    s = rng.uniform(1e-3, 1e-2, 5).astype(np.float32)
+    y, bound = O.linear_w8a32(x, q, s)
+    w = O.dequant_weight(q, s)
+    for m in range(3):
+        for n in range(5):
+            acc = np.float32(0)
+            for k in range(256):
+                acc = np.float32(acc + np.float32(x[m, k] * w[n, k]))
+            assert abs(float(acc) - y[m, n]) <= bound[m, n]
