@@ -25,20 +25,27 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
-// The scale rule: float32(peak / 127), correctly rounded. The quotient is taken in
-// float64 and rounded once to float32; for a single division that equals the correctly
-// rounded float32 quotient (53 >= 2*24 + 2).
-__device__ __forceinline__ float scale_of(float peak) {
-  return (float)((double)peak / 127.0);
-}
+// The scale rule: float32(peak / 127), correctly rounded (HIP's f32 division is the IEEE
+// correctly rounded one; __fdiv_rn makes that explicit).
+__device__ __forceinline__ float scale_of(float peak) { return __fdiv_rn(peak, 127.0f); }
 
-// q = clip(rint(f64(v) / f64(s)), -127, 127); s == 0 gives 0. The float64 quotient of
-// two float32 values is never moved onto or off a .5 tie by its own rounding, so rint
-// (round half to even) of it is the exact-quotient rounding.
-__device__ __forceinline__ int quant_one(float v, double s) {
-  if (s == 0.0) return 0;
-  double r = rint((double)v / s);
-  r = r > 127.0 ? 127.0 : (r < -127.0 ? -127.0 : r);
+// q = clip(rint(v / s), -127, 127) of the EXACT quotient, half to even; s == 0 gives 0.
+// f = fl32(v / s) is the correctly rounded quotient. Rounding is monotonic and k + 0.5 is
+// representable for |k| <= 127, so rint(f) equals rint(v / s) unless f lands exactly on
+// k + 0.5 while v / s does not; then the sign of the exact remainder v - (k + 0.5)·s, which
+// one fma rounds without changing its sign, picks k or k + 1. (|v / s| <= 127.00001 since
+// s >= max|v| / 127 · (1 - 2^-24).)
+__device__ __forceinline__ int quant_one(float v, float s) {
+  if (s == 0.f) return 0;
+  const float f = __fdiv_rn(v, s);
+  float r = rintf(f);
+  const float fl = floorf(f);
+  if (f - fl == 0.5f) {
+    const float d = __fmaf_rn(-f, s, v);
+    if (d > 0.f) r = fl + 1.f;
+    else if (d < 0.f) r = fl;
+  }
+  r = fminf(fmaxf(r, -127.f), 127.f);
   return (int)r;
 }
 

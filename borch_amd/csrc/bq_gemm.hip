@@ -142,7 +142,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
     s_sw[i] = n < p.N ? p.sW[n] : 0.f;
     s_b[i] = (n < p.N && p.bias) ? p.bias[n] : 0.f;
   }
-  const double s_out = p.q_out ? (double)p.s_out[0] : 0.0;
+  const float s_out = p.q_out ? p.s_out[0] : 0.f;
 
   // Each thread loads 16-byte chunk `kc` of rows lr + i * ROWS_PER_PASS.
   const int kc = tid & 7;

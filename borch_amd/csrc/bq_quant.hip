@@ -66,7 +66,7 @@ __global__ __launch_bounds__(QR_THREADS) void quantize_rows_kernel(const float* 
     }
     const float sc = scale_of(block_max(m, red));
     if (t == 0) s[row] = sc;
-    const double sd = sc;
+    const float sd = sc;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int k = (t + i * QR_THREADS) * 4;
@@ -79,7 +79,7 @@ __global__ __launch_bounds__(QR_THREADS) void quantize_rows_kernel(const float* 
     for (int k = t; k < K; k += QR_THREADS) m = fmaxf(m, fabsf(xr[k]));
     const float sc = scale_of(block_max(m, red));
     if (t == 0) s[row] = sc;
-    const double sd = sc;
+    const float sd = sc;
     for (int k = t; k < K; k += QR_THREADS) qr[k] = (int8_t)quant_one(xr[k], sd);
   }
 }
@@ -132,7 +132,7 @@ __global__ __launch_bounds__(QT_THREADS) void quantize_tensor_kernel(const float
   for (int i = 1; i < QT_THREADS / 64; ++i) peak = fmaxf(peak, red[i]);
   const float sc = s_given ? s_given[0] : scale_of(peak);
   if (!s_given && blockIdx.x == 0 && threadIdx.x == 0) s[0] = sc;
-  const double sd = sc;
+  const float sd = sc;
   const int64_t total = P * (int64_t)Cpad;
   const int64_t words = (total + 3) / 4;
   const bool flat = (C == Cpad) && ((uintptr_t)x & 15) == 0 && ((uintptr_t)q & 3) == 0 && (total & 3) == 0;
@@ -173,7 +173,7 @@ __global__ __launch_bounds__(QT_THREADS) void quantize_pad16_kernel(const float*
   for (int i = 1; i < QT_THREADS / 64; ++i) peak = fmaxf(peak, red[i]);
   const float sc = s_given ? s_given[0] : scale_of(peak);
   if (!s_given && blockIdx.x == 0 && threadIdx.x == 0) s[0] = sc;
-  const double sd = sc;
+  const float sd = sc;
   const int chunks = Cpad / 16;
   const int64_t total = P * chunks;
   for (int64_t i = (int64_t)blockIdx.x * QT_THREADS + threadIdx.x; i < total; i += (int64_t)gridDim.x * QT_THREADS) {

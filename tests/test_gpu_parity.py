@@ -283,3 +283,43 @@ def test_w8a32_module(dev):
     y = n(lin(x))
     y_o, bound = O.linear_w8a32(n(x), n(lin.int8.q), n(lin.int8.s), n(lin.bias))
     assert np.all(np.abs(y - y_o) <= bound)
+
+
+def _false_ties(count=512, seed=21):
+    """(v, s) pairs whose correctly rounded f32 quotient is exactly k + 0.5 while the exact
+    quotient is not a tie (plus true ties), found by search and checked with rationals."""
+    from fractions import Fraction
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < count:
+        s = np.float32(rng.uniform(0.01, 1.0))
+        k = int(rng.integers(-126, 126))
+        v0 = np.float32((k + 0.5) * float(s))
+        for d in (-2, -1, 0, 1, 2):
+            v = v0
+            for _ in range(abs(d)):
+                v = np.nextafter(v, np.float32(np.inf if d > 0 else -np.inf))
+            if np.float32(v) / s == np.float32(k + 0.5):
+                exact = Fraction(float(v)) / Fraction(float(s))
+                out.append((v, s, exact == Fraction(2 * k + 1, 2)))
+    return out
+
+
+def test_quantize_false_ties(dev):
+    """Rows built from such pairs: each row's scale is forced to s by a peak element 127·s."""
+    say("quantize false ties (f32 quotient exactly k+0.5, exact quotient not)")
+    pairs = _false_ties()
+    rows = []
+    for v, s, _ in pairs[:256]:
+        peak = np.float32(127) * s
+        if np.float32(peak) / np.float32(127) != s:
+            continue
+        rows.append(np.array([peak, v, -v, 0.0], np.float32))
+    x = np.stack(rows)
+    assert len(rows) > 50
+    q, s = I.quantize_rows(t(x, dev))
+    qo, so = O.quantize_rows(x)
+    assert np.array_equal(n(s), so)
+    assert np.array_equal(n(q), qo)
+    n_false = sum(1 for _, _, tie in pairs if not tie)
+    say(f"  {len(rows)} rows, {n_false} of {len(pairs)} pairs are false ties")
