@@ -100,39 +100,24 @@ __device__ __forceinline__ void interleave() {
   if constexpr (ON) interleave_impl<MASK, COUNT, NMMA>(std::make_integer_sequence<int, NMMA>{});
 }
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, bool CONV, bool SCHED = true>
-__global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const GemmP p) {
+// Main loop with register staging: each K stage is loaded global -> VGPRs -> LDS.
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool CONV, int PIPE>
+__device__ __forceinline__ void mainloop_regs(const GemmP& p, int m0, int n0, int8_t* lds, float* s_sa, float* s_sw,
+                                              float* s_b, v16i (&c)[BM / WAVES_M / 32][BN / WAVES_N / 32]) {
+  constexpr bool SCHED = PIPE != 0;
   constexpr int T = WAVES_M * WAVES_N * 64;
-  constexpr int WTM = BM / WAVES_M;  // wave tile rows
+  constexpr int WTM = BM / WAVES_M;
   constexpr int WTN = BN / WAVES_N;
   constexpr int TM = WTM / 32;
   constexpr int TN = WTN / 32;
-  constexpr int ROWS_PER_PASS = T / 8;  // rows one pass of all threads loads (8 chunks a row)
+  constexpr int ROWS_PER_PASS = T / 8;
   constexpr int A_LD = BM / ROWS_PER_PASS;
   constexpr int B_LD = BN / ROWS_PER_PASS;
-  static_assert(BM % ROWS_PER_PASS == 0 && BN % ROWS_PER_PASS == 0, "tile/threads");
-  static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile");
-
-  __shared__ __attribute__((aligned(16))) int8_t lds[2 * (BM + BN) * BK];
-  // Per-tile scales and bias, staged once so the epilogue reads no global memory: on
-  // gfx9 stores and loads share one counter, and a load between stores waits for them.
-  __shared__ __attribute__((aligned(16))) float s_sa[BM];
-  __shared__ __attribute__((aligned(16))) float s_sw[BN];
-  __shared__ __attribute__((aligned(16))) float s_b[BN];
-
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int wm = wave / WAVES_N;
   const int wn = wave % WAVES_N;
-
-  const int tiles_m = (p.M + BM - 1) / BM;
-  const int tiles_n = (p.N + BN - 1) / BN;
-  int bm, bn;
-  tile_of(blockIdx.x, gridDim.x, tiles_m, tiles_n, bm, bn);
-  const int m0 = bm * BM;
-  const int n0 = bn * BN;
-
   for (int i = tid; i < BM; i += T) {
     const int m = m0 + i;
     s_sa[i] = m < p.M ? p.sA[p.sa_per_row ? m : 0] : 0.f;
@@ -142,8 +127,6 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
     s_sw[i] = n < p.N ? p.sW[n] : 0.f;
     s_b[i] = (n < p.N && p.bias) ? p.bias[n] : 0.f;
   }
-  const float s_out = p.q_out ? p.s_out[0] : 0.f;
-
   // Each thread loads 16-byte chunk `kc` of rows lr + i * ROWS_PER_PASS.
   const int kc = tid & 7;
   const int lr = tid >> 3;
@@ -219,12 +202,6 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
     for (int j = 0; j < TN; ++j) bf[j] = *reinterpret_cast<const v4i*>(bs + lds_off(wn * WTN + j * 32 + fr, ks * 2 + fh));
   };
 
-  v16i c[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j) c[i][j] = v16i{};
-
   // Pipeline over the four 32-byte K slices (ks) of a 128-byte stage:
   //   ks0: MFMAs of slice 0  | LDS reads of slice 1
   //   ks1: MFMAs of slice 1  | LDS reads of slice 2, LDS writes of stage kt+1 (other buffer)
@@ -256,14 +233,17 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
     interleave<SCHED, 0x100, NRD, NMMA>();
     __builtin_amdgcn_sched_barrier(0);
     frags(cur, 2, af[0], bf[0]);
-    store(cur ^ 1, ga, gb);  // unconditional: past the last stage it writes a buffer no one reads
+    if constexpr (PIPE != 2) store(cur ^ 1, ga, gb);  // unconditional: past the last stage it writes a buffer no one reads
     mma(af[1], bf[1]);
-    interleave<SCHED, 0x100 | 0x200, NRD + NLD, NMMA>();
+    if constexpr (PIPE != 2) interleave<SCHED, 0x100 | 0x200, NRD + NLD, NMMA>();
+    else interleave<SCHED, 0x100, NRD, NMMA>();
     __builtin_amdgcn_sched_barrier(0);
     frags(cur, 3, af[1], bf[1]);
+    if constexpr (PIPE == 2) store(cur ^ 1, ga, gb);
     load(kt + 2, ga, gb);  // past K every offset is out of range: zeros, no memory access
     mma(af[0], bf[0]);
-    interleave<SCHED, 0x100 | 0x020, NRD + NLD, NMMA>();
+    if constexpr (PIPE != 2) interleave<SCHED, 0x100 | 0x020, NRD + NLD, NMMA>();
+    else interleave<SCHED, 0x100 | 0x200 | 0x020, NRD + 2 * NLD, NMMA>();
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
     frags(cur ^ 1, 0, af[0], bf[0]);
@@ -272,6 +252,223 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
     __builtin_amdgcn_sched_barrier(0);
   }
   __syncthreads();
+}
+
+// One 16-byte-per-lane load straight into LDS (no VGPR staging): lane l's 16 bytes land at
+// LDS byte address m0v + 16 * l. Issued from inline assembly so that the compiler, which
+// cannot tell these writes from the fragment reads of the other buffer, does not add a
+// full vmcnt wait before every LDS read; the caller waits (vmcnt) before the barrier that
+// publishes a stage. M0 is written here and used by nothing else in these kernels; the
+// s_nop covers the M0-write -> LDS-DMA hazard.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t m0v) {
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "s"(m0v)
+               : "m0");
+#pragma clang diagnostic pop
+}
+__device__ __forceinline__ void wait_dma_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Main loop with direct-to-LDS loads. A stage's LDS image is written by wave-wide DMAs of
+// 8 rows (1 KB) each: lane l covers row 8*band + l/8 and LDS chunk slot l%8, and fetches the
+// global 16-byte chunk that the XOR swizzle maps to that slot, so the LDS layout (and the
+// fragment reads) are those of the register-staged loop. Stage kt+2 is fetched into the
+// buffer stage kt just left, right after the barrier that ends stage kt, and must land by
+// the barrier that ends stage kt+1: one whole stage of MFMAs covers its latency.
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool CONV>
+__device__ __forceinline__ void mainloop_dma(const GemmP& p, int m0, int n0, int8_t* lds, float* s_sa, float* s_sw,
+                                             float* s_b, v16i (&c)[BM / WAVES_M / 32][BN / WAVES_N / 32]) {
+  constexpr int WAVES = WAVES_M * WAVES_N;
+  constexpr int T = WAVES * 64;
+  constexpr int WTM = BM / WAVES_M;
+  constexpr int WTN = BN / WAVES_N;
+  constexpr int TM = WTM / 32;
+  constexpr int TN = WTN / 32;
+  constexpr int BAND = 8 * WAVES;  // rows one DMA per wave covers
+  constexpr int A_DMA = BM / BAND;
+  constexpr int B_DMA = BN / BAND;
+  static_assert(BM % BAND == 0 && BN % BAND == 0 && (WAVES % 2) == 0, "tile/waves");
+  static_assert(BM <= T && BN <= T, "one scale per thread");
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave / WAVES_N;
+  const int wn = wave % WAVES_N;
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+
+  // Scales and bias: loaded now, written to LDS after the loop (their latency hides
+  // behind the main loop instead of delaying its start).
+  const int sm = m0 + tid, sn = n0 + tid;
+  const float r_sa = (tid < BM && sm < p.M) ? p.sA[p.sa_per_row ? sm : 0] : 0.f;
+  const float r_sw = (tid < BN && sn < p.N) ? p.sW[sn] : 0.f;
+  const float r_b = (tid < BN && sn < p.N && p.bias) ? p.bias[sn] : 0.f;
+
+  // This lane's row within each band and the global chunk it fetches. Every band starts at
+  // a multiple of 16 rows (WAVES even), so the swizzle term is the same in every band.
+  const int drow = wv * 8 + (lane >> 3);
+  const int dch = (lane & 7) ^ ((drow >> 1) & 7);
+  const uint32_t lds_base = (uint32_t)(uintptr_t)lds;
+
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.W + (size_t)n0 * p.K, (uint32_t)(min(BN, p.N - n0) * p.K));
+  __amdgpu_buffer_rsrc_t ra;
+  uint32_t a_pix[A_DMA];
+  int a_ih0[A_DMA], a_iw0[A_DMA];
+  if constexpr (CONV) {
+    ra = make_rsrc(p.A, (uint32_t)((size_t)p.Nimg_HWC));
+    const int plane = p.OH * p.OW;
+#pragma unroll
+    for (int i = 0; i < A_DMA; ++i) {
+      const int m = m0 + i * BAND + drow;
+      const int n = m / plane;
+      const int r = m - n * plane;
+      const int oh = r / p.OW;
+      const int ow = r - oh * p.OW;
+      const bool ok = m < p.M;
+      a_ih0[i] = ok ? oh * p.stride - p.pad : -(1 << 20);  // an invalid row never passes the bounds test
+      a_iw0[i] = ow * p.stride - p.pad;
+      a_pix[i] = (uint32_t)(n * p.H * p.Wd * p.C);
+    }
+  } else {
+    ra = make_rsrc(p.A + (size_t)m0 * p.K, (uint32_t)(min(BM, p.M - m0) * p.K));
+#pragma unroll
+    for (int i = 0; i < A_DMA; ++i) {
+      a_pix[i] = (uint32_t)((i * BAND + drow) * p.K);
+      a_ih0[i] = a_iw0[i] = 0;
+    }
+  }
+  uint32_t b_row[B_DMA];
+#pragma unroll
+  for (int i = 0; i < B_DMA; ++i) b_row[i] = (uint32_t)((i * BAND + drow) * p.K);
+
+  auto dma_stage = [&](int buf, int kt) {
+    const int k0 = kt * BK + dch * 16;
+    const bool kin = k0 < p.K;
+    const uint32_t am0 = lds_base + (uint32_t)(buf * (BM + BN) * BK + wv * 1024);
+    const uint32_t bm0 = am0 + BM * BK;
+    if constexpr (CONV) {
+      const int tap = k0 / p.C;
+      const int c0 = k0 - tap * p.C;
+      const int kh = tap / p.KWd;
+      const int kw = tap - kh * p.KWd;
+#pragma unroll
+      for (int i = 0; i < A_DMA; ++i) {
+        const int ih = a_ih0[i] + kh, iw = a_iw0[i] + kw;
+        const bool ok = kin && (unsigned)ih < (unsigned)p.H && (unsigned)iw < (unsigned)p.Wd;
+        dma16(ra, ok ? a_pix[i] + (uint32_t)((ih * p.Wd + iw) * p.C + c0) : OOB, am0 + i * BAND * BK);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < A_DMA; ++i) dma16(ra, kin ? a_pix[i] + (uint32_t)k0 : OOB, am0 + i * BAND * BK);
+    }
+#pragma unroll
+    for (int i = 0; i < B_DMA; ++i) dma16(rb, kin ? b_row[i] + (uint32_t)k0 : OOB, bm0 + i * BAND * BK);
+  };
+  const int fr = lane & 31;
+  const int fh = lane >> 5;
+  auto frags = [&](int buf, int ks, v4i (&af)[TM], v4i (&bf)[TN]) {
+    const int8_t* as = lds + buf * (BM + BN) * BK;
+    const int8_t* bs = as + BM * BK;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const v4i*>(as + lds_off(wm * WTM + i * 32 + fr, ks * 2 + fh));
+#pragma unroll
+    for (int j = 0; j < TN; ++j) bf[j] = *reinterpret_cast<const v4i*>(bs + lds_off(wn * WTN + j * 32 + fr, ks * 2 + fh));
+  };
+  auto mma = [&](const v4i (&a)[TM], const v4i (&b)[TN]) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) c[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], c[i][j], 0, 0, 0);
+  };
+  constexpr int NMMA = TM * TN, NRD = TM + TN;
+
+  // Stage pipeline (ks = the four 32-byte K slices of a 128-byte stage):
+  //   ks0..ks2: MFMAs of slice ks | LDS reads of slice ks+1
+  //   wait for this wave's DMAs of stage kt+1; barrier (stage kt+1 landed for every wave;
+  //   every read of stage kt is done, so its buffer is free)
+  //   DMAs of stage kt+2 into that buffer
+  //   ks3: MFMAs of slice 3 | LDS reads of slice 0 of stage kt+1
+  const int KT = (p.K + BK - 1) / BK;
+  dma_stage(0, 0);
+  dma_stage(1, 1);
+  wait_dma_all();
+  __syncthreads();
+  v4i af[2][TM], bf[2][TN];
+  frags(0, 0, af[0], bf[0]);
+  for (int kt = 0; kt < KT; ++kt) {
+    const int cur = kt & 1;
+    frags(cur, 1, af[1], bf[1]);
+    mma(af[0], bf[0]);
+    interleave<true, 0x100, NRD, NMMA>();
+    __builtin_amdgcn_sched_barrier(0);
+    frags(cur, 2, af[0], bf[0]);
+    mma(af[1], bf[1]);
+    interleave<true, 0x100, NRD, NMMA>();
+    __builtin_amdgcn_sched_barrier(0);
+    frags(cur, 3, af[1], bf[1]);
+    mma(af[0], bf[0]);
+    interleave<true, 0x100, NRD, NMMA>();
+    __builtin_amdgcn_sched_barrier(0);
+    wait_dma_all();
+    __syncthreads();
+    frags(cur ^ 1, 0, af[0], bf[0]);  // past the last stage: data no one uses
+    dma_stage(cur, kt + 2);           // unconditional: past K every offset is out of range (zeros)
+    mma(af[1], bf[1]);
+    interleave<true, 0x100, NRD, NMMA>();
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  wait_dma_all();  // the zero-filling DMAs past K land before the epilogue reuses the buffers
+  if (tid < BM) s_sa[tid] = r_sa;
+  if (tid < BN) {
+    s_sw[tid] = r_sw;
+    s_b[tid] = r_b;
+  }
+  __syncthreads();
+}
+
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool CONV, int PIPE = 1>
+__global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const GemmP p) {
+  constexpr bool SCHED = PIPE != 0;
+  constexpr int T = WAVES_M * WAVES_N * 64;
+  constexpr int WTM = BM / WAVES_M;  // wave tile rows
+  constexpr int WTN = BN / WAVES_N;
+  constexpr int TM = WTM / 32;
+  constexpr int TN = WTN / 32;
+  constexpr int ROWS_PER_PASS = T / 8;  // rows one pass of all threads loads (8 chunks a row)
+  constexpr int A_LD = BM / ROWS_PER_PASS;
+  constexpr int B_LD = BN / ROWS_PER_PASS;
+  static_assert(BM % ROWS_PER_PASS == 0 && BN % ROWS_PER_PASS == 0, "tile/threads");
+  static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile");
+
+  __shared__ __attribute__((aligned(16))) int8_t lds[2 * (BM + BN) * BK];
+  // Per-tile scales and bias, staged once so the epilogue reads no global memory: on
+  // gfx9 stores and loads share one counter, and a load between stores waits for them.
+  __shared__ __attribute__((aligned(16))) float s_sa[BM];
+  __shared__ __attribute__((aligned(16))) float s_sw[BN];
+  __shared__ __attribute__((aligned(16))) float s_b[BN];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave / WAVES_N;
+  const int wn = wave % WAVES_N;
+
+  const int tiles_m = (p.M + BM - 1) / BM;
+  const int tiles_n = (p.N + BN - 1) / BN;
+  int bm, bn;
+  tile_of(blockIdx.x, gridDim.x, tiles_m, tiles_n, bm, bn);
+  const int m0 = bm * BM;
+  const int n0 = bn * BN;
+
+  const float s_out = p.q_out ? p.s_out[0] : 0.f;
+  v16i c[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) c[i][j] = v16i{};
+  if constexpr (PIPE == 3)
+    mainloop_dma<BM, BN, WAVES_M, WAVES_N, CONV>(p, m0, n0, lds, s_sa, s_sw, s_b, c);
+  else
+    mainloop_regs<BM, BN, WAVES_M, WAVES_N, CONV, PIPE>(p, m0, n0, lds, s_sa, s_sw, s_b, c);
 
   // Epilogue, one 32-row slice of the wave tile at a time: the int32 results go through a
   // per-wave LDS patch (exact), come back as four consecutive columns of one row per lane,
@@ -460,11 +657,11 @@ __device__ __forceinline__ int wave_sum(int v) {
   return v;
 }
 
-template <int MR, int KC, int RPW>
-__global__ __launch_bounds__(GV_WAVES * 64) void gemv_i8_kernel(const GemmP p) {
+template <int MR, int KC, int RPW, int WAVES = GV_WAVES>
+__global__ __launch_bounds__(WAVES * 64) void gemv_i8_kernel(const GemmP p) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int row0 = (blockIdx.x * GV_WAVES + wave) * RPW;
+  const int row0 = (blockIdx.x * WAVES + wave) * RPW;
   if (row0 >= p.N) return;
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.W + (size_t)row0 * p.K, (uint32_t)(min(RPW, p.N - row0) * p.K));
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, (uint32_t)(p.M * p.K));
@@ -522,16 +719,35 @@ __global__ __launch_bounds__(GV_WAVES * 64) void gemv_i8_kernel(const GemmP p) {
   }
 }
 
-template <int MR>
-static bool launch_gemv(const GemmP& p, hipStream_t st) {
-  constexpr int RPW = 2;
-  const unsigned grid = (unsigned)((p.N + GV_WAVES * RPW - 1) / (GV_WAVES * RPW));
-  if (p.K <= 1024) gemv_i8_kernel<MR, 1, RPW><<<grid, GV_WAVES * 64, 0, st>>>(p);
-  else if (p.K <= 2048) gemv_i8_kernel<MR, 2, RPW><<<grid, GV_WAVES * 64, 0, st>>>(p);
-  else if (p.K <= 4096) gemv_i8_kernel<MR, 4, RPW><<<grid, GV_WAVES * 64, 0, st>>>(p);
-  else if (p.K <= 8192) gemv_i8_kernel<MR, 8, RPW><<<grid, GV_WAVES * 64, 0, st>>>(p);
+static int forced_gemv() {
+  static int cfg = [] {
+    const char* e = getenv("BQ_GEMV_CFG");
+    return e ? atoi(e) : 0;
+  }();
+  return cfg;
+}
+
+template <int MR, int RPW, int WAVES>
+static bool launch_gemv_cfg(const GemmP& p, hipStream_t st) {
+  const unsigned grid = (unsigned)((p.N + WAVES * RPW - 1) / (WAVES * RPW));
+  if (p.K <= 1024) gemv_i8_kernel<MR, 1, RPW, WAVES><<<grid, WAVES * 64, 0, st>>>(p);
+  else if (p.K <= 2048) gemv_i8_kernel<MR, 2, RPW, WAVES><<<grid, WAVES * 64, 0, st>>>(p);
+  else if (p.K <= 4096) gemv_i8_kernel<MR, 4, RPW, WAVES><<<grid, WAVES * 64, 0, st>>>(p);
+  else if (p.K <= 8192) gemv_i8_kernel<MR, 8, RPW, WAVES><<<grid, WAVES * 64, 0, st>>>(p);
   else return false;
   return true;
+}
+
+template <int MR>
+static bool launch_gemv(const GemmP& p, hipStream_t st) {
+  switch (forced_gemv()) {
+    case 1: return launch_gemv_cfg<MR, 1, 8>(p, st);
+    case 2: return launch_gemv_cfg<MR, 4, 8>(p, st);
+    case 3: return launch_gemv_cfg<MR, 2, 4>(p, st);
+    case 4: return launch_gemv_cfg<MR, 1, 4>(p, st);
+    case 5: return launch_gemv_cfg<MR, 4, 4>(p, st);
+    default: return launch_gemv_cfg<MR, 2, 8>(p, st);
+  }
 }
 
 // -------------------------------------------------------------------------- depthwise
@@ -598,10 +814,10 @@ __global__ __launch_bounds__(256) void dwconv_i8_kernel(const int8_t* __restrict
 
 // ---------------------------------------------------------------------------- dispatch
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, bool CONV, bool SCHED = true>
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool CONV, int PIPE = 1>
 static void launch_tiled(const GemmP& p, hipStream_t st) {
   const int tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
-  gemm_i8_kernel<BM, BN, WAVES_M, WAVES_N, CONV, SCHED><<<tiles, WAVES_M * WAVES_N * 64, 0, st>>>(p);
+  gemm_i8_kernel<BM, BN, WAVES_M, WAVES_N, CONV, PIPE><<<tiles, WAVES_M * WAVES_N * 64, 0, st>>>(p);
 }
 
 // BQ_GEMM_CFG forces one tile configuration (tuning sweeps); unset = the shape rule.
@@ -623,8 +839,17 @@ static void launch_gemm(const GemmP& p, hipStream_t st) {
     case 6: return launch_tiled<128, 256, 2, 2, CONV>(p, st);
     case 7: return launch_tiled<64, 64, 2, 2, CONV>(p, st);
     case 8: return launch_tiled<256, 64, 4, 1, CONV>(p, st);
-    case 9: return launch_tiled<256, 256, 2, 4, CONV, false>(p, st);
-    case 10: return launch_tiled<256, 256, 2, 2, CONV, false>(p, st);
+    case 9: return launch_tiled<256, 256, 2, 4, CONV, 0>(p, st);
+    case 10: return launch_tiled<256, 256, 2, 2, CONV, 0>(p, st);
+    case 11: return launch_tiled<256, 256, 2, 4, CONV, 2>(p, st);
+    case 12: return launch_tiled<256, 256, 2, 2, CONV, 2>(p, st);
+    case 13: return launch_tiled<128, 128, 2, 2, CONV, 2>(p, st);
+    case 21: return launch_tiled<256, 256, 2, 4, CONV, 3>(p, st);
+    case 23: return launch_tiled<256, 256, 2, 2, CONV, 3>(p, st);
+    case 24: return launch_tiled<128, 128, 2, 2, CONV, 3>(p, st);
+    case 25: return launch_tiled<256, 128, 2, 2, CONV, 3>(p, st);
+    case 27: return launch_tiled<64, 64, 2, 2, CONV, 3>(p, st);
+    case 28: return launch_tiled<256, 64, 4, 1, CONV, 3>(p, st);
     default: break;
   }
   // The largest tile that still fills the chip (>= 192 / 128 workgroups) without wasting
@@ -633,13 +858,13 @@ static void launch_gemm(const GemmP& p, hipStream_t st) {
   const long long t128 = (long long)((p.M + 127) / 128) * ((p.N + 127) / 128);
   const long long t256x64 = (long long)((p.M + 255) / 256) * ((p.N + 63) / 64);
   if (p.N <= 64 && t256x64 >= 128)
-    launch_tiled<256, 64, 4, 1, CONV>(p, st);
+    launch_tiled<256, 64, 4, 1, CONV, 3>(p, st);
   else if (t256 >= 192 && p.N >= 192)
-    launch_tiled<256, 256, 2, 4, CONV>(p, st);
+    launch_tiled<256, 256, 2, 4, CONV, 3>(p, st);
   else if (t128 >= 128 && p.N >= 96)
-    launch_tiled<128, 128, 2, 2, CONV>(p, st);
+    launch_tiled<128, 128, 2, 2, CONV, 3>(p, st);
   else
-    launch_tiled<64, 64, 2, 2, CONV>(p, st);
+    launch_tiled<64, 64, 2, 2, CONV, 3>(p, st);
 }
 
 static bool aligned16(const void* q) { return ((uintptr_t)q & 15) == 0; }
