@@ -6,10 +6,13 @@
 // channel). Both operands are K-contiguous, so each MFMA lane reads 16 contiguous bytes
 // of one row of each — no transposes anywhere.
 //
-// Tiles: BM x BN output per workgroup, K walked in 128-byte steps (one 128 B cache line
-// per row per step), double-buffered in LDS with an XOR swizzle of the 16-byte chunks.
-// Each wave owns a (BM/WAVES_M) x (BN/WAVES_N) sub-tile of 32x32 v_mfma_i32_32x32x32_i8
-// results; the next K step's global loads are in flight while the current one computes.
+// Tiles: BM x BN output per workgroup, K walked in 128-byte stages (one 128 B cache line
+// per row per stage) through a ring of NBUF LDS stage buffers, XOR-swizzled by 16-byte
+// chunk, that direct-to-LDS buffer loads fill (no VGPR staging) while earlier stages
+// compute. Each wave owns a (BM/WAVES_M) x (BN/WAVES_N) sub-tile of 32x32
+// v_mfma_i32_32x32x32_i8 results. With random int8 operands the MFMA pipe is power-limited
+// near 22 ns per 32x32x32 MFMA per SIMD (measured, about 3.0 POPS chip-wide), which the
+// main loop of the 256x256 tile reaches to within about 15%.
 //
 // Skinny path (M <= 64): the weight is streamed once at HBM rate. A workgroup owns 16
 // output channels; its waves split K; each lane loads 64 contiguous weight bytes per step
@@ -100,160 +103,6 @@ __device__ __forceinline__ void interleave() {
   if constexpr (ON) interleave_impl<MASK, COUNT, NMMA>(std::make_integer_sequence<int, NMMA>{});
 }
 
-// Main loop with register staging: each K stage is loaded global -> VGPRs -> LDS.
-template <int BM, int BN, int WAVES_M, int WAVES_N, bool CONV, int PIPE>
-__device__ __forceinline__ void mainloop_regs(const GemmP& p, int m0, int n0, int8_t* lds, float* s_sa, float* s_sw,
-                                              float* s_b, v16i (&c)[BM / WAVES_M / 32][BN / WAVES_N / 32]) {
-  constexpr bool SCHED = PIPE != 0;
-  constexpr int T = WAVES_M * WAVES_N * 64;
-  constexpr int WTM = BM / WAVES_M;
-  constexpr int WTN = BN / WAVES_N;
-  constexpr int TM = WTM / 32;
-  constexpr int TN = WTN / 32;
-  constexpr int ROWS_PER_PASS = T / 8;
-  constexpr int A_LD = BM / ROWS_PER_PASS;
-  constexpr int B_LD = BN / ROWS_PER_PASS;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wm = wave / WAVES_N;
-  const int wn = wave % WAVES_N;
-  for (int i = tid; i < BM; i += T) {
-    const int m = m0 + i;
-    s_sa[i] = m < p.M ? p.sA[p.sa_per_row ? m : 0] : 0.f;
-  }
-  for (int i = tid; i < BN; i += T) {
-    const int n = n0 + i;
-    s_sw[i] = n < p.N ? p.sW[n] : 0.f;
-    s_b[i] = (n < p.N && p.bias) ? p.bias[n] : 0.f;
-  }
-  // Each thread loads 16-byte chunk `kc` of rows lr + i * ROWS_PER_PASS.
-  const int kc = tid & 7;
-  const int lr = tid >> 3;
-
-  // B (weights): rows n0.., range-checked at the last valid row.
-  const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.W + (size_t)n0 * p.K, (uint32_t)(min(BN, p.N - n0) * p.K));
-  // A: dense rows m0.., or the whole NHWC activation for the implicit im2col.
-  __amdgpu_buffer_rsrc_t ra;
-  uint32_t a_pix[A_LD];  // conv: byte offset of image n's pixel (0, 0); dense: row offset
-  int a_ih0[A_LD], a_iw0[A_LD];
-  if constexpr (CONV) {
-    ra = make_rsrc(p.A, (uint32_t)((size_t)p.Nimg_HWC));
-    const int plane = p.OH * p.OW;
-#pragma unroll
-    for (int i = 0; i < A_LD; ++i) {
-      const int m = m0 + lr + i * ROWS_PER_PASS;
-      const int n = m / plane;
-      const int r = m - n * plane;
-      const int oh = r / p.OW;
-      const int ow = r - oh * p.OW;
-      const bool ok = m < p.M;
-      a_ih0[i] = ok ? oh * p.stride - p.pad : -(1 << 20);  // an invalid row never passes the bounds test
-      a_iw0[i] = ow * p.stride - p.pad;
-      a_pix[i] = (uint32_t)(n * p.H * p.Wd * p.C);
-    }
-  } else {
-    ra = make_rsrc(p.A + (size_t)m0 * p.K, (uint32_t)(min(BM, p.M - m0) * p.K));
-#pragma unroll
-    for (int i = 0; i < A_LD; ++i) {
-      a_pix[i] = (uint32_t)((lr + i * ROWS_PER_PASS) * p.K);
-      a_ih0[i] = a_iw0[i] = 0;
-    }
-  }
-
-  auto load = [&](int kt, v4i (&ga)[A_LD], v4i (&gb)[B_LD]) {
-    const int k0 = kt * BK + kc * 16;
-    const bool kin = k0 < p.K;
-    if constexpr (CONV) {
-      const int tap = k0 / p.C;
-      const int c0 = k0 - tap * p.C;
-      const int kh = tap / p.KWd;
-      const int kw = tap - kh * p.KWd;
-#pragma unroll
-      for (int i = 0; i < A_LD; ++i) {
-        const int ih = a_ih0[i] + kh, iw = a_iw0[i] + kw;
-        const bool ok = kin && (unsigned)ih < (unsigned)p.H && (unsigned)iw < (unsigned)p.Wd;
-        ga[i] = buf_load16(ra, ok ? a_pix[i] + (uint32_t)((ih * p.Wd + iw) * p.C + c0) : OOB);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < A_LD; ++i) ga[i] = buf_load16(ra, kin ? a_pix[i] + (uint32_t)k0 : OOB);
-    }
-#pragma unroll
-    for (int i = 0; i < B_LD; ++i)
-      gb[i] = buf_load16(rb, kin ? (uint32_t)((lr + i * ROWS_PER_PASS) * p.K + k0) : OOB);
-  };
-  auto store = [&](int buf, const v4i (&ga)[A_LD], const v4i (&gb)[B_LD]) {
-    int8_t* as = lds + buf * (BM + BN) * BK;
-    int8_t* bs = as + BM * BK;
-#pragma unroll
-    for (int i = 0; i < A_LD; ++i) *reinterpret_cast<v4i*>(as + lds_off(lr + i * ROWS_PER_PASS, kc)) = ga[i];
-#pragma unroll
-    for (int i = 0; i < B_LD; ++i) *reinterpret_cast<v4i*>(bs + lds_off(lr + i * ROWS_PER_PASS, kc)) = gb[i];
-  };
-  const int fr = lane & 31;  // fragment row within a 32-row block
-  const int fh = lane >> 5;  // which 16-byte half of the 32-byte K slice
-  auto frags = [&](int buf, int ks, v4i (&af)[TM], v4i (&bf)[TN]) {
-    const int8_t* as = lds + buf * (BM + BN) * BK;
-    const int8_t* bs = as + BM * BK;
-#pragma unroll
-    for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const v4i*>(as + lds_off(wm * WTM + i * 32 + fr, ks * 2 + fh));
-#pragma unroll
-    for (int j = 0; j < TN; ++j) bf[j] = *reinterpret_cast<const v4i*>(bs + lds_off(wn * WTN + j * 32 + fr, ks * 2 + fh));
-  };
-
-  // Pipeline over the four 32-byte K slices (ks) of a 128-byte stage:
-  //   ks0: MFMAs of slice 0  | LDS reads of slice 1
-  //   ks1: MFMAs of slice 1  | LDS reads of slice 2, LDS writes of stage kt+1 (other buffer)
-  //   ks2: MFMAs of slice 2  | LDS reads of slice 3, global loads of stage kt+2
-  //   barrier (stage kt+1 written by every wave; every read of stage kt issued and done)
-  //   ks3: MFMAs of slice 3  | LDS reads of slice 0 of stage kt+1
-  // One barrier per stage, placed so the next stage's first fragments load under the last
-  // slice's MFMAs; the MFMAs of each slice are interleaved with its memory instructions.
-  const int KT = (p.K + BK - 1) / BK;
-  v4i ga[A_LD], gb[B_LD];
-  load(0, ga, gb);
-  store(0, ga, gb);
-  load(1, ga, gb);
-  __syncthreads();
-  v4i af[2][TM], bf[2][TN];
-  frags(0, 0, af[0], bf[0]);
-  auto mma = [&](const v4i (&a)[TM], const v4i (&b)[TN]) {
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j) c[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], c[i][j], 0, 0, 0);
-  };
-  constexpr int NMMA = TM * TN, NRD = TM + TN;
-  constexpr int NLD = A_LD + B_LD;
-  for (int kt = 0; kt < KT; ++kt) {
-    const int cur = kt & 1;
-    frags(cur, 1, af[1], bf[1]);
-    mma(af[0], bf[0]);
-    interleave<SCHED, 0x100, NRD, NMMA>();
-    __builtin_amdgcn_sched_barrier(0);
-    frags(cur, 2, af[0], bf[0]);
-    if constexpr (PIPE != 2) store(cur ^ 1, ga, gb);  // unconditional: past the last stage it writes a buffer no one reads
-    mma(af[1], bf[1]);
-    if constexpr (PIPE != 2) interleave<SCHED, 0x100 | 0x200, NRD + NLD, NMMA>();
-    else interleave<SCHED, 0x100, NRD, NMMA>();
-    __builtin_amdgcn_sched_barrier(0);
-    frags(cur, 3, af[1], bf[1]);
-    if constexpr (PIPE == 2) store(cur ^ 1, ga, gb);
-    load(kt + 2, ga, gb);  // past K every offset is out of range: zeros, no memory access
-    mma(af[0], bf[0]);
-    if constexpr (PIPE != 2) interleave<SCHED, 0x100 | 0x020, NRD + NLD, NMMA>();
-    else interleave<SCHED, 0x100 | 0x200 | 0x020, NRD + 2 * NLD, NMMA>();
-    __builtin_amdgcn_sched_barrier(0);
-    __syncthreads();
-    frags(cur ^ 1, 0, af[0], bf[0]);
-    mma(af[1], bf[1]);
-    interleave<SCHED, 0x100, NRD, NMMA>();
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  __syncthreads();
-}
-
 // One 16-byte-per-lane load straight into LDS (no VGPR staging): lane l's 16 bytes land at
 // LDS byte address m0v + 16 * l. Issued from inline assembly so that the compiler, which
 // cannot tell these writes from the fragment reads of the other buffer, does not add a
@@ -268,14 +117,20 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, u
 #pragma clang diagnostic pop
 }
 __device__ __forceinline__ void wait_dma_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+template <int N>
+__device__ __forceinline__ void wait_dma() {
+  static_assert(N >= 0 && N <= 63, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
 
-// Main loop with direct-to-LDS loads. A stage's LDS image is written by wave-wide DMAs of
-// 8 rows (1 KB) each: lane l covers row 8*band + l/8 and LDS chunk slot l%8, and fetches the
-// global 16-byte chunk that the XOR swizzle maps to that slot, so the LDS layout (and the
-// fragment reads) are those of the register-staged loop. Stage kt+2 is fetched into the
-// buffer stage kt just left, right after the barrier that ends stage kt, and must land by
-// the barrier that ends stage kt+1: one whole stage of MFMAs covers its latency.
-template <int BM, int BN, int WAVES_M, int WAVES_N, bool CONV>
+// Main loop with direct-to-LDS loads into a ring of NBUF stage buffers. A stage's LDS image
+// is written by wave-wide DMAs of 8 rows (1 KB) each: lane l covers row 8*band + l/8 and
+// LDS chunk slot l%8, and fetches the global 16-byte chunk that the XOR swizzle maps to that
+// slot, so the LDS layout (and the fragment reads) are those of the register-staged loop.
+// Stage kt+NBUF is fetched into the buffer stage kt just left, right after the barrier that
+// ends stage kt, and must land by the barrier that ends stage kt+NBUF-1: NBUF-1 stages of
+// MFMAs cover its latency (small tiles, whose stages are short, take deep rings).
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool CONV, int NBUF, int FD>
 __device__ __forceinline__ void mainloop_dma(const GemmP& p, int m0, int n0, int8_t* lds, float* s_sa, float* s_sw,
                                              float* s_b, v16i (&c)[BM / WAVES_M / 32][BN / WAVES_N / 32]) {
   constexpr int WAVES = WAVES_M * WAVES_N;
@@ -289,6 +144,8 @@ __device__ __forceinline__ void mainloop_dma(const GemmP& p, int m0, int n0, int
   constexpr int B_DMA = BN / BAND;
   static_assert(BM % BAND == 0 && BN % BAND == 0 && (WAVES % 2) == 0, "tile/waves");
   static_assert(BM <= T && BN <= T, "one scale per thread");
+  constexpr int PER = A_DMA + B_DMA;  // DMAs a wave issues per stage
+  static_assert(NBUF >= 2 && (NBUF - 1) * PER <= 63, "ring depth / vmcnt range");
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -383,19 +240,53 @@ __device__ __forceinline__ void mainloop_dma(const GemmP& p, int m0, int n0, int
 
   // Stage pipeline (ks = the four 32-byte K slices of a 128-byte stage):
   //   ks0..ks2: MFMAs of slice ks | LDS reads of slice ks+1
-  //   wait for this wave's DMAs of stage kt+1; barrier (stage kt+1 landed for every wave;
-  //   every read of stage kt is done, so its buffer is free)
-  //   DMAs of stage kt+2 into that buffer
+  //   wait for this wave's DMAs of stage kt+1 (the NBUF-2 later stages may stay in flight);
+  //   barrier (stage kt+1 landed for every wave; every read of stage kt is done, so its
+  //   buffer is free)
+  //   DMAs of stage kt+NBUF into that buffer
   //   ks3: MFMAs of slice 3 | LDS reads of slice 0 of stage kt+1
+  // Stages past K are fetched too: every offset is then out of range and the DMA writes zeros.
   const int KT = (p.K + BK - 1) / BK;
-  dma_stage(0, 0);
-  dma_stage(1, 1);
-  wait_dma_all();
+#pragma unroll
+  for (int st = 0; st < NBUF; ++st) dma_stage(st, st);
+  wait_dma<(NBUF - 1) * PER>();
   __syncthreads();
+  if constexpr (FD == 2) {
+    // Fragments two slices ahead (four register sets, one per slice); the barrier sits
+    // after slice 1 so that slices 0 and 1 of stage kt+1 are read under slices 2 and 3.
+    v4i af[4][TM], bf[4][TN];
+    frags(0, 0, af[0], bf[0]);
+    frags(0, 1, af[1], bf[1]);
+    int cur = 0;
+    for (int kt = 0; kt < KT; ++kt) {
+      const int nxt = cur + 1 == NBUF ? 0 : cur + 1;
+      frags(cur, 2, af[2], bf[2]);
+      mma(af[0], bf[0]);
+      interleave<true, 0x100, NRD, NMMA>();
+      __builtin_amdgcn_sched_barrier(0);
+      frags(cur, 3, af[3], bf[3]);
+      mma(af[1], bf[1]);
+      interleave<true, 0x100, NRD, NMMA>();
+      __builtin_amdgcn_sched_barrier(0);
+      wait_dma<(NBUF - 2) * PER>();
+      __syncthreads();
+      frags(nxt, 0, af[0], bf[0]);  // past the last stage: data no one uses
+      dma_stage(cur, kt + NBUF);
+      mma(af[2], bf[2]);
+      interleave<true, 0x100, NRD, NMMA>();
+      __builtin_amdgcn_sched_barrier(0);
+      frags(nxt, 1, af[1], bf[1]);
+      mma(af[3], bf[3]);
+      interleave<true, 0x100, NRD, NMMA>();
+      __builtin_amdgcn_sched_barrier(0);
+      cur = nxt;
+    }
+  } else {
   v4i af[2][TM], bf[2][TN];
   frags(0, 0, af[0], bf[0]);
+  int cur = 0;
   for (int kt = 0; kt < KT; ++kt) {
-    const int cur = kt & 1;
+    const int nxt = cur + 1 == NBUF ? 0 : cur + 1;
     frags(cur, 1, af[1], bf[1]);
     mma(af[0], bf[0]);
     interleave<true, 0x100, NRD, NMMA>();
@@ -408,13 +299,15 @@ __device__ __forceinline__ void mainloop_dma(const GemmP& p, int m0, int n0, int
     mma(af[0], bf[0]);
     interleave<true, 0x100, NRD, NMMA>();
     __builtin_amdgcn_sched_barrier(0);
-    wait_dma_all();
+    wait_dma<(NBUF - 2) * PER>();
     __syncthreads();
-    frags(cur ^ 1, 0, af[0], bf[0]);  // past the last stage: data no one uses
-    dma_stage(cur, kt + 2);           // unconditional: past K every offset is out of range (zeros)
+    frags(nxt, 0, af[0], bf[0]);  // past the last stage: data no one uses
+    dma_stage(cur, kt + NBUF);
     mma(af[1], bf[1]);
     interleave<true, 0x100, NRD, NMMA>();
     __builtin_amdgcn_sched_barrier(0);
+    cur = nxt;
+  }
   }
   wait_dma_all();  // the zero-filling DMAs past K land before the epilogue reuses the buffers
   if (tid < BM) s_sa[tid] = r_sa;
@@ -425,21 +318,16 @@ __device__ __forceinline__ void mainloop_dma(const GemmP& p, int m0, int n0, int
   __syncthreads();
 }
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, bool CONV, int PIPE = 1>
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool CONV, int NBUF, int FD>
 __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const GemmP p) {
-  constexpr bool SCHED = PIPE != 0;
   constexpr int T = WAVES_M * WAVES_N * 64;
   constexpr int WTM = BM / WAVES_M;  // wave tile rows
   constexpr int WTN = BN / WAVES_N;
   constexpr int TM = WTM / 32;
   constexpr int TN = WTN / 32;
-  constexpr int ROWS_PER_PASS = T / 8;  // rows one pass of all threads loads (8 chunks a row)
-  constexpr int A_LD = BM / ROWS_PER_PASS;
-  constexpr int B_LD = BN / ROWS_PER_PASS;
-  static_assert(BM % ROWS_PER_PASS == 0 && BN % ROWS_PER_PASS == 0, "tile/threads");
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile");
 
-  __shared__ __attribute__((aligned(16))) int8_t lds[2 * (BM + BN) * BK];
+  __shared__ __attribute__((aligned(16))) int8_t lds[NBUF * (BM + BN) * BK];
   // Per-tile scales and bias, staged once so the epilogue reads no global memory: on
   // gfx9 stores and loads share one counter, and a load between stores waits for them.
   __shared__ __attribute__((aligned(16))) float s_sa[BM];
@@ -465,17 +353,14 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
   for (int i = 0; i < TM; ++i)
 #pragma unroll
     for (int j = 0; j < TN; ++j) c[i][j] = v16i{};
-  if constexpr (PIPE == 3)
-    mainloop_dma<BM, BN, WAVES_M, WAVES_N, CONV>(p, m0, n0, lds, s_sa, s_sw, s_b, c);
-  else
-    mainloop_regs<BM, BN, WAVES_M, WAVES_N, CONV, PIPE>(p, m0, n0, lds, s_sa, s_sw, s_b, c);
+  mainloop_dma<BM, BN, WAVES_M, WAVES_N, CONV, NBUF, FD>(p, m0, n0, lds, s_sa, s_sw, s_b, c);
 
   // Epilogue, one 32-row slice of the wave tile at a time: the int32 results go through a
   // per-wave LDS patch (exact), come back as four consecutive columns of one row per lane,
   // and leave as 16-byte stores of whole 256-byte row segments. 32x32 result layout:
   // lane l, register r holds row 8*(r/4) + 4*(l/32) + r%4, column l%32.
   constexpr int PITCH = WTN + 8;  // ints; 4*PITCH % 64 == 32 keeps both half-waves' rows apart
-  static_assert(WAVES_M * WAVES_N * 32 * PITCH * 4 <= 2 * (BM + BN) * BK, "epilogue patch");
+  static_assert(WAVES_M * WAVES_N * 32 * PITCH * 4 <= NBUF * (BM + BN) * BK, "epilogue patch");
   static_assert((PITCH * 4) % 16 == 0 && (4 * PITCH) % 64 == 32, "patch pitch");
   int* patch = reinterpret_cast<int*>(lds) + wave * 32 * PITCH;
   constexpr int C4 = WTN / 4;                 // float4 columns per row
@@ -814,10 +699,10 @@ __global__ __launch_bounds__(256) void dwconv_i8_kernel(const int8_t* __restrict
 
 // ---------------------------------------------------------------------------- dispatch
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, bool CONV, int PIPE = 1>
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool CONV, int NBUF, int FD>
 static void launch_tiled(const GemmP& p, hipStream_t st) {
   const int tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
-  gemm_i8_kernel<BM, BN, WAVES_M, WAVES_N, CONV, PIPE><<<tiles, WAVES_M * WAVES_N * 64, 0, st>>>(p);
+  gemm_i8_kernel<BM, BN, WAVES_M, WAVES_N, CONV, NBUF, FD><<<tiles, WAVES_M * WAVES_N * 64, 0, st>>>(p);
 }
 
 // BQ_GEMM_CFG forces one tile configuration (tuning sweeps); unset = the shape rule.
@@ -831,25 +716,16 @@ static int forced_cfg() {
 
 template <bool CONV>
 static void launch_gemm(const GemmP& p, hipStream_t st) {
-  switch (forced_cfg()) {
-    case 1: return launch_tiled<256, 256, 2, 4, CONV>(p, st);
-    case 3: return launch_tiled<256, 256, 2, 2, CONV>(p, st);
-    case 4: return launch_tiled<128, 128, 2, 2, CONV>(p, st);
-    case 5: return launch_tiled<256, 128, 2, 2, CONV>(p, st);
-    case 6: return launch_tiled<128, 256, 2, 2, CONV>(p, st);
-    case 7: return launch_tiled<64, 64, 2, 2, CONV>(p, st);
-    case 8: return launch_tiled<256, 64, 4, 1, CONV>(p, st);
-    case 9: return launch_tiled<256, 256, 2, 4, CONV, 0>(p, st);
-    case 10: return launch_tiled<256, 256, 2, 2, CONV, 0>(p, st);
-    case 11: return launch_tiled<256, 256, 2, 4, CONV, 2>(p, st);
-    case 12: return launch_tiled<256, 256, 2, 2, CONV, 2>(p, st);
-    case 13: return launch_tiled<128, 128, 2, 2, CONV, 2>(p, st);
-    case 21: return launch_tiled<256, 256, 2, 4, CONV, 3>(p, st);
-    case 23: return launch_tiled<256, 256, 2, 2, CONV, 3>(p, st);
-    case 24: return launch_tiled<128, 128, 2, 2, CONV, 3>(p, st);
-    case 25: return launch_tiled<256, 128, 2, 2, CONV, 3>(p, st);
-    case 27: return launch_tiled<64, 64, 2, 2, CONV, 3>(p, st);
-    case 28: return launch_tiled<256, 64, 4, 1, CONV, 3>(p, st);
+  switch (forced_cfg()) {  // <BM, BN, waves M x N, ring depth, fragment distance>
+    case 1: return launch_tiled<256, 256, 2, 4, CONV, 2, 1>(p, st);
+    case 2: return launch_tiled<256, 256, 2, 4, CONV, 2, 2>(p, st);
+    case 3: return launch_tiled<256, 256, 2, 2, CONV, 2, 2>(p, st);
+    case 4: return launch_tiled<128, 128, 2, 2, CONV, 4, 2>(p, st);
+    case 5: return launch_tiled<128, 128, 2, 2, CONV, 2, 2>(p, st);
+    case 6: return launch_tiled<256, 128, 2, 2, CONV, 3, 1>(p, st);
+    case 7: return launch_tiled<64, 64, 2, 2, CONV, 4, 2>(p, st);
+    case 8: return launch_tiled<256, 64, 4, 1, CONV, 3, 1>(p, st);
+    case 9: return launch_tiled<64, 64, 2, 2, CONV, 8, 1>(p, st);
     default: break;
   }
   // The largest tile that still fills the chip (>= 192 / 128 workgroups) without wasting
@@ -857,14 +733,22 @@ static void launch_gemm(const GemmP& p, hipStream_t st) {
   const long long t256 = (long long)((p.M + 255) / 256) * ((p.N + 255) / 256);
   const long long t128 = (long long)((p.M + 127) / 128) * ((p.N + 127) / 128);
   const long long t256x64 = (long long)((p.M + 255) / 256) * ((p.N + 63) / 64);
+  // Ring depth: deep rings keep several stages of a small tile's operands in flight; when
+  // there are more tiles than CUs, a 128x128 tile takes the 2-deep ring instead so that two
+  // workgroups share a CU (64 KB of LDS each). The 256x256 tile's 64 KB stages leave room
+  // for two buffers only.
+  // Small tiles read their fragments two K slices ahead (their MFMA runs are short).
   if (p.N <= 64 && t256x64 >= 128)
-    launch_tiled<256, 64, 4, 1, CONV, 3>(p, st);
+    launch_tiled<256, 64, 4, 1, CONV, 3, 1>(p, st);
   else if (t256 >= 192 && p.N >= 192)
-    launch_tiled<256, 256, 2, 4, CONV, 3>(p, st);
-  else if (t128 >= 128 && p.N >= 96)
-    launch_tiled<128, 128, 2, 2, CONV, 3>(p, st);
-  else
-    launch_tiled<64, 64, 2, 2, CONV, 3>(p, st);
+    launch_tiled<256, 256, 2, 4, CONV, 2, 1>(p, st);
+  else if (t128 >= 128 && p.N >= 96) {
+    if (t128 > 256)
+      launch_tiled<128, 128, 2, 2, CONV, 2, 2>(p, st);
+    else
+      launch_tiled<128, 128, 2, 2, CONV, 4, 2>(p, st);
+  } else
+    launch_tiled<64, 64, 2, 2, CONV, 4, 2>(p, st);
 }
 
 static bool aligned16(const void* q) { return ((uintptr_t)q & 15) == 0; }
