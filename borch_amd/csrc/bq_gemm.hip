@@ -126,7 +126,7 @@ __device__ __forceinline__ void wait_dma() {
 // Main loop with direct-to-LDS loads into a ring of NBUF stage buffers. A stage's LDS image
 // is written by wave-wide DMAs of 8 rows (1 KB) each: lane l covers row 8*band + l/8 and
 // LDS chunk slot l%8, and fetches the global 16-byte chunk that the XOR swizzle maps to that
-// slot, so the LDS layout (and the fragment reads) are those of the register-staged loop.
+// slot, so each 16 bytes land where lds_off() places them for the fragment reads.
 // Stage kt+NBUF is fetched into the buffer stage kt just left, right after the barrier that
 // ends stage kt, and must land by the barrier that ends stage kt+NBUF-1: NBUF-1 stages of
 // MFMAs cover its latency (small tiles, whose stages are short, take deep rings).
@@ -544,31 +544,38 @@ __device__ __forceinline__ int wave_sum(int v) {
 
 template <int MR, int KC, int RPW, int WAVES = GV_WAVES>
 __global__ __launch_bounds__(WAVES * 64) void gemv_i8_kernel(const GemmP p) {
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  constexpr int T = WAVES * 64;
+  constexpr int XCH = MR * KC * 64;          // 16-byte chunks of the (padded) activation rows
+  constexpr int XPT = (XCH + T - 1) / T;     // chunks a thread loads
+  // The activation rows, loaded once per workgroup (not once per wave) and shared from LDS:
+  // row m's chunk c (1 KB, 64 lanes x 16 bytes) at (m * KC + c) * 1024.
+  __shared__ __attribute__((aligned(16))) int8_t xs[MR * KC * 1024];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
   const int row0 = (blockIdx.x * WAVES + wave) * RPW;
-  if (row0 >= p.N) return;
-  const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.W + (size_t)row0 * p.K, (uint32_t)(min(RPW, p.N - row0) * p.K));
+  const int nrows = max(0, min(RPW, p.N - row0));  // 0 for a wave past N: all its loads are out of range
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.W + (size_t)min(row0, p.N) * p.K, (uint32_t)(nrows * p.K));
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, (uint32_t)(p.M * p.K));
+  v4i xr[XPT];
+#pragma unroll
+  for (int i = 0; i < XPT; ++i) {
+    const int ch = tid + i * T;
+    const int m = ch / (KC * 64);
+    const int k = (ch - m * (KC * 64)) * 16;
+    xr[i] = buf_load16(ra, (ch < XCH && m < p.M && k < p.K) ? (uint32_t)(m * p.K + k) : OOB);
+  }
   // Lane j*MR + m stores output (m, row0 + j); its scales and bias are fetched now, ahead
   // of the weight stream, so the tail does not wait on another memory round trip.
   const int my_j = lane / MR, my_m = lane % MR;
   const int my_n = row0 + my_j;
-  const bool writer = lane < RPW * MR && my_n < p.N && my_m < p.M;
+  const bool writer = lane < RPW * MR && my_j < nrows && my_m < p.M;
   float e_sa = 0.f, e_sw = 0.f, e_b = 0.f;
   if (writer) {
     e_sa = p.sa_per_row ? p.sA[my_m] : p.sA[0];
     e_sw = p.sW[my_n];
     e_b = p.bias ? p.bias[my_n] : 0.f;
   }
-  v4i x[MR][KC];
-#pragma unroll
-  for (int m = 0; m < MR; ++m)
-#pragma unroll
-    for (int c = 0; c < KC; ++c) {
-      const int k = c * 1024 + lane * 16;
-      x[m][c] = buf_load16(ra, (m < p.M && k < p.K) ? (uint32_t)(m * p.K + k) : OOB);
-    }
   v4i w[RPW][KC];
 #pragma unroll
   for (int j = 0; j < RPW; ++j)
@@ -577,7 +584,18 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_i8_kernel(const GemmP p) {
       const int k = c * 1024 + lane * 16;
       w[j][c] = buf_load16(rw, k < p.K ? (uint32_t)(j * p.K + k) : OOB);
     }
-  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_sched_barrier(0);  // every load of the wave in flight before anything waits
+#pragma unroll
+  for (int i = 0; i < XPT; ++i) {
+    const int ch = tid + i * T;
+    if (ch < XCH) *reinterpret_cast<v4i*>(xs + ch * 16) = xr[i];
+  }
+  __syncthreads();
+  v4i x[MR][KC];
+#pragma unroll
+  for (int m = 0; m < MR; ++m)
+#pragma unroll
+    for (int c = 0; c < KC; ++c) x[m][c] = *reinterpret_cast<const v4i*>(xs + (m * KC + c) * 1024 + lane * 16);
   int acc[RPW][MR];
 #pragma unroll
   for (int j = 0; j < RPW; ++j)
@@ -623,15 +641,18 @@ static bool launch_gemv_cfg(const GemmP& p, hipStream_t st) {
   return true;
 }
 
+// One weight row per wave (the most rows in flight per byte of activation); four waves a
+// workgroup for one or two activation rows, eight for three or four (measured).
 template <int MR>
 static bool launch_gemv(const GemmP& p, hipStream_t st) {
   switch (forced_gemv()) {
     case 1: return launch_gemv_cfg<MR, 1, 8>(p, st);
-    case 2: return launch_gemv_cfg<MR, 4, 8>(p, st);
+    case 2: return launch_gemv_cfg<MR, 2, 8>(p, st);
     case 3: return launch_gemv_cfg<MR, 2, 4>(p, st);
     case 4: return launch_gemv_cfg<MR, 1, 4>(p, st);
-    case 5: return launch_gemv_cfg<MR, 4, 4>(p, st);
-    default: return launch_gemv_cfg<MR, 2, 8>(p, st);
+    default:
+      if constexpr (MR <= 2) return launch_gemv_cfg<MR, 1, 4>(p, st);
+      else return launch_gemv_cfg<MR, 1, 8>(p, st);
   }
 }
 

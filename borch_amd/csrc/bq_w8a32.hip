@@ -26,17 +26,24 @@ __device__ __forceinline__ float wave_fsum(float v) {
 }
 
 constexpr int WA_WAVES = 8;
+constexpr int WA_XLDS = 16384;  // f32 activation elements a workgroup stages in LDS (64 KB)
 
-template <int KC, int RPW>
+// XL: the activation rows (M rows of KC * 1024 floats, K padded to whole 1 KB weight chunks)
+// are staged in LDS once per workgroup and every wave reads them from there; otherwise each
+// wave reads them from L2.
+template <int KC, int RPW, bool XL>
 __global__ __launch_bounds__(WA_WAVES * 64) void gemv_w8a32_kernel(const float* __restrict__ x, const int8_t* W,
                                                                    int M, int N, int K, const float* __restrict__ sW,
                                                                    const float* __restrict__ bias, int act,
                                                                    float* __restrict__ out) {
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  __shared__ __attribute__((aligned(16))) float xs[XL ? WA_XLDS : 4];
+  constexpr int T = WA_WAVES * 64;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
   const int row0 = (blockIdx.x * WA_WAVES + wave) * RPW;
-  if (row0 >= N) return;
-  const __amdgpu_buffer_rsrc_t rw = w_rsrc(W + (size_t)row0 * K, (uint32_t)(min(RPW, N - row0) * K));
+  const int nrows = max(0, min(RPW, N - row0));  // 0 past N: every weight load out of range
+  const __amdgpu_buffer_rsrc_t rw = w_rsrc(W + (size_t)min(row0, N) * K, (uint32_t)(nrows * K));
   v4i w[RPW][KC];
 #pragma unroll
   for (int j = 0; j < RPW; ++j)
@@ -47,8 +54,22 @@ __global__ __launch_bounds__(WA_WAVES * 64) void gemv_w8a32_kernel(const float* 
     }
   float sc[RPW];
 #pragma unroll
-  for (int j = 0; j < RPW; ++j) sc[j] = row0 + j < N ? sW[row0 + j] : 0.f;
+  for (int j = 0; j < RPW; ++j) sc[j] = j < nrows ? sW[row0 + j] : 0.f;
   __builtin_amdgcn_sched_barrier(0);
+  if constexpr (XL) {
+    // Row m's float4 number c*256 + l*4 + t (the t-th of lane l's four in 1 KB chunk c) is
+    // stored at float4 (m*KC + c)*256 + t*64 + l, so the four reads of a chunk each take
+    // 64 consecutive float4s across the wave (no bank conflicts).
+    const int k4 = K / 4;
+    const int n4 = M * k4;
+    for (int i = tid; i < n4; i += T) {
+      const int m = i / k4;
+      const int r = i - m * k4;
+      const int dst = (m * KC + (r >> 8)) * 256 + (r & 3) * 64 + ((r >> 2) & 63);
+      reinterpret_cast<float4*>(xs)[dst] = reinterpret_cast<const float4*>(x)[i];
+    }
+    __syncthreads();
+  }
   for (int m = 0; m < M; ++m) {
     float acc[RPW];
 #pragma unroll
@@ -57,11 +78,12 @@ __global__ __launch_bounds__(WA_WAVES * 64) void gemv_w8a32_kernel(const float* 
     for (int c = 0; c < KC; ++c) {
       const int k = c * 1024 + lane * 16;
       if (k >= K) break;
-      const float4* xp = reinterpret_cast<const float4*>(x + (size_t)m * K + k);
+      const float4* xp = XL ? reinterpret_cast<const float4*>(xs) + (m * KC + c) * 256 + lane
+                            : reinterpret_cast<const float4*>(x + (size_t)m * K + k);
       float xv[16];
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        const float4 v = xp[t];
+        const float4 v = xp[XL ? t * 64 : t];
         xv[t * 4] = v.x; xv[t * 4 + 1] = v.y; xv[t * 4 + 2] = v.z; xv[t * 4 + 3] = v.w;
       }
 #pragma unroll
@@ -76,7 +98,7 @@ __global__ __launch_bounds__(WA_WAVES * 64) void gemv_w8a32_kernel(const float* 
     for (int j = 0; j < RPW; ++j) {
       const float s = wave_fsum(acc[j]);
       const int n = row0 + j;
-      if (lane == 0 && n < N) {
+      if (lane == 0 && j < nrows) {
         float v = bias ? __fadd_rn(s, bias[n]) : s;
         if (act == BQ_ACT_RELU) v = v > 0.f ? v : 0.f;
         else if (act == BQ_ACT_SILU) v = silu(v);
@@ -124,10 +146,18 @@ int bq_gemv_w8a32(const float* x, const int8_t* W, int64_t M, int64_t N, int64_t
   const unsigned grid = (unsigned)((N + WA_WAVES * RPW - 1) / (WA_WAVES * RPW));
   hipStream_t st = (hipStream_t)stream;
   const int m = (int)M, n = (int)N, k = (int)K;
-  if (K <= 1024) gemv_w8a32_kernel<1, RPW><<<grid, WA_WAVES * 64, 0, st>>>(x, W, m, n, k, sW, bias, act, out);
-  else if (K <= 2048) gemv_w8a32_kernel<2, RPW><<<grid, WA_WAVES * 64, 0, st>>>(x, W, m, n, k, sW, bias, act, out);
-  else if (K <= 4096) gemv_w8a32_kernel<4, RPW><<<grid, WA_WAVES * 64, 0, st>>>(x, W, m, n, k, sW, bias, act, out);
-  else gemv_w8a32_kernel<8, RPW><<<grid, WA_WAVES * 64, 0, st>>>(x, W, m, n, k, sW, bias, act, out);
+  const int64_t kc = K <= 1024 ? 1 : K <= 2048 ? 2 : K <= 4096 ? 4 : 8;  // the kernel's KC
+  if (M * kc * 1024 <= WA_XLDS) {
+    if (K <= 1024) gemv_w8a32_kernel<1, RPW, true><<<grid, WA_WAVES * 64, 0, st>>>(x, W, m, n, k, sW, bias, act, out);
+    else if (K <= 2048) gemv_w8a32_kernel<2, RPW, true><<<grid, WA_WAVES * 64, 0, st>>>(x, W, m, n, k, sW, bias, act, out);
+    else if (K <= 4096) gemv_w8a32_kernel<4, RPW, true><<<grid, WA_WAVES * 64, 0, st>>>(x, W, m, n, k, sW, bias, act, out);
+    else gemv_w8a32_kernel<8, RPW, true><<<grid, WA_WAVES * 64, 0, st>>>(x, W, m, n, k, sW, bias, act, out);
+  } else {
+    if (K <= 1024) gemv_w8a32_kernel<1, RPW, false><<<grid, WA_WAVES * 64, 0, st>>>(x, W, m, n, k, sW, bias, act, out);
+    else if (K <= 2048) gemv_w8a32_kernel<2, RPW, false><<<grid, WA_WAVES * 64, 0, st>>>(x, W, m, n, k, sW, bias, act, out);
+    else if (K <= 4096) gemv_w8a32_kernel<4, RPW, false><<<grid, WA_WAVES * 64, 0, st>>>(x, W, m, n, k, sW, bias, act, out);
+    else gemv_w8a32_kernel<8, RPW, false><<<grid, WA_WAVES * 64, 0, st>>>(x, W, m, n, k, sW, bias, act, out);
+  }
   return check_launch(what);
 }
 
