@@ -11,7 +11,7 @@
  *
  * Arithmetic (one rule for weights and activations):
  *   s = float32(max|v| / 127)                 correctly rounded
- *   q = clip(rint(f64(v) / f64(s)), -127, 127) exact quotient, round half to even
+ *   q = clip(rint(v / s), -127, 127)          of the exact quotient, round half to even
  *   s == 0 (all-zero row / tensor)  ->  q = 0
  *   acc = sum_k qa * qw                        exact int32
  *   y = ((f32(acc) * sA) * sW[n]) + bias[n], then + residual, then the activation,
@@ -117,7 +117,7 @@ int bq_conv2d_i8_nhwc(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t 
                       bq_stream_t stream);
 
 /* bq_conv2d_i8_nhwc that also writes the output's int8 twin with a calibrated scale:
- * q_out int8 [N, OH, OW, O] = clip(rint(f64(y) / f64(s_out[0])), +-127) of the final f32 y
+ * q_out int8 [N, OH, OW, O] = clip(rint(y / s_out[0]), +-127) (exact quotient, half to even) of the final f32 y
  * (after residual and activation), the next conv's input with no quantize pass.
  * O % 16 == 0 (the twin is then the next layer's padded NHWC layout). Replaces the
  * quantOut store of convForwardInt8 / sumSplitsConv (borch-ts/src/kernels.ts:2177-2190,
