@@ -169,6 +169,16 @@ def bench_models(dev, stream, steps):
             out[key]["int8_static_graph_ms"] = round(s_ms, 4)
             out[key]["static_max_abs_diff_vs_f32_rel"] = round(float((ys - ref).abs().max() / ref.abs().max()), 5)
             del c2, ys
+            # the reference's own conv rule (convInt8Fits): 13 of the 20 convs int8, the rest f32
+            bt.clear_int8(model)
+            n_ref = bt.quantize_for_int8(model, rule="reference")
+            c3 = bt.compiled(model, int8=False, graph=True, fuse=False)
+            with torch.no_grad():
+                c3(x)
+                r_ms = time_events(lambda i: c3(x), steps, stream)
+            out[key]["int8_reference_rule_graph_ms"] = round(r_ms, 4)
+            out[key]["int8_layers_reference_rule"] = n_ref
+            del c3
         log(f"{key}: {out[key]}")
         del model, c, x, y, ref
         torch.cuda.empty_cache()

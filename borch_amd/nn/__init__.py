@@ -140,11 +140,39 @@ class Conv2d(_tnn.Module):
             return None
         return f"groups={self.groups} (only 1 or depthwise)"
 
-    def quantize_int8(self) -> bool:
+    def reference_rule_refusal(self):
+        """Why the reference's int8 conv would not take this layer (None if it would): the
+        shape rules of its ``convInt8Fits`` (borch-ts/src/kernels.ts:2096-2103) — 2-D,
+        groups 1, dilation 1, stride 1, kernel at most 3, input channels in 32s, output
+        channels in 16s. Its band and workgroup-storage limits (WebGPU tiling constraints
+        with no counterpart on this device) are not applied."""
+        refusal = self.int8_refusal()
+        if refusal is not None:
+            return refusal
+        stride, _ = self._geometry()
+        kh, kw = _pair(self.kernel_size)
+        if self.groups != 1:
+            return f"groups={self.groups}"
+        if stride != 1:
+            return f"stride {stride}"
+        if kh > 3 or kw > 3:
+            return f"kernel {kh}x{kw} > 3"
+        if self.in_channels % 32:
+            return f"in_channels={self.in_channels} not a multiple of 32"
+        if self.out_channels % 16:
+            return f"out_channels={self.out_channels} not a multiple of 16"
+        return None
+
+    def quantize_int8(self, rule: str = "all") -> bool:
         """Packs the weight once per output channel (quant.ts:80-103's scale rule) where
         the kernels take the layer; returns False (the layer stays f32) otherwise, as
-        borch-ts/src/nn.ts:967-980 does."""
-        if self.int8_refusal() is not None:
+        borch-ts/src/nn.ts:967-980 does. ``rule="reference"`` takes only the layers the
+        reference's conv kernel takes (``reference_rule_refusal``), for comparison."""
+        if rule not in ("all", "reference"):
+            raise ValueError(f"rule must be 'all' or 'reference', not {rule!r}")
+        refusal = self.reference_rule_refusal() if rule == "reference" else self.int8_refusal()
+        self.int8_why = refusal  # why the last quantize_int8 left this layer f32 (int8_report)
+        if refusal is not None:
             return False
         require_device(self.weight.device)
         with torch.no_grad():
@@ -232,11 +260,16 @@ def _int8_layers(model):
             yield name, mod
 
 
-def quantize_for_int8(model, linear: bool = True, conv: bool = True, weight_only: bool = False) -> int:
+def quantize_for_int8(model, linear: bool = True, conv: bool = True, weight_only: bool = False,
+                      rule: str = "all") -> int:
     """Every Linear / Conv2d of ``model`` the int8 kernels take, quantized once; returns
     how many took it (borch-ts/src/nn.ts:6770-6780). Refused by name where the device has
     no int8 kernels (nn.ts:6771-6773): the path is an accuracy trade a caller asks for and
-    must not silently become the f32 forward."""
+    must not silently become the f32 forward. ``rule="reference"`` restricts convs to the
+    shapes the reference's int8 conv takes (13 of CIFAR ResNet-18's 20), for comparison
+    with its published numbers; the default takes every conv this library can."""
+    if rule not in ("all", "reference"):
+        raise ValueError(f"rule must be 'all' or 'reference', not {rule!r}")
     layers = list(_int8_layers(model))
     dev = next((m.weight.device for _, m in layers), None)
     if dev is not None:
@@ -250,7 +283,7 @@ def quantize_for_int8(model, linear: bool = True, conv: bool = True, weight_only
         if isinstance(mod, Linear) and linear:
             taken += bool(mod.quantize_int8(weight_only))
         elif isinstance(mod, Conv2d) and conv:
-            taken += bool(mod.quantize_int8())
+            taken += bool(mod.quantize_int8(rule))
     return taken
 
 
@@ -298,7 +331,7 @@ def int8_report(model):
     rows = []
     for name, mod in _int8_layers(model):
         kind = type(mod).__name__
-        why = None if isinstance(mod, Linear) else mod.int8_refusal()
+        why = None if isinstance(mod, Linear) else (getattr(mod, "int8_why", None) or mod.int8_refusal())
         rows.append((name, kind, mod.int8 is not None, why))
     return rows
 

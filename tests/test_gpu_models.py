@@ -130,6 +130,29 @@ def test_c3_resnet18(dev):
     assert gap < 0.05
 
 
+def test_c3_resnet18_reference_rule(dev):
+    say("C3 ResNet-18 b16 under the reference's conv rule (13 of 20 convs int8)")
+    model = nets.build("resnet18", seed=0, device=dev)
+    xt = torch.from_numpy(WL.c3_input(16, 0)).to(dev)
+    with torch.no_grad():
+        f32_logits = n(model(xt))
+    assert bt.quantize_for_int8(model, rule="reference") == 13
+    convs = [m for m in model.modules() if isinstance(m, bt.nn.Conv2d)]
+    f32_convs = [m for m in convs if m.int8 is None]
+    assert len(f32_convs) == 7 and all(m.reference_rule_refusal() is not None for m in f32_convs)
+    recs, hooks = capture(model)
+    with torch.no_grad():
+        logits = n(model(xt))
+    for h in hooks:
+        h.remove()
+    assert len(recs) == 13
+    for rec in recs:
+        check_layer(*rec)
+    gap = np.abs(logits - f32_logits).max() / np.abs(f32_logits).max()
+    say(f"  int8 (reference rule) vs f32 logits: max |diff| / max |logit| = {gap:.3g}")
+    assert gap < 0.05
+
+
 # --------------------------------------------------------------------------- C4
 
 def test_c4_efficientnet_b0_layers(dev):

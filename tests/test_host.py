@@ -1,0 +1,49 @@
+"""Host-side logic of the int8 surface (no GPU): which layers the int8 kernels take, under
+this library's rule and under the reference's (borch-ts/src/kernels.ts:2096-2103)."""
+import pytest
+import torch
+
+import borch_amd as bt
+from borch_amd import nets
+from borch_amd.nn import Conv2d, _int8_layers
+
+
+def _convs(model):
+    return [m for _, m in _int8_layers(model) if isinstance(m, Conv2d)]
+
+
+def test_resnet18_layer_rules():
+    model = nets.build("resnet18", seed=0, device="cpu")
+    convs = _convs(model)
+    assert len(convs) == 20
+    assert sum(c.int8_refusal() is None for c in convs) == 20
+    # The reference's convInt8Fits takes 13 of the 20: not the stem (C = 3), the three
+    # stride-2 3x3 convs or the three stride-2 1x1 downsamples.
+    refused = [c.reference_rule_refusal() for c in convs]
+    assert sum(r is None for r in refused) == 13
+    assert sorted(r for r in refused if r is not None) == ["in_channels=3 not a multiple of 32"] + ["stride 2"] * 6
+
+
+def test_efficientnet_depthwise_not_in_reference_rule():
+    model = nets.build("efficientnet_b0", seed=0, device="cpu")
+    convs = _convs(model)
+    dw = [c for c in convs if c.groups != 1]
+    assert dw and all(c.int8_refusal() is None for c in dw)
+    assert all(c.reference_rule_refusal() == f"groups={c.groups}" for c in dw)
+
+
+def test_reference_rule_refusals_by_name():
+    assert Conv2d(3, 64, 3, padding=1).reference_rule_refusal() == "in_channels=3 not a multiple of 32"
+    assert Conv2d(64, 128, 3, stride=2, padding=1).reference_rule_refusal() == "stride 2"
+    assert Conv2d(64, 64, 5, padding=2).reference_rule_refusal() == "kernel 5x5 > 3"
+    assert Conv2d(64, 40, 1).reference_rule_refusal() == "out_channels=40 not a multiple of 16"
+    assert Conv2d(64, 64, 3, padding=1, groups=64).reference_rule_refusal() == "groups=64"
+    assert Conv2d(64, 64, 3, padding=1, dilation=2).reference_rule_refusal().startswith("stride/padding")
+    assert Conv2d(64, 64, 3, padding=1).reference_rule_refusal() is None
+
+
+def test_rule_argument_checked():
+    with pytest.raises(ValueError, match="rule must be"):
+        bt.quantize_for_int8(torch.nn.Sequential(), rule="fast")
+    with pytest.raises(ValueError, match="rule must be"):
+        Conv2d(64, 64, 3, padding=1).quantize_int8("fast")
