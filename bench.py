@@ -139,12 +139,12 @@ def bench_models(dev, stream, steps):
     import borch_amd as bt
     from borch_amd import nets, workloads as WL
     out = {}
-    cases = [("resnet18_b16", "resnet18", lambda: WL.c3_input(16, 0)),
-             ("efficientnet_b0_b64", "efficientnet_b0", lambda: WL.c4_input(64, 0)),
-             ("vit_b16_b32", "vit_b16", lambda: WL.c5_input(32, 197, 768, 0))]
-    for key, name, make in cases:
+    cases = [("resnet18_b16", "resnet18", lambda s: WL.c3_input(16, s)),
+             ("efficientnet_b0_b64", "efficientnet_b0", lambda s: WL.c4_input(64, s)),
+             ("vit_b16_b32", "vit_b16", lambda s: WL.c5_input(32, 197, 768, s))]
+    for key, name, make_seeded in cases:
         model = nets.build(name, seed=0, device=dev)
-        x = torch.from_numpy(make()).to(dev)
+        x = torch.from_numpy(make_seeded(0)).to(dev)
         with torch.no_grad():
             f32_ms = time_events(lambda i: model(x), 3, stream)
             f32_ms = time_events(lambda i: model(x), steps, stream)
@@ -158,9 +158,10 @@ def bench_models(dev, stream, steps):
         out[key] = {"int8_graph_ms": round(g_ms, 4), "int8_eager_ms": round(eager_ms, 4),
                     "f32_ms": round(f32_ms, 4), "int8_layers": c.int8_layers,
                     "max_abs_diff_vs_f32_rel": round(gap, 5)}
-        if name == "resnet18":
-            # calibrated static scales + int8 twins (calibrate_int8): one quantize pass a forward
-            calib = [torch.from_numpy(WL.c3_input(16, s)).to(dev) for s in (11, 12)]
+        if name in ("resnet18", "efficientnet_b0"):
+            # calibrated static scales + int8 twins (calibrate_int8): no max pass, and no
+            # quantize pass where the producer writes the next layer's int8 input
+            calib = [torch.from_numpy(make_seeded(s)).to(dev) for s in (11, 12)]
             bt.calibrate_int8(model, calib)
             c2 = bt.compiled(model, int8=False, graph=True, fuse=False)
             with torch.no_grad():
@@ -168,7 +169,8 @@ def bench_models(dev, stream, steps):
                 s_ms = time_events(lambda i: c2(x), steps, stream)
             out[key]["int8_static_graph_ms"] = round(s_ms, 4)
             out[key]["static_max_abs_diff_vs_f32_rel"] = round(float((ys - ref).abs().max() / ref.abs().max()), 5)
-            del c2, ys
+            del c2, ys, calib
+        if name == "resnet18":
             # the reference's own conv rule (convInt8Fits): 13 of the 20 convs int8, the rest f32
             bt.clear_int8(model)
             n_ref = bt.quantize_for_int8(model, rule="reference")

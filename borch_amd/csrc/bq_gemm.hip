@@ -718,6 +718,99 @@ __global__ __launch_bounds__(256) void dwconv_i8_kernel(const int8_t* __restrict
   }
 }
 
+// Register-blocked depthwise conv for square KS x KS filters at stride S (the shapes of
+// EfficientNet-style networks). One thread: OWB consecutive output pixels of one output row
+// for CPT consecutive channels. Each input column the OWB outputs need is loaded and
+// unpacked once and reused by every output whose window covers it (stride 1: NCOL = OWB +
+// KS - 1 columns instead of OWB * KS); the kernel row's weights are unpacked once per row.
+// All index arithmetic is 32-bit (the host checks the ranges). Same arithmetic as
+// dwconv_i8_kernel: exact int32 tap sums, then the shared dequant epilogue.
+template <int KS, int S, int CPT, int OWB>
+__global__ __launch_bounds__(256) void dwconv_blk_kernel(const int8_t* __restrict__ x, int H, int Wd, int C,
+                                                         const int8_t* __restrict__ w, int pad, int OH, int OW,
+                                                         int rows, const float* __restrict__ sA,
+                                                         const float* __restrict__ sW, const float* __restrict__ bias,
+                                                         int act, float* __restrict__ out, int32_t* __restrict__ acc) {
+  typedef int vw __attribute__((ext_vector_type(CPT / 4)));
+  constexpr int NCOL = (OWB - 1) * S + KS;
+  const int CG = C / CPT;
+  const int items = ((OW + OWB - 1) / OWB) * CG;
+  const int total = rows * items;
+  const float sa = sA[0];
+  for (int g = blockIdx.x * 256 + threadIdx.x; g < total; g += gridDim.x * 256) {
+    const int row = g / items;  // n * OH + oh
+    const int it = g - row * items;
+    const int owb = it / CG;
+    const int cg = it - owb * CG;
+    const int n = row / OH;
+    const int oh = row - n * OH;
+    const int c = cg * CPT;
+    const int ow0 = owb * OWB;
+    const int iw0 = ow0 * S - pad;
+    int a[OWB][CPT];
+#pragma unroll
+    for (int o = 0; o < OWB; ++o)
+#pragma unroll
+      for (int j = 0; j < CPT; ++j) a[o][j] = 0;
+#pragma unroll 1
+    for (int kh = 0; kh < KS; ++kh) {
+      const int ih = oh * S - pad + kh;
+      if ((unsigned)ih >= (unsigned)H) continue;
+      const int8_t* xrow = x + ((size_t)(n * H + ih) * Wd) * C + c;
+      int wr[KS][CPT];
+#pragma unroll
+      for (int kw = 0; kw < KS; ++kw) {
+        const vw wv = *reinterpret_cast<const vw*>(w + (size_t)(kh * KS + kw) * C + c);
+#pragma unroll
+        for (int q = 0; q < CPT / 4; ++q)
+#pragma unroll
+          for (int b = 0; b < 4; ++b) wr[kw][q * 4 + b] = (int)(int8_t)(((uint32_t)wv[q] >> (8 * b)) & 0xff);
+      }
+#pragma unroll
+      for (int j = 0; j < NCOL; ++j) {
+        const int iw = iw0 + j;
+        vw xv = {};
+        if ((unsigned)iw < (unsigned)Wd) xv = *reinterpret_cast<const vw*>(xrow + (size_t)iw * C);
+        int xe[CPT];
+#pragma unroll
+        for (int q = 0; q < CPT / 4; ++q)
+#pragma unroll
+          for (int b = 0; b < 4; ++b) xe[q * 4 + b] = (int)(int8_t)(((uint32_t)xv[q] >> (8 * b)) & 0xff);
+#pragma unroll
+        for (int o = 0; o < OWB; ++o) {
+          const int kw = j - o * S;
+          if (kw >= 0 && kw < KS) {
+#pragma unroll
+            for (int cc = 0; cc < CPT; ++cc) a[o][cc] += xe[cc] * wr[kw][cc];
+          }
+        }
+      }
+    }
+    float swv[CPT], bv[CPT];
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+      swv[j] = sW[c + j];
+      bv[j] = bias ? bias[c + j] : 0.f;
+    }
+#pragma unroll
+    for (int o = 0; o < OWB; ++o) {
+      if (ow0 + o >= OW) break;
+      const size_t idx = ((size_t)row * OW + ow0 + o) * C + c;
+#pragma unroll
+      for (int q = 0; q < CPT / 4; ++q) {
+        float v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          v[j] = dequant_one(a[o][q * 4 + j], sa, swv[q * 4 + j], bv[q * 4 + j], bias != nullptr, 0.f, false, act);
+        *reinterpret_cast<float4*>(out + idx + q * 4) = make_float4(v[0], v[1], v[2], v[3]);
+        if (acc)
+          *reinterpret_cast<int4*>(acc + idx + q * 4) =
+              make_int4(a[o][q * 4], a[o][q * 4 + 1], a[o][q * 4 + 2], a[o][q * 4 + 3]);
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------- dispatch
 
 template <int BM, int BN, int WAVES_M, int WAVES_N, bool CONV, int NBUF, int FD>
@@ -747,20 +840,29 @@ static void launch_gemm(const GemmP& p, hipStream_t st) {
     case 7: return launch_tiled<64, 64, 2, 2, CONV, 4, 2>(p, st);
     case 8: return launch_tiled<256, 64, 4, 1, CONV, 3, 1>(p, st);
     case 9: return launch_tiled<64, 64, 2, 2, CONV, 8, 1>(p, st);
+    case 10: return launch_tiled<64, 64, 2, 2, CONV, 2, 2>(p, st);
+    case 11: return launch_tiled<128, 64, 4, 1, CONV, 2, 1>(p, st);
+    case 12: return launch_tiled<128, 32, 4, 1, CONV, 2, 1>(p, st);
+    case 13: return launch_tiled<256, 64, 4, 1, CONV, 2, 1>(p, st);
+    case 14: return launch_tiled<128, 64, 4, 1, CONV, 3, 1>(p, st);
     default: break;
   }
-  // The largest tile that still fills the chip (>= 192 / 128 workgroups) without wasting
-  // most of its columns; narrow outputs (N <= 64) take a tall 256x64 tile.
+  // Narrow outputs (N <= 64: 1x1 convs of mobile networks, the stem, early ResNet layers)
+  // take small-LDS tiles that fit several workgroups per CU (measured 2-2.5x over a 256x64
+  // tile at K <= 240 and 5-15% at K = 2304-4096). Otherwise the largest tile that still
+  // fills the chip (>= 192 / 128 workgroups) without wasting most of its columns.
+  // Ring depth: deep rings keep several stages of a small tile's operands in flight; when
+  // there are more tiles than CUs, a small tile takes the 2-deep ring instead so that
+  // several workgroups share a CU. The 256x256 tile's 64 KB stages leave room for two
+  // buffers only. Small tiles read their fragments two K slices ahead (short MFMA runs).
   const long long t256 = (long long)((p.M + 255) / 256) * ((p.N + 255) / 256);
   const long long t128 = (long long)((p.M + 127) / 128) * ((p.N + 127) / 128);
-  const long long t256x64 = (long long)((p.M + 255) / 256) * ((p.N + 63) / 64);
-  // Ring depth: deep rings keep several stages of a small tile's operands in flight; when
-  // there are more tiles than CUs, a 128x128 tile takes the 2-deep ring instead so that two
-  // workgroups share a CU (64 KB of LDS each). The 256x256 tile's 64 KB stages leave room
-  // for two buffers only.
-  // Small tiles read their fragments two K slices ahead (their MFMA runs are short).
-  if (p.N <= 64 && t256x64 >= 128)
-    launch_tiled<256, 64, 4, 1, CONV, 3, 1>(p, st);
+  const long long t128x32 = (long long)((p.M + 127) / 128) * ((p.N + 31) / 32);
+  const long long t64 = (long long)((p.M + 63) / 64) * ((p.N + 63) / 64);
+  if (p.N <= 32 && t128x32 >= 128)
+    launch_tiled<128, 32, 4, 1, CONV, 2, 1>(p, st);
+  else if (p.N <= 64 && t64 > 256)
+    launch_tiled<64, 64, 2, 2, CONV, 2, 2>(p, st);
   else if (t256 >= 192 && p.N >= 192)
     launch_tiled<256, 256, 2, 4, CONV, 2, 1>(p, st);
   else if (t128 >= 128 && p.N >= 96) {
@@ -895,15 +997,45 @@ int bq_dwconv_i8_nhwc(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t 
     return set_error(BQ_ERR_ARG, "%s: misaligned pointer", what);
   if (act < BQ_ACT_NONE || act > BQ_ACT_SILU) return set_error(BQ_ERR_ARG, "%s: bad activation %d", what, act);
   const bool wide = (C % 8 == 0) && ((uintptr_t)x & 7) == 0 && ((uintptr_t)w & 7) == 0;
+  hipStream_t st = (hipStream_t)stream;
+  // Square 3x3 / 5x5 filters at stride 1 or 2: the register-blocked kernel (32-bit indices).
+  if (KH == KW && (KH == 3 || KH == 5) && (stride == 1 || stride == 2) && N * OH * OW * C < ((int64_t)1 << 31)) {
+    const int rows = (int)(N * OH);
+    const int cpt = wide ? 8 : 4;
+    auto launch = [&](auto kern, int owb) {
+      const int64_t items = (OW + owb - 1) / owb * (C / cpt);
+      int64_t blocks = (rows * items + 255) / 256;
+      if (blocks > 65536) blocks = 65536;
+      kern<<<(unsigned)blocks, 256, 0, st>>>(x, (int)H, (int)W, (int)C, w, (int)pad, (int)OH, (int)OW, rows, sA, sW,
+                                             bias, act, out, acc);
+    };
+    const int key = (int)KH * 10 + (int)stride;
+    if (wide) {
+      switch (key) {
+        case 31: launch(dwconv_blk_kernel<3, 1, 8, 4>, 4); break;
+        case 32: launch(dwconv_blk_kernel<3, 2, 8, 4>, 4); break;
+        case 51: launch(dwconv_blk_kernel<5, 1, 8, 4>, 4); break;
+        default: launch(dwconv_blk_kernel<5, 2, 8, 2>, 2); break;
+      }
+    } else {
+      switch (key) {
+        case 31: launch(dwconv_blk_kernel<3, 1, 4, 4>, 4); break;
+        case 32: launch(dwconv_blk_kernel<3, 2, 4, 4>, 4); break;
+        case 51: launch(dwconv_blk_kernel<5, 1, 4, 4>, 4); break;
+        default: launch(dwconv_blk_kernel<5, 2, 4, 2>, 2); break;
+      }
+    }
+    return check_launch(what);
+  }
   const int64_t total = N * OH * OW * (C / (wide ? 8 : 4));
   int64_t blocks = (total + 255) / 256;
   if (blocks > 65536) blocks = 65536;
   if (wide)
-    dwconv_i8_kernel<8><<<(unsigned)blocks, 256, 0, (hipStream_t)stream>>>(
+    dwconv_i8_kernel<8><<<(unsigned)blocks, 256, 0, st>>>(
         x, (int)N, (int)H, (int)W, (int)C, w, (int)KH, (int)KW, (int)stride, (int)pad, (int)OH, (int)OW, sA, sW,
         bias, act, out, acc);
   else
-    dwconv_i8_kernel<4><<<(unsigned)blocks, 256, 0, (hipStream_t)stream>>>(
+    dwconv_i8_kernel<4><<<(unsigned)blocks, 256, 0, st>>>(
         x, (int)N, (int)H, (int)W, (int)C, w, (int)KH, (int)KW, (int)stride, (int)pad, (int)OH, (int)OW, sA, sW,
         bias, act, out, acc);
   return check_launch(what);

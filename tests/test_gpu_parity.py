@@ -223,8 +223,11 @@ def test_conv2d(dev, N, C, H, O_, k, stride, pad):
         assert_f32(n(y), y_o)
 
 
+# 3x3 / 5x5 at stride 1 / 2 take the register-blocked kernel (8 or 4 channels a thread;
+# output widths that are not a multiple of its pixel block); 7x7 and the rest the generic one.
 DW_CASES = [(2, 32, 16, 3, 1, 1), (2, 96, 15, 3, 2, 1), (2, 144, 14, 5, 1, 2), (2, 240, 13, 5, 2, 2),
-            (1, 6, 7, 3, 1, 1), (4, 1152, 7, 5, 1, 2)]
+            (1, 6, 7, 3, 1, 1), (4, 1152, 7, 5, 1, 2), (2, 12, 9, 3, 2, 1), (1, 20, 11, 5, 1, 2),
+            (3, 40, 10, 3, 1, 0), (1, 16, 10, 7, 1, 3), (1, 24, 9, 5, 2, 1)]
 
 
 @pytest.mark.parametrize("N,C,H,k,stride,pad", DW_CASES)
