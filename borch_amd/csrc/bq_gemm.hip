@@ -46,6 +46,9 @@ struct GemmP {
 };
 
 constexpr int BK = 128;  // bytes of K per LDS stage: one cache line per row
+// The largest K whose int32 sum of products is exact for any int8 operands in [-127, 127]:
+// K * 127^2 <= 2^31 - 1.
+constexpr int KMAX_EXACT = 133152;
 
 // Buffer resources: raw (stride 0) descriptors whose range check returns zero for any
 // 16-byte load at or past `bytes` — the tile edges (rows past M or N, the K tail, conv
@@ -117,6 +120,9 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, u
 #pragma clang diagnostic pop
 }
 __device__ __forceinline__ void wait_dma_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// A barrier orders LDS stores, not loads still in flight: before a barrier after which a
+// buffer this wave read is refilled, its reads must have returned.
+__device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 template <int N>
 __device__ __forceinline__ void wait_dma() {
   static_assert(N >= 0 && N <= 63, "vmcnt range");
@@ -131,8 +137,9 @@ __device__ __forceinline__ void wait_dma() {
 // ends stage kt, and must land by the barrier that ends stage kt+NBUF-1: NBUF-1 stages of
 // MFMAs cover its latency (small tiles, whose stages are short, take deep rings).
 template <int BM, int BN, int WAVES_M, int WAVES_N, bool CONV, int NBUF, int FD>
-__device__ __forceinline__ void mainloop_dma(const GemmP& p, int m0, int n0, int8_t* lds, float* s_sa, float* s_sw,
-                                             float* s_b, v16i (&c)[BM / WAVES_M / 32][BN / WAVES_N / 32]) {
+__device__ __forceinline__ void mainloop_dma(const GemmP& p, int m0, int n0, int kt0, int KT, int8_t* lds,
+                                             float* s_sa, float* s_sw, float* s_b,
+                                             v16i (&c)[BM / WAVES_M / 32][BN / WAVES_N / 32]) {
   constexpr int WAVES = WAVES_M * WAVES_N;
   constexpr int T = WAVES * 64;
   constexpr int WTM = BM / WAVES_M;
@@ -197,9 +204,12 @@ __device__ __forceinline__ void mainloop_dma(const GemmP& p, int m0, int n0, int
 #pragma unroll
   for (int i = 0; i < B_DMA; ++i) b_row[i] = (uint32_t)((i * BAND + drow) * p.K);
 
+  // Stages kt0 .. kt0+KT-1 of K (a split-K slice, or all of K); past them every offset is
+  // out of range and reads zeros.
+  const int kend = min(p.K, (kt0 + KT) * BK);
   auto dma_stage = [&](int buf, int kt) {
-    const int k0 = kt * BK + dch * 16;
-    const bool kin = k0 < p.K;
+    const int k0 = (kt0 + kt) * BK + dch * 16;
+    const bool kin = k0 < kend;
     const uint32_t am0 = lds_base + (uint32_t)(buf * (BM + BN) * BK + wv * 1024);
     const uint32_t bm0 = am0 + BM * BK;
     if constexpr (CONV) {
@@ -246,7 +256,6 @@ __device__ __forceinline__ void mainloop_dma(const GemmP& p, int m0, int n0, int
   //   DMAs of stage kt+NBUF into that buffer
   //   ks3: MFMAs of slice 3 | LDS reads of slice 0 of stage kt+1
   // Stages past K are fetched too: every offset is then out of range and the DMA writes zeros.
-  const int KT = (p.K + BK - 1) / BK;
 #pragma unroll
   for (int st = 0; st < NBUF; ++st) dma_stage(st, st);
   wait_dma<(NBUF - 1) * PER>();
@@ -269,6 +278,7 @@ __device__ __forceinline__ void mainloop_dma(const GemmP& p, int m0, int n0, int
       interleave<true, 0x100, NRD, NMMA>();
       __builtin_amdgcn_sched_barrier(0);
       wait_dma<(NBUF - 2) * PER>();
+      wait_lds();  // this wave's reads of the buffer about to be refilled have returned
       __syncthreads();
       frags(nxt, 0, af[0], bf[0]);  // past the last stage: data no one uses
       dma_stage(cur, kt + NBUF);
@@ -300,6 +310,7 @@ __device__ __forceinline__ void mainloop_dma(const GemmP& p, int m0, int n0, int
     interleave<true, 0x100, NRD, NMMA>();
     __builtin_amdgcn_sched_barrier(0);
     wait_dma<(NBUF - 2) * PER>();
+    wait_lds();  // this wave's reads of the buffer about to be refilled have returned
     __syncthreads();
     frags(nxt, 0, af[0], bf[0]);  // past the last stage: data no one uses
     dma_stage(cur, kt + NBUF);
@@ -342,6 +353,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
 
   const int tiles_m = (p.M + BM - 1) / BM;
   const int tiles_n = (p.N + BN - 1) / BN;
+  const int KT = (p.K + BK - 1) / BK;
   int bm, bn;
   tile_of(blockIdx.x, gridDim.x, tiles_m, tiles_n, bm, bn);
   const int m0 = bm * BM;
@@ -353,7 +365,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
   for (int i = 0; i < TM; ++i)
 #pragma unroll
     for (int j = 0; j < TN; ++j) c[i][j] = v16i{};
-  mainloop_dma<BM, BN, WAVES_M, WAVES_N, CONV, NBUF, FD>(p, m0, n0, lds, s_sa, s_sw, s_b, c);
+  mainloop_dma<BM, BN, WAVES_M, WAVES_N, CONV, NBUF, FD>(p, m0, n0, 0, KT, lds, s_sa, s_sw, s_b, c);
 
   // Epilogue, one 32-row slice of the wave tile at a time: the int32 results go through a
   // per-wave LDS patch (exact), come back as four consecutive columns of one row per lane,
@@ -886,8 +898,11 @@ int bq_gemm_i8(const int8_t* A, const int8_t* W, int64_t M, int64_t N, int64_t K
                const float* sW, const float* bias, int act, float* out, int32_t* acc, bq_stream_t stream) {
   const char* what = "bq_gemm_i8";
   if (M < 0 || N < 0 || K < 0) return set_error(BQ_ERR_ARG, "%s: negative size", what);
-  if (M > 0x7fffffff || N > 0x7fffffff || K >= (1 << 23) || M * N > ((int64_t)1 << 40))
-    return set_error(BQ_ERR_ARG, "%s: size too large (K must be < 2^23)", what);
+  if (M > 0x7fffffff || N > 0x7fffffff || M * N > ((int64_t)1 << 40))
+    return set_error(BQ_ERR_ARG, "%s: size too large", what);
+  if (K > KMAX_EXACT)
+    return set_error(BQ_ERR_UNSUPPORTED, "%s: K=%lld > %d: int32 accumulators could overflow", what, (long long)K,
+                     KMAX_EXACT);
   if (M == 0 || N == 0) return BQ_OK;
   if (K % 16) return set_error(BQ_ERR_UNSUPPORTED, "%s: K=%lld is not a multiple of 16", what, (long long)K);
   if (!A || !W || !sA || !sW || !out) return set_error(BQ_ERR_ARG, "%s: null pointer", what);
@@ -935,9 +950,11 @@ static int conv_impl(const char* what, const int8_t* x, int64_t N, int64_t H, in
   if (H + 2 * pad < KH || W + 2 * pad < KW || OH < 1 || OW < 1)
     return set_error(BQ_ERR_ARG, "%s: the filter is larger than the input.", what);
   const int64_t M = N * OH * OW, K = KH * KW * C;
-  if (M > 0x7fffffff || K >= (1 << 23) || O > 0x7fffffff || N * H * W * C >= ((int64_t)1 << 31) ||
-      O * K >= ((int64_t)1 << 31))
+  if (M > 0x7fffffff || O > 0x7fffffff || N * H * W * C >= ((int64_t)1 << 31) || O * K >= ((int64_t)1 << 31))
     return set_error(BQ_ERR_ARG, "%s: size too large (activation and weight must each be < 2 GiB)", what);
+  if (K > KMAX_EXACT)
+    return set_error(BQ_ERR_UNSUPPORTED, "%s: KH*KW*C=%lld > %d: int32 accumulators could overflow", what,
+                     (long long)K, KMAX_EXACT);
   if (M == 0) return BQ_OK;
   if (!x || !w || !sA || !sW || !out) return set_error(BQ_ERR_ARG, "%s: null pointer", what);
   if (!aligned16(x) || !aligned16(w)) return set_error(BQ_ERR_ARG, "%s: x and w must be 16-byte aligned", what);

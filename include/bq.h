@@ -96,7 +96,8 @@ int bq_quantize_nhwc_scaled(const float* x, int64_t P, int64_t C, int64_t Cpad, 
  *   A int8 [M, K] (per-row scales sA f32 [M]), W int8 [N, K] (per-channel sW f32 [N]),
  *   out f32 [M, N] = ((f32(A @ W.T) * sA[m]) * sW[n]) + bias[n] (bias nullable), then
  *   the activation `act` (BQ_ACT_*). `acc` (nullable) receives the exact int32 [M, N].
- * K % 16 == 0; A, W 16-byte aligned. Replaces matmulInt8(M,K,N,scaled)
+ * K % 16 == 0 and K <= 133152 (K * 127^2 < 2^31: the int32 sums are exact for any
+ * operands); A, W 16-byte aligned. Replaces matmulInt8(M,K,N,scaled)
  * (borch-ts/src/kernels.ts:1808-1852), which took only whole 32s. */
 int bq_gemm_i8(const int8_t* A, const int8_t* W, int64_t M, int64_t N, int64_t K,
                const float* sA, const float* sW, const float* bias, int act, float* out,
@@ -106,7 +107,8 @@ int bq_gemm_i8(const int8_t* A, const int8_t* W, int64_t M, int64_t N, int64_t K
  *   x int8 [N, H, W, C] (C % 16 == 0, per-tensor scale sA f32 [1]),
  *   w int8 [O, KH, KW, C] (per-channel scale sW f32 [O]),
  *   out f32 [N, OH, OW, O] = ((f32(acc) * sA) * sW[o]) + bias[o] + residual, then act.
- * bias, residual (f32 [N, OH, OW, O]) and acc (int32 [N*OH*OW, O]) are nullable.
+ * bias, residual (f32 [N, OH, OW, O]) and acc (int32 [N*OH*OW, O]) are nullable;
+ * KH*KW*C <= 133152 (exact int32 sums).
  * Replaces convForwardInt8 (+ sumSplitsConv) and its ConvEpilogue
  * (borch-ts/src/kernels.ts:2156-2302, 4230-4244, 5860-5914), which took stride 1, k <= 3,
  * C % 32 and O % 16 only. */
