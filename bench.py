@@ -73,6 +73,53 @@ def time_graph(g, calls, replays, stream):
     return time_events(lambda i: g.replay(), replays, stream) / calls
 
 
+def probes(dev, stream, qa, qw, wcopies):
+    """The day's ceilings on this GPU (libbqprobe, include/bq_probe.h), measured in the same
+    run as the kernels they bound:
+    * the int8 MFMA rate with no memory traffic, on fragments of the 4096^3 GEMM's own
+      quantized operands (the MFMA clock falls with the power the operand bits draw), in the
+      GEMM tile's per-wave shape and occupancy (8 waves a CU); best of 3;
+    * the plain streaming read of the GEMV's cache-cold 16 MiB weight copies: best of four
+      load depths per lane; the floor of any kernel that reads those bytes once."""
+    import ctypes
+    import torch
+    lib = ctypes.CDLL(str(ROOT / "borch_amd" / "lib" / "libbqprobe.so"))
+    lib.bqp_mfma_rate.restype = ctypes.c_int
+    lib.bqp_mfma_rate.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int,
+                                  ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    lib.bqp_stream_read.restype = ctypes.c_int
+    lib.bqp_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    lib.bqp_last_error.restype = ctypes.c_char_p
+
+    def ok(rc):
+        if rc != 0:
+            raise RuntimeError(lib.bqp_last_error().decode())
+
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    sink = torch.empty(cus * 512, dtype=torch.int32, device=dev)
+    iters = 400
+    st = stream.cuda_stream
+    ok(lib.bqp_mfma_rate(qa.data_ptr(), qa.numel(), qw.data_ptr(), qw.numel(), cus, 8, sink.data_ptr(), st))
+    best = min(time_events(lambda i: ok(lib.bqp_mfma_rate(qa.data_ptr(), qa.numel(), qw.data_ptr(), qw.numel(),
+                                                          cus, iters, sink.data_ptr(), st)), 1, stream)
+               for _ in range(3))
+    mfma_tops = cus * 8 * iters * 32 * 65536 / (best * 1e-3) / 1e12
+    nbytes = wcopies[0].numel()
+    rsink = torch.empty(nbytes // 4096 + 1, dtype=torch.int32, device=dev)
+    read_us = {}
+    for ch in (1, 2, 4, 8):
+        g = capture(lambda i: ok(lib.bqp_stream_read(wcopies[i].data_ptr(), nbytes, ch, rsink.data_ptr(),
+                                                     torch.cuda.current_stream().cuda_stream)), len(wcopies))
+        read_us[ch] = time_graph(g, len(wcopies), 8, stream) * 1e3
+        del g
+    ch = min(read_us, key=read_us.get)
+    return {"mfma_int8_TOPS_no_memory": round(mfma_tops, 1), "mfma_probe": f"{cus} CUs x 8 waves, "
+            f"{iters * 32} v_mfma_i32_32x32x32_i8 a wave on the 4096^3 operands' bytes, {best:.3f} ms",
+            "read_16MiB_cold_us": round(read_us[ch], 3), "read_GBps": round(nbytes / (read_us[ch] * 1e-6) / 1e9, 1),
+            "read_probe": f"plain streaming read of {nbytes} B over {len(wcopies)} rotated copies, "
+                          f"{ch} x 16 B loads a lane (best of 1/2/4/8)"}
+
+
 def cpu_baseline(M_sample=512):
     """The reference's CPU path on the host cores, on a bounded sample of the same workload.
 
@@ -280,11 +327,16 @@ def main():
         g_e = capture(lambda i: (lambda q_s: I.gemm_i8(q_s[0], qws[i], q_s[1], sw_m, Bm))(I.quantize_rows(Am)), copies)
         t_e2e = time_graph(g_e, copies, 8, stream)
         del g_k, g_e
+        if m == 1:
+            ceilings = probes(dev, stream, qa, qw, qws)
+            log(f"ceilings: {ceilings}")
         byts = WL.gemm_bytes(m)
         sweep[f"M{m}"] = {"kernel_us": round(t_k * 1e3, 3), "GBps": round(byts / (t_k * 1e-3) / 1e9, 1),
                           "hbm_frac": round(byts / (t_k * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
                           "TOPS": round(WL.gemm_ops(m) / (t_k * 1e-3) / 1e12, 2),
-                          "e2e_us_with_quantize": round(t_e2e * 1e3, 3), "bytes": byts}
+                          "e2e_us_with_quantize": round(t_e2e * 1e3, 3), "bytes": byts,
+                          "read_floor_us": ceilings["read_16MiB_cold_us"],
+                          "frac_of_read_floor": round(ceilings["read_16MiB_cold_us"] / (t_k * 1e3), 4)}
         del qws, Am
         log(f"M={m}: {sweep[f'M{m}']}")
     # weight-only W8A32 decode GEMV (M = 1): f32 x against the int8 weight, cache-cold
@@ -335,7 +387,10 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(gemm_tops, 2), "peak": PEAK_INT8_TOPS, "unit": "TOPS",
                      "frac": round(gemm_tops / PEAK_INT8_TOPS, 4), "traffic": traffic,
                      "kernel": "gemm_i8_kernel 256x256 (bq_gemm_i8)", "kernel_ms": round(gemm_ms, 5),
-                     "timing": "HIP events around HIP-graph replays on the launch stream"},
+                     "timing": "HIP events around HIP-graph replays on the launch stream",
+                     "measured_ceiling_TOPS": ceilings["mfma_int8_TOPS_no_memory"],
+                     "frac_of_measured_ceiling": round(gemm_tops / ceilings["mfma_int8_TOPS_no_memory"], 4)},
+        "ceilings": ceilings,
         "sweep": sweep,
         "models": models,
     }

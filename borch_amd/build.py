@@ -20,6 +20,7 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIBDIR = PKG / "lib"
 LIB = LIBDIR / "libbq.so"
+PROBE_LIB = LIBDIR / "libbqprobe.so"  # bench.py's measurement probes (include/bq_probe.h)
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -50,25 +51,35 @@ def _compile(src: Path, obj: Path) -> None:
         sys.stderr.write("\n".join(noise) + "\n")
 
 
+def _link(objs, out: Path) -> None:
+    tmp = out.with_suffix(".so.tmp")
+    cmd = [hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", *map(str, objs), "-o", str(tmp)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link of {out.name} failed:\n{r.stderr}")
+    os.replace(tmp, out)
+
+
 def build(verbose: bool = True) -> Path:
-    """Compile every ``csrc/*.hip`` and link ``lib/libbq.so``; returns its path."""
+    """Compile every ``csrc/*.hip`` and link ``lib/libbq.so`` (returned), and the probes of
+    ``csrc/probe/*.hip`` into ``lib/libbqprobe.so``."""
     srcs = sorted(CSRC.glob("*.hip"))
+    probe_srcs = sorted((CSRC / "probe").glob("*.hip"))
     if not srcs:
         raise RuntimeError(f"no HIP sources under {CSRC}")
     objdir = PKG / "_build"
     objdir.mkdir(exist_ok=True)
     LIBDIR.mkdir(exist_ok=True)
     objs = [objdir / (s.stem + ".o") for s in srcs]
-    with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
-        list(ex.map(_compile, srcs, objs))
-    tmp = LIB.with_suffix(".so.tmp")
-    cmd = [hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", *map(str, objs), "-o", str(tmp)]
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError(f"link failed:\n{r.stderr}")
-    os.replace(tmp, LIB)
+    probe_objs = [objdir / ("probe_" + s.stem + ".o") for s in probe_srcs]
+    with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs) + len(probe_srcs))) as ex:
+        list(ex.map(_compile, srcs + probe_srcs, objs + probe_objs))
+    _link(objs, LIB)
+    if probe_objs:
+        _link(probe_objs, PROBE_LIB)
     if verbose:
-        print(f"built {LIB.relative_to(ROOT)} from {len(srcs)} sources")
+        print(f"built {LIB.relative_to(ROOT)} from {len(srcs)} sources"
+              + (f", {PROBE_LIB.relative_to(ROOT)} from {len(probe_srcs)}" if probe_objs else ""))
     return LIB
 
 

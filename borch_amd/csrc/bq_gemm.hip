@@ -105,6 +105,14 @@ template <bool ON, int MASK, int COUNT, int NMMA>
 __device__ __forceinline__ void interleave() {
   if constexpr (ON) interleave_impl<MASK, COUNT, NMMA>(std::make_integer_sequence<int, NMMA>{});
 }
+// The same with the COUNT instructions spread over the first SPREAD MFMAs only, the rest
+// of the NMMA MFMAs after them: used for the LDS reads that precede a wait for them, so that
+// they have returned by the time the wave reaches the wait.
+template <int MASK, int COUNT, int NMMA, int SPREAD>
+__device__ __forceinline__ void interleave_front() {
+  interleave_impl<MASK, COUNT, SPREAD>(std::make_integer_sequence<int, SPREAD>{});
+  sched_group<0x008, NMMA - SPREAD>();
+}
 
 // One 16-byte-per-lane load straight into LDS (no VGPR staging): lane l's 16 bytes land at
 // LDS byte address m0v + 16 * l. Issued from inline assembly so that the compiler, which
@@ -275,7 +283,7 @@ __device__ __forceinline__ void mainloop_dma(const GemmP& p, int m0, int n0, int
       __builtin_amdgcn_sched_barrier(0);
       frags(cur, 3, af[3], bf[3]);
       mma(af[1], bf[1]);
-      interleave<true, 0x100, NRD, NMMA>();
+      interleave_front<0x100, NRD, NMMA, (NMMA + 1) / 2>();
       __builtin_amdgcn_sched_barrier(0);
       wait_dma<(NBUF - 2) * PER>();
       wait_lds();  // this wave's reads of the buffer about to be refilled have returned
@@ -307,7 +315,7 @@ __device__ __forceinline__ void mainloop_dma(const GemmP& p, int m0, int n0, int
     __builtin_amdgcn_sched_barrier(0);
     frags(cur, 3, af[1], bf[1]);
     mma(af[0], bf[0]);
-    interleave<true, 0x100, NRD, NMMA>();
+    interleave_front<0x100, NRD, NMMA, (NMMA + 1) / 2>();
     __builtin_amdgcn_sched_barrier(0);
     wait_dma<(NBUF - 2) * PER>();
     wait_lds();  // this wave's reads of the buffer about to be refilled have returned

@@ -84,3 +84,32 @@ def test_quantize_for_int8_refuses_without_device():
     m = bt.nn.Sequential(bt.nn.Linear(16, 8), bt.nn.ReLU())
     with pytest.raises(Int8Unavailable, match="int8"):
         bt.quantize_for_int8(m)
+
+
+PROBE_HEADER = ROOT / "include" / "bq_probe.h"
+
+
+def probe_lib():
+    lib = ctypes.CDLL(str(ROOT / "borch_amd" / "lib" / "libbqprobe.so"))
+    lib.bqp_last_error.restype = ctypes.c_char_p
+    return lib
+
+
+def test_probe_library_exports_its_header():
+    """bench.py's measurement probes (libbqprobe): every declared symbol is exported, and bad
+    arguments are refused on the host."""
+    text = re.sub(r"/\*.*?\*/", "", PROBE_HEADER.read_text(), flags=re.S)
+    names = sorted(set(re.findall(r"\b(bqp_[a-z0-9_]+)\s*\(", text)))
+    assert names == ["bqp_last_error", "bqp_mfma_rate", "bqp_stream_read"]
+    lib = probe_lib()
+    for n in names:
+        assert hasattr(lib, n), n
+    i64, p = ctypes.c_int64, ctypes.c_void_p
+    lib.bqp_mfma_rate.argtypes = [p, i64, p, i64, ctypes.c_int, ctypes.c_int, p, p]
+    lib.bqp_stream_read.argtypes = [p, i64, ctypes.c_int, p, p]
+    assert lib.bqp_mfma_rate(None, 4096, None, 4096, 1, 1, None, None) == -1
+    assert b"null" in lib.bqp_last_error()
+    assert lib.bqp_mfma_rate(16, 4000, 16, 4096, 1, 1, 16, None) == -1
+    assert lib.bqp_stream_read(16, 24, 1, 16, None) == -1
+    assert lib.bqp_stream_read(16, 32, 3, 16, None) == -1
+    assert b"chunks" in lib.bqp_last_error()

@@ -5,10 +5,13 @@ held to the task's tolerance (1e-5 relative / 1e-6 absolute) and, since the epil
 one float32 rounding per operation in the oracle's order, are also checked bit-exact.
 """
 import sys
+from pathlib import Path
 
 import numpy as np
 import pytest
 import torch
+
+ROOT = Path(__file__).resolve().parent.parent
 
 from borch_amd import int8 as I
 from borch_amd import workloads as WL
@@ -326,3 +329,28 @@ def test_quantize_false_ties(dev):
     assert np.array_equal(n(q), qo)
     n_false = sum(1 for _, _, tie in pairs if not tie)
     say(f"  {len(rows)} rows, {n_false} of {len(pairs)} pairs are false ties")
+
+
+@pytest.mark.gpu
+def test_probe_stream_read_folds_every_byte(dev):
+    """The read-floor probe bench.py times reads every 16-byte chunk once: its per-workgroup
+    XOR fold equals the host's fold of the same bytes, for each load depth."""
+    import ctypes
+    lib = ctypes.CDLL(str(ROOT / "borch_amd" / "lib" / "libbqprobe.so"))
+    lib.bqp_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    g = torch.Generator().manual_seed(5)
+    n16 = 3 * 2048 + 37  # a ragged last workgroup for every depth
+    words = torch.randint(-2**31, 2**31 - 1, (n16 * 4,), dtype=torch.int64, generator=g).to(torch.int32)
+    src = words.to(dev)
+    st = torch.cuda.current_stream().cuda_stream
+    for ch in (1, 2, 4, 8):
+        per = 256 * ch
+        nblk = (n16 + per - 1) // per
+        sink = torch.zeros(nblk, dtype=torch.int32, device=dev)
+        assert lib.bqp_stream_read(src.data_ptr(), n16 * 16, ch, sink.data_ptr(), st) == 0
+        w = words.view(n16, 4).numpy()
+        chunk_x = np.bitwise_xor.reduce(w, axis=1)
+        pad = np.zeros(nblk * per, dtype=np.int32)
+        pad[:n16] = chunk_x
+        want = np.bitwise_xor.reduce(pad.reshape(nblk, per), axis=1)
+        np.testing.assert_array_equal(sink.cpu().numpy(), want)
