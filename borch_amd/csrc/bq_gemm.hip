@@ -19,6 +19,7 @@
 // and v_mfma_i32_16x16x64_i8 multiplies them against up to four 16-row activation tiles.
 #include <stdlib.h>
 
+#include <algorithm>
 #include <utility>
 
 #include "bq_common.h"
@@ -39,13 +40,43 @@ struct GemmP {
   int32_t* acc;  // [M, N] or null
   // conv geometry (CONV only)
   int H, Wd, C, OH, OW, KWd, stride, pad;
+  // k / C and tap / KW of the implicit im2col as multiply-high and shift (FastDiv)
+  uint32_t c_mul, kw_mul;
+  int c_shift, kw_shift;
   int64_t Nimg_HWC;  // conv: bytes of the NHWC activation
   int vec_ok;        // N % 4 == 0 and out/res/acc 16-byte aligned: float4 epilogue
   const float* s_out;  // static output scale [1] (nullable): the int8 twin of the output
   int8_t* q_out;       // [M, N] int8 = clip(rint(y / s_out)) (nullable)
+  // Split-K (tiled kernel only): ksplit workgroups per output tile, each over a contiguous
+  // run of K stages; each stores its int32 partial tile in `part` and bumps the tile's
+  // counter in `cnt`; the last to arrive adds the partials and runs the epilogue, then
+  // resets the counter to zero. ksplit == 1: no partials, no counters.
+  int ksplit;
+  int32_t* part;  // [tiles][ksplit][BM * BN] int32, in the accumulator register order
+  int* cnt;       // [tiles], zero between launches
 };
 
+// Division by a run-time invariant d >= 1 of any n < 2^31 as (umulhi(n, mul) + n) >> shift
+// with shift = ceil(log2 d) and mul = floor(2^32 (2^shift - d) / d) + 1 (Granlund and
+// Montgomery, "Division by invariant integers using multiplication", PLDI 1994, the
+// round-up method; the sum cannot overflow 32 bits for n < 2^31). Three instructions
+// instead of a full integer division in the conv loader's per-stage address arithmetic.
+struct FastDiv {
+  uint32_t mul;
+  int shift;
+};
+static inline FastDiv fast_div(uint32_t d) {
+  int l = 0;
+  while ((1ull << l) < d) ++l;
+  return FastDiv{(uint32_t)(((1ull << 32) * ((1ull << l) - d)) / d + 1), l};
+}
+__device__ __forceinline__ int fdiv(int n, uint32_t mul, int shift) {
+  return (int)((__umulhi((uint32_t)n, mul) + (uint32_t)n) >> shift);
+}
+
 constexpr int BK = 128;  // bytes of K per LDS stage: one cache line per row
+// Split-K is compiled into (and offered to) tiles of at most this many outputs only.
+constexpr int SPLIT_MAX_TILE = 64 * 64;
 // The largest K whose int32 sum of products is exact for any int8 operands in [-127, 127]:
 // K * 127^2 <= 2^31 - 1.
 constexpr int KMAX_EXACT = 133152;
@@ -70,13 +101,16 @@ __device__ __forceinline__ v4i buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off
 __device__ __forceinline__ int lds_off(int r, int c) { return r * BK + ((c ^ ((r >> 1) & 7)) << 4); }
 
 // Workgroup -> output tile. Workgroups are dispatched round-robin over the 8 XCDs (each
-// with its own L2), so workgroup id is first regrouped by XCD, then tiles are handed out
+// with its own L2), so workgroup id is first regrouped by XCD (xcd_order: consecutive
+// regrouped ids run on one XCD; the K splits of a tile are consecutive), then tiles are handed out
 // in bands of 8 tile columns walking down M: the 32 workgroups of one XCD at a 4096^2
 // problem cover a 4 x 8 block of tiles, and each K step's A and W slabs are fetched into
 // that XCD's L2 once and then shared.
-__device__ __forceinline__ void tile_of(int id, int G, int tiles_m, int tiles_n, int& bm, int& bn) {
+__device__ __forceinline__ int xcd_order(int id, int G) {
   constexpr int XCDS = 8;
-  if (G % XCDS == 0) id = (id % XCDS) * (G / XCDS) + id / XCDS;
+  return G % XCDS == 0 ? (id % XCDS) * (G / XCDS) + id / XCDS : id;
+}
+__device__ __forceinline__ void tile_of(int id, int tiles_m, int tiles_n, int& bm, int& bn) {
   constexpr int GROUP = 8;
   const int per_group = GROUP * tiles_m;
   const int g = id / per_group;
@@ -221,9 +255,9 @@ __device__ __forceinline__ void mainloop_dma(const GemmP& p, int m0, int n0, int
     const uint32_t am0 = lds_base + (uint32_t)(buf * (BM + BN) * BK + wv * 1024);
     const uint32_t bm0 = am0 + BM * BK;
     if constexpr (CONV) {
-      const int tap = k0 / p.C;
+      const int tap = fdiv(k0, p.c_mul, p.c_shift);
       const int c0 = k0 - tap * p.C;
-      const int kh = tap / p.KWd;
+      const int kh = fdiv(tap, p.kw_mul, p.kw_shift);
       const int kw = tap - kh * p.KWd;
 #pragma unroll
       for (int i = 0; i < A_DMA; ++i) {
@@ -352,6 +386,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
   __shared__ __attribute__((aligned(16))) float s_sa[BM];
   __shared__ __attribute__((aligned(16))) float s_sw[BN];
   __shared__ __attribute__((aligned(16))) float s_b[BN];
+  __shared__ int s_last;  // split-K: this workgroup is the last of its tile
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -362,10 +397,16 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
   const int tiles_m = (p.M + BM - 1) / BM;
   const int tiles_n = (p.N + BN - 1) / BN;
   const int KT = (p.K + BK - 1) / BK;
+  constexpr bool CAN_SPLIT = BM * BN <= SPLIT_MAX_TILE;
+  const int S = CAN_SPLIT ? p.ksplit : 1;
+  const int L = xcd_order(blockIdx.x, gridDim.x);
+  const int split = L % S;
   int bm, bn;
-  tile_of(blockIdx.x, gridDim.x, tiles_m, tiles_n, bm, bn);
+  tile_of(L / S, tiles_m, tiles_n, bm, bn);
   const int m0 = bm * BM;
   const int n0 = bn * BN;
+  const int per = (KT + S - 1) / S;  // stages of each split (the host picks S with no empty split)
+  const int kt0 = split * per;
 
   const float s_out = p.q_out ? p.s_out[0] : 0.f;
   v16i c[TM][TN];
@@ -373,7 +414,68 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
   for (int i = 0; i < TM; ++i)
 #pragma unroll
     for (int j = 0; j < TN; ++j) c[i][j] = v16i{};
-  mainloop_dma<BM, BN, WAVES_M, WAVES_N, CONV, NBUF, FD>(p, m0, n0, 0, KT, lds, s_sa, s_sw, s_b, c);
+  mainloop_dma<BM, BN, WAVES_M, WAVES_N, CONV, NBUF, FD>(p, m0, n0, kt0, min(per, KT - kt0), lds, s_sa, s_sw,
+                                                         s_b, c);
+  if (CAN_SPLIT && S > 1) {
+    // Exact split-K reduction in the same launch. Partials are int32, so the sum is exact
+    // whatever the order. Each lane stores its accumulator registers as 8-byte chunks at
+    // [tile][split][chunk][lane] (contiguous across the workgroup); the last workgroup of
+    // the tile reads the other splits' chunks at its own lanes' offsets, so no re-layout is
+    // needed. No workgroup ever waits for another: the counter only elects the one that
+    // finishes the tile.
+    // Coherence across XCDs (each has its own L2) without cache-wide write-back or
+    // invalidation: partials are written and read with device-scope relaxed atomics
+    // (write-through stores and L2-bypassing loads at agent scope); every store has
+    // completed (vmcnt 0) before the workgroup's counter increment, and the last
+    // workgroup's loads are issued after its increment returned S - 1.
+    constexpr int NV = TM * TN * 8;  // 8-byte chunks per lane
+    const int tile = bm * tiles_n + bn;
+    uint64_t* const part = reinterpret_cast<uint64_t*>(p.part);
+    uint64_t* mine = part + ((size_t)(tile * S + split) * NV) * T + tid;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+          const uint64_t v = (uint64_t)(uint32_t)c[i][j][2 * g] | ((uint64_t)(uint32_t)c[i][j][2 * g + 1] << 32);
+          __hip_atomic_store(mine + (size_t)((i * TN + j) * 8 + g) * T, v, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+        }
+    wait_dma_all();  // every partial store of this lane has completed
+    __syncthreads();
+    if (tid == 0)
+      s_last = __hip_atomic_fetch_add(p.cnt + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1;
+    __syncthreads();
+    if (!s_last) return;  // uniform across the workgroup
+    // Four splits' chunks are loaded before any is added, so their round trips overlap.
+    constexpr int BATCH = 4;
+    for (int sp0 = 0; sp0 < S; sp0 += BATCH) {
+      uint64_t v[BATCH][NV];
+#pragma unroll
+      for (int u = 0; u < BATCH; ++u) {
+        const int sp = sp0 + u;
+        const bool use = sp < S && sp != split;
+        uint64_t* other = part + ((size_t)(tile * S + (use ? sp : split)) * NV) * T + tid;
+#pragma unroll
+        for (int e = 0; e < NV; ++e)
+          v[u][e] = use ? __hip_atomic_load(other + (size_t)e * T, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
+      }
+#pragma unroll
+      for (int u = 0; u < BATCH; ++u)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int g = 0; g < 8; ++g) {
+              const uint64_t w = v[u][(i * TN + j) * 8 + g];
+              c[i][j][2 * g] += (int)(uint32_t)w;
+              c[i][j][2 * g + 1] += (int)(uint32_t)(w >> 32);
+            }
+    }
+    if (tid == 0) __hip_atomic_store(p.cnt + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 
   // Epilogue, one 32-row slice of the wave tile at a time: the int32 results go through a
   // per-wave LDS patch (exact), come back as four consecutive columns of one row per lane,
@@ -833,10 +935,62 @@ __global__ __launch_bounds__(256) void dwconv_blk_kernel(const int8_t* __restric
 
 // ---------------------------------------------------------------------------- dispatch
 
+// Split-K workspace: the tile counters first (SPLIT_CNT_BYTES), the int32 partial tiles
+// after. Splitting is offered to tiles of at most SPLIT_MAX_TILE outputs, and only when the
+// grid has fewer than SPLIT_MAX_TILES tiles; with S <= ceil(256 / tiles) the partials take
+// at most (256 + SPLIT_MAX_TILES) tiles' worth, which bounds the workspace for every shape.
+constexpr int SPLIT_MAX_TILES = 160;
+constexpr size_t SPLIT_CNT_BYTES = 4096;
+constexpr size_t SPLIT_WS_BYTES = SPLIT_CNT_BYTES + (size_t)(256 + SPLIT_MAX_TILES) * SPLIT_MAX_TILE * 4;
+
+struct Ws {
+  void* ptr;
+  size_t bytes;
+};
+
+// BQ_GEMM_SPLIT forces the number of K splits of the tiled kernel (tuning sweeps; still
+// subject to the workspace); unset = the rule below.
+static int forced_split() {
+  static int v = [] {
+    const char* e = getenv("BQ_GEMM_SPLIT");
+    return e ? atoi(e) : 0;
+  }();
+  return v;
+}
+
+// K splits for a grid of `tiles` tiles of `KT` stages: enough workgroups to cover the
+// chip's 256 CUs, each split at least 4 stages long, and no split left empty. The split
+// costs a fixed 2-3 us (partials written through to the device-coherent level, the counter
+// round trip, the last workgroup's reads); measured on 64x64 tiles it pays from 16 stages
+// for a conv (whose loader makes a stage dearer) and from 32 for a dense GEMM.
+static int pick_split(long long tiles, int KT, bool conv) {
+  int S;
+  if (forced_split() > 0) {
+    S = forced_split();
+  } else {
+    if (tiles >= SPLIT_MAX_TILES || KT < (conv ? 16 : 32)) return 1;
+    S = (int)std::min<long long>((256 + tiles - 1) / tiles, KT / 4);
+  }
+  S = std::max(1, std::min(S, KT));
+  const int per = (KT + S - 1) / S;
+  return (KT + per - 1) / per;
+}
+
 template <int BM, int BN, int WAVES_M, int WAVES_N, bool CONV, int NBUF, int FD>
-static void launch_tiled(const GemmP& p, hipStream_t st) {
-  const int tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
-  gemm_i8_kernel<BM, BN, WAVES_M, WAVES_N, CONV, NBUF, FD><<<tiles, WAVES_M * WAVES_N * 64, 0, st>>>(p);
+static void launch_tiled(GemmP p, hipStream_t st, const Ws& ws) {
+  const long long tiles = (long long)((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
+  int S = BM * BN <= SPLIT_MAX_TILE ? pick_split(tiles, (p.K + BK - 1) / BK, CONV) : 1;
+  if (S > 1) {
+    const size_t need = SPLIT_CNT_BYTES + (size_t)tiles * S * BM * BN * 4;
+    if (!ws.ptr || ws.bytes < need || tiles * 4 > (long long)SPLIT_CNT_BYTES || tiles * S > 0x7fffffffll) {
+      S = 1;
+    } else {
+      p.cnt = static_cast<int*>(ws.ptr);
+      p.part = reinterpret_cast<int32_t*>(static_cast<char*>(ws.ptr) + SPLIT_CNT_BYTES);
+    }
+  }
+  p.ksplit = S;
+  gemm_i8_kernel<BM, BN, WAVES_M, WAVES_N, CONV, NBUF, FD><<<(unsigned)(tiles * S), WAVES_M * WAVES_N * 64, 0, st>>>(p);
 }
 
 // BQ_GEMM_CFG forces one tile configuration (tuning sweeps); unset = the shape rule.
@@ -849,22 +1003,22 @@ static int forced_cfg() {
 }
 
 template <bool CONV>
-static void launch_gemm(const GemmP& p, hipStream_t st) {
+static void launch_gemm(const GemmP& p, hipStream_t st, const Ws& ws) {
   switch (forced_cfg()) {  // <BM, BN, waves M x N, ring depth, fragment distance>
-    case 1: return launch_tiled<256, 256, 2, 4, CONV, 2, 1>(p, st);
-    case 2: return launch_tiled<256, 256, 2, 4, CONV, 2, 2>(p, st);
-    case 3: return launch_tiled<256, 256, 2, 2, CONV, 2, 2>(p, st);
-    case 4: return launch_tiled<128, 128, 2, 2, CONV, 4, 2>(p, st);
-    case 5: return launch_tiled<128, 128, 2, 2, CONV, 2, 2>(p, st);
-    case 6: return launch_tiled<256, 128, 2, 2, CONV, 3, 1>(p, st);
-    case 7: return launch_tiled<64, 64, 2, 2, CONV, 4, 2>(p, st);
-    case 8: return launch_tiled<256, 64, 4, 1, CONV, 3, 1>(p, st);
-    case 9: return launch_tiled<64, 64, 2, 2, CONV, 8, 1>(p, st);
-    case 10: return launch_tiled<64, 64, 2, 2, CONV, 2, 2>(p, st);
-    case 11: return launch_tiled<128, 64, 4, 1, CONV, 2, 1>(p, st);
-    case 12: return launch_tiled<128, 32, 4, 1, CONV, 2, 1>(p, st);
-    case 13: return launch_tiled<256, 64, 4, 1, CONV, 2, 1>(p, st);
-    case 14: return launch_tiled<128, 64, 4, 1, CONV, 3, 1>(p, st);
+    case 1: return launch_tiled<256, 256, 2, 4, CONV, 2, 1>(p, st, ws);
+    case 2: return launch_tiled<256, 256, 2, 4, CONV, 2, 2>(p, st, ws);
+    case 3: return launch_tiled<256, 256, 2, 2, CONV, 2, 2>(p, st, ws);
+    case 4: return launch_tiled<128, 128, 2, 2, CONV, 4, 2>(p, st, ws);
+    case 5: return launch_tiled<128, 128, 2, 2, CONV, 2, 2>(p, st, ws);
+    case 6: return launch_tiled<256, 128, 2, 2, CONV, 3, 1>(p, st, ws);
+    case 7: return launch_tiled<64, 64, 2, 2, CONV, 4, 2>(p, st, ws);
+    case 8: return launch_tiled<256, 64, 4, 1, CONV, 3, 1>(p, st, ws);
+    case 9: return launch_tiled<64, 64, 2, 2, CONV, 8, 1>(p, st, ws);
+    case 10: return launch_tiled<64, 64, 2, 2, CONV, 2, 2>(p, st, ws);
+    case 11: return launch_tiled<128, 64, 4, 1, CONV, 2, 1>(p, st, ws);
+    case 12: return launch_tiled<128, 32, 4, 1, CONV, 2, 1>(p, st, ws);
+    case 13: return launch_tiled<256, 64, 4, 1, CONV, 2, 1>(p, st, ws);
+    case 14: return launch_tiled<128, 64, 4, 1, CONV, 3, 1>(p, st, ws);
     default: break;
   }
   // Narrow outputs (N <= 64: 1x1 convs of mobile networks, the stem, early ResNet layers)
@@ -880,18 +1034,18 @@ static void launch_gemm(const GemmP& p, hipStream_t st) {
   const long long t128x32 = (long long)((p.M + 127) / 128) * ((p.N + 31) / 32);
   const long long t64 = (long long)((p.M + 63) / 64) * ((p.N + 63) / 64);
   if (p.N <= 32 && t128x32 >= 128)
-    launch_tiled<128, 32, 4, 1, CONV, 2, 1>(p, st);
+    launch_tiled<128, 32, 4, 1, CONV, 2, 1>(p, st, ws);
   else if (p.N <= 64 && t64 > 256)
-    launch_tiled<64, 64, 2, 2, CONV, 2, 2>(p, st);
+    launch_tiled<64, 64, 2, 2, CONV, 2, 2>(p, st, ws);
   else if (t256 >= 192 && p.N >= 192)
-    launch_tiled<256, 256, 2, 4, CONV, 2, 1>(p, st);
+    launch_tiled<256, 256, 2, 4, CONV, 2, 1>(p, st, ws);
   else if (t128 >= 128 && p.N >= 96) {
     if (t128 > 256)
-      launch_tiled<128, 128, 2, 2, CONV, 2, 2>(p, st);
+      launch_tiled<128, 128, 2, 2, CONV, 2, 2>(p, st, ws);
     else
-      launch_tiled<128, 128, 2, 2, CONV, 4, 2>(p, st);
+      launch_tiled<128, 128, 2, 2, CONV, 4, 2>(p, st, ws);
   } else
-    launch_tiled<64, 64, 2, 2, CONV, 4, 2>(p, st);
+    launch_tiled<64, 64, 2, 2, CONV, 4, 2>(p, st, ws);
 }
 
 static bool aligned16(const void* q) { return ((uintptr_t)q & 15) == 0; }
@@ -902,8 +1056,11 @@ using namespace bq;
 
 extern "C" {
 
+size_t bq_gemm_ws_bytes(void) { return SPLIT_WS_BYTES; }
+
 int bq_gemm_i8(const int8_t* A, const int8_t* W, int64_t M, int64_t N, int64_t K, const float* sA,
-               const float* sW, const float* bias, int act, float* out, int32_t* acc, bq_stream_t stream) {
+               const float* sW, const float* bias, int act, float* out, int32_t* acc, void* ws, size_t ws_bytes,
+               bq_stream_t stream) {
   const char* what = "bq_gemm_i8";
   if (M < 0 || N < 0 || K < 0) return set_error(BQ_ERR_ARG, "%s: negative size", what);
   if (M > 0x7fffffff || N > 0x7fffffff || M * N > ((int64_t)1 << 40))
@@ -941,7 +1098,7 @@ int bq_gemm_i8(const int8_t* A, const int8_t* W, int64_t M, int64_t N, int64_t K
       default: skinny_i8_kernel<4, 8, 1><<<grid, 8 * 64, 0, st>>>(p); break;
     }
   } else {
-    launch_gemm<false>(p, st);
+    launch_gemm<false>(p, st, Ws{ws, ws_bytes});
   }
   return check_launch(what);
 }
@@ -949,7 +1106,8 @@ int bq_gemm_i8(const int8_t* A, const int8_t* W, int64_t M, int64_t N, int64_t K
 static int conv_impl(const char* what, const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t C,
                      const int8_t* w, int64_t O, int64_t KH, int64_t KW, int64_t stride, int64_t pad,
                      const float* sA, const float* sW, const float* bias, const float* residual, int act,
-                     float* out, int32_t* acc, const float* s_out, int8_t* q_out, bq_stream_t stream) {
+                     float* out, int32_t* acc, const float* s_out, int8_t* q_out, void* ws, size_t ws_bytes,
+                     bq_stream_t stream) {
   if (N < 0 || H < 1 || W < 1 || C < 1 || O < 1 || KH < 1 || KW < 1 || stride < 1 || pad < 0)
     return set_error(BQ_ERR_ARG, "%s: bad geometry", what);
   if (C % 16) return set_error(BQ_ERR_UNSUPPORTED, "%s: C=%lld is not a multiple of 16 (pad it)", what, (long long)C);
@@ -973,34 +1131,37 @@ static int conv_impl(const char* what, const int8_t* x, int64_t N, int64_t H, in
   p.out = out; p.acc = acc;
   p.H = (int)H; p.Wd = (int)W; p.C = (int)C; p.OH = (int)OH; p.OW = (int)OW; p.KWd = (int)KW;
   p.stride = (int)stride; p.pad = (int)pad;
+  const FastDiv dc = fast_div((uint32_t)C), dkw = fast_div((uint32_t)KW);
+  p.c_mul = dc.mul; p.c_shift = dc.shift; p.kw_mul = dkw.mul; p.kw_shift = dkw.shift;
   p.Nimg_HWC = N * H * W * C;
   p.vec_ok = (O % 4 == 0) && aligned16(out) && aligned16(acc) && aligned16(residual) && ((uintptr_t)q_out & 3) == 0;
   p.s_out = s_out;
   p.q_out = q_out;
   hipStream_t st = (hipStream_t)stream;
   if (KH == 1 && KW == 1 && stride == 1 && pad == 0)
-    launch_gemm<false>(p, st);  // a 1x1 conv is the dense GEMM on [N*H*W, C]
+    launch_gemm<false>(p, st, Ws{ws, ws_bytes});  // a 1x1 conv is the dense GEMM on [N*H*W, C]
   else
-    launch_gemm<true>(p, st);
+    launch_gemm<true>(p, st, Ws{ws, ws_bytes});
   return check_launch(what);
 }
 
 int bq_conv2d_i8_nhwc(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t C, const int8_t* w,
                       int64_t O, int64_t KH, int64_t KW, int64_t stride, int64_t pad, const float* sA,
                       const float* sW, const float* bias, const float* residual, int act, float* out,
-                      int32_t* acc, bq_stream_t stream) {
+                      int32_t* acc, void* ws, size_t ws_bytes, bq_stream_t stream) {
   return conv_impl("bq_conv2d_i8_nhwc", x, N, H, W, C, w, O, KH, KW, stride, pad, sA, sW, bias, residual, act, out,
-                   acc, nullptr, nullptr, stream);
+                   acc, nullptr, nullptr, ws, ws_bytes, stream);
 }
 
 int bq_conv2d_i8_nhwc_q(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t C, const int8_t* w,
                         int64_t O, int64_t KH, int64_t KW, int64_t stride, int64_t pad, const float* sA,
                         const float* sW, const float* bias, const float* residual, int act, float* out,
-                        int32_t* acc, const float* s_out, int8_t* q_out, bq_stream_t stream) {
+                        int32_t* acc, const float* s_out, int8_t* q_out, void* ws, size_t ws_bytes,
+                        bq_stream_t stream) {
   if (!s_out || !q_out) return set_error(BQ_ERR_ARG, "bq_conv2d_i8_nhwc_q: null s_out or q_out");
   if (O % 16) return set_error(BQ_ERR_UNSUPPORTED, "bq_conv2d_i8_nhwc_q: O=%lld is not a multiple of 16", (long long)O);
   return conv_impl("bq_conv2d_i8_nhwc_q", x, N, H, W, C, w, O, KH, KW, stride, pad, sA, sW, bias, residual, act,
-                   out, acc, s_out, q_out, stream);
+                   out, acc, s_out, q_out, ws, ws_bytes, stream);
 }
 
 int bq_dwconv_i8_nhwc(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t C, const int8_t* w, int64_t KH,

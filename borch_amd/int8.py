@@ -20,7 +20,7 @@ __all__ = [
     "quantize_rows", "quantize_weight_per_channel", "quantize_tensor", "quantize_nhwc",
     "gemm_i8", "conv2d_i8_nhwc", "conv2d_i8_nhwc_q", "dwconv_i8_nhwc", "pack_linear_weight", "pack_conv_weight",
     "quantize_nhwc_scaled", "linear_w8a32", "dequant_weight",
-    "pack_dw_weight", "linear", "conv2d", "depthwise_conv2d", "round_up",
+    "pack_dw_weight", "linear", "conv2d", "depthwise_conv2d", "round_up", "split_workspace",
 ]
 
 
@@ -34,6 +34,33 @@ def _ptr(t):
 
 def _stream(t: torch.Tensor):
     return torch.cuda.current_stream(t.device).cuda_stream
+
+
+# The split-K workspace of bq_gemm_i8 / bq_conv2d_i8_nhwc(_q) (bq_gemm_ws_bytes): one
+# zero-filled buffer per device, made outside any graph capture and kept for the life of
+# the process, since a captured HIP graph keeps using the pointer it recorded. The kernels
+# leave its counters zero after every call. Calls issued through this module on one device
+# share it, so they must not overlap on two streams.
+_SPLIT_WS: dict = {}
+
+
+def split_workspace(device: torch.device):
+    """The device's split-K workspace, or None while a graph is being captured before one
+    exists (the calls then run unsplit: same results)."""
+    idx = torch.device(device).index
+    idx = torch.cuda.current_device() if idx is None else idx
+    ws = _SPLIT_WS.get(idx)
+    if ws is None:
+        if torch.cuda.is_current_stream_capturing():
+            return None
+        ws = torch.zeros(int(lib().bq_gemm_ws_bytes()), dtype=torch.uint8, device=torch.device("cuda", idx))
+        _SPLIT_WS[idx] = ws
+    return ws
+
+
+def _ws_args(device):
+    ws = split_workspace(device)
+    return (None, 0) if ws is None else (ws.data_ptr(), ws.numel())
 
 
 def _need(t: torch.Tensor, name: str, dtype: torch.dtype) -> None:
@@ -259,7 +286,7 @@ def gemm_i8(qa, qw, sa, sw, bias=None, act=ACT_NONE, want_acc=False):
     out = torch.empty((M, N), dtype=torch.float32, device=qa.device)
     acc = torch.empty((M, N), dtype=torch.int32, device=qa.device) if want_acc else None
     check(lib().bq_gemm_i8(qa.data_ptr(), qw.data_ptr(), M, N, K, sa.data_ptr(), sw.data_ptr(), _ptr(b), act,
-                           out.data_ptr(), _ptr(acc), _stream(qa)))
+                           out.data_ptr(), _ptr(acc), *_ws_args(qa.device), _stream(qa)))
     return (out, acc) if want_acc else out
 
 
@@ -286,7 +313,7 @@ def conv2d_i8_nhwc(qx, sa, wq: Int8ConvWeight, stride=1, pad=0, bias=None, resid
     b = None if bias is None else bias.contiguous().float()
     check(lib().bq_conv2d_i8_nhwc(qx.contiguous().data_ptr(), N, H, W, C, wq.q.data_ptr(), wq.O, wq.KH, wq.KW,
                                   stride, pad, sa.data_ptr(), wq.s.data_ptr(), _ptr(b), _ptr(res), act,
-                                  out.data_ptr(), _ptr(acc), _stream(qx)))
+                                  out.data_ptr(), _ptr(acc), *_ws_args(qx.device), _stream(qx)))
     return (out, acc) if want_acc else out
 
 
@@ -311,7 +338,8 @@ def conv2d_i8_nhwc_q(qx, sa, wq: Int8ConvWeight, s_out, stride=1, pad=0, bias=No
     b = None if bias is None else bias.contiguous().float()
     check(lib().bq_conv2d_i8_nhwc_q(qx.contiguous().data_ptr(), N, H, W, C, wq.q.data_ptr(), wq.O, wq.KH, wq.KW,
                                     stride, pad, sa.data_ptr(), wq.s.data_ptr(), _ptr(b), _ptr(res), act,
-                                    out.data_ptr(), None, s_out.data_ptr(), q.data_ptr(), _stream(qx)))
+                                    out.data_ptr(), None, s_out.data_ptr(), q.data_ptr(), *_ws_args(qx.device),
+                                    _stream(qx)))
     return out, q
 
 

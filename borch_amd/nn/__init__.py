@@ -178,6 +178,8 @@ class Conv2d(_tnn.Module):
         with torch.no_grad():
             w = self.weight.detach()
             self.int8 = _i8.pack_conv_weight(w) if self.groups == 1 else _i8.pack_dw_weight(w)
+        if self.groups == 1:
+            _i8.split_workspace(self.weight.device)  # made now, before any graph capture
         return True
 
     def _int8_input(self, x):

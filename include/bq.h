@@ -92,23 +92,37 @@ int bq_quantize_nhwc(const float* x, int64_t P, int64_t C, int64_t Cpad, int8_t*
 int bq_quantize_nhwc_scaled(const float* x, int64_t P, int64_t C, int64_t Cpad, const float* s, int8_t* q,
                             bq_stream_t stream);
 
+/* Bytes of the split-K workspace `ws` that bq_gemm_i8 / bq_conv2d_i8_nhwc(_q) can use, for
+ * any shape (about 6.5 MiB). With it, a grid that would leave most CUs idle (few output
+ * tiles, long K: e.g. the late layers of a CIFAR ResNet at small batch) is split along K
+ * into several workgroups per tile; the int32 partial tiles are added exactly by the last
+ * workgroup of each tile, in the same launch, so results are bit-identical to the unsplit
+ * kernel. `ws` must be zero-filled before its first use; every call leaves its counters
+ * zero again. Calls that share one `ws` must not run concurrently (use one per stream).
+ * ws == NULL (or ws_bytes smaller than this) runs the unsplit kernel. The reference splits
+ * K with f32 slabs and a second pass (convInt8Split / sumSplitsConv,
+ * borch-ts/src/kernels.ts:2120-2127, 5860-5914). */
+size_t bq_gemm_ws_bytes(void);
+
 /* W8A8 GEMM with the fused dequant epilogue, Linear layout (x @ W.T):
  *   A int8 [M, K] (per-row scales sA f32 [M]), W int8 [N, K] (per-channel sW f32 [N]),
  *   out f32 [M, N] = ((f32(A @ W.T) * sA[m]) * sW[n]) + bias[n] (bias nullable), then
  *   the activation `act` (BQ_ACT_*). `acc` (nullable) receives the exact int32 [M, N].
  * K % 16 == 0 and K <= 133152 (K * 127^2 < 2^31: the int32 sums are exact for any
- * operands); A, W 16-byte aligned. Replaces matmulInt8(M,K,N,scaled)
+ * operands); A, W 16-byte aligned. ws: the split-K workspace (nullable, see
+ * bq_gemm_ws_bytes). Replaces matmulInt8(M,K,N,scaled)
  * (borch-ts/src/kernels.ts:1808-1852), which took only whole 32s. */
 int bq_gemm_i8(const int8_t* A, const int8_t* W, int64_t M, int64_t N, int64_t K,
                const float* sA, const float* sW, const float* bias, int act, float* out,
-               int32_t* acc, bq_stream_t stream);
+               int32_t* acc, void* ws, size_t ws_bytes, bq_stream_t stream);
 
 /* Implicit-GEMM int8 convolution, NHWC, groups 1, dilation 1:
  *   x int8 [N, H, W, C] (C % 16 == 0, per-tensor scale sA f32 [1]),
  *   w int8 [O, KH, KW, C] (per-channel scale sW f32 [O]),
  *   out f32 [N, OH, OW, O] = ((f32(acc) * sA) * sW[o]) + bias[o] + residual, then act.
  * bias, residual (f32 [N, OH, OW, O]) and acc (int32 [N*OH*OW, O]) are nullable;
- * KH*KW*C <= 133152 (exact int32 sums).
+ * KH*KW*C <= 133152 (exact int32 sums). ws: the split-K workspace (nullable, see
+ * bq_gemm_ws_bytes).
  * Replaces convForwardInt8 (+ sumSplitsConv) and its ConvEpilogue
  * (borch-ts/src/kernels.ts:2156-2302, 4230-4244, 5860-5914), which took stride 1, k <= 3,
  * C % 32 and O % 16 only. */
@@ -116,7 +130,7 @@ int bq_conv2d_i8_nhwc(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t 
                       const int8_t* w, int64_t O, int64_t KH, int64_t KW, int64_t stride,
                       int64_t pad, const float* sA, const float* sW, const float* bias,
                       const float* residual, int act, float* out, int32_t* acc,
-                      bq_stream_t stream);
+                      void* ws, size_t ws_bytes, bq_stream_t stream);
 
 /* bq_conv2d_i8_nhwc that also writes the output's int8 twin with a calibrated scale:
  * q_out int8 [N, OH, OW, O] = clip(rint(y / s_out[0]), +-127) (exact quotient, half to even) of the final f32 y
@@ -127,7 +141,8 @@ int bq_conv2d_i8_nhwc(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t 
 int bq_conv2d_i8_nhwc_q(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t C, const int8_t* w,
                         int64_t O, int64_t KH, int64_t KW, int64_t stride, int64_t pad, const float* sA,
                         const float* sW, const float* bias, const float* residual, int act, float* out,
-                        int32_t* acc, const float* s_out, int8_t* q_out, bq_stream_t stream);
+                        int32_t* acc, const float* s_out, int8_t* q_out, void* ws, size_t ws_bytes,
+                        bq_stream_t stream);
 
 /* Depthwise int8 convolution, NHWC (groups = C, channel multiplier 1):
  *   x int8 [N, H, W, C] (C % 4 == 0, per-tensor sA f32 [1]), w int8 [KH*KW, C]

@@ -226,6 +226,76 @@ def test_conv2d(dev, N, C, H, O_, k, stride, pad):
         assert_f32(n(y), y_o)
 
 
+# ---------------------------------------------------------------------------- split-K
+
+def _gemm_c(qa, qw, sa, sw, b, out, acc, ws):
+    from borch_amd import _lib
+    M, K = qa.shape
+    N = qw.shape[0]
+    wp, wn = (None, 0) if ws is None else (ws.data_ptr(), ws.numel())
+    _lib.check(_lib.lib().bq_gemm_i8(qa.data_ptr(), qw.data_ptr(), M, N, K, sa.data_ptr(), sw.data_ptr(),
+                                     b.data_ptr(), 0, out.data_ptr(), acc.data_ptr(), wp, wn,
+                                     torch.cuda.current_stream().cuda_stream))
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 512, 4608), (100, 200, 4112), (1024, 256, 4096), (65, 64, 8192),
+                                   (130, 700, 5008), (1024, 256, 2304)])
+def test_split_k_matches_unsplit(dev, M, N, K):
+    """Grids of few 64x64 tiles over long K split along K (one launch, exact int32 partials,
+    the last workgroup of a tile reduces; 4 to 16 splits here, ragged tiles included):
+    bit-identical to the unsplit kernel (no workspace) and to the oracle, on repeated calls
+    and on graph replays (the tile counters reset themselves). The last shape stays unsplit
+    (too few stages): the same check holds trivially."""
+    say(f"split-K M={M} N={N} K={K}")
+    rng = np.random.default_rng(M * 7 + N + K)
+    qa = t(rng.integers(-127, 128, size=(M, K)).astype(np.int8), dev)
+    qw = t(rng.integers(-127, 128, size=(N, K)).astype(np.int8), dev)
+    sa = t(rng.uniform(1e-3, 1e-2, M).astype(np.float32), dev)
+    sw = t(rng.uniform(1e-3, 1e-2, N).astype(np.float32), dev)
+    b = t(rng.normal(size=N).astype(np.float32), dev)
+    ws = I.split_workspace(dev)
+    outs = [(torch.empty(M, N, device=dev), torch.empty(M, N, dtype=torch.int32, device=dev)) for _ in range(4)]
+    _gemm_c(qa, qw, sa, sw, b, *outs[0], None)
+    for o in outs[1:3]:
+        _gemm_c(qa, qw, sa, sw, b, *o, ws)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        _gemm_c(qa, qw, sa, sw, b, *outs[3], ws)
+    for _ in range(3):
+        outs[3][0].zero_()
+        outs[3][1].zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(outs[3][1], outs[0][1]) and torch.equal(outs[3][0], outs[0][0])
+    torch.cuda.synchronize()
+    for o in outs[1:]:
+        assert torch.equal(o[1], outs[0][1])
+        assert torch.equal(o[0], outs[0][0])
+    assert np.array_equal(n(outs[0][1]), O.gemm_i8_i32(n(qa), n(qw)))
+    assert int(ws[:4096].count_nonzero()) == 0  # every tile counter back at zero
+
+
+def test_split_k_conv_twin_residual(dev):
+    """A CIFAR ResNet stage-4 conv at batch 16 (256 pixels, K = 4608: 32 tiles split 8 ways)
+    with residual, ReLU and the int8 output twin: bit-exact against the oracle."""
+    say("split-K conv stage 4 with residual + twin")
+    rng = np.random.default_rng(44)
+    N, C, H, O_ = 16, 512, 4, 512
+    x = np.maximum(rng.normal(size=(N, C, H, H)), 0).astype(np.float32)
+    w = (rng.normal(size=(O_, C, 3, 3)) * np.sqrt(2.0 / (C * 9))).astype(np.float32)
+    b = (rng.normal(size=O_) * 0.1).astype(np.float32)
+    res = rng.normal(size=(N, O_, H, H)).astype(np.float32)
+    w8 = I.pack_conv_weight(t(w, dev))
+    y_o, acc_o, sa_o, _ = O.conv2d_int8(x, w, b, 1, 1, True, res, C)
+    qx, sa = I.quantize_nhwc(t(x, dev), C)
+    s_out_v = float(np.float32(np.abs(y_o).max()) / np.float32(127.0))
+    s_out = torch.tensor([s_out_v], dtype=torch.float32, device=dev)
+    y, q = I.conv2d_i8_nhwc_q(qx, sa, w8, s_out, 1, 1, t(b, dev), t(res, dev), I.ACT_RELU)
+    assert_f32(n(y), y_o)
+    q_o = O.quantize_with_scale(y_o.transpose(0, 2, 3, 1), np.float32(s_out_v))
+    assert np.array_equal(n(q), q_o)
+
+
 # 3x3 / 5x5 at stride 1 / 2 take the register-blocked kernel (8 or 4 channels a thread;
 # output widths that are not a multiple of its pixel block); 7x7 and the rest the generic one.
 DW_CASES = [(2, 32, 16, 3, 1, 1), (2, 96, 15, 3, 2, 1), (2, 144, 14, 5, 1, 2), (2, 240, 13, 5, 2, 2),
