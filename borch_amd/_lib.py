@@ -46,10 +46,12 @@ SIGNATURES = {
                             _c_size, _c_p]),
     "bq_conv2d_i8_nhwc_q": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i64,
                                      _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_int, _c_p, _c_p, _c_p, _c_p,
-                                     _c_p, _c_size, _c_p]),
+                                     _c_p, _c_p, _c_size, _c_p]),
+    "bq_conv2d_absmax_parts": (_c_i64, [_c_i64] * 9),
     "bq_conv2d_i8_nhwc": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i64,
-                                   _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_int, _c_p, _c_p, _c_p, _c_size,
-                                   _c_p]),
+                                   _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_int, _c_p, _c_p, _c_p, _c_p,
+                                   _c_size, _c_p]),
+    "bq_quantize_nhwc_parts": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_p]),
     "bq_dwconv_i8_nhwc": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i64,
                                    _c_i64, _c_p, _c_p, _c_p, _c_int, _c_p, _c_p, _c_p]),
     "bq_gemv_w8a32": (_c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_int, _c_p, _c_p]),

@@ -54,6 +54,10 @@ struct GemmP {
   int ksplit;
   int32_t* part;  // [tiles][ksplit][BM * BN] int32, in the accumulator register order
   int* cnt;       // [tiles], zero between launches
+  // Tiled kernel only (nullable): max |y| over each output tile's final values (after bias,
+  // residual and activation), one float per tile at bm * tiles_n + bn — the partial maxima
+  // from which the next layer's per-tensor quantizer takes its scale without a max pass.
+  float* amax;
 };
 
 // Division by a run-time invariant d >= 1 of any n < 2^31 as (umulhi(n, mul) + n) >> shift
@@ -387,6 +391,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
   __shared__ __attribute__((aligned(16))) float s_sw[BN];
   __shared__ __attribute__((aligned(16))) float s_b[BN];
   __shared__ int s_last;  // split-K: this workgroup is the last of its tile
+  __shared__ float s_wmax[WAVES_M * WAVES_N];  // per-wave max |y| (p.amax)
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -488,6 +493,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
   constexpr int C4 = WTN / 4;                 // float4 columns per row
   constexpr int ROWS_PER_STORE = 64 / C4;     // rows one 64-lane store covers
   const bool has_r = p.res != nullptr;
+  float amax = 0.f;  // max |y| of the values this lane stores (fmaxf: a NaN is skipped)
   // One slice per compile-time i (a run-time i would index the accumulators dynamically
   // and send them to scratch memory).
   auto slice = [&](auto ic) {
@@ -537,6 +543,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
           if (p.q_out)
             *reinterpret_cast<uint32_t*>(p.q_out + idx) =
                 pack4(quant_one(o.x, s_out), quant_one(o.y, s_out), quant_one(o.z, s_out), quant_one(o.w, s_out));
+          amax = fmaxf(amax, fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w))));
         }
       }
     } else if (!p.vec_ok) {
@@ -555,6 +562,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
             p.out[idx] = o;
             if (p.acc) p.acc[idx] = a;
             if (p.q_out) p.q_out[idx] = (int8_t)quant_one(o, s_out);
+            amax = fmaxf(amax, fabsf(o));
           }
         }
       }
@@ -565,6 +573,17 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
   [&]<int... Is>(std::integer_sequence<int, Is...>) {
     (slice(std::integral_constant<int, Is>{}), ...);
   }(std::make_integer_sequence<int, TM>{});
+  if (p.amax) {  // uniform: every wave of the workgroup takes it
+    amax = wave_max(amax);
+    if (lane == 0) s_wmax[wave] = amax;
+    __syncthreads();
+    if (tid == 0) {
+      float m = s_wmax[0];
+#pragma unroll
+      for (int w = 1; w < WAVES_M * WAVES_N; ++w) m = fmaxf(m, s_wmax[w]);
+      p.amax[bm * tiles_n + bn] = m;
+    }
+  }
 }
 
 // ----------------------------------------------------------------------------- skinny
@@ -1002,16 +1021,55 @@ static int forced_cfg() {
   return cfg;
 }
 
+// Tiled-kernel configurations, by id: <BM, BN, waves M x N, ring depth, fragment distance>.
+//   1 <256,256,2,4,2,1>  2 <256,256,2,4,2,2>  3 <256,256,2,2,2,2>  4 <128,128,2,2,4,2>
+//   5 <128,128,2,2,2,2>  6 <256,128,2,2,3,1>  7 <64,64,2,2,4,2>    8 <256,64,4,1,3,1>
+//   9 <64,64,2,2,8,1>   10 <64,64,2,2,2,2>   11 <128,64,4,1,2,1>  12 <128,32,4,1,2,1>
+//  13 <256,64,4,1,2,1>  14 <128,64,4,1,3,1>
+struct TileDims {
+  int bm, bn;
+};
+constexpr TileDims CFG_TILES[15] = {{0, 0},    {256, 256}, {256, 256}, {256, 256}, {128, 128},
+                                    {128, 128}, {256, 128}, {64, 64},   {256, 64},  {64, 64},
+                                    {64, 64},   {128, 64},  {128, 32},  {256, 64},  {128, 64}};
+
+// The configuration the tiled kernel runs for M x N x K. Narrow outputs (N <= 64: 1x1 convs
+// of mobile networks, the stem, early ResNet layers) take small-LDS tiles that fit several
+// workgroups per CU (measured 2-2.5x over a 256x64 tile at K <= 240 and 5-15% at
+// K = 2304-4096). Otherwise the largest tile that still fills the chip (>= 192 / 128
+// workgroups) without wasting most of its columns. Ring depth: deep rings keep several
+// stages of a small tile's operands in flight; when there are more tiles than CUs, a small
+// tile takes the 2-deep ring instead so that several workgroups share a CU. The 256x256
+// tile's 64 KB stages leave room for two buffers only. Small tiles read their fragments two
+// K slices ahead (short MFMA runs).
+static int choose_cfg(const GemmP& p) {
+  if (forced_cfg() >= 1 && forced_cfg() <= 14) return forced_cfg();
+  const long long t256 = (long long)((p.M + 255) / 256) * ((p.N + 255) / 256);
+  const long long t128 = (long long)((p.M + 127) / 128) * ((p.N + 127) / 128);
+  const long long t128x32 = (long long)((p.M + 127) / 128) * ((p.N + 31) / 32);
+  const long long t64 = (long long)((p.M + 63) / 64) * ((p.N + 63) / 64);
+  if (p.N <= 32 && t128x32 >= 128) return 12;
+  if (p.N <= 64 && t64 > 256) return 10;
+  if (t256 >= 192 && p.N >= 192) return 1;
+  if (t128 >= 128 && p.N >= 96) return t128 > 256 ? 5 : 4;
+  return 7;
+}
+
+// Output tiles of the tiled kernel for this problem (the length of its absmax output).
+static long long out_tiles(const GemmP& p) {
+  const TileDims d = CFG_TILES[choose_cfg(p)];
+  return (long long)((p.M + d.bm - 1) / d.bm) * ((p.N + d.bn - 1) / d.bn);
+}
+
 template <bool CONV>
 static void launch_gemm(const GemmP& p, hipStream_t st, const Ws& ws) {
-  switch (forced_cfg()) {  // <BM, BN, waves M x N, ring depth, fragment distance>
+  switch (choose_cfg(p)) {
     case 1: return launch_tiled<256, 256, 2, 4, CONV, 2, 1>(p, st, ws);
     case 2: return launch_tiled<256, 256, 2, 4, CONV, 2, 2>(p, st, ws);
     case 3: return launch_tiled<256, 256, 2, 2, CONV, 2, 2>(p, st, ws);
     case 4: return launch_tiled<128, 128, 2, 2, CONV, 4, 2>(p, st, ws);
     case 5: return launch_tiled<128, 128, 2, 2, CONV, 2, 2>(p, st, ws);
     case 6: return launch_tiled<256, 128, 2, 2, CONV, 3, 1>(p, st, ws);
-    case 7: return launch_tiled<64, 64, 2, 2, CONV, 4, 2>(p, st, ws);
     case 8: return launch_tiled<256, 64, 4, 1, CONV, 3, 1>(p, st, ws);
     case 9: return launch_tiled<64, 64, 2, 2, CONV, 8, 1>(p, st, ws);
     case 10: return launch_tiled<64, 64, 2, 2, CONV, 2, 2>(p, st, ws);
@@ -1019,33 +1077,8 @@ static void launch_gemm(const GemmP& p, hipStream_t st, const Ws& ws) {
     case 12: return launch_tiled<128, 32, 4, 1, CONV, 2, 1>(p, st, ws);
     case 13: return launch_tiled<256, 64, 4, 1, CONV, 2, 1>(p, st, ws);
     case 14: return launch_tiled<128, 64, 4, 1, CONV, 3, 1>(p, st, ws);
-    default: break;
+    default: return launch_tiled<64, 64, 2, 2, CONV, 4, 2>(p, st, ws);
   }
-  // Narrow outputs (N <= 64: 1x1 convs of mobile networks, the stem, early ResNet layers)
-  // take small-LDS tiles that fit several workgroups per CU (measured 2-2.5x over a 256x64
-  // tile at K <= 240 and 5-15% at K = 2304-4096). Otherwise the largest tile that still
-  // fills the chip (>= 192 / 128 workgroups) without wasting most of its columns.
-  // Ring depth: deep rings keep several stages of a small tile's operands in flight; when
-  // there are more tiles than CUs, a small tile takes the 2-deep ring instead so that
-  // several workgroups share a CU. The 256x256 tile's 64 KB stages leave room for two
-  // buffers only. Small tiles read their fragments two K slices ahead (short MFMA runs).
-  const long long t256 = (long long)((p.M + 255) / 256) * ((p.N + 255) / 256);
-  const long long t128 = (long long)((p.M + 127) / 128) * ((p.N + 127) / 128);
-  const long long t128x32 = (long long)((p.M + 127) / 128) * ((p.N + 31) / 32);
-  const long long t64 = (long long)((p.M + 63) / 64) * ((p.N + 63) / 64);
-  if (p.N <= 32 && t128x32 >= 128)
-    launch_tiled<128, 32, 4, 1, CONV, 2, 1>(p, st, ws);
-  else if (p.N <= 64 && t64 > 256)
-    launch_tiled<64, 64, 2, 2, CONV, 2, 2>(p, st, ws);
-  else if (t256 >= 192 && p.N >= 192)
-    launch_tiled<256, 256, 2, 4, CONV, 2, 1>(p, st, ws);
-  else if (t128 >= 128 && p.N >= 96) {
-    if (t128 > 256)
-      launch_tiled<128, 128, 2, 2, CONV, 2, 2>(p, st, ws);
-    else
-      launch_tiled<128, 128, 2, 2, CONV, 4, 2>(p, st, ws);
-  } else
-    launch_tiled<64, 64, 2, 2, CONV, 4, 2>(p, st, ws);
 }
 
 static bool aligned16(const void* q) { return ((uintptr_t)q & 15) == 0; }
@@ -1106,8 +1139,8 @@ int bq_gemm_i8(const int8_t* A, const int8_t* W, int64_t M, int64_t N, int64_t K
 static int conv_impl(const char* what, const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t C,
                      const int8_t* w, int64_t O, int64_t KH, int64_t KW, int64_t stride, int64_t pad,
                      const float* sA, const float* sW, const float* bias, const float* residual, int act,
-                     float* out, int32_t* acc, const float* s_out, int8_t* q_out, void* ws, size_t ws_bytes,
-                     bq_stream_t stream) {
+                     float* out, int32_t* acc, const float* s_out, int8_t* q_out, float* amax, void* ws,
+                     size_t ws_bytes, bq_stream_t stream) {
   if (N < 0 || H < 1 || W < 1 || C < 1 || O < 1 || KH < 1 || KW < 1 || stride < 1 || pad < 0)
     return set_error(BQ_ERR_ARG, "%s: bad geometry", what);
   if (C % 16) return set_error(BQ_ERR_UNSUPPORTED, "%s: C=%lld is not a multiple of 16 (pad it)", what, (long long)C);
@@ -1137,6 +1170,7 @@ static int conv_impl(const char* what, const int8_t* x, int64_t N, int64_t H, in
   p.vec_ok = (O % 4 == 0) && aligned16(out) && aligned16(acc) && aligned16(residual) && ((uintptr_t)q_out & 3) == 0;
   p.s_out = s_out;
   p.q_out = q_out;
+  p.amax = amax;
   hipStream_t st = (hipStream_t)stream;
   if (KH == 1 && KW == 1 && stride == 1 && pad == 0)
     launch_gemm<false>(p, st, Ws{ws, ws_bytes});  // a 1x1 conv is the dense GEMM on [N*H*W, C]
@@ -1145,23 +1179,37 @@ static int conv_impl(const char* what, const int8_t* x, int64_t N, int64_t H, in
   return check_launch(what);
 }
 
+int64_t bq_conv2d_absmax_parts(int64_t N, int64_t H, int64_t W, int64_t C, int64_t O, int64_t KH, int64_t KW,
+                               int64_t stride, int64_t pad) {
+  if (N < 0 || H < 1 || W < 1 || C < 1 || O < 1 || KH < 1 || KW < 1 || stride < 1 || pad < 0 ||
+      H + 2 * pad < KH || W + 2 * pad < KW)
+    return set_error(BQ_ERR_ARG, "bq_conv2d_absmax_parts: bad geometry");
+  const int64_t OH = (H + 2 * pad - KH) / stride + 1;
+  const int64_t OW = (W + 2 * pad - KW) / stride + 1;
+  if (N * OH * OW > 0x7fffffff || O > 0x7fffffff) return set_error(BQ_ERR_ARG, "bq_conv2d_absmax_parts: size too large");
+  GemmP p{};
+  p.M = (int)(N * OH * OW);
+  p.N = (int)O;
+  return p.M == 0 ? 0 : out_tiles(p);
+}
+
 int bq_conv2d_i8_nhwc(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t C, const int8_t* w,
                       int64_t O, int64_t KH, int64_t KW, int64_t stride, int64_t pad, const float* sA,
                       const float* sW, const float* bias, const float* residual, int act, float* out,
-                      int32_t* acc, void* ws, size_t ws_bytes, bq_stream_t stream) {
+                      int32_t* acc, float* absmax_parts, void* ws, size_t ws_bytes, bq_stream_t stream) {
   return conv_impl("bq_conv2d_i8_nhwc", x, N, H, W, C, w, O, KH, KW, stride, pad, sA, sW, bias, residual, act, out,
-                   acc, nullptr, nullptr, ws, ws_bytes, stream);
+                   acc, nullptr, nullptr, absmax_parts, ws, ws_bytes, stream);
 }
 
 int bq_conv2d_i8_nhwc_q(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t C, const int8_t* w,
                         int64_t O, int64_t KH, int64_t KW, int64_t stride, int64_t pad, const float* sA,
                         const float* sW, const float* bias, const float* residual, int act, float* out,
-                        int32_t* acc, const float* s_out, int8_t* q_out, void* ws, size_t ws_bytes,
-                        bq_stream_t stream) {
+                        int32_t* acc, const float* s_out, int8_t* q_out, float* absmax_parts, void* ws,
+                        size_t ws_bytes, bq_stream_t stream) {
   if (!s_out || !q_out) return set_error(BQ_ERR_ARG, "bq_conv2d_i8_nhwc_q: null s_out or q_out");
   if (O % 16) return set_error(BQ_ERR_UNSUPPORTED, "bq_conv2d_i8_nhwc_q: O=%lld is not a multiple of 16", (long long)O);
   return conv_impl("bq_conv2d_i8_nhwc_q", x, N, H, W, C, w, O, KH, KW, stride, pad, sA, sW, bias, residual, act,
-                   out, acc, s_out, q_out, ws, ws_bytes, stream);
+                   out, acc, s_out, q_out, absmax_parts, ws, ws_bytes, stream);
 }
 
 int bq_dwconv_i8_nhwc(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t C, const int8_t* w, int64_t KH,

@@ -261,21 +261,31 @@ int bq_quantize_weight_per_channel(const float* w, int64_t N, int64_t K, int8_t*
 
 size_t bq_quantize_tensor_ws_bytes(int64_t n) { return (size_t)nparts_for(n < 0 ? 0 : n) * sizeof(float); }
 
+// Per-tensor quantization of x [P, C] into q [P, Cpad]. The scale is, in this order of
+// precedence: s_given (calibrated); from given_parts (partial maxima a producer wrote, e.g.
+// the conv epilogue's per-tile max |y|); else from partial maxima computed here into ws.
 static int quantize_nhwc_impl(const char* what, const float* x, int64_t P, int64_t C, int64_t Cpad, int8_t* q,
-                              float* s, const float* s_given, void* ws, size_t ws_bytes, hipStream_t st) {
+                              float* s, const float* s_given, void* ws, size_t ws_bytes, hipStream_t st,
+                              const float* given_parts = nullptr, int64_t given_np = 0) {
   if (P < 0 || C < 0 || Cpad < C) return set_error(BQ_ERR_ARG, "%s: bad sizes P=%lld C=%lld Cpad=%lld", what, (long long)P, (long long)C, (long long)Cpad);
-  if (!x || !q || (!s && !s_given) || (!ws && !s_given)) return set_error(BQ_ERR_ARG, "%s: null pointer", what);
+  if (!x || !q || (!s && !s_given) || (!ws && !s_given && !given_parts))
+    return set_error(BQ_ERR_ARG, "%s: null pointer", what);
   if (Cpad > 0x7fffffff) return set_error(BQ_ERR_ARG, "%s: too many channels", what);
   const int64_t n = P * C;
   int np = 0;
-  float* parts = nullptr;
-  if (!s_given) {
+  const float* parts = nullptr;
+  if (given_parts) {
+    if (given_np < 1 || given_np > 0x7fffffff) return set_error(BQ_ERR_ARG, "%s: bad partial count %lld", what, (long long)given_np);
+    parts = given_parts;
+    np = (int)given_np;
+  } else if (!s_given) {
     np = nparts_for(n);
     if (ws_bytes < (size_t)np * sizeof(float))
       return set_error(BQ_ERR_ARG, "%s: workspace %zu bytes, need %zu", what, ws_bytes, (size_t)np * sizeof(float));
-    parts = (float*)ws;
+    float* wparts = (float*)ws;
+    parts = wparts;
     const int64_t chunk = n == 0 ? 1 : (n + np - 1) / np;
-    absmax_parts_kernel<<<np, QT_THREADS, 0, st>>>(x, n, ((chunk + 3) / 4) * 4, parts);
+    absmax_parts_kernel<<<np, QT_THREADS, 0, st>>>(x, n, ((chunk + 3) / 4) * 4, wparts);
     if (int r = check_launch(what)) return r;
   }
   if (C != Cpad && Cpad % 16 == 0 && ((uintptr_t)q & 15) == 0) {
@@ -297,6 +307,13 @@ static int quantize_nhwc_impl(const char* what, const float* x, int64_t P, int64
 int bq_quantize_nhwc(const float* x, int64_t P, int64_t C, int64_t Cpad, int8_t* q, float* s, void* ws,
                      size_t ws_bytes, bq_stream_t stream) {
   return quantize_nhwc_impl("bq_quantize_nhwc", x, P, C, Cpad, q, s, nullptr, ws, ws_bytes, (hipStream_t)stream);
+}
+
+int bq_quantize_nhwc_parts(const float* x, int64_t P, int64_t C, int64_t Cpad, const float* absmax_parts,
+                           int64_t nparts, int8_t* q, float* s, bq_stream_t stream) {
+  if (!absmax_parts) return set_error(BQ_ERR_ARG, "bq_quantize_nhwc_parts: null partial maxima");
+  return quantize_nhwc_impl("bq_quantize_nhwc_parts", x, P, C, Cpad, q, s, nullptr, nullptr, 0, (hipStream_t)stream,
+                            absmax_parts, nparts);
 }
 
 int bq_quantize_nhwc_scaled(const float* x, int64_t P, int64_t C, int64_t Cpad, const float* s, int8_t* q,

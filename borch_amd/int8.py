@@ -120,7 +120,9 @@ def quantize_tensor(x: torch.Tensor):
 def quantize_nhwc(x: torch.Tensor, cpad: int | None = None):
     """Per-tensor int8 of an NCHW f32 activation into NHWC int8 with channels padded to
     ``cpad`` (zeros) → ``(q int8 [N, H, W, cpad], s f32 [1])``. A channels-last input is
-    read in place; a contiguous NCHW input is converted first."""
+    read in place; a contiguous NCHW input is converted first. An unmodified output of
+    ``conv2d_i8_nhwc`` carries its per-tile maxima, and then one pass suffices
+    (bq_quantize_nhwc_parts); otherwise partial maxima are computed first (bq_quantize_nhwc)."""
     if x.dtype != torch.float32:
         raise TypeError(f"int8 path takes float32 activations, got {x.dtype}")
     require_device(x.device)
@@ -130,6 +132,12 @@ def quantize_nhwc(x: torch.Tensor, cpad: int | None = None):
     q = torch.empty((N, H, W, cpad), dtype=torch.int8, device=x.device)
     s = torch.empty((1,), dtype=torch.float32, device=x.device)
     P = N * H * W
+    parts = getattr(xl, "_bq_absmax", None)
+    if parts is not None and parts[2] == xl._version:
+        # the producing conv's per-tile max |y| (bq_conv2d_i8_nhwc): no max pass over x
+        check(lib().bq_quantize_nhwc_parts(xl.data_ptr(), P, C, cpad, parts[0].data_ptr(), parts[1], q.data_ptr(),
+                                           s.data_ptr(), _stream(x)))
+        return q, s
     ws = _ws(P * C, x.device)
     check(lib().bq_quantize_nhwc(xl.data_ptr(), P, C, cpad, q.data_ptr(), s.data_ptr(), ws.data_ptr(),
                                  ws.numel(), _stream(x)))
@@ -311,10 +319,20 @@ def conv2d_i8_nhwc(qx, sa, wq: Int8ConvWeight, stride=1, pad=0, bias=None, resid
         res = residual.float().contiguous(memory_format=torch.channels_last)
     acc = torch.empty((N * OH * OW, wq.O), dtype=torch.int32, device=qx.device) if want_acc else None
     b = None if bias is None else bias.contiguous().float()
+    parts, nparts = _absmax_parts(N, H, W, C, wq, stride, pad, qx.device)
     check(lib().bq_conv2d_i8_nhwc(qx.contiguous().data_ptr(), N, H, W, C, wq.q.data_ptr(), wq.O, wq.KH, wq.KW,
                                   stride, pad, sa.data_ptr(), wq.s.data_ptr(), _ptr(b), _ptr(res), act,
-                                  out.data_ptr(), _ptr(acc), *_ws_args(qx.device), _stream(qx)))
+                                  out.data_ptr(), _ptr(acc), parts.data_ptr(), *_ws_args(qx.device), _stream(qx)))
+    out._bq_absmax = (parts, nparts, out._version)
     return (out, acc) if want_acc else out
+
+
+def _absmax_parts(N, H, W, C, wq, stride, pad, device):
+    """The buffer a conv's epilogue fills with its per-tile max |y| (bq_conv2d_absmax_parts)."""
+    n = int(lib().bq_conv2d_absmax_parts(N, H, W, C, wq.O, wq.KH, wq.KW, stride, pad))
+    if n < 0:
+        check(n)
+    return torch.empty((max(n, 1),), dtype=torch.float32, device=device), max(n, 1)
 
 
 def conv2d_i8_nhwc_q(qx, sa, wq: Int8ConvWeight, s_out, stride=1, pad=0, bias=None, residual=None, act=ACT_NONE):
@@ -336,10 +354,11 @@ def conv2d_i8_nhwc_q(qx, sa, wq: Int8ConvWeight, s_out, stride=1, pad=0, bias=No
             raise RuntimeError(f"residual shape {tuple(residual.shape)} != output {(N, wq.O, OH, OW)}")
         res = residual.float().contiguous(memory_format=torch.channels_last)
     b = None if bias is None else bias.contiguous().float()
+    # no per-tile maxima: a calibrated layer's consumer takes the twin or its own static scale
     check(lib().bq_conv2d_i8_nhwc_q(qx.contiguous().data_ptr(), N, H, W, C, wq.q.data_ptr(), wq.O, wq.KH, wq.KW,
                                     stride, pad, sa.data_ptr(), wq.s.data_ptr(), _ptr(b), _ptr(res), act,
-                                    out.data_ptr(), None, s_out.data_ptr(), q.data_ptr(), *_ws_args(qx.device),
-                                    _stream(qx)))
+                                    out.data_ptr(), None, s_out.data_ptr(), q.data_ptr(), None,
+                                    *_ws_args(qx.device), _stream(qx)))
     return out, q
 
 

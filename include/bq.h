@@ -86,6 +86,14 @@ int bq_quantize_tensor(const float* x, int64_t n, int8_t* q, float* s, void* ws,
 int bq_quantize_nhwc(const float* x, int64_t P, int64_t C, int64_t Cpad, int8_t* q, float* s,
                      void* ws, size_t ws_bytes, bq_stream_t stream);
 
+/* The same quantization with the scale taken from partial maxima a producer already wrote:
+ * absmax_parts f32 [nparts] whose maximum is max|x| (bq_conv2d_i8_nhwc's per-tile output
+ * maxima). One pass over x, no max pass; the scale is bit-identical to bq_quantize_nhwc's
+ * (a maximum does not depend on how it is split). The reference's producer-side shortcut
+ * is the calibrated twin (tensor.ts:11909-11913); this is its dynamic-scale counterpart. */
+int bq_quantize_nhwc_parts(const float* x, int64_t P, int64_t C, int64_t Cpad, const float* absmax_parts,
+                           int64_t nparts, int8_t* q, float* s, bq_stream_t stream);
+
 /* The same quantization with a given (calibrated) scale s f32 [1]: one pass, no maximum.
  * The static-scale input of borch-ts (int8.inMax, tensor.ts:11912-11913; calibrateInt8
  * nn.ts:6790-6824). Values beyond the calibrated range clamp to +-127. */
@@ -122,7 +130,9 @@ int bq_gemm_i8(const int8_t* A, const int8_t* W, int64_t M, int64_t N, int64_t K
  *   out f32 [N, OH, OW, O] = ((f32(acc) * sA) * sW[o]) + bias[o] + residual, then act.
  * bias, residual (f32 [N, OH, OW, O]) and acc (int32 [N*OH*OW, O]) are nullable;
  * KH*KW*C <= 133152 (exact int32 sums). ws: the split-K workspace (nullable, see
- * bq_gemm_ws_bytes).
+ * bq_gemm_ws_bytes). absmax_parts (nullable, bq_conv2d_absmax_parts floats) receives
+ * max|out| of each output tile: the next conv's bq_quantize_nhwc_parts then needs no max
+ * pass over this output.
  * Replaces convForwardInt8 (+ sumSplitsConv) and its ConvEpilogue
  * (borch-ts/src/kernels.ts:2156-2302, 4230-4244, 5860-5914), which took stride 1, k <= 3,
  * C % 32 and O % 16 only. */
@@ -130,7 +140,12 @@ int bq_conv2d_i8_nhwc(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t 
                       const int8_t* w, int64_t O, int64_t KH, int64_t KW, int64_t stride,
                       int64_t pad, const float* sA, const float* sW, const float* bias,
                       const float* residual, int act, float* out, int32_t* acc,
-                      void* ws, size_t ws_bytes, bq_stream_t stream);
+                      float* absmax_parts, void* ws, size_t ws_bytes, bq_stream_t stream);
+
+/* The number of floats bq_conv2d_i8_nhwc(_q) writes to a non-null `absmax_parts` for this
+ * geometry (its output tile count), or a negative BQ_ERR_* for a bad geometry. */
+int64_t bq_conv2d_absmax_parts(int64_t N, int64_t H, int64_t W, int64_t C, int64_t O, int64_t KH, int64_t KW,
+                               int64_t stride, int64_t pad);
 
 /* bq_conv2d_i8_nhwc that also writes the output's int8 twin with a calibrated scale:
  * q_out int8 [N, OH, OW, O] = clip(rint(y / s_out[0]), +-127) (exact quotient, half to even) of the final f32 y
@@ -141,8 +156,8 @@ int bq_conv2d_i8_nhwc(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t 
 int bq_conv2d_i8_nhwc_q(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t C, const int8_t* w,
                         int64_t O, int64_t KH, int64_t KW, int64_t stride, int64_t pad, const float* sA,
                         const float* sW, const float* bias, const float* residual, int act, float* out,
-                        int32_t* acc, const float* s_out, int8_t* q_out, void* ws, size_t ws_bytes,
-                        bq_stream_t stream);
+                        int32_t* acc, const float* s_out, int8_t* q_out, float* absmax_parts, void* ws,
+                        size_t ws_bytes, bq_stream_t stream);
 
 /* Depthwise int8 convolution, NHWC (groups = C, channel multiplier 1):
  *   x int8 [N, H, W, C] (C % 4 == 0, per-tensor sA f32 [1]), w int8 [KH*KW, C]

@@ -50,9 +50,9 @@ def test_argument_checks_run_on_host():
     assert lib.bq_gemm_i8(None, None, -1, 4, 16, None, None, None, 0, None, None, None, 0, None) == _lib.BQ_ERR_ARG
     assert lib.bq_gemm_i8(None, None, 4, 4, 16, None, None, None, 0, None, None, None, 0, None) == _lib.BQ_ERR_ARG
     assert lib.bq_conv2d_i8_nhwc(None, 1, 4, 4, 8, None, 8, 3, 3, 1, 1, None, None, None, None, 0, None, None,
-                                 None, 0, None) == _lib.BQ_ERR_UNSUPPORTED
+                                 None, None, 0, None) == _lib.BQ_ERR_UNSUPPORTED
     assert lib.bq_conv2d_i8_nhwc(None, 1, 2, 2, 16, None, 8, 5, 5, 1, 0, None, None, None, None, 0, None, None,
-                                 None, 0, None) == _lib.BQ_ERR_ARG
+                                 None, None, 0, None) == _lib.BQ_ERR_ARG
     assert "larger than the input" in _lib.last_error()
     assert lib.bq_dwconv_i8_nhwc(None, 1, 4, 4, 6, None, 3, 3, 1, 1, None, None, None, 0, None, None,
                                  None) == _lib.BQ_ERR_UNSUPPORTED
@@ -61,7 +61,7 @@ def test_argument_checks_run_on_host():
     assert lib.bq_gemm_i8(None, None, 4, 4, 133168, None, None, None, 0, None, None, None, 0, None) == _lib.BQ_ERR_UNSUPPORTED
     assert "overflow" in _lib.last_error()
     assert lib.bq_conv2d_i8_nhwc(None, 1, 9, 9, 16656, None, 8, 3, 3, 1, 1, None, None, None, None, 0, None, None,
-                                 None, 0, None) == _lib.BQ_ERR_UNSUPPORTED
+                                 None, None, 0, None) == _lib.BQ_ERR_UNSUPPORTED
     assert "overflow" in _lib.last_error()
     # zero-size work is a no-op success
     assert lib.bq_gemm_i8(None, None, 0, 4, 16, None, None, None, 0, None, None, None, 0, None) == 0

@@ -296,6 +296,35 @@ def test_split_k_conv_twin_residual(dev):
     assert np.array_equal(n(q), q_o)
 
 
+@pytest.mark.parametrize("N,C,H,O_,k,stride,pad,res", [(16, 64, 32, 64, 3, 1, 1, False), (16, 256, 8, 256, 3, 1, 1, True),
+                                                     (16, 512, 4, 512, 3, 1, 1, True), (3, 40, 9, 50, 1, 1, 0, False),
+                                                     (2, 16, 13, 24, 3, 2, 1, True)])
+def test_conv_absmax_parts_feed_the_next_quantizer(dev, N, C, H, O_, k, stride, pad, res):
+    """A conv's epilogue writes max |y| per output tile; the next layer's per-tensor
+    quantizer takes its scale from those (no max pass) and gives the same int8 bytes and
+    scale as the two-pass quantizer on the same tensor (split-K and ragged tiles included)."""
+    say(f"absmax parts N={N} C={C} H={H} O={O_} k={k} s={stride} res={res}")
+    rng = np.random.default_rng(N + C + H + O_)
+    x = rng.normal(size=(N, C, H, H)).astype(np.float32)
+    w = (rng.normal(size=(O_, C, k, k)) * np.sqrt(2.0 / (C * k * k))).astype(np.float32)
+    OH = (H + 2 * pad - k) // stride + 1
+    r = t(rng.normal(size=(N, O_, OH, OH)).astype(np.float32), dev) if res else None
+    w8 = I.pack_conv_weight(t(w, dev))
+    qx, sa = I.quantize_nhwc(t(x, dev), I.round_up(C, 16))
+    y = I.conv2d_i8_nhwc(qx, sa, w8, stride, pad, None, r, I.ACT_RELU if res else I.ACT_NONE)
+    parts, nparts, _ = y._bq_absmax
+    assert float(parts[:nparts].max()) == float(y.abs().max())
+    cpad = I.round_up(O_, 16)
+    q1, s1 = I.quantize_nhwc(y, cpad)            # from the epilogue's partial maxima
+    y2 = y.clone(memory_format=torch.channels_last)  # a copy carries no maxima
+    assert getattr(y2, "_bq_absmax", None) is None
+    q2, s2 = I.quantize_nhwc(y2, cpad)           # two passes
+    assert torch.equal(s1, s2) and torch.equal(q1, q2)
+    y.add_(0.0)                                  # modified in place: the maxima no longer apply
+    q3, s3 = I.quantize_nhwc(y, cpad)
+    assert torch.equal(s3, s2) and torch.equal(q3, q2)
+
+
 # 3x3 / 5x5 at stride 1 / 2 take the register-blocked kernel (8 or 4 channels a thread;
 # output widths that are not a multiple of its pixel block); 7x7 and the rest the generic one.
 DW_CASES = [(2, 32, 16, 3, 1, 1), (2, 96, 15, 3, 2, 1), (2, 144, 14, 5, 1, 2), (2, 240, 13, 5, 2, 2),
