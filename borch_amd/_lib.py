@@ -23,7 +23,7 @@ BQ_ERR_DEVICE = -2
 BQ_ERR_LAUNCH = -3
 BQ_ERR_UNSUPPORTED = -4
 
-ACT_NONE, ACT_RELU, ACT_SILU = 0, 1, 2
+ACT_NONE, ACT_RELU, ACT_SILU, ACT_GELU = 0, 1, 2, 3
 
 _c_i64 = ctypes.c_int64
 _c_p = ctypes.c_void_p
@@ -42,7 +42,7 @@ SIGNATURES = {
     "bq_quantize_nhwc": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_size, _c_p]),
     "bq_quantize_nhwc_scaled": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p]),
     "bq_gemm_ws_bytes": (_c_size, []),
-    "bq_gemm_i8": (_c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_int, _c_p, _c_p, _c_p,
+    "bq_gemm_i8": (_c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_int, _c_p, _c_p, _c_p,
                             _c_size, _c_p]),
     "bq_conv2d_i8_nhwc_q": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i64,
                                      _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_int, _c_p, _c_p, _c_p, _c_p,

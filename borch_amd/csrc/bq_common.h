@@ -56,16 +56,32 @@ __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
 
 __device__ __forceinline__ float silu(float v) { return __fdiv_rn(v, __fadd_rn(1.0f, expf(-v))); }
 
+// GELU, erf form, in the order of torch's f32 kernel: (v * 0.5) * (1 + erf(v * sqrt(1/2))).
+// Out of line: erff inlined at every epilogue store grows the GEMM kernels by a third and
+// slows layers that never use it; only GELU layers pay for the call.
+__device__ __attribute__((noinline)) float gelu(float v) {
+  return __fmul_rn(__fmul_rn(v, 0.5f), __fadd_rn(1.0f, erff(__fmul_rn(v, 0.70710678118654752f))));
+}
+
+__device__ __attribute__((noinline)) float4 gelu4(float4 v) {
+  return make_float4(gelu(v.x), gelu(v.y), gelu(v.z), gelu(v.w));
+}
+
+__device__ __forceinline__ float activate(float v, int act) {
+  if (act == BQ_ACT_RELU) return v > 0.f ? v : 0.f;
+  if (act == BQ_ACT_SILU) return silu(v);
+  if (act == BQ_ACT_GELU) return gelu(v);
+  return v;
+}
+
 // The f32 epilogue, one rounding per operation (no contraction into FMA):
-// y = ((f32(acc) * sa) * sw) + b, then + residual, then relu.
+// y = ((f32(acc) * sa) * sw) + b, then + residual, then the activation.
 __device__ __forceinline__ float dequant_one(int acc, float sa, float sw, float b, bool has_b,
                                              float r, bool has_r, int act) {
   float v = __fmul_rn(__fmul_rn((float)acc, sa), sw);
   if (has_b) v = __fadd_rn(v, b);
   if (has_r) v = __fadd_rn(v, r);
-  if (act == BQ_ACT_RELU) v = v > 0.f ? v : 0.f;
-  else if (act == BQ_ACT_SILU) v = silu(v);
-  return v;
+  return activate(v, act);
 }
 
 }  // namespace bq

@@ -511,10 +511,8 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
     const float4 sw4 = *reinterpret_cast<const float4*>(&s_sw[ncol]);
     const float4 b4 = *reinterpret_cast<const float4*>(&s_b[ncol]);
     if (p.vec_ok && n < p.N) {
-      // Rolled on purpose: an unrolled copy per row and slice overflows the instruction
-      // cache. Bias 0 when absent: y + 0.0f == y for every y this produces (no -0.0).
-#pragma unroll 1
-      for (int rr = 0; rr < 32; rr += ROWS_PER_STORE) {
+      // Bias 0 when absent: y + 0.0f == y for every y this produces (no -0.0).
+      auto store_row = [&](int rr, float4 rv, bool with_r) {
         const int row = rr + lane / C4;
         const int mloc = wm * WTM + i * 32 + row;
         const int m = m0 + mloc;
@@ -527,8 +525,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
           o.y = __fadd_rn(__fmul_rn(__fmul_rn((float)a.y, sa), sw4.y), b4.y);
           o.z = __fadd_rn(__fmul_rn(__fmul_rn((float)a.z, sa), sw4.z), b4.z);
           o.w = __fadd_rn(__fmul_rn(__fmul_rn((float)a.w, sa), sw4.w), b4.w);
-          if (has_r) {
-            const float4 rv = *reinterpret_cast<const float4*>(p.res + idx);
+          if (with_r) {
             o.x = __fadd_rn(o.x, rv.x); o.y = __fadd_rn(o.y, rv.y);
             o.z = __fadd_rn(o.z, rv.z); o.w = __fadd_rn(o.w, rv.w);
           }
@@ -537,6 +534,8 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
             o.z = o.z > 0.f ? o.z : 0.f; o.w = o.w > 0.f ? o.w : 0.f;
           } else if (p.act == BQ_ACT_SILU) {
             o.x = silu(o.x); o.y = silu(o.y); o.z = silu(o.z); o.w = silu(o.w);
+          } else if (p.act == BQ_ACT_GELU) {
+            o = gelu4(o);
           }
           *reinterpret_cast<float4*>(p.out + idx) = o;
           if (p.acc) *reinterpret_cast<int4*>(p.acc + idx) = a;
@@ -545,6 +544,27 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
                 pack4(quant_one(o.x, s_out), quant_one(o.y, s_out), quant_one(o.z, s_out), quant_one(o.w, s_out));
           amax = fmaxf(amax, fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w))));
         }
+      };
+      if (has_r) {
+        // The slice's residual rows are all loaded before any of its stores: on gfx9 a
+        // load issued after stores waits (vmcnt) for them too, so a load per row would
+        // serialize the stores. Unrolled, so the values stay in registers; this path's
+        // code runs only for residual layers.
+        constexpr int NR = 32 / ROWS_PER_STORE;
+        float4 rv[NR];
+#pragma unroll
+        for (int k = 0; k < NR; ++k) {
+          const int m = m0 + wm * WTM + i * 32 + k * ROWS_PER_STORE + lane / C4;
+          rv[k] = m < p.M ? *reinterpret_cast<const float4*>(p.res + (size_t)m * p.N + n)
+                          : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int k = 0; k < NR; ++k) store_row(k * ROWS_PER_STORE, rv[k], true);
+      } else {
+        // Rolled on purpose: an unrolled copy per row and slice overflows the instruction
+        // cache.
+#pragma unroll 1
+        for (int rr = 0; rr < 32; rr += ROWS_PER_STORE) store_row(rr, make_float4(0.f, 0.f, 0.f, 0.f), false);
       }
     } else if (!p.vec_ok) {
 #pragma unroll 1
@@ -1092,8 +1112,8 @@ extern "C" {
 size_t bq_gemm_ws_bytes(void) { return SPLIT_WS_BYTES; }
 
 int bq_gemm_i8(const int8_t* A, const int8_t* W, int64_t M, int64_t N, int64_t K, const float* sA,
-               const float* sW, const float* bias, int act, float* out, int32_t* acc, void* ws, size_t ws_bytes,
-               bq_stream_t stream) {
+               const float* sW, const float* bias, const float* residual, int act, float* out, int32_t* acc,
+               void* ws, size_t ws_bytes, bq_stream_t stream) {
   const char* what = "bq_gemm_i8";
   if (M < 0 || N < 0 || K < 0) return set_error(BQ_ERR_ARG, "%s: negative size", what);
   if (M > 0x7fffffff || N > 0x7fffffff || M * N > ((int64_t)1 << 40))
@@ -1105,12 +1125,12 @@ int bq_gemm_i8(const int8_t* A, const int8_t* W, int64_t M, int64_t N, int64_t K
   if (K % 16) return set_error(BQ_ERR_UNSUPPORTED, "%s: K=%lld is not a multiple of 16", what, (long long)K);
   if (!A || !W || !sA || !sW || !out) return set_error(BQ_ERR_ARG, "%s: null pointer", what);
   if (!aligned16(A) || !aligned16(W)) return set_error(BQ_ERR_ARG, "%s: A and W must be 16-byte aligned", what);
-  if (act < BQ_ACT_NONE || act > BQ_ACT_SILU) return set_error(BQ_ERR_ARG, "%s: bad activation %d", what, act);
+  if (act < BQ_ACT_NONE || act > BQ_ACT_GELU) return set_error(BQ_ERR_ARG, "%s: bad activation %d", what, act);
   GemmP p{};
   p.A = A; p.W = W; p.M = (int)M; p.N = (int)N; p.K = (int)K;
-  p.sA = sA; p.sa_per_row = 1; p.sW = sW; p.bias = bias; p.res = nullptr; p.act = act;
+  p.sA = sA; p.sa_per_row = 1; p.sW = sW; p.bias = bias; p.res = residual; p.act = act;
   p.out = out; p.acc = acc;
-  p.vec_ok = (N % 4 == 0) && aligned16(out) && aligned16(acc);
+  p.vec_ok = (N % 4 == 0) && aligned16(out) && aligned16(acc) && aligned16(residual);
   hipStream_t st = (hipStream_t)stream;
   bool done = false;
   if (M <= 4) {
@@ -1157,7 +1177,7 @@ static int conv_impl(const char* what, const int8_t* x, int64_t N, int64_t H, in
   if (M == 0) return BQ_OK;
   if (!x || !w || !sA || !sW || !out) return set_error(BQ_ERR_ARG, "%s: null pointer", what);
   if (!aligned16(x) || !aligned16(w)) return set_error(BQ_ERR_ARG, "%s: x and w must be 16-byte aligned", what);
-  if (act < BQ_ACT_NONE || act > BQ_ACT_SILU) return set_error(BQ_ERR_ARG, "%s: bad activation %d", what, act);
+  if (act < BQ_ACT_NONE || act > BQ_ACT_GELU) return set_error(BQ_ERR_ARG, "%s: bad activation %d", what, act);
   GemmP p{};
   p.A = x; p.W = w; p.M = (int)M; p.N = (int)O; p.K = (int)K;
   p.sA = sA; p.sa_per_row = 0; p.sW = sW; p.bias = bias; p.res = residual; p.act = act;
@@ -1229,7 +1249,7 @@ int bq_dwconv_i8_nhwc(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t 
   if (!x || !w || !sA || !sW || !out) return set_error(BQ_ERR_ARG, "%s: null pointer", what);
   if (((uintptr_t)x & 3) || ((uintptr_t)w & 3) || ((uintptr_t)out & 15) || ((uintptr_t)acc & 15))
     return set_error(BQ_ERR_ARG, "%s: misaligned pointer", what);
-  if (act < BQ_ACT_NONE || act > BQ_ACT_SILU) return set_error(BQ_ERR_ARG, "%s: bad activation %d", what, act);
+  if (act < BQ_ACT_NONE || act > BQ_ACT_GELU) return set_error(BQ_ERR_ARG, "%s: bad activation %d", what, act);
   const bool wide = (C % 8 == 0) && ((uintptr_t)x & 7) == 0 && ((uintptr_t)w & 7) == 0;
   hipStream_t st = (hipStream_t)stream;
   // Square 3x3 / 5x5 filters at stride 1 or 2: the register-blocked kernel (32-bit indices).

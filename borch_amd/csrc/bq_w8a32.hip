@@ -100,8 +100,7 @@ __global__ __launch_bounds__(WA_WAVES * 64) void gemv_w8a32_kernel(const float* 
       const int n = row0 + j;
       if (lane == 0 && j < nrows) {
         float v = bias ? __fadd_rn(s, bias[n]) : s;
-        if (act == BQ_ACT_RELU) v = v > 0.f ? v : 0.f;
-        else if (act == BQ_ACT_SILU) v = silu(v);
+        v = activate(v, act);
         out[(size_t)m * N + n] = v;
       }
     }
@@ -141,7 +140,7 @@ int bq_gemv_w8a32(const float* x, const int8_t* W, int64_t M, int64_t N, int64_t
   if (N > 0x7fffffff || (int64_t)N * K >= ((int64_t)1 << 31)) return set_error(BQ_ERR_ARG, "%s: size too large", what);
   if (!x || !W || !sW || !out) return set_error(BQ_ERR_ARG, "%s: null pointer", what);
   if (((uintptr_t)x & 15) || ((uintptr_t)W & 15)) return set_error(BQ_ERR_ARG, "%s: x and W must be 16-byte aligned", what);
-  if (act < BQ_ACT_NONE || act > BQ_ACT_SILU) return set_error(BQ_ERR_ARG, "%s: bad activation %d", what, act);
+  if (act < BQ_ACT_NONE || act > BQ_ACT_GELU) return set_error(BQ_ERR_ARG, "%s: bad activation %d", what, act);
   constexpr int RPW = 2;
   const unsigned grid = (unsigned)((N + WA_WAVES * RPW - 1) / (WA_WAVES * RPW));
   hipStream_t st = (hipStream_t)stream;

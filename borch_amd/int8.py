@@ -13,10 +13,10 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from ._lib import ACT_NONE, ACT_RELU, ACT_SILU, check, lib, require_device
+from ._lib import ACT_GELU, ACT_NONE, ACT_RELU, ACT_SILU, check, lib, require_device
 
 __all__ = [
-    "ACT_NONE", "ACT_RELU", "ACT_SILU", "Int8Weight", "Int8ConvWeight", "Int8DwWeight",
+    "ACT_NONE", "ACT_RELU", "ACT_SILU", "ACT_GELU", "Int8Weight", "Int8ConvWeight", "Int8DwWeight",
     "quantize_rows", "quantize_weight_per_channel", "quantize_tensor", "quantize_nhwc",
     "gemm_i8", "conv2d_i8_nhwc", "conv2d_i8_nhwc_q", "dwconv_i8_nhwc", "pack_linear_weight", "pack_conv_weight",
     "quantize_nhwc_scaled", "linear_w8a32", "dequant_weight",
@@ -241,11 +241,7 @@ def linear_w8a32(x: torch.Tensor, w8: Int8Weight, bias=None, act=ACT_NONE) -> to
         check(lib().bq_gemv_w8a32(x2.data_ptr(), w8.q.data_ptr(), M, N, K, w8.s.data_ptr(), _ptr(b), act,
                                   out.data_ptr(), _stream(x2)))
     else:
-        out = torch.nn.functional.linear(x2, dequant_weight(w8), bias)
-        if act == ACT_RELU:
-            out = torch.relu(out)
-        elif act == ACT_SILU:
-            out = torch.nn.functional.silu(out)
+        out = _act_f32(torch.nn.functional.linear(x2, dequant_weight(w8), bias), act)
     return out.reshape(*lead, N)
 
 
@@ -277,9 +273,9 @@ def pack_dw_weight(w: torch.Tensor) -> Int8DwWeight:
 
 # --------------------------------------------------------------------------- int8 ops
 
-def gemm_i8(qa, qw, sa, sw, bias=None, act=ACT_NONE, want_acc=False):
-    """``out = ((f32(qa @ qw.T) * sa[m]) * sw[n]) + bias[n]`` then act (bq_gemm_i8).
-    Returns ``out`` or ``(out, acc int32)``."""
+def gemm_i8(qa, qw, sa, sw, bias=None, act=ACT_NONE, want_acc=False, residual=None):
+    """``out = ((f32(qa @ qw.T) * sa[m]) * sw[n]) + bias[n]`` (+ ``residual [M, N]``) then
+    act (bq_gemm_i8). Returns ``out`` or ``(out, acc int32)``."""
     _need(qa, "A", torch.int8)
     _need(qw, "W", torch.int8)
     M, K = qa.shape
@@ -291,10 +287,15 @@ def gemm_i8(qa, qw, sa, sw, bias=None, act=ACT_NONE, want_acc=False):
     if sa.numel() != M or sw.numel() != N:
         raise ValueError("scale sizes do not match the operands")
     b = None if bias is None else bias.contiguous().float()
+    r = None
+    if residual is not None:
+        if tuple(residual.shape) != (M, N):
+            raise RuntimeError(f"residual shape {tuple(residual.shape)} != output {(M, N)}")
+        r = residual.float().contiguous()
     out = torch.empty((M, N), dtype=torch.float32, device=qa.device)
     acc = torch.empty((M, N), dtype=torch.int32, device=qa.device) if want_acc else None
-    check(lib().bq_gemm_i8(qa.data_ptr(), qw.data_ptr(), M, N, K, sa.data_ptr(), sw.data_ptr(), _ptr(b), act,
-                           out.data_ptr(), _ptr(acc), *_ws_args(qa.device), _stream(qa)))
+    check(lib().bq_gemm_i8(qa.data_ptr(), qw.data_ptr(), M, N, K, sa.data_ptr(), sw.data_ptr(), _ptr(b), _ptr(r),
+                           act, out.data_ptr(), _ptr(acc), *_ws_args(qa.device), _stream(qa)))
     return (out, acc) if want_acc else out
 
 
@@ -388,12 +389,16 @@ def dwconv_i8_nhwc(qx, sa, wq: Int8DwWeight, stride=1, pad=0, bias=None, act=ACT
 
 # ----------------------------------------------------------------- float-in, float-out
 
-def linear(x: torch.Tensor, w8: Int8Weight, bias=None, act=ACT_NONE) -> torch.Tensor:
+def linear(x: torch.Tensor, w8: Int8Weight, bias=None, act=ACT_NONE, residual=None) -> torch.Tensor:
     """Dynamic-quant int8 Linear: per-row activations, per-channel weights, f32 out
-    ``[..., N]`` (the numpy core's ``x @ W.T + b``, borch/_nn.py:413-415, in W8A8). A
-    weight-only packing runs ``linear_w8a32`` instead."""
+    ``[..., N]`` (the numpy core's ``x @ W.T + b``, borch/_nn.py:413-415, in W8A8), with an
+    optional ``residual [..., N]`` added in the epilogue before ``act``. A weight-only
+    packing runs ``linear_w8a32`` instead."""
     if w8.weight_only:
-        return linear_w8a32(x, w8, bias, act)
+        out = linear_w8a32(x, w8, bias, ACT_NONE if residual is not None else act)
+        if residual is not None:
+            out = _act_f32(out + residual, act)
+        return out
     if x.shape[-1] != w8.in_features:
         a = "x".join(str(n) for n in (x.reshape(-1, x.shape[-1]).shape if x.dim() else ()))
         raise RuntimeError(
@@ -403,8 +408,20 @@ def linear(x: torch.Tensor, w8: Int8Weight, bias=None, act=ACT_NONE) -> torch.Te
     if w8.kpad != w8.in_features:
         x2 = torch.nn.functional.pad(x2, (0, w8.kpad - w8.in_features))
     qa, sa = quantize_rows(x2)
-    out = gemm_i8(qa, w8.q, sa, w8.s, bias, act)
+    r = None if residual is None else residual.reshape(-1, w8.out_features)
+    out = gemm_i8(qa, w8.q, sa, w8.s, bias, act, residual=r)
     return out.reshape(*lead, w8.out_features)
+
+
+def _act_f32(out: torch.Tensor, act: int) -> torch.Tensor:
+    """The epilogue activations as torch f32 ops (the f32 paths and fallbacks)."""
+    if act == ACT_RELU:
+        return torch.relu(out)
+    if act == ACT_SILU:
+        return torch.nn.functional.silu(out)
+    if act == ACT_GELU:
+        return torch.nn.functional.gelu(out)
+    return out
 
 
 def conv2d(x: torch.Tensor, w8: Int8ConvWeight, bias=None, stride=1, padding=0, act=ACT_NONE,

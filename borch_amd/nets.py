@@ -13,7 +13,8 @@
   this one follows the paper.
 * ``ViTEncoder`` — ViT-B/16's encoder (Dosovitskiy et al. 2021; torchvision's pre-norm
   layout, LayerNorm eps 1e-6): QKV / proj / MLP Linears are int8 dynamic-quant;
-  LayerNorm, softmax attention and GELU stay f32.
+  LayerNorm, softmax attention and GELU stay f32. ``fuse()`` puts the two skip additions
+  into the proj / fc2 epilogues.
 
 Weights are random, from a seeded ``torch.Generator`` on the host: Kaiming-normal
 (fan_out, ReLU gain) convs, BN running statistics as export_resnet18.py:84-91 (mean
@@ -230,8 +231,10 @@ class EncoderLayer(tnn.Module):
         self.ln2 = tnn.LayerNorm(d, eps=1e-6)
         self.fc1 = nn.Linear(d, mlp)
         self.fc2 = nn.Linear(mlp, d)
+        self.proj_f = self.fc2_f = None
 
-    def attention(self, h):
+    def heads_out(self, h):
+        """Multi-head softmax attention in f32 up to (not including) the output projection."""
         B, T, D = h.shape
         H, dh = self.heads, D // self.heads
         qkv = self.qkv(h).reshape(B, T, 3, H, dh).permute(2, 0, 3, 1, 4)
@@ -239,11 +242,27 @@ class EncoderLayer(tnn.Module):
         # f32 attention; the transposed operand is made contiguous before the batched product
         att = torch.matmul(q, k.transpose(-2, -1).contiguous()) * (dh ** -0.5)
         o = torch.matmul(torch.softmax(att, dim=-1), v)
-        return self.proj(o.transpose(1, 2).reshape(B, T, D))
+        return o.transpose(1, 2).reshape(B, T, D)
+
+    def attention(self, h):
+        return self.proj(self.heads_out(h))
 
     def forward(self, x):
+        if self.proj_f is not None:
+            # fused: the skip additions ride in the projections' epilogues, the GELU in fc1's
+            x = self.proj_f(self.heads_out(self.ln1(x)), x)
+            return self.fc2_f(torch.nn.functional.gelu(self.fc1(self.ln2(x))), x)
         x = x + self.attention(self.ln1(x))
         return x + self.fc2(torch.nn.functional.gelu(self.fc1(self.ln2(x))))
+
+    def fuse(self):
+        """proj and fc2 -> LinearAdd (x + W·o in the epilogue): the same f32 arithmetic as
+        forward's separate add (addition commutes exactly). fc1's GELU stays a separate f32
+        op: erf is VALU-bound, and in fc1's epilogue it costs what the separate pass costs
+        (measured), so ``LinearGELU`` is not used here."""
+        self.proj_f = I.LinearAdd(self.proj)
+        self.fc2_f = I.LinearAdd(self.fc2)
+        return self
 
 
 class ViTEncoder(tnn.Module):
@@ -256,6 +275,12 @@ class ViTEncoder(tnn.Module):
 
     def forward(self, x):
         return self.ln(self.layers(x))
+
+    def fuse(self):
+        self.eval()
+        for layer in self.layers:
+            layer.fuse()
+        return self
 
 
 def build(name: str, seed: int = 0, device="cuda"):

@@ -75,11 +75,15 @@ class Linear(_tnn.Module):
             self.int8 = _i8.pack_linear_weight(self.weight.detach(), weight_only)
         return True
 
-    def forward(self, x):
+    def forward(self, x, residual=None):
+        """``x @ W.T + b``; the fused modules (``LinearReLU``, ``LinearGELU``, ``LinearAdd``)
+        add ``residual`` and apply the activation in the same epilogue."""
         if self.int8 is not None:
-            return _i8.linear(x, self.int8, self.bias, self.act)
+            return _i8.linear(x, self.int8, self.bias, self.act, residual)
         out = functional._f32_linear(x, self.weight, self.bias)
-        return torch.relu(out) if self.act == _i8.ACT_RELU else out
+        if residual is not None:
+            out = out + residual
+        return _i8._act_f32(out, self.act)
 
     def extra_repr(self):
         return (f"in_features={self.in_features}, out_features={self.out_features}, "
@@ -201,11 +205,7 @@ class Conv2d(_tnn.Module):
                                      self.groups, self.padding_mode)
         if residual is not None:
             out = out + residual
-        if self.act == _i8.ACT_RELU:
-            out = torch.relu(out)
-        elif self.act == _i8.ACT_SILU:
-            out = torch.nn.functional.silu(out)
-        return out
+        return _i8._act_f32(out, self.act)
 
     def forward(self, x, residual=None):
         if self.int8 is not None and _CALIBRATING:
@@ -240,11 +240,7 @@ class Conv2d(_tnn.Module):
                                      self.groups, self.padding_mode)
         if residual is not None:
             out = out + residual
-        if self.act == _i8.ACT_RELU:
-            out = torch.relu(out)
-        elif self.act == _i8.ACT_SILU:
-            out = torch.nn.functional.silu(out)
-        return out
+        return _i8._act_f32(out, self.act)
 
     def extra_repr(self):
         s = (f"{self.in_channels}, {self.out_channels}, kernel_size={self.kernel_size}, "

@@ -81,3 +81,33 @@ class ConvSiLU2d(_tnn.Module):
 
     def forward(self, x):
         return self.conv(x)
+
+
+class LinearGELU(_tnn.Module):
+    """``gelu(linear(x))`` in one kernel: the erf GELU evaluated in f32 in the epilogue (a
+    transformer MLP's first projection). Not a torch.ao name; the shape of ``LinearReLU``."""
+
+    def __init__(self, linear):
+        super().__init__()
+        self.linear = linear
+        self.linear.act = _i8.ACT_GELU
+        self.training = False
+
+    def forward(self, x):
+        return self.linear(x)
+
+
+class LinearAdd(_tnn.Module):
+    """``linear(x1) + x2`` in one kernel (a transformer's projection and skip connection):
+    the Linear counterpart of ``ConvAdd2d`` (nn.ts:6717-6731)."""
+
+    def __init__(self, linear):
+        super().__init__()
+        self.linear = linear
+        self.linear.act = _i8.ACT_NONE
+        self.training = False
+
+    def forward(self, x, residual=None):
+        if residual is None:
+            raise TypeError("LinearAdd.forward takes (x1, x2)")
+        return self.linear(x, residual)

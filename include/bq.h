@@ -47,6 +47,7 @@ typedef void* bq_stream_t; /* a hipStream_t; NULL = the null stream */
 #define BQ_ACT_NONE 0
 #define BQ_ACT_RELU 1
 #define BQ_ACT_SILU 2
+#define BQ_ACT_GELU 3 /* erf form, f32: (y * 0.5) * (1 + erf(y * sqrt(1/2))) */
 
 /* Library version, (major << 16) | minor. */
 int bq_version(void);
@@ -115,14 +116,15 @@ size_t bq_gemm_ws_bytes(void);
 /* W8A8 GEMM with the fused dequant epilogue, Linear layout (x @ W.T):
  *   A int8 [M, K] (per-row scales sA f32 [M]), W int8 [N, K] (per-channel sW f32 [N]),
  *   out f32 [M, N] = ((f32(A @ W.T) * sA[m]) * sW[n]) + bias[n] (bias nullable), then
- *   the activation `act` (BQ_ACT_*). `acc` (nullable) receives the exact int32 [M, N].
+ *   + residual[m, n] (f32 [M, N], nullable: a transformer's skip connection), then the
+ *   activation `act` (BQ_ACT_*). `acc` (nullable) receives the exact int32 [M, N].
  * K % 16 == 0 and K <= 133152 (K * 127^2 < 2^31: the int32 sums are exact for any
  * operands); A, W 16-byte aligned. ws: the split-K workspace (nullable, see
  * bq_gemm_ws_bytes). Replaces matmulInt8(M,K,N,scaled)
  * (borch-ts/src/kernels.ts:1808-1852), which took only whole 32s. */
 int bq_gemm_i8(const int8_t* A, const int8_t* W, int64_t M, int64_t N, int64_t K,
-               const float* sA, const float* sW, const float* bias, int act, float* out,
-               int32_t* acc, void* ws, size_t ws_bytes, bq_stream_t stream);
+               const float* sA, const float* sW, const float* bias, const float* residual, int act,
+               float* out, int32_t* acc, void* ws, size_t ws_bytes, bq_stream_t stream);
 
 /* Implicit-GEMM int8 convolution, NHWC, groups 1, dilation 1:
  *   x int8 [N, H, W, C] (C % 16 == 0, per-tensor scale sA f32 [1]),

@@ -19,7 +19,7 @@ import numpy as np
 
 from . import quant as Q
 
-ACT_NONE, ACT_RELU, ACT_SILU = 0, 1, 2
+ACT_NONE, ACT_RELU, ACT_SILU, ACT_GELU = 0, 1, 2, 3
 
 
 def _act(y, act):
@@ -27,6 +27,8 @@ def _act(y, act):
         return np.where(y > 0, y, np.float32(0)).astype(np.float32)
     if act == ACT_SILU:
         return Q.silu(y)
+    if act == ACT_GELU:
+        return Q.gelu(y)
     return y
 
 
@@ -66,8 +68,9 @@ def dwconv_layer(x_nchw, w, b, stride, pad, act=ACT_NONE):
     return y.transpose(0, 3, 1, 2), acc[..., :C], sA, sW, qw
 
 
-def linear_layer(x, w, b, act=ACT_NONE):
-    """Returns ``(y [..., N], acc [M, N], sA [M], sW, qw)``."""
+def linear_layer(x, w, b, act=ACT_NONE, residual=None):
+    """Returns ``(y [..., N], acc [M, N], sA [M], sW, qw)``; ``residual [..., N]`` is added
+    after the bias and before ``act`` (the fused ``LinearAdd`` epilogue)."""
     x = np.asarray(x, np.float32)
     lead = x.shape[:-1]
     K = x.shape[-1]
@@ -79,7 +82,8 @@ def linear_layer(x, w, b, act=ACT_NONE):
     qa, sA = Q.quantize_rows(x2)
     qw, sW = Q.quantize_weight_per_channel(wp)
     acc = Q.gemm_i8_i32(qa, qw)
-    y = _act(Q.dequant(acc, sA, sW, b), act)
+    r = None if residual is None else np.asarray(residual, np.float32).reshape(-1, w.shape[0])
+    y = _act(Q.dequant(acc, sA, sW, b, residual=r), act)
     return y.reshape(*lead, w.shape[0]), acc, sA, sW, qw
 
 

@@ -201,6 +201,14 @@ def silu(y):
     return (y64 / (1.0 + np.exp(-y64))).astype(np.float32)
 
 
+def gelu(y):
+    """f32 GELU, erf form ``y·Φ(y) = 0.5·y·(1 + erf(y/√2))`` (closed form; float64 then
+    rounded): the activation of a transformer MLP (torch's default ``gelu``)."""
+    from scipy.special import erf
+    y64 = np.asarray(y, dtype=np.float64)
+    return (0.5 * y64 * (1.0 + erf(y64 / np.sqrt(2.0)))).astype(np.float32)
+
+
 def im2col_nhwc(xq, KH, KW, stride, pad):
     """``(N, H, W, C)`` → ``(N·OH·OW, KH·KW·C)``, zero outside, tap-major then channel.
 

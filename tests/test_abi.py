@@ -45,10 +45,10 @@ def test_argument_checks_run_on_host():
     """Bad sizes are refused before any launch (no device memory is touched)."""
     from borch_amd import _lib
     lib = _lib.lib()
-    assert lib.bq_gemm_i8(None, None, 4, 4, 20, None, None, None, 0, None, None, None, 0, None) == _lib.BQ_ERR_UNSUPPORTED
+    assert lib.bq_gemm_i8(None, None, 4, 4, 20, None, None, None, None, 0, None, None, None, 0, None) == _lib.BQ_ERR_UNSUPPORTED
     assert "multiple of 16" in _lib.last_error()
-    assert lib.bq_gemm_i8(None, None, -1, 4, 16, None, None, None, 0, None, None, None, 0, None) == _lib.BQ_ERR_ARG
-    assert lib.bq_gemm_i8(None, None, 4, 4, 16, None, None, None, 0, None, None, None, 0, None) == _lib.BQ_ERR_ARG
+    assert lib.bq_gemm_i8(None, None, -1, 4, 16, None, None, None, None, 0, None, None, None, 0, None) == _lib.BQ_ERR_ARG
+    assert lib.bq_gemm_i8(None, None, 4, 4, 16, None, None, None, None, 0, None, None, None, 0, None) == _lib.BQ_ERR_ARG
     assert lib.bq_conv2d_i8_nhwc(None, 1, 4, 4, 8, None, 8, 3, 3, 1, 1, None, None, None, None, 0, None, None,
                                  None, None, 0, None) == _lib.BQ_ERR_UNSUPPORTED
     assert lib.bq_conv2d_i8_nhwc(None, 1, 2, 2, 16, None, 8, 5, 5, 1, 0, None, None, None, None, 0, None, None,
@@ -58,13 +58,13 @@ def test_argument_checks_run_on_host():
                                  None) == _lib.BQ_ERR_UNSUPPORTED
     assert lib.bq_quantize_nhwc(None, 4, 3, 2, None, None, None, 0, None) == _lib.BQ_ERR_ARG
     # past K = 133152 an int32 sum of int8 products could wrap: refused, not computed
-    assert lib.bq_gemm_i8(None, None, 4, 4, 133168, None, None, None, 0, None, None, None, 0, None) == _lib.BQ_ERR_UNSUPPORTED
+    assert lib.bq_gemm_i8(None, None, 4, 4, 133168, None, None, None, None, 0, None, None, None, 0, None) == _lib.BQ_ERR_UNSUPPORTED
     assert "overflow" in _lib.last_error()
     assert lib.bq_conv2d_i8_nhwc(None, 1, 9, 9, 16656, None, 8, 3, 3, 1, 1, None, None, None, None, 0, None, None,
                                  None, None, 0, None) == _lib.BQ_ERR_UNSUPPORTED
     assert "overflow" in _lib.last_error()
     # zero-size work is a no-op success
-    assert lib.bq_gemm_i8(None, None, 0, 4, 16, None, None, None, 0, None, None, None, 0, None) == 0
+    assert lib.bq_gemm_i8(None, None, 0, 4, 16, None, None, None, None, 0, None, None, None, 0, None) == 0
 
 
 def test_cpu_tensors_are_refused_by_name():
@@ -113,3 +113,16 @@ def test_probe_library_exports_its_header():
     assert lib.bqp_stream_read(16, 24, 1, 16, None) == -1
     assert lib.bqp_stream_read(16, 32, 3, 16, None) == -1
     assert b"chunks" in lib.bqp_last_error()
+
+
+def test_ctypes_signatures_match_the_header():
+    """Every entry point's ctypes argument list has as many parameters as its declaration
+    in include/bq.h (a stale or mismatched binding shifts every argument after the change)."""
+    from borch_amd import _lib
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    decls = dict((m.group(1), m.group(2)) for m in re.finditer(r"\b(bq_[a-z0-9_]+)\s*\(([^)]*)\)\s*;", text))
+    assert sorted(decls) == sorted(_lib.SIGNATURES)
+    for name, params in decls.items():
+        params = params.strip()
+        n = 0 if params in ("", "void") else params.count(",") + 1
+        assert n == len(_lib.SIGNATURES[name][1]), (name, n, len(_lib.SIGNATURES[name][1]))

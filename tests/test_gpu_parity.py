@@ -172,6 +172,32 @@ def test_gemm_shapes(dev, M, N, K, act):
     assert_f32(n(y), O.dequant(acc_o, sa, sw, b, relu=bool(act)))
 
 
+@pytest.mark.parametrize("M,N,K", [(6304 // 8, 3072, 768), (3, 200, 64), (40, 96, 256), (300, 130, 512)])
+def test_gemm_gelu_and_residual_epilogue(dev, M, N, K):
+    """The transformer epilogues: fc1's GELU (erf form, f32) and proj/fc2's skip addition
+    (residual after the bias, before the activation), on the tiled, skinny and GEMV paths.
+    Accumulators bit-exact; GELU within 1e-5 rel / 1e-6 abs of the closed form and of torch's
+    own f32 gelu; the residual epilogue bit-exact."""
+    say(f"gemm GELU / residual epilogue M={M} N={N} K={K}")
+    rng = np.random.default_rng(M * 3 + N + K)
+    qa = rng.integers(-127, 128, size=(M, K)).astype(np.int8)
+    qw = rng.integers(-127, 128, size=(N, K)).astype(np.int8)
+    sa = rng.uniform(1e-4, 1e-3, M).astype(np.float32)
+    sw = rng.uniform(1e-4, 1e-3, N).astype(np.float32)
+    b = rng.normal(size=N).astype(np.float32)
+    res = rng.normal(size=(M, N)).astype(np.float32)
+    acc_o = O.gemm_i8_i32(qa, qw)
+    y, acc = I.gemm_i8(t(qa, dev), t(qw, dev), t(sa, dev), t(sw, dev), t(b, dev), act=I.ACT_GELU, want_acc=True)
+    assert np.array_equal(n(acc), acc_o)
+    pre = O.dequant(acc_o, sa, sw, b)
+    np.testing.assert_allclose(n(y), O.gelu(pre), rtol=RTOL, atol=ATOL)
+    np.testing.assert_allclose(n(y), n(torch.nn.functional.gelu(t(pre, dev))), rtol=RTOL, atol=ATOL)
+    y2 = I.gemm_i8(t(qa, dev), t(qw, dev), t(sa, dev), t(sw, dev), t(b, dev), residual=t(res, dev))
+    assert_f32(n(y2), O.dequant(acc_o, sa, sw, b, residual=res))
+    y3 = I.gemm_i8(t(qa, dev), t(qw, dev), t(sa, dev), t(sw, dev), t(b, dev), act=I.ACT_RELU, residual=t(res, dev))
+    assert_f32(n(y3), O.dequant(acc_o, sa, sw, b, relu=True, residual=res))
+
+
 def test_gemm_no_bias_extremes(dev):
     say("gemm extremes (all +-127, K=4096)")
     K = 4096
@@ -234,7 +260,7 @@ def _gemm_c(qa, qw, sa, sw, b, out, acc, ws):
     N = qw.shape[0]
     wp, wn = (None, 0) if ws is None else (ws.data_ptr(), ws.numel())
     _lib.check(_lib.lib().bq_gemm_i8(qa.data_ptr(), qw.data_ptr(), M, N, K, sa.data_ptr(), sw.data_ptr(),
-                                     b.data_ptr(), 0, out.data_ptr(), acc.data_ptr(), wp, wn,
+                                     b.data_ptr(), None, 0, out.data_ptr(), acc.data_ptr(), wp, wn,
                                      torch.cuda.current_stream().cuda_stream))
 
 

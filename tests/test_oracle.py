@@ -328,3 +328,24 @@ def test_linear_w8a32_bound_holds_for_f32_accumulation():
             for k in range(256):
                 acc = np.float32(acc + np.float32(x[m, k] * w[n, k]))
             assert abs(float(acc) - y[m, n]) <= bound[m, n]
+
+
+def test_gelu_closed_form():
+    """oracle.gelu against the definition with math.erf element by element, the exact
+    identity gelu(x) - gelu(-x) = x (Φ(x) + Φ(-x) = 1), gelu(0) = 0, the large-|x| limits,
+    and torch's own CPU gelu (a library routine) at float32 precision."""
+    import math
+
+    import torch
+    rng = np.random.default_rng(3)
+    x = np.concatenate([rng.normal(size=2000) * 3, [0.0, 1e-8, -1e-8, 8.0, -8.0, 30.0, -30.0]]).astype(np.float32)
+    g = O.gelu(x)
+    ref = np.array([0.5 * float(v) * (1.0 + math.erf(float(v) / math.sqrt(2.0))) for v in x], np.float64)
+    np.testing.assert_allclose(g, ref.astype(np.float32), rtol=0, atol=0)
+    x64 = x.astype(np.float64)
+    odd = O.gelu(x).astype(np.float64) - O.gelu(-x).astype(np.float64)
+    np.testing.assert_allclose(odd, x64, rtol=2e-7, atol=1e-12)
+    assert O.gelu(np.float32(0.0)) == 0.0
+    assert O.gelu(np.float32(30.0)) == np.float32(30.0) and O.gelu(np.float32(-30.0)) == 0.0
+    tg = torch.nn.functional.gelu(torch.from_numpy(x)).numpy()
+    np.testing.assert_allclose(g, tg, rtol=1e-5, atol=1e-6)  # torch rounds in f32: 1 + erf cancels
