@@ -52,6 +52,8 @@ SIGNATURES = {
                                    _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_int, _c_p, _c_p, _c_p, _c_p,
                                    _c_size, _c_p]),
     "bq_quantize_nhwc_parts": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_p]),
+    "bq_quantize_nhwc_chscale": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_p,
+                                          _c_size, _c_p]),
     "bq_dwconv_i8_nhwc": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i64,
                                    _c_i64, _c_p, _c_p, _c_p, _c_int, _c_p, _c_p, _c_p]),
     "bq_gemv_w8a32": (_c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_int, _c_p, _c_p]),

@@ -18,6 +18,24 @@ int set_error(int code, const char* fmt, ...);
 // Maps the launch status (hipGetLastError) onto the return codes.
 int check_launch(const char* what);
 
+// Division by a run-time invariant d >= 1 of any n < 2^31 as (umulhi(n, mul) + n) >> shift
+// with shift = ceil(log2 d) and mul = floor(2^32 (2^shift - d) / d) + 1 (Granlund and
+// Montgomery, "Division by invariant integers using multiplication", PLDI 1994, the
+// round-up method; the sum cannot overflow 32 bits for n < 2^31). Three instructions
+// instead of a full integer division in per-element or per-stage index arithmetic.
+struct FastDiv {
+  uint32_t mul;
+  int shift;
+};
+static inline FastDiv fast_div(uint32_t d) {
+  int l = 0;
+  while ((1ull << l) < d) ++l;
+  return FastDiv{(uint32_t)(((1ull << 32) * ((1ull << l) - d)) / d + 1), l};
+}
+__device__ __forceinline__ int fdiv(int n, uint32_t mul, int shift) {
+  return (int)((__umulhi((uint32_t)n, mul) + (uint32_t)n) >> shift);
+}
+
 // Wave64 max of a non-negative float.
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll

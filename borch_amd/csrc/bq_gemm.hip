@@ -60,24 +60,6 @@ struct GemmP {
   float* amax;
 };
 
-// Division by a run-time invariant d >= 1 of any n < 2^31 as (umulhi(n, mul) + n) >> shift
-// with shift = ceil(log2 d) and mul = floor(2^32 (2^shift - d) / d) + 1 (Granlund and
-// Montgomery, "Division by invariant integers using multiplication", PLDI 1994, the
-// round-up method; the sum cannot overflow 32 bits for n < 2^31). Three instructions
-// instead of a full integer division in the conv loader's per-stage address arithmetic.
-struct FastDiv {
-  uint32_t mul;
-  int shift;
-};
-static inline FastDiv fast_div(uint32_t d) {
-  int l = 0;
-  while ((1ull << l) < d) ++l;
-  return FastDiv{(uint32_t)(((1ull << 32) * ((1ull << l) - d)) / d + 1), l};
-}
-__device__ __forceinline__ int fdiv(int n, uint32_t mul, int shift) {
-  return (int)((__umulhi((uint32_t)n, mul) + (uint32_t)n) >> shift);
-}
-
 constexpr int BK = 128;  // bytes of K per LDS stage: one cache line per row
 // Split-K is compiled into (and offered to) tiles of at most this many outputs only.
 constexpr int SPLIT_MAX_TILE = 64 * 64;

@@ -195,6 +195,88 @@ __global__ __launch_bounds__(QT_THREADS) void quantize_pad16_kernel(const float*
   }
 }
 
+// Per-(image, channel) pre-scaled per-tensor quantization (a squeeze-excite product feeding
+// a conv): the value quantized is v = fl(x[p, c] * cs[p / HW, c]), one f32 multiply, never
+// stored. x [P, C] channels-last with C % 4 == 0; cs [N, C]; P * Cpad < 2^31 (32-bit
+// indices). Thread: one 4-channel group of one pixel; the (pixel, group) walk advances by a
+// fixed stride, so no per-element division; the image index is a multiply-high division.
+struct ChWalk {
+  int pix, g;            // current pixel and 4-channel group
+  int step_pix, step_g;  // the grid stride in (pixels, groups)
+  int groups;
+  __device__ ChWalk(int groups_, int start, int stride) : groups(groups_) {
+    pix = start / groups;
+    g = start - pix * groups;
+    step_pix = stride / groups;
+    step_g = stride - step_pix * groups;
+  }
+  __device__ void next() {
+    pix += step_pix;
+    g += step_g;
+    if (g >= groups) {
+      g -= groups;
+      ++pix;
+    }
+  }
+};
+
+__device__ __forceinline__ float4 chscaled(const float* __restrict__ x, const float* __restrict__ cs, int pix, int g,
+                                           int C, uint32_t hw_mul, int hw_shift) {
+  const float4 v = *reinterpret_cast<const float4*>(x + (size_t)pix * C + g * 4);
+  const int n = fdiv(pix, hw_mul, hw_shift);
+  const float4 k = *reinterpret_cast<const float4*>(cs + (size_t)n * C + g * 4);
+  return make_float4(__fmul_rn(v.x, k.x), __fmul_rn(v.y, k.y), __fmul_rn(v.z, k.z), __fmul_rn(v.w, k.w));
+}
+
+__global__ __launch_bounds__(QT_THREADS) void absmax_chscale_kernel(const float* __restrict__ x,
+                                                                    const float* __restrict__ cs, int P, int C,
+                                                                    uint32_t hw_mul, int hw_shift,
+                                                                    float* __restrict__ parts) {
+  __shared__ float red[QT_THREADS / 64];
+  const int stride = gridDim.x * QT_THREADS;
+  float m = 0.f;
+  for (ChWalk w(C / 4, blockIdx.x * QT_THREADS + threadIdx.x, stride); w.pix < P; w.next()) {
+    const float4 v = chscaled(x, cs, w.pix, w.g, C, hw_mul, hw_shift);
+    m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+  }
+  m = wave_max(m);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float r = red[0];
+    for (int i = 1; i < QT_THREADS / 64; ++i) r = fmaxf(r, red[i]);
+    parts[blockIdx.x] = r;
+  }
+}
+
+// q [P, Cpad]: channels C..Cpad-1 zero (Cpad % 4 == 0). Thread: one 4-byte word.
+__global__ __launch_bounds__(QT_THREADS) void quantize_chscale_kernel(const float* __restrict__ x,
+                                                                      const float* __restrict__ cs, int P, int C,
+                                                                      int Cpad, uint32_t hw_mul, int hw_shift,
+                                                                      const float* __restrict__ parts, int nparts,
+                                                                      int8_t* __restrict__ q, float* __restrict__ s,
+                                                                      const float* __restrict__ s_given) {
+  __shared__ float red[QT_THREADS / 64];
+  float m = 0.f;
+  for (int i = threadIdx.x; i < nparts; i += QT_THREADS) m = fmaxf(m, parts[i]);
+  m = wave_max(m);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  float peak = red[0];
+  for (int i = 1; i < QT_THREADS / 64; ++i) peak = fmaxf(peak, red[i]);
+  const float sc = s_given ? s_given[0] : scale_of(peak);
+  if (!s_given && blockIdx.x == 0 && threadIdx.x == 0) s[0] = sc;
+  const int c4n = C / 4;
+  for (ChWalk w(Cpad / 4, blockIdx.x * QT_THREADS + threadIdx.x, gridDim.x * QT_THREADS); w.pix < P; w.next()) {
+    uint32_t word = 0;
+    if (w.g < c4n) {
+      const float4 v = chscaled(x, cs, w.pix, w.g, C, hw_mul, hw_shift);
+      word = pack4(quant_one(v.x, sc), quant_one(v.y, sc), quant_one(v.z, sc), quant_one(v.w, sc));
+    }
+    *reinterpret_cast<uint32_t*>(q + (size_t)w.pix * Cpad + w.g * 4) = word;
+  }
+}
+
 static int nparts_for(int64_t n) {
   int64_t p = (n + QT_THREADS * 16 - 1) / (QT_THREADS * 16);
   if (p < 1) p = 1;
@@ -314,6 +396,39 @@ int bq_quantize_nhwc_parts(const float* x, int64_t P, int64_t C, int64_t Cpad, c
   if (!absmax_parts) return set_error(BQ_ERR_ARG, "bq_quantize_nhwc_parts: null partial maxima");
   return quantize_nhwc_impl("bq_quantize_nhwc_parts", x, P, C, Cpad, q, s, nullptr, nullptr, 0, (hipStream_t)stream,
                             absmax_parts, nparts);
+}
+
+int bq_quantize_nhwc_chscale(const float* x, int64_t N, int64_t HW, int64_t C, int64_t Cpad, const float* cs,
+                             int8_t* q, float* s, const float* s_given, void* ws, size_t ws_bytes,
+                             bq_stream_t stream) {
+  const char* what = "bq_quantize_nhwc_chscale";
+  if (N < 0 || HW < 1 || C < 1 || Cpad < C) return set_error(BQ_ERR_ARG, "%s: bad sizes", what);
+  if (C % 4 || Cpad % 4) return set_error(BQ_ERR_UNSUPPORTED, "%s: C and Cpad must be multiples of 4", what);
+  if (Cpad > 0x7fffffff) return set_error(BQ_ERR_ARG, "%s: too many channels", what);
+  if (!x || !cs || !q || (!s && !s_given)) return set_error(BQ_ERR_ARG, "%s: null pointer", what);
+  if (((uintptr_t)x | (uintptr_t)cs) & 15 || (uintptr_t)q & 3)
+    return set_error(BQ_ERR_ARG, "%s: x and cs must be 16-byte aligned, q 4-byte aligned", what);
+  const int64_t P = N * HW;
+  if (P == 0) return BQ_OK;
+  if (P * Cpad >= ((int64_t)1 << 31) || HW > 0x7fffffff)
+    return set_error(BQ_ERR_ARG, "%s: size too large (P * Cpad must be < 2^31)", what);
+  hipStream_t st = (hipStream_t)stream;
+  const FastDiv dhw = fast_div((uint32_t)HW);
+  int np = 0;
+  float* parts = nullptr;
+  if (!s_given) {
+    np = nparts_for(P * C);
+    if (!ws || ws_bytes < (size_t)np * sizeof(float))
+      return set_error(BQ_ERR_ARG, "%s: workspace %zu bytes, need %zu", what, ws_bytes, (size_t)np * sizeof(float));
+    parts = (float*)ws;
+    absmax_chscale_kernel<<<np, QT_THREADS, 0, st>>>(x, cs, (int)P, (int)C, dhw.mul, dhw.shift, parts);
+    if (int r = check_launch(what)) return r;
+  }
+  int64_t blocks = (P * (Cpad / 4) + QT_THREADS - 1) / QT_THREADS;
+  if (blocks > 8192) blocks = 8192;
+  quantize_chscale_kernel<<<(unsigned)blocks, QT_THREADS, 0, st>>>(x, cs, (int)P, (int)C, (int)Cpad, dhw.mul,
+                                                                   dhw.shift, parts, np, q, s, s_given);
+  return check_launch(what);
 }
 
 int bq_quantize_nhwc_scaled(const float* x, int64_t P, int64_t C, int64_t Cpad, const float* s, int8_t* q,

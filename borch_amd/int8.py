@@ -19,7 +19,7 @@ __all__ = [
     "ACT_NONE", "ACT_RELU", "ACT_SILU", "ACT_GELU", "Int8Weight", "Int8ConvWeight", "Int8DwWeight",
     "quantize_rows", "quantize_weight_per_channel", "quantize_tensor", "quantize_nhwc",
     "gemm_i8", "conv2d_i8_nhwc", "conv2d_i8_nhwc_q", "dwconv_i8_nhwc", "pack_linear_weight", "pack_conv_weight",
-    "quantize_nhwc_scaled", "linear_w8a32", "dequant_weight",
+    "quantize_nhwc_scaled", "quantize_nhwc_chscale", "linear_w8a32", "dequant_weight",
     "pack_dw_weight", "linear", "conv2d", "depthwise_conv2d", "round_up", "split_workspace",
 ]
 
@@ -141,6 +141,32 @@ def quantize_nhwc(x: torch.Tensor, cpad: int | None = None):
     ws = _ws(P * C, x.device)
     check(lib().bq_quantize_nhwc(xl.data_ptr(), P, C, cpad, q.data_ptr(), s.data_ptr(), ws.data_ptr(),
                                  ws.numel(), _stream(x)))
+    return q, s
+
+
+def quantize_nhwc_chscale(x: torch.Tensor, cs: torch.Tensor, cpad: int | None = None, scale=None):
+    """Per-tensor int8 of ``x * cs[:, :, None, None]`` (x NCHW f32, cs [N, C] f32: a
+    squeeze-excite gate) into NHWC int8 ``[N, H, W, cpad]`` without storing the product
+    (bq_quantize_nhwc_chscale): ``(q, s [1])``, the same bytes as quantizing the product.
+    With ``scale`` (a calibrated [1] tensor) one pass and that scale."""
+    if x.dtype != torch.float32 or cs.dtype != torch.float32:
+        raise TypeError("int8 path takes float32 activations and gates")
+    require_device(x.device)
+    N, C, H, W = x.shape
+    if tuple(cs.shape) != (N, C):
+        raise RuntimeError(f"channel scale shape {tuple(cs.shape)} != {(N, C)}")
+    cpad = C if cpad is None else int(cpad)
+    xl = x.contiguous(memory_format=torch.channels_last)
+    csc = cs.contiguous()
+    q = torch.empty((N, H, W, cpad), dtype=torch.int8, device=x.device)
+    if scale is not None:
+        check(lib().bq_quantize_nhwc_chscale(xl.data_ptr(), N, H * W, C, cpad, csc.data_ptr(), q.data_ptr(), None,
+                                             scale.data_ptr(), None, 0, _stream(x)))
+        return q, scale
+    s = torch.empty((1,), dtype=torch.float32, device=x.device)
+    ws = _ws(N * H * W * C, x.device)
+    check(lib().bq_quantize_nhwc_chscale(xl.data_ptr(), N, H * W, C, cpad, csc.data_ptr(), q.data_ptr(),
+                                         s.data_ptr(), None, ws.data_ptr(), ws.numel(), _stream(x)))
     return q, s
 
 

@@ -159,16 +159,25 @@ class MBConv(tnn.Module):
         self.residual = stride == 1 and cin == cout
         self.fused = False
 
+    def _se_gate(self, h):
+        """Squeeze-excite gates [N, C] in f32: the 1x1 convs on the pooled 1x1 map run as
+        the equal matrix products on [N, C] (one small GEMM each instead of a conv)."""
+        s = h.mean(dim=(2, 3))
+        s = torch.nn.functional.silu(torch.nn.functional.linear(s, self.se_reduce.weight.flatten(1),
+                                                               self.se_reduce.bias))
+        return torch.sigmoid(torch.nn.functional.linear(s, self.se_expand.weight.flatten(1), self.se_expand.bias))
+
     def _se(self, h):
-        s = h.mean(dim=(2, 3), keepdim=True)
-        s = torch.sigmoid(self.se_expand(torch.nn.functional.silu(self.se_reduce(s))))
-        return h * s
+        return h * self._se_gate(h)[:, :, None, None]
 
     def forward(self, x):
         if self.fused:
+            # the gate multiplies the projection's input inside its int8 quantization
+            # (f32: a plain product): the gated tensor is never stored
             h = self.expand(x) if self.expand is not None else x
-            h = self._se(self.dw(h))
-            return self.project(h, x) if self.residual else self.project(h)
+            h = self.dw(h)
+            g = self._se_gate(h)
+            return self.project(h, x, channel_scale=g) if self.residual else self.project(h, channel_scale=g)
         h = torch.nn.functional.silu(self.bn0(self.expand(x))) if self.has_expand else x
         h = torch.nn.functional.silu(self.bn1(self.dw(h)))
         h = self.bn2(self.project(self._se(h)))

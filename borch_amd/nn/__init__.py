@@ -186,12 +186,16 @@ class Conv2d(_tnn.Module):
             _i8.split_workspace(self.weight.device)  # made now, before any graph capture
         return True
 
-    def _int8_input(self, x):
+    def _int8_input(self, x, channel_scale=None):
         """(q NHWC int8, scale [1]) for the int8 kernels, cheapest first, as
         tensor.ts:11909-11921: the producer's int8 twin when its scale is this layer's
         calibrated input scale and ``x`` is unchanged since; else one pass with the static
-        scale; else the dynamic per-tensor quantization."""
+        scale; else the dynamic per-tensor quantization. With ``channel_scale`` [N, C] the
+        layer's input is ``x * channel_scale`` (a squeeze-excite gate), quantized without
+        storing the product."""
         cpad = self.int8.cpad
+        if channel_scale is not None:
+            return _i8.quantize_nhwc_chscale(x, channel_scale, cpad, self.in_scale)
         if self.in_scale is not None:
             twin = getattr(x, "_int8_twin", None)
             if (twin is not None and twin[2] == self.in_scale_v and twin[3] == x._version
@@ -207,7 +211,13 @@ class Conv2d(_tnn.Module):
             out = out + residual
         return _i8._act_f32(out, self.act)
 
-    def forward(self, x, residual=None):
+    def forward(self, x, residual=None, channel_scale=None):
+        """``conv(x) (+ residual)`` then the activation. ``channel_scale`` [N, C] (optional)
+        multiplies the input per image and channel first (a squeeze-excite gate); the int8
+        path folds it into the input's quantization."""
+        if channel_scale is not None and (self.int8 is None or _CALIBRATING):
+            x = x * channel_scale[:, :, None, None]
+            channel_scale = None
         if self.int8 is not None and _CALIBRATING:
             out = self._f32_forward(x, residual)
             cin, cout = x.detach().abs().amax(), out.detach().abs().amax()
@@ -219,7 +229,7 @@ class Conv2d(_tnn.Module):
             if x.dim() != 4 or x.shape[1] != self.in_channels:
                 raise RuntimeError(f"channels do not match: input {x.shape[1] if x.dim() > 1 else x.shape}, "
                                    f"filter {self.in_channels}")
-            qx, sa = self._int8_input(x)
+            qx, sa = self._int8_input(x, channel_scale)
             if isinstance(self.int8, _i8.Int8DwWeight):
                 out = _i8.dwconv_i8_nhwc(qx, sa, self.int8, stride, pad, self.bias,
                                          self.act if residual is None else _i8.ACT_NONE)

@@ -34,10 +34,10 @@ class ConvAdd2d(_tnn.Module):
         self.conv.act = _i8.ACT_NONE
         self.training = False
 
-    def forward(self, x, residual=None):
+    def forward(self, x, residual=None, channel_scale=None):
         if residual is None:
             raise TypeError("ConvAdd2d.forward takes (x1, x2)")
-        return self.conv(x, residual)
+        return self.conv(x, residual, channel_scale)
 
 
 class ConvAddReLU2d(_tnn.Module):

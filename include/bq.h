@@ -95,6 +95,17 @@ int bq_quantize_nhwc(const float* x, int64_t P, int64_t C, int64_t Cpad, int8_t*
 int bq_quantize_nhwc_parts(const float* x, int64_t P, int64_t C, int64_t Cpad, const float* absmax_parts,
                            int64_t nparts, int8_t* q, float* s, bq_stream_t stream);
 
+/* Per-tensor quantization of a per-(image, channel) scaled activation: the value quantized
+ * is fl(x[n, p, c] * cs[n, c]) (one f32 multiply, never stored), x f32 [N*HW, C]
+ * channels-last, cs f32 [N, C] (a squeeze-excite's sigmoid gates), into q int8
+ * [N*HW, Cpad] (channels C..Cpad-1 zero). The scale is s_given[0] when s_given is non-null
+ * (calibrated; one pass), else float32(max|fl(x*cs)| / 127) into s[0] (two passes, partial
+ * maxima in ws, bq_quantize_tensor_ws_bytes(N*HW*C) bytes). The same bytes as quantizing
+ * the stored product. C and Cpad multiples of 4; x, cs 16-byte aligned. */
+int bq_quantize_nhwc_chscale(const float* x, int64_t N, int64_t HW, int64_t C, int64_t Cpad, const float* cs,
+                             int8_t* q, float* s, const float* s_given, void* ws, size_t ws_bytes,
+                             bq_stream_t stream);
+
 /* The same quantization with a given (calibrated) scale s f32 [1]: one pass, no maximum.
  * The static-scale input of borch-ts (int8.inMax, tensor.ts:11912-11913; calibrateInt8
  * nn.ts:6790-6824). Values beyond the calibrated range clamp to +-127. */

@@ -43,9 +43,12 @@ def capture(model, rows=None):
     may return row indices to keep (Linear inputs flattened to [M, K])."""
     recs, hooks = [], []
     for name, m in int8_modules(model):
-        def hook(mod, args, out, name=name):
+        def hook(mod, args, kwargs, out, name=name):
             x = args[0].detach()
             res = args[1].detach() if len(args) > 1 and args[1] is not None else None
+            gate = args[2] if len(args) > 2 else kwargs.get("channel_scale")
+            if gate is not None:  # the layer's input is x * gate (the kernel forms the same f32 products)
+                x = x * gate.detach()[:, :, None, None]
             if isinstance(mod, bt.nn.Linear):
                 x2, y2 = x.reshape(-1, x.shape[-1]), out.detach().reshape(-1, out.shape[-1])
                 r2 = None if res is None else res.reshape(-1, res.shape[-1])
@@ -56,7 +59,7 @@ def capture(model, rows=None):
                 recs.append((name, mod, n(x2), None if r2 is None else n(r2), n(y2)))
             else:
                 recs.append((name, mod, n(x), None if res is None else n(res), n(out)))
-        hooks.append(m.register_forward_hook(hook))
+        hooks.append(m.register_forward_hook(hook, with_kwargs=True))
     return recs, hooks
 
 

@@ -87,6 +87,26 @@ def test_quantize_nhwc(dev, shape, cpad, cl):
     assert np.array_equal(n(q), qo)
 
 
+@pytest.mark.parametrize("N,C,H,cpad", [(4, 96, 14, 96), (3, 36, 9, 48), (64, 1152, 7, 1152), (2, 8, 5, 16)])
+def test_quantize_chscale(dev, N, C, H, cpad):
+    """The squeeze-excite-gated quantizer equals quantizing the stored product x * gate
+    (bytes and scale), dynamic and with a calibrated scale; padding channels are zero."""
+    say(f"quantize_nhwc_chscale N={N} C={C} H={H} cpad={cpad}")
+    rng = np.random.default_rng(N + C + H)
+    x = t(rng.normal(size=(N, C, H, H)).astype(np.float32), dev).contiguous(memory_format=torch.channels_last)
+    g = t(rng.uniform(0, 1, size=(N, C)).astype(np.float32), dev)
+    prod = x * g[:, :, None, None]
+    q1, s1 = I.quantize_nhwc_chscale(x, g, cpad)
+    q2, s2 = I.quantize_nhwc(prod.clone(memory_format=torch.channels_last), cpad)
+    assert torch.equal(s1, s2) and torch.equal(q1, q2)
+    qo, so = O.quantize_act_nhwc(n(prod), cpad)
+    assert np.array_equal(n(q1), qo) and np.array_equal(n(s1), so)
+    sc = torch.tensor([float(s2) * 0.5], dtype=torch.float32, device=dev)  # saturates the top half
+    q3, _ = I.quantize_nhwc_chscale(x, g, cpad, sc)
+    q4 = I.quantize_nhwc_scaled(prod, sc, cpad)
+    assert torch.equal(q3, q4)
+
+
 def test_quantize_tensor(dev):
     say("quantize_tensor")
     rng = np.random.default_rng(11)
