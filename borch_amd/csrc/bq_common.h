@@ -67,6 +67,33 @@ __device__ __forceinline__ int quant_one(float v, float s) {
   return (int)r;
 }
 
+// The same rounding without a division per element. One quantizer per scale s holds
+// r = 1/s (correctly rounded). f = fl(v * r) is within |v/s| * 1.2e-7 of the exact quotient
+// t = v/s (two roundings of 2^-24 each), i.e. within 1.6e-5 for |t| <= 127.00002 (s is at
+// least max|v| / 127 * (1 - 2^-24)). So rint(f) = rint(t) unless f lies within 4e-5 of a
+// half-integer b; there the sign of the exact remainder v - b*s (one fma: its rounding
+// keeps the sign and the zero) picks the side, and an exact tie goes to even. A
+// non-finite f (a subnormal s whose reciprocal overflows, or a non-finite v) takes
+// quant_one. Beyond the clamp (|t| > 127.5, possible with a calibrated scale) both
+// roundings clamp to the same +-127.
+struct Quantizer {
+  float s, r;
+  __device__ explicit Quantizer(float s_) : s(s_), r(s_ == 0.f ? 0.f : __fdiv_rn(1.0f, s_)) {}
+  __device__ __forceinline__ int operator()(float v) const {
+    if (s == 0.f) return 0;
+    const float f = __fmul_rn(v, r);
+    float k = rintf(f);
+    if (!(fabsf(__fsub_rn(f, k)) < 0.49996f)) {
+      if (!__builtin_isfinite(f)) return quant_one(v, s);
+      const float b = __fadd_rn(k, __builtin_copysignf(0.5f, __fsub_rn(f, k)));  // the half-integer f is near
+      const float d = __fmaf_rn(-b, s, v);
+      const float lo = __fsub_rn(b, 0.5f);
+      k = d > 0.f ? __fadd_rn(b, 0.5f) : d < 0.f ? lo : ((((int)lo) & 1) ? __fadd_rn(lo, 1.0f) : lo);
+    }
+    return (int)fminf(fmaxf(k, -127.f), 127.f);
+  }
+};
+
 __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
   return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
          ((uint32_t)(d & 0xff) << 24);

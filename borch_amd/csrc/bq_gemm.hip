@@ -395,7 +395,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
   const int per = (KT + S - 1) / S;  // stages of each split (the host picks S with no empty split)
   const int kt0 = split * per;
 
-  const float s_out = p.q_out ? p.s_out[0] : 0.f;
+  const Quantizer qz_out(p.q_out ? p.s_out[0] : 0.f);
   v16i c[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
@@ -523,7 +523,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
           if (p.acc) *reinterpret_cast<int4*>(p.acc + idx) = a;
           if (p.q_out)
             *reinterpret_cast<uint32_t*>(p.q_out + idx) =
-                pack4(quant_one(o.x, s_out), quant_one(o.y, s_out), quant_one(o.z, s_out), quant_one(o.w, s_out));
+                pack4(qz_out(o.x), qz_out(o.y), qz_out(o.z), qz_out(o.w));
           amax = fmaxf(amax, fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w))));
         }
       };
@@ -563,7 +563,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
             const float o = dequant_one(a, s_sa[mloc], s_sw[ncol + q], s_b[ncol + q], true, rv, has_r, p.act);
             p.out[idx] = o;
             if (p.acc) p.acc[idx] = a;
-            if (p.q_out) p.q_out[idx] = (int8_t)quant_one(o, s_out);
+            if (p.q_out) p.q_out[idx] = (int8_t)qz_out(o);
             amax = fmaxf(amax, fabsf(o));
           }
         }

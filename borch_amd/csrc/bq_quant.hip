@@ -66,21 +66,20 @@ __global__ __launch_bounds__(QR_THREADS) void quantize_rows_kernel(const float* 
     }
     const float sc = scale_of(block_max(m, red));
     if (t == 0) s[row] = sc;
-    const float sd = sc;
+    const Quantizer qz(sc);
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int k = (t + i * QR_THREADS) * 4;
       if (k < K)
-        *reinterpret_cast<uint32_t*>(qr + k) =
-            pack4(quant_one(v[i].x, sd), quant_one(v[i].y, sd), quant_one(v[i].z, sd), quant_one(v[i].w, sd));
+        *reinterpret_cast<uint32_t*>(qr + k) = pack4(qz(v[i].x), qz(v[i].y), qz(v[i].z), qz(v[i].w));
     }
   } else {
     float m = 0.f;
     for (int k = t; k < K; k += QR_THREADS) m = fmaxf(m, fabsf(xr[k]));
     const float sc = scale_of(block_max(m, red));
     if (t == 0) s[row] = sc;
-    const float sd = sc;
-    for (int k = t; k < K; k += QR_THREADS) qr[k] = (int8_t)quant_one(xr[k], sd);
+    const Quantizer qz(sc);
+    for (int k = t; k < K; k += QR_THREADS) qr[k] = (int8_t)qz(xr[k]);
   }
 }
 
@@ -132,7 +131,7 @@ __global__ __launch_bounds__(QT_THREADS) void quantize_tensor_kernel(const float
   for (int i = 1; i < QT_THREADS / 64; ++i) peak = fmaxf(peak, red[i]);
   const float sc = s_given ? s_given[0] : scale_of(peak);
   if (!s_given && blockIdx.x == 0 && threadIdx.x == 0) s[0] = sc;
-  const float sd = sc;
+  const Quantizer qz(sc);
   const int64_t total = P * (int64_t)Cpad;
   const int64_t words = (total + 3) / 4;
   const bool flat = (C == Cpad) && ((uintptr_t)x & 15) == 0 && ((uintptr_t)q & 3) == 0 && (total & 3) == 0;
@@ -142,14 +141,14 @@ __global__ __launch_bounds__(QT_THREADS) void quantize_tensor_kernel(const float
     if (flat) {
       const float4 v = *reinterpret_cast<const float4*>(x + e0);
       *reinterpret_cast<uint32_t*>(q + e0) =
-          pack4(quant_one(v.x, sd), quant_one(v.y, sd), quant_one(v.z, sd), quant_one(v.w, sd));
+          pack4(qz(v.x), qz(v.y), qz(v.z), qz(v.w));
     } else {
       for (int j = 0; j < 4; ++j) {
         const int64_t e = e0 + j;
         if (e >= total) break;
         const int64_t p = e / Cpad;
         const int c = (int)(e - p * Cpad);
-        q[e] = c < C ? (int8_t)quant_one(x[p * C + c], sd) : (int8_t)0;
+        q[e] = c < C ? (int8_t)qz(x[p * C + c]) : (int8_t)0;
       }
     }
   }
@@ -173,7 +172,7 @@ __global__ __launch_bounds__(QT_THREADS) void quantize_pad16_kernel(const float*
   for (int i = 1; i < QT_THREADS / 64; ++i) peak = fmaxf(peak, red[i]);
   const float sc = s_given ? s_given[0] : scale_of(peak);
   if (!s_given && blockIdx.x == 0 && threadIdx.x == 0) s[0] = sc;
-  const float sd = sc;
+  const Quantizer qz(sc);
   const int chunks = Cpad / 16;
   const int64_t total = P * chunks;
   for (int64_t i = (int64_t)blockIdx.x * QT_THREADS + threadIdx.x; i < total; i += (int64_t)gridDim.x * QT_THREADS) {
@@ -187,7 +186,7 @@ __global__ __launch_bounds__(QT_THREADS) void quantize_pad16_kernel(const float*
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const int c = c0 + j * 4 + t;
-        b[t] = c < C ? quant_one(xp[j * 4 + t], sd) : 0;
+        b[t] = c < C ? qz(xp[j * 4 + t]) : 0;
       }
       wv[j] = pack4(b[0], b[1], b[2], b[3]);
     }
@@ -267,11 +266,12 @@ __global__ __launch_bounds__(QT_THREADS) void quantize_chscale_kernel(const floa
   const float sc = s_given ? s_given[0] : scale_of(peak);
   if (!s_given && blockIdx.x == 0 && threadIdx.x == 0) s[0] = sc;
   const int c4n = C / 4;
+  const Quantizer qz(sc);
   for (ChWalk w(Cpad / 4, blockIdx.x * QT_THREADS + threadIdx.x, gridDim.x * QT_THREADS); w.pix < P; w.next()) {
     uint32_t word = 0;
     if (w.g < c4n) {
       const float4 v = chscaled(x, cs, w.pix, w.g, C, hw_mul, hw_shift);
-      word = pack4(quant_one(v.x, sc), quant_one(v.y, sc), quant_one(v.z, sc), quant_one(v.w, sc));
+      word = pack4(qz(v.x), qz(v.y), qz(v.z), qz(v.w));
     }
     *reinterpret_cast<uint32_t*>(q + (size_t)w.pix * Cpad + w.g * 4) = word;
   }
