@@ -349,3 +349,69 @@ def test_gelu_closed_form():
     assert O.gelu(np.float32(30.0)) == np.float32(30.0) and O.gelu(np.float32(-30.0)) == 0.0
     tg = torch.nn.functional.gelu(torch.from_numpy(x)).numpy()
     np.testing.assert_allclose(g, tg, rtol=1e-5, atol=1e-6)  # torch rounds in f32: 1 + erf cancels
+
+
+def test_silu_closed_form():
+    """oracle.silu against the definition with math.exp element by element, the identity
+    silu(x) - silu(-x) = x (σ(x) + σ(-x) = 1), silu(0) = 0, and torch's CPU silu."""
+    import math
+
+    import torch
+    rng = np.random.default_rng(4)
+    x = np.concatenate([rng.normal(size=2000) * 4, [0.0, 1e-8, -1e-8, 20.0, -20.0, 80.0, -80.0]]).astype(np.float32)
+    g = O.silu(x)
+    ref = np.array([float(v) / (1.0 + math.exp(-float(v))) for v in x], np.float64)
+    np.testing.assert_array_equal(g, ref.astype(np.float32))
+    odd = O.silu(x).astype(np.float64) - O.silu(-x).astype(np.float64)
+    np.testing.assert_allclose(odd, x.astype(np.float64), rtol=2e-7, atol=1e-30)
+    assert O.silu(np.float32(0.0)) == 0.0
+    np.testing.assert_allclose(g, torch.nn.functional.silu(torch.from_numpy(x)).numpy(), rtol=1e-5, atol=1e-6)
+
+
+def _on_grid(rng, shape, step):
+    """Values q * step with q in [-127, 127] and some |q| = 127 per row (quantization by the
+    rule is then exact: the scale is step, the bytes are q)."""
+    q = rng.integers(-127, 128, size=shape).astype(np.float64)
+    q.reshape(shape[0], -1)[:, 0] = 127.0
+    return (q * step).astype(np.float32)
+
+
+def test_composed_layers_on_exact_grids():
+    """The oracle's composed int8 layers (oracle/models.py conv_layer / dwconv_layer /
+    linear_layer, oracle/quant.py conv2d_int8) on inputs whose quantization loses nothing
+    (activations on a per-tensor grid, weights on per-channel grids, a power-of-two step so
+    every product is exact): then y = conv(x, w) + b (+ residual) exactly in float64, which
+    torch's float64 conv2d / linear (library routines) give independently, to a few f32 ulps."""
+    import torch
+    from oracle import models as OM
+    F = torch.nn.functional
+    rng = np.random.default_rng(5)
+    step_x = 2.0 ** -6
+    for (N, C, H, O_, k, stride, pad) in [(2, 3, 9, 8, 3, 1, 1), (1, 20, 8, 12, 3, 2, 1), (2, 16, 7, 16, 1, 1, 0),
+                                          (1, 5, 11, 6, 5, 2, 2)]:
+        x = _on_grid(rng, (N, C, H, H), step_x)
+        x.reshape(-1)[0] = np.float32(127 * step_x)  # the tensor's peak is exactly 127 steps
+        x = np.clip(x, -127 * step_x, 127 * step_x).astype(np.float32)
+        w = np.stack([_on_grid(rng, (1, C, k, k), 2.0 ** -int(rng.integers(3, 9)))[0] for _ in range(O_)])
+        b = (rng.integers(-64, 64, size=O_) * 2.0 ** -8).astype(np.float32)
+        OH = (H + 2 * pad - k) // stride + 1
+        res = (rng.integers(-64, 64, size=(N, O_, OH, OH)) * 2.0 ** -8).astype(np.float32)
+        want = F.conv2d(torch.from_numpy(x).double(), torch.from_numpy(w).double(), torch.from_numpy(b).double(),
+                        stride, pad).numpy()
+        y, acc, sA, sW, qw = OM.conv_layer(x, w, b, stride, pad, OM.ACT_RELU, res)
+        np.testing.assert_allclose(y, np.maximum(want + res, 0), rtol=1e-6, atol=1e-7)
+        y2, _, _, _ = O.conv2d_int8(x, w, b, stride, pad, True, res, (C + 15) // 16 * 16)
+        np.testing.assert_array_equal(y2, y)
+        wd = np.stack([_on_grid(rng, (1, 1, k, k), 2.0 ** -5)[0] for _ in range(C)])
+        yd, _, _, _, _ = OM.dwconv_layer(x, wd, b[:1].repeat(C), stride, pad)
+        wantd = F.conv2d(torch.from_numpy(x).double(), torch.from_numpy(wd).double(),
+                         torch.from_numpy(b[:1].repeat(C)).double(), stride, pad, groups=C).numpy()
+        np.testing.assert_allclose(yd, wantd, rtol=1e-6, atol=1e-7)
+    # Linear, per-row activations: each row on its own grid; residual and GELU after the bias
+    xl = np.stack([_on_grid(rng, (1, 40), 2.0 ** -int(rng.integers(2, 8)))[0] for _ in range(6)])
+    wl = np.stack([_on_grid(rng, (1, 40), 2.0 ** -int(rng.integers(4, 9)))[0] for _ in range(10)])
+    bl = (rng.integers(-64, 64, size=10) * 2.0 ** -8).astype(np.float32)
+    rl = (rng.integers(-64, 64, size=(6, 10)) * 2.0 ** -8).astype(np.float32)
+    want = F.linear(torch.from_numpy(xl).double(), torch.from_numpy(wl).double(), torch.from_numpy(bl).double())
+    y, _, _, _, _ = OM.linear_layer(xl, wl, bl, OM.ACT_GELU, rl)
+    np.testing.assert_allclose(y, O.gelu((want.numpy() + rl).astype(np.float32)), rtol=1e-6, atol=1e-7)
