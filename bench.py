@@ -120,6 +120,53 @@ def probes(dev, stream, qa, qw, wcopies):
                           f"{ch} x 16 B loads a lane (best of 1/2/4/8)"}
 
 
+# EfficientNet-B0 b64 depthwise layers (channels, input size, kernel, stride) timed alone
+B0_DW = [(96, 112, 3, 2), (144, 56, 3, 1), (144, 56, 5, 2), (240, 28, 5, 1), (672, 14, 5, 1), (1152, 7, 5, 1)]
+
+
+def hbm_kernels(dev):
+    """The bandwidth-bound kernels alone, for counter runs (FETCH_SIZE / WRITE_SIZE and the
+    kernel trace): one JSON line of what ran, with the algorithmic bytes of each."""
+    import torch
+    from borch_amd import int8 as I
+    from borch_amd import workloads as WL
+    g = torch.Generator().manual_seed(0)
+    ran = {}
+    a1, w1, b1 = WL.c2_gemm(16, 0)
+    qw, sw = I.quantize_weight_per_channel(torch.from_numpy(w1).to(dev))
+    qws = [qw.clone() for _ in range(24)]
+    B = torch.from_numpy(b1).to(dev)
+    for m in (1, 16):
+        qa, sa = I.quantize_rows(torch.from_numpy(a1[:m]).to(dev))
+        for q in qws:
+            I.gemm_i8(qa, q, sa, sw, B)
+        ran[f"gemm M={m} (24 rotated weights)"] = WL.gemm_bytes(m)
+    A = torch.from_numpy(WL.c2_gemm(4096, 0)[0]).to(dev)
+    for _ in range(5):
+        I.quantize_rows(A)
+    ran["quantize_rows 4096x4096 (5x)"] = 5 * 4096 * 4096 + 4 * 4096
+    del A
+    for C, H, k, st in B0_DW:
+        x = torch.randn(64, C, H, H, generator=g).to(dev).contiguous(memory_format=torch.channels_last)
+        w8 = I.pack_dw_weight(torch.randn(C, 1, k, k, generator=g).to(dev))
+        qx, sa = I.quantize_nhwc(x, w8.cpad)
+        for _ in range(3):
+            I.dwconv_i8_nhwc(qx, sa, w8, st, k // 2, None, I.ACT_SILU)
+        OH = (H + 2 * (k // 2) - k) // st + 1
+        ran[f"dwconv C={C} H={H} k={k} s={st} (3x)"] = 64 * H * H * w8.cpad + 64 * OH * OH * w8.cpad * 4 + k * k * w8.cpad
+        del x, qx
+    x = torch.randn(64, 144, 56, 56, generator=g).to(dev).contiguous(memory_format=torch.channels_last)
+    for _ in range(3):
+        I.quantize_nhwc(x, 144)
+    ran["quantize_nhwc 64x144x56x56 two-pass (3x)"] = 64 * 144 * 56 * 56 * 9
+    src = torch.randn(16 << 20, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"hbm_kernels": ran, "copy_launches": 5, "copy_bytes": 64 << 20}))
+
+
 def cpu_baseline(M_sample=512):
     """The reference's CPU path on the host cores, on a bounded sample of the same workload.
 
@@ -243,6 +290,10 @@ def main():
     ap.add_argument("--kernels-only", action="store_true",
                     help="for counter runs: 5 launches of the 4096^3 GEMM and 5 of a 64 MiB device copy "
                          "(the copy calibrates FETCH_SIZE / WRITE_SIZE), nothing else")
+    ap.add_argument("--hbm-kernels", action="store_true",
+                    help="for counter runs: the bandwidth-bound kernels alone (GEMV M=1 and skinny M=16 over 24 "
+                         "rotated weights, the 4096x4096 per-row quantize, EfficientNet-B0 b64 depthwise layers, a "
+                         "per-tensor quantize) and 5 launches of a 64 MiB device copy; prints their shapes and bytes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this build runs on one GPU only: the int8 path is measured on 1 MI355X "
@@ -258,6 +309,10 @@ def main():
     require_device(dev)
     stream = torch.cuda.current_stream(dev)
     M = N = K = 4096
+
+    if args.hbm_kernels:
+        hbm_kernels(dev)
+        return
 
     if args.kernels_only:
         from borch_amd import workloads as WL2
