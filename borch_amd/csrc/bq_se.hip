@@ -1,0 +1,208 @@
+// Squeeze-excite gates in f32 for a channels-last activation (EfficientNet's MBConv):
+//   pooled[n, c] = (sum over the HW pixels of x[n, p, c]) * (1 / HW)
+//   z[n, j]      = silu(b1[j] + sum_c w1[j, c] * pooled[n, c])        (j < S, the squeeze width)
+//   gate[n, c]   = sigmoid(b2[c] + sum_j w2t[j, c] * z[n, j])   (w2t: the expand weight transposed)
+// the operation of borch's CPU runner "se" node (borch-ts/src/cpu/runner.ts:256-268:
+// meanRows, gemmBiasAct(swish), gemmBiasAct(sigmoid); lib.rs:222-244 mean_rows). The gate
+// multiplies the activation inside the next conv's quantizer (bq_quantize_nhwc_chscale)
+// instead of the runner's scaleRows pass. Two kernels: partial sums over row chunks (the
+// bandwidth pass), then one workgroup per image finishes the mean and runs the small MLP.
+// Every sum has a fixed order: results do not depend on scheduling.
+#include <algorithm>
+
+#include "bq_common.h"
+
+namespace bq {
+
+constexpr int SE_THREADS = 256;    // the partial-sum pass
+constexpr int GATE_THREADS = 1024; // the per-image pass: 16 waves cover the squeeze outputs and channels
+
+__device__ __forceinline__ float sigmoid_f(float v) {
+  return __builtin_amdgcn_rcpf(__fadd_rn(1.0f, __builtin_amdgcn_exp2f(__fmul_rn(v, -1.4426950408889634f))));
+}
+
+// Block (n, chunk): rows [chunk * rows_per, ...) of image n; thread t sums channel group
+// g = t % G (4 channels) over the rows r = t / G, t / G + TR, ... of the chunk (TR = 256 / G
+// row lanes, G >= 1 groups a pass, more passes when C / 4 > 256), eight rows' loads issued
+// before they are added in row order; the TR row-lane sums of a group are then added in
+// lane order through LDS. partial[(n * chunks + chunk) * C + c].
+__global__ __launch_bounds__(SE_THREADS) void se_partial_kernel(const float* __restrict__ x, int HW, int C,
+                                                                int chunks, int rows_per,
+                                                                float* __restrict__ partial) {
+  __shared__ float4 red[SE_THREADS];
+  const int n = blockIdx.x / chunks, chunk = blockIdx.x - n * chunks;
+  const int r0 = chunk * rows_per, r1 = min(HW, r0 + rows_per);
+  const int groups = C / 4;
+  const int G = min(groups, SE_THREADS);
+  const int TR = SE_THREADS / G;
+  const int t = threadIdx.x;
+  const int lane_r = t / G, g0 = t - lane_r * G;
+  const float* xn = x + (size_t)n * HW * C;
+  constexpr int U = 8;
+  for (int gb = 0; gb < groups; gb += G) {
+    const int g = gb + g0;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (lane_r < TR && g < groups) {
+      const float* xg = xn + g * 4;
+      for (int r = r0 + lane_r; r < r1; r += U * TR) {
+        float4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int rr = r + u * TR;
+          v[u] = rr < r1 ? *reinterpret_cast<const float4*>(xg + (size_t)rr * C) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          acc.x = __fadd_rn(acc.x, v[u].x); acc.y = __fadd_rn(acc.y, v[u].y);
+          acc.z = __fadd_rn(acc.z, v[u].z); acc.w = __fadd_rn(acc.w, v[u].w);
+        }
+      }
+    }
+    red[t] = acc;
+    __syncthreads();
+    if (t < G && gb + t < groups) {
+      float4 s = red[t];
+      for (int k = 1; k < TR; ++k) {
+        const float4 v = red[k * G + t];
+        s.x = __fadd_rn(s.x, v.x); s.y = __fadd_rn(s.y, v.y);
+        s.z = __fadd_rn(s.z, v.z); s.w = __fadd_rn(s.w, v.w);
+      }
+      *reinterpret_cast<float4*>(partial + ((size_t)n * chunks + chunk) * C + (gb + t) * 4) = s;
+    }
+    __syncthreads();
+  }
+}
+
+// One block per image: pooled (in LDS), z = silu(W1 pooled + b1) (one wave per output
+// j, its lanes over c, a wave tree), gate = sigmoid(W2 z + b2) (one thread per channel,
+// reading the transposed expand weight w2t [S, C] so a wave's loads are contiguous).
+__global__ __launch_bounds__(GATE_THREADS) void se_gate_kernel(const float* __restrict__ partial, int chunks, int HW,
+                                                             int C, int S, const float* __restrict__ w1,
+                                                             const float* __restrict__ b1,
+                                                             const float* __restrict__ w2t,
+                                                             const float* __restrict__ b2, float* __restrict__ gate) {
+  extern __shared__ float sm[];  // pooled [C], z [S]
+  float* pooled = sm;
+  float* z = sm + C;
+  const int n = blockIdx.x;
+  const float inv = __fdiv_rn(1.0f, (float)HW);
+  for (int c = threadIdx.x; c < C; c += GATE_THREADS) {
+    float s = 0.f;
+    for (int k0 = 0; k0 < chunks; k0 += 8) {  // eight loads in flight, added in chunk order
+      float v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] = k0 + k < chunks ? partial[((size_t)n * chunks + k0 + k) * C + c] : 0.f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        if (k0 + k < chunks) s = __fadd_rn(s, v[k]);
+    }
+    pooled[c] = __fmul_rn(s, inv);
+  }
+  __syncthreads();
+  // z: each wave builds JW outputs at once, its lanes over c (c = lane, lane + 64, ... in
+  // order for every output), all loads of a batch issued before its FMAs; then a wave tree.
+  constexpr int JW = 4, CU = 4;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int j0 = wave * JW; j0 < S; j0 += (GATE_THREADS / 64) * JW) {
+    float acc[JW];
+#pragma unroll
+    for (int q = 0; q < JW; ++q) acc[q] = 0.f;
+    for (int c0 = lane; c0 < C; c0 += 64 * CU) {
+      float pv[CU], wv[JW][CU];
+#pragma unroll
+      for (int u = 0; u < CU; ++u) {
+        const int c = c0 + 64 * u;
+        pv[u] = c < C ? pooled[c] : 0.f;
+#pragma unroll
+        for (int q = 0; q < JW; ++q) wv[q][u] = (c < C && j0 + q < S) ? w1[(size_t)(j0 + q) * C + c] : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < CU; ++u)
+#pragma unroll
+        for (int q = 0; q < JW; ++q) acc[q] = __fmaf_rn(wv[q][u], pv[u], acc[q]);
+    }
+#pragma unroll
+    for (int q = 0; q < JW; ++q) {
+      float v = acc[q];
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) v = __fadd_rn(v, __shfl_xor(v, off, 64));
+      if (lane == 0 && j0 + q < S) z[j0 + q] = silu(__fadd_rn(v, b1 ? b1[j0 + q] : 0.f));
+    }
+  }
+  __syncthreads();
+  // gate: each thread CW channels at once (c0, c0 + 256, ...), j in order, JU loads of w2t a
+  // channel issued before their FMAs.
+  constexpr int CW = 4, JU = 8;
+  for (int c0 = threadIdx.x; c0 < C; c0 += GATE_THREADS * CW) {
+    float acc[CW];
+#pragma unroll
+    for (int u = 0; u < CW; ++u) {
+      const int c = c0 + GATE_THREADS * u;
+      acc[u] = (b2 && c < C) ? b2[c] : 0.f;
+    }
+    for (int j0 = 0; j0 < S; j0 += JU) {
+      float wv[JU][CW], zv[JU];
+#pragma unroll
+      for (int v = 0; v < JU; ++v) {
+        zv[v] = j0 + v < S ? z[j0 + v] : 0.f;
+#pragma unroll
+        for (int u = 0; u < CW; ++u) {
+          const int c = c0 + GATE_THREADS * u;
+          wv[v][u] = (j0 + v < S && c < C) ? w2t[(size_t)(j0 + v) * C + c] : 0.f;
+        }
+      }
+#pragma unroll
+      for (int v = 0; v < JU; ++v)
+#pragma unroll
+        for (int u = 0; u < CW; ++u) acc[u] = __fmaf_rn(wv[v][u], zv[v], acc[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < CW; ++u) {
+      const int c = c0 + GATE_THREADS * u;
+      if (c < C) gate[(size_t)n * C + c] = sigmoid_f(acc[u]);
+    }
+  }
+}
+
+static int se_chunks(int64_t HW, int64_t C) {
+  int64_t k = HW * C / 16384;
+  k = std::min<int64_t>(k, std::min<int64_t>(HW, 64));
+  return (int)std::max<int64_t>(k, 1);
+}
+
+}  // namespace bq
+
+using namespace bq;
+
+extern "C" {
+
+size_t bq_se_gate_ws_bytes(int64_t N, int64_t HW, int64_t C) {
+  if (N < 0 || HW < 1 || C < 0) return 0;
+  return (size_t)N * se_chunks(HW, C) * C * sizeof(float);
+}
+
+int bq_se_gate_nhwc(const float* x, int64_t N, int64_t HW, int64_t C, const float* w1, const float* b1, int64_t S,
+                    const float* w2t, const float* b2, float* gate, void* ws, size_t ws_bytes, bq_stream_t stream) {
+  const char* what = "bq_se_gate_nhwc";
+  if (N < 0 || HW < 1 || C < 4 || S < 1) return set_error(BQ_ERR_ARG, "%s: bad sizes", what);
+  if (C % 4) return set_error(BQ_ERR_UNSUPPORTED, "%s: C=%lld is not a multiple of 4", what, (long long)C);
+  if (N * HW * C >= ((int64_t)1 << 40) || HW > 0x7fffffff || C > 65536 || S > 65536)
+    return set_error(BQ_ERR_ARG, "%s: size too large", what);
+  if (N == 0) return BQ_OK;
+  if (!x || !w1 || !w2t || !gate) return set_error(BQ_ERR_ARG, "%s: null pointer", what);
+  if ((uintptr_t)x & 15) return set_error(BQ_ERR_ARG, "%s: x must be 16-byte aligned", what);
+  const int chunks = se_chunks(HW, C);
+  const size_t need = (size_t)N * chunks * C * sizeof(float);
+  if (!ws || ws_bytes < need) return set_error(BQ_ERR_ARG, "%s: workspace %zu bytes, need %zu", what, ws_bytes, need);
+  if ((uintptr_t)ws & 15) return set_error(BQ_ERR_ARG, "%s: workspace must be 16-byte aligned", what);
+  if ((C + S) * sizeof(float) > 64 * 1024) return set_error(BQ_ERR_UNSUPPORTED, "%s: C + S too large", what);
+  hipStream_t st = (hipStream_t)stream;
+  const int rows_per = (int)((HW + chunks - 1) / chunks);
+  se_partial_kernel<<<(unsigned)(N * chunks), SE_THREADS, 0, st>>>(x, (int)HW, (int)C, chunks, rows_per, (float*)ws);
+  if (int r = check_launch(what)) return r;
+  se_gate_kernel<<<(unsigned)N, GATE_THREADS, (size_t)(C + S) * sizeof(float), st>>>(
+      (const float*)ws, chunks, (int)HW, (int)C, (int)S, w1, b1, w2t, b2, gate);
+  return check_launch(what);
+}
+
+}  // extern "C"

@@ -19,7 +19,7 @@ __all__ = [
     "ACT_NONE", "ACT_RELU", "ACT_SILU", "ACT_GELU", "Int8Weight", "Int8ConvWeight", "Int8DwWeight",
     "quantize_rows", "quantize_weight_per_channel", "quantize_tensor", "quantize_nhwc",
     "gemm_i8", "conv2d_i8_nhwc", "conv2d_i8_nhwc_q", "dwconv_i8_nhwc", "pack_linear_weight", "pack_conv_weight",
-    "quantize_nhwc_scaled", "quantize_nhwc_chscale", "linear_w8a32", "dequant_weight",
+    "quantize_nhwc_scaled", "quantize_nhwc_chscale", "se_gate_nhwc", "linear_w8a32", "dequant_weight",
     "pack_dw_weight", "linear", "conv2d", "depthwise_conv2d", "round_up", "split_workspace",
 ]
 
@@ -168,6 +168,31 @@ def quantize_nhwc_chscale(x: torch.Tensor, cs: torch.Tensor, cpad: int | None = 
     check(lib().bq_quantize_nhwc_chscale(xl.data_ptr(), N, H * W, C, cpad, csc.data_ptr(), q.data_ptr(),
                                          s.data_ptr(), None, ws.data_ptr(), ws.numel(), _stream(x)))
     return q, s
+
+
+def se_gate_nhwc(x: torch.Tensor, w1: torch.Tensor, b1, w2: torch.Tensor, b2, w2t: torch.Tensor | None = None):
+    """Squeeze-excite gates ``sigmoid(w2 · silu(w1 · mean_hw(x) + b1) + b2)`` in f32 for an
+    NCHW activation (channels-last memory is read in place): ``[N, C]`` (bq_se_gate_nhwc;
+    borch's CPU runner "se" node, runner.ts:256-268). ``w1 [S, C]``, ``w2 [C, S]``; ``w2t``
+    (optional) is ``w2`` already transposed to ``[S, C]`` contiguous, as the kernel reads it."""
+    if x.dtype != torch.float32:
+        raise TypeError(f"squeeze-excite takes float32 activations, got {x.dtype}")
+    require_device(x.device)
+    N, C, H, W = x.shape
+    S = w1.shape[0]
+    if tuple(w1.shape) != (S, C) or tuple(w2.shape) != (C, S):
+        raise RuntimeError(f"squeeze-excite weights {tuple(w1.shape)} / {tuple(w2.shape)} do not fit C={C}")
+    xl = x.contiguous(memory_format=torch.channels_last)
+    w1c = w1.float().contiguous()
+    w2c = w2.float().t().contiguous() if w2t is None else w2t
+    b1c = None if b1 is None else b1.float().contiguous()
+    b2c = None if b2 is None else b2.float().contiguous()
+    gate = torch.empty((N, C), dtype=torch.float32, device=x.device)
+    nb = int(lib().bq_se_gate_ws_bytes(N, H * W, C))
+    ws = torch.empty((max(nb // 4, 4),), dtype=torch.float32, device=x.device)
+    check(lib().bq_se_gate_nhwc(xl.data_ptr(), N, H * W, C, w1c.data_ptr(), _ptr(b1c), S, w2c.data_ptr(), _ptr(b2c),
+                                gate.data_ptr(), ws.data_ptr(), ws.numel() * 4, _stream(x)))
+    return gate
 
 
 def quantize_nhwc_scaled(x: torch.Tensor, scale: torch.Tensor, cpad: int | None = None):

@@ -27,6 +27,7 @@ import math
 import torch
 import torch.nn as tnn
 
+from . import int8 as I8
 from . import nn
 from .nn import intrinsic as I
 from .nn.utils.fusion import fuse_conv_bn_eval
@@ -160,8 +161,16 @@ class MBConv(tnn.Module):
         self.fused = False
 
     def _se_gate(self, h):
-        """Squeeze-excite gates [N, C] in f32: the 1x1 convs on the pooled 1x1 map run as
-        the equal matrix products on [N, C] (one small GEMM each instead of a conv)."""
+        """Squeeze-excite gates [N, C] in f32. With the block on the int8 path: one fused
+        kernel pair (bq_se_gate_nhwc: mean, the two 1x1 layers with SiLU and sigmoid). In
+        f32: torch ops, the 1x1 convs on the pooled 1x1 map as the equal matrix products."""
+        conv = getattr(self.dw, "conv", self.dw)
+        if getattr(conv, "int8", None) is not None:
+            w2 = self.se_expand.weight
+            if getattr(self, "_se_w2t", None) is None or self._se_w2t[1] != w2._version:
+                self._se_w2t = (w2.detach().flatten(1).t().contiguous(), w2._version)  # made once, before capture
+            return I8.se_gate_nhwc(h, self.se_reduce.weight.flatten(1), self.se_reduce.bias,
+                                   w2.flatten(1), self.se_expand.bias, self._se_w2t[0])
         s = h.mean(dim=(2, 3))
         s = torch.nn.functional.silu(torch.nn.functional.linear(s, self.se_reduce.weight.flatten(1),
                                                                self.se_reduce.bias))

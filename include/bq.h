@@ -182,6 +182,18 @@ int bq_dwconv_i8_nhwc(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t 
                       const float* sA, const float* sW, const float* bias, int act,
                       float* out, int32_t* acc, bq_stream_t stream);
 
+/* Bytes of `ws` bq_se_gate_nhwc needs (the per-chunk partial sums). */
+size_t bq_se_gate_ws_bytes(int64_t N, int64_t HW, int64_t C);
+
+/* Squeeze-excite gates in f32 of a channels-last activation x f32 [N, HW, C] (C % 4 == 0):
+ *   pooled = mean over HW (sum in a fixed order, then * f32(1/HW)),
+ *   z = silu(w1 [S, C] . pooled + b1),  gate f32 [N, C] = sigmoid(w2 . z + b2)
+ * with the expand weight w2 [C, S] passed transposed as w2t [S, C] (b1, b2 nullable). The gate is then folded into the next conv's input quantization
+ * (bq_quantize_nhwc_chscale). Replaces the CPU runner's "se" node (meanRows, gemmBiasAct
+ * swish and sigmoid; borch-ts/src/cpu/runner.ts:256-268, wasm/src/lib.rs:222-244). */
+int bq_se_gate_nhwc(const float* x, int64_t N, int64_t HW, int64_t C, const float* w1, const float* b1, int64_t S,
+                    const float* w2t, const float* b2, float* gate, void* ws, size_t ws_bytes, bq_stream_t stream);
+
 /* Weight-only int8 (W8A32) GEMV for the decode shape, M <= 8: f32 x [M, K] against int8
  * W [N, K] with per-channel sW [N]; out f32 [M, N] = sum_k x * f32(f32(q) * sW[n]) (f32 FMA
  * accumulation, wave-tree reduction) + bias, then act. K % 16 == 0, K <= 8192.

@@ -142,3 +142,15 @@ def resnet18_features_static(params, scales, x):
         side = run(f"body.{i}.down", h, ACT_NONE) if f"body.{i}.down" in params else h
         h = run(f"body.{i}.c2", out, ACT_RELU, side)
     return h
+
+
+def se_gate(x_nchw, w1, b1, w2, b2):
+    """Squeeze-excite gates [N, C] in float64, then rounded to f32: the mean over H, W, then
+    ``silu(w1 · p + b1)`` and ``sigmoid(w2 · z + b2)`` (the CPU runner's "se" node,
+    borch-ts/src/cpu/runner.ts:256-268: meanRows, gemmBiasAct swish and sigmoid)."""
+    x = np.asarray(x_nchw, np.float64)
+    p = x.mean(axis=(2, 3))
+    z = p @ np.asarray(w1, np.float64).T + (0.0 if b1 is None else np.asarray(b1, np.float64))
+    z = z / (1.0 + np.exp(-z))
+    g = z @ np.asarray(w2, np.float64).T + (0.0 if b2 is None else np.asarray(b2, np.float64))
+    return (1.0 / (1.0 + np.exp(-g))).astype(np.float32)

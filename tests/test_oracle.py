@@ -415,3 +415,19 @@ def test_composed_layers_on_exact_grids():
     want = F.linear(torch.from_numpy(xl).double(), torch.from_numpy(wl).double(), torch.from_numpy(bl).double())
     y, _, _, _, _ = OM.linear_layer(xl, wl, bl, OM.ACT_GELU, rl)
     np.testing.assert_allclose(y, O.gelu((want.numpy() + rl).astype(np.float32)), rtol=1e-6, atol=1e-7)
+
+
+def test_se_gate_against_torch_float64():
+    """oracle.models.se_gate equals torch's float64 mean / linear / silu / sigmoid (library
+    routines) composed as the CPU runner's squeeze-excite node."""
+    import torch
+    from oracle import models as OM
+    rng = np.random.default_rng(6)
+    x = rng.normal(size=(3, 24, 5, 7)).astype(np.float32)
+    w1, b1 = rng.normal(size=(6, 24)).astype(np.float32), rng.normal(size=6).astype(np.float32)
+    w2, b2 = rng.normal(size=(24, 6)).astype(np.float32), rng.normal(size=24).astype(np.float32)
+    T = lambda a: torch.from_numpy(a).double()
+    p = T(x).mean(dim=(2, 3))
+    z = torch.nn.functional.silu(torch.nn.functional.linear(p, T(w1), T(b1)))
+    want = torch.sigmoid(torch.nn.functional.linear(z, T(w2), T(b2))).float().numpy()
+    np.testing.assert_allclose(OM.se_gate(x, w1, b1, w2, b2), want, rtol=1e-7, atol=1e-9)
