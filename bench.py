@@ -73,6 +73,99 @@ def time_graph(g, calls, replays, stream):
     return time_events(lambda i: g.replay(), replays, stream) / calls
 
 
+# the borch_amd.int8 wrappers that launch a model layer's int8 kernel (the input already int8)
+_LAYER_KERNELS = ("conv2d_i8_nhwc", "conv2d_i8_nhwc_q", "dwconv_i8_nhwc", "gemm_i8")
+
+
+def record_layers(model, x):
+    """One eager forward of the int8 ``model`` with the wrappers that launch the conv,
+    depthwise and GEMM kernels recording their bound arguments. Returns
+    ``[(layer name, wrapper name, wrapper, arguments)]`` in launch order."""
+    import inspect
+    import torch
+    from borch_amd import int8 as I8, nn as bnn
+    calls, current, saved, hooks = [], [""], {}, []
+    for name, m in model.named_modules():
+        if isinstance(m, (bnn.Conv2d, bnn.Linear)):
+            hooks.append(m.register_forward_pre_hook(lambda mod, inp, _n=name: current.__setitem__(0, _n)))
+    for n in _LAYER_KERNELS:
+        f = saved[n] = getattr(I8, n)
+
+        def rec(*a, _f=f, _n=n, **k):
+            bound = inspect.signature(_f).bind(*a, **k)
+            bound.apply_defaults()
+            calls.append((current[0], _n, _f, dict(bound.arguments)))
+            return _f(*a, **k)
+        setattr(I8, n, rec)
+    try:
+        with torch.no_grad():
+            model(x)
+    finally:
+        for n, f in saved.items():
+            setattr(I8, n, f)
+        for h in hooks:
+            h.remove()
+    return calls
+
+
+def layer_work(kind, a):
+    """(GEMM view (M, N, K), int8 ops, algorithmic bytes) of one recorded launch. Convs are
+    implicit GEMMs: M = N·OH·OW pixels, N = output channels, K = KH·KW·Cpad; bytes = the
+    int8 input and weight read once, the f32 output (and int8 twin, residual) once. Depthwise:
+    2·KH·KW ops per output, bytes = int8 input + f32 output + taps."""
+    if kind == "gemm_i8":
+        M, K = a["qa"].shape
+        N = a["qw"].shape[0]
+        byts = M * K + N * K + 4 * M + 8 * N + 4 * M * N * (2 if a["residual"] is not None else 1)
+        return (M, N, K), 2 * M * N * K, byts
+    n, h, w, c = a["qx"].shape
+    wq, s, p = a["wq"], a["stride"], a["pad"]
+    oh, ow = (h + 2 * p - wq.KH) // s + 1, (w + 2 * p - wq.KW) // s + 1
+    m = n * oh * ow
+    if kind == "dwconv_i8_nhwc":
+        return (m, c, wq.KH * wq.KW), 2 * m * c * wq.KH * wq.KW, n * h * w * c + 4 * m * c + wq.KH * wq.KW * c
+    k = wq.KH * wq.KW * c
+    out_b = 4 * m * wq.O * (2 if a.get("residual") is not None else 1) + (m * wq.O if kind.endswith("_q") else 0)
+    return (m, wq.O, k), 2 * m * wq.O * k, n * h * w * c + wq.O * k + out_b
+
+
+def layer_table(model, x, stream, calls=10, replays=5):
+    """Each int8 layer of one forward timed alone: its recorded launch replayed ``calls``
+    times in a HIP graph (operands warm in cache, as in the forward, where the producer
+    has just written them), HIP events around ``replays`` replays. One row per layer."""
+    import torch
+    rows = []
+    for name, kind, f, a in record_layers(model, x):
+        g = capture(lambda i: f(**a), calls)
+        ms = time_graph(g, calls, replays, stream)
+        del g
+        (M, N, K), ops, byts = layer_work(kind, a)
+        rows.append({"layer": name, "kernel": kind, "M": M, "N": N, "K": K, "us": round(ms * 1e3, 2),
+                     "ops": ops, "bytes": byts, "TOPS": round(ops / (ms * 1e-3) / 1e12, 1),
+                     "mfma_frac": round(ops / (ms * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4),
+                     "GBps": round(byts / (ms * 1e-3) / 1e9, 1)})
+    torch.cuda.synchronize()
+    return rows
+
+
+def layer_summary(rows):
+    """Totals of a layer table: the MFMA layers (convs, GEMMs) and the depthwise ones."""
+    out = {}
+    mm = [r for r in rows if r["kernel"] != "dwconv_i8_nhwc"]
+    dw = [r for r in rows if r["kernel"] == "dwconv_i8_nhwc"]
+    if mm:
+        ops, us = sum(r["ops"] for r in mm), sum(r["us"] for r in mm)
+        out["mfma_layers"] = {"count": len(mm), "ops": ops, "us": round(us, 1),
+                              "TOPS": round(ops / (us * 1e-6) / 1e12, 1),
+                              "mfma_frac": round(ops / (us * 1e-6) / 1e12 / PEAK_INT8_TOPS, 4)}
+    if dw:
+        byts, us = sum(r["bytes"] for r in dw), sum(r["us"] for r in dw)
+        out["depthwise_layers"] = {"count": len(dw), "bytes": byts, "us": round(us, 1),
+                                   "GBps": round(byts / (us * 1e-6) / 1e9, 1),
+                                   "hbm_frac": round(byts / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)}
+    return out
+
+
 def probes(dev, stream, qa, qw, wcopies):
     """The day's ceilings on this GPU (libbqprobe, include/bq_probe.h), measured in the same
     run as the kernels they bound:
@@ -226,9 +319,10 @@ def cpu_baseline(M_sample=512):
     return out
 
 
-def bench_models(dev, stream, steps):
+def bench_models(dev, stream, steps, layers_out=None):
     """Forward ms of the model configurations: int8 (HIP-graph replay of the compiled
-    model, and eager) beside the same folded model in f32 (torch-ROCm ops)."""
+    model, and eager) beside the same folded model in f32 (torch-ROCm ops), and each int8
+    layer timed alone (``layer_table``; the rows go into ``layers_out`` when given)."""
     import torch
     import borch_amd as bt
     from borch_amd import nets, workloads as WL
@@ -252,6 +346,12 @@ def bench_models(dev, stream, steps):
         out[key] = {"int8_graph_ms": round(g_ms, 4), "int8_eager_ms": round(eager_ms, 4),
                     "f32_ms": round(f32_ms, 4), "int8_layers": c.int8_layers,
                     "max_abs_diff_vs_f32_rel": round(gap, 5)}
+        rows = layer_table(model, x, stream)
+        out[key]["layers_alone"] = layer_summary(rows)
+        if name == "resnet18":  # per-layer MFMA fraction: [layer, M, N, K, us, fraction of 5.0 POP/s]
+            out[key]["per_layer"] = [[r["layer"], r["M"], r["N"], r["K"], r["us"], r["mfma_frac"]] for r in rows]
+        if layers_out is not None:
+            layers_out[key] = rows
         if name in ("resnet18", "efficientnet_b0"):
             # calibrated static scales + int8 twins (calibrate_int8): no max pass, and no
             # quantize pass where the producer writes the next layer's int8 input
@@ -281,6 +381,22 @@ def bench_models(dev, stream, steps):
     return out
 
 
+def print_layer_tables(models, tables):
+    """Markdown: per model, the forward times and one row per int8 layer timed alone."""
+    for key, rows in tables.items():
+        m = models[key]
+        print(f"## {key}\n")
+        print(f"int8 forward (HIP graph, dynamic scales): {m['int8_graph_ms']} ms; "
+              f"static scales: {m.get('int8_static_graph_ms', '-')} ms; f32 (torch-ROCm): {m['f32_ms']} ms; "
+              f"layers alone: {json.dumps(m['layers_alone'])}\n")
+        print("| layer | kernel | M | N | K | ops | bytes | us alone | TOPS | of 5.0 POP/s | GB/s |")
+        print("|---|---|---|---|---|---|---|---|---|---|---|")
+        for r in rows:
+            print(f"| {r['layer']} | {r['kernel']} | {r['M']} | {r['N']} | {r['K']} | {r['ops']} | {r['bytes']} | "
+                  f"{r['us']} | {r['TOPS']} | {r['mfma_frac']} | {r['GBps']} |")
+        print()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -294,6 +410,9 @@ def main():
                     help="for counter runs: the bandwidth-bound kernels alone (GEMV M=1 and skinny M=16 over 24 "
                          "rotated weights, the 4096x4096 per-row quantize, EfficientNet-B0 b64 depthwise layers, a "
                          "per-tensor quantize) and 5 launches of a 64 MiB device copy; prints their shapes and bytes")
+    ap.add_argument("--layers", action="store_true",
+                    help="the model configurations only, then every int8 layer's table as markdown "
+                         "(GEMM shape, ops, bytes, us alone, TOPS, MFMA fraction, GB/s)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this build runs on one GPU only: the int8 path is measured on 1 MI355X "
@@ -312,6 +431,12 @@ def main():
 
     if args.hbm_kernels:
         hbm_kernels(dev)
+        return
+
+    if args.layers:
+        tables = {}
+        models = bench_models(dev, stream, steps=max(args.steps // 2, 10), layers_out=tables)
+        print_layer_tables(models, tables)
         return
 
     if args.kernels_only:
@@ -408,6 +533,25 @@ def main():
                          "hbm_frac": round(wbytes / (t_w * 1e-3) / 1e9 / PEAK_HBM_GBS, 4), "bytes": wbytes}
     log(f"W8A32 M=1: {sweep['W8A32_M1']}")
     del g_w, qws, w8v, w8s
+    # C1: the Linear 16x512x512 through nn.Linear (per-row quantize + GEMM), latency
+    from borch_amd import nn as bnn
+    x_c1, w_c1, b_c1 = WL.c1_linear(0)
+    lin = bnn.Linear(512, 512, device=dev)
+    with torch.no_grad():
+        lin.weight.copy_(torch.from_numpy(w_c1))
+        lin.bias.copy_(torch.from_numpy(b_c1))
+    lin.quantize_int8()
+    X_c1 = torch.from_numpy(x_c1).to(dev)
+    g_l = capture(lambda i: lin(X_c1), 10)
+    t_l = time_graph(g_l, 10, 8, stream)
+    qa_c1, sa_c1 = I.quantize_rows(X_c1)
+    g_l2 = capture(lambda i: I.gemm_i8(qa_c1, lin.int8.q, sa_c1, lin.int8.s, lin.bias), 10)
+    t_l2 = time_graph(g_l2, 10, 8, stream)
+    del g_l, g_l2
+    sweep["C1_linear_16x512x512"] = {"e2e_us_with_quantize": round(t_l * 1e3, 3), "kernel_us": round(t_l2 * 1e3, 3),
+                                     "ops": 2 * 16 * 512 * 512,
+                                     "bytes": 16 * 512 + 512 * 512 + 4 * 16 + 8 * 512 + 4 * 16 * 512}
+    log(f"C1: {sweep['C1_linear_16x512x512']}")
     sweep["M4096"] = {"kernel_us": round(gemm_ms * 1e3, 3), "TOPS": round(gemm_tops, 1),
                       "mfma_frac": round(gemm_tops / PEAK_INT8_TOPS, 4),
                       "quantize_us": round(quant_ms * 1e3, 3),

@@ -36,11 +36,20 @@ __device__ __forceinline__ int fdiv(int n, uint32_t mul, int shift) {
   return (int)((__umulhi((uint32_t)n, mul) + (uint32_t)n) >> shift);
 }
 
-// Wave64 max of a non-negative float.
+// Wave64 max of a non-negative float; every lane of the wave must be active (each caller
+// reaches it with the whole workgroup, before a barrier or a per-wave store). Within each
+// row of 16 lanes by DPP (quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror, row_mirror),
+// then the four row maxima read out of lanes 0, 16, 32, 48: no LDS round trips.
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-  return v;
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false)));
+  const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return fmaxf(fmaxf(a, b), fmaxf(c, d));
 }
 
 // The scale rule: float32(peak / 127), correctly rounded (HIP's f32 division is the IEEE
@@ -67,6 +76,11 @@ __device__ __forceinline__ int quant_one(float v, float s) {
   return (int)r;
 }
 
+__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
+  return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
+         ((uint32_t)(d & 0xff) << 24);
+}
+
 // The same rounding without a division per element. One quantizer per scale s holds
 // r = 1/s (correctly rounded). f = fl(v * r) is within |v/s| * 1.2e-7 of the exact quotient
 // t = v/s (two roundings of 2^-24 each), i.e. within 1.6e-5 for |t| <= 127.00002 (s is at
@@ -79,25 +93,40 @@ __device__ __forceinline__ int quant_one(float v, float s) {
 struct Quantizer {
   float s, r;
   __device__ explicit Quantizer(float s_) : s(s_), r(s_ == 0.f ? 0.f : __fdiv_rn(1.0f, s_)) {}
+  static __device__ __forceinline__ bool near_half(float f, float k) {
+    return !(fabsf(__fsub_rn(f, k)) < 0.49996f);
+  }
+  // The rounding of v when f = v * r lies near a half-integer (or is not finite).
+  __device__ float settle(float v, float f, float k) const {
+    if (!__builtin_isfinite(f)) return (float)quant_one(v, s);
+    const float b = __fadd_rn(k, __builtin_copysignf(0.5f, __fsub_rn(f, k)));  // the half-integer f is near
+    const float d = __fmaf_rn(-b, s, v);
+    const float lo = __fsub_rn(b, 0.5f);
+    return d > 0.f ? __fadd_rn(b, 0.5f) : d < 0.f ? lo : ((((int)lo) & 1) ? __fadd_rn(lo, 1.0f) : lo);
+  }
+  static __device__ __forceinline__ int clamp127(float k) { return (int)fminf(fmaxf(k, -127.f), 127.f); }
   __device__ __forceinline__ int operator()(float v) const {
     if (s == 0.f) return 0;
     const float f = __fmul_rn(v, r);
     float k = rintf(f);
-    if (!(fabsf(__fsub_rn(f, k)) < 0.49996f)) {
-      if (!__builtin_isfinite(f)) return quant_one(v, s);
-      const float b = __fadd_rn(k, __builtin_copysignf(0.5f, __fsub_rn(f, k)));  // the half-integer f is near
-      const float d = __fmaf_rn(-b, s, v);
-      const float lo = __fsub_rn(b, 0.5f);
-      k = d > 0.f ? __fadd_rn(b, 0.5f) : d < 0.f ? lo : ((((int)lo) & 1) ? __fadd_rn(lo, 1.0f) : lo);
+    if (near_half(f, k)) k = settle(v, f, k);
+    return clamp127(k);
+  }
+  // Four values, packed low byte first: the same rounding with one branch for the four
+  // (the near-half case is rare: about 8e-5 of uniformly spread quotients).
+  __device__ __forceinline__ uint32_t pack(float4 v) const {
+    if (s == 0.f) return 0u;
+    const float f0 = __fmul_rn(v.x, r), f1 = __fmul_rn(v.y, r), f2 = __fmul_rn(v.z, r), f3 = __fmul_rn(v.w, r);
+    float k0 = rintf(f0), k1 = rintf(f1), k2 = rintf(f2), k3 = rintf(f3);
+    if ((int)near_half(f0, k0) | (int)near_half(f1, k1) | (int)near_half(f2, k2) | (int)near_half(f3, k3)) {
+      if (near_half(f0, k0)) k0 = settle(v.x, f0, k0);
+      if (near_half(f1, k1)) k1 = settle(v.y, f1, k1);
+      if (near_half(f2, k2)) k2 = settle(v.z, f2, k2);
+      if (near_half(f3, k3)) k3 = settle(v.w, f3, k3);
     }
-    return (int)fminf(fmaxf(k, -127.f), 127.f);
+    return pack4(clamp127(k0), clamp127(k1), clamp127(k2), clamp127(k3));
   }
 };
-
-__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
-  return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
-         ((uint32_t)(d & 0xff) << 24);
-}
 
 // SiLU v * sigmoid(v) = v / (1 + e^-v) from the hardware exp2 and reciprocal (v_exp_f32,
 // v_rcp_f32, about 1 ulp each): five instructions instead of a full-precision expf and an

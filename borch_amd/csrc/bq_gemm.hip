@@ -523,7 +523,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
           if (p.acc) *reinterpret_cast<int4*>(p.acc + idx) = a;
           if (p.q_out)
             *reinterpret_cast<uint32_t*>(p.q_out + idx) =
-                pack4(qz_out(o.x), qz_out(o.y), qz_out(o.z), qz_out(o.w));
+                qz_out.pack(o);
           amax = fmaxf(amax, fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w))));
         }
       };

@@ -1,7 +1,8 @@
 // Quantizers: per-row (activations, Linear weights) and per-tensor (conv activations).
 //
-// Per-row: one 256-thread block a row, the row held in registers between the max and the
-// quantize, so x is read from HBM once (read 4 B + write 1 B per element: HBM-bound).
+// Per-row: one 256-thread block a row (many rows of up to 1024 floats: one wave a row),
+// the row held in registers between the max and the quantize, so x is read from HBM once
+// (read 4 B + write 1 B per element: HBM-bound).
 // Per-tensor: partial maxima (one per block) into a workspace, then every block of the
 // quantize kernel reduces the partials itself — no atomics, no zeroing, deterministic.
 #include <stdarg.h>
@@ -71,7 +72,7 @@ __global__ __launch_bounds__(QR_THREADS) void quantize_rows_kernel(const float* 
     for (int i = 0; i < NV; ++i) {
       const int k = (t + i * QR_THREADS) * 4;
       if (k < K)
-        *reinterpret_cast<uint32_t*>(qr + k) = pack4(qz(v[i].x), qz(v[i].y), qz(v[i].z), qz(v[i].w));
+        *reinterpret_cast<uint32_t*>(qr + k) = qz.pack(v[i]);
     }
   } else {
     float m = 0.f;
@@ -80,6 +81,41 @@ __global__ __launch_bounds__(QR_THREADS) void quantize_rows_kernel(const float* 
     if (t == 0) s[row] = sc;
     const Quantizer qz(sc);
     for (int k = t; k < K; k += QR_THREADS) qr[k] = (int8_t)qz(xr[k]);
+  }
+}
+
+// One wave per row, QW_WAVES rows per block, for rows of up to NV * 256 floats (NV <= 4): every lane
+// loads its NV float4 (coalesced: lane l reads bytes [16 l, 16 l + 16) of each 1 KB run)
+// before any arithmetic, so a wave has NV KB in flight; the max is a wave reduction (no
+// LDS, no barrier). The same max, scale and rounding as the block-per-row kernel.
+constexpr int QW_WAVES = 4;
+
+template <int NV>
+__global__ __launch_bounds__(QW_WAVES * 64) void quantize_rows_wave_kernel(const float* __restrict__ x, int M,
+                                                                          int K, int8_t* __restrict__ q,
+                                                                          float* __restrict__ s) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * QW_WAVES + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const float* xr = x + (size_t)row * K;
+  int8_t* qr = q + (size_t)row * K;
+  float4 v[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int k = (lane + i * 64) * 4;
+    v[i] = k < K ? *reinterpret_cast<const float4*>(xr + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  float m = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+    m = fmaxf(m, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+  const float sc = scale_of(wave_max(m));  // the whole wave is here: rows are per wave
+  if (lane == 0) s[row] = sc;
+  const Quantizer qz(sc);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int k = (lane + i * 64) * 4;
+    if (k < K) *reinterpret_cast<uint32_t*>(qr + k) = qz.pack(v[i]);
   }
 }
 
@@ -141,7 +177,7 @@ __global__ __launch_bounds__(QT_THREADS) void quantize_tensor_kernel(const float
     if (flat) {
       const float4 v = *reinterpret_cast<const float4*>(x + e0);
       *reinterpret_cast<uint32_t*>(q + e0) =
-          pack4(qz(v.x), qz(v.y), qz(v.z), qz(v.w));
+          qz.pack(v);
     } else {
       for (int j = 0; j < 4; ++j) {
         const int64_t e = e0 + j;
@@ -271,7 +307,7 @@ __global__ __launch_bounds__(QT_THREADS) void quantize_chscale_kernel(const floa
     uint32_t word = 0;
     if (w.g < c4n) {
       const float4 v = chscaled(x, cs, w.pix, w.g, C, hw_mul, hw_shift);
-      word = pack4(qz(v.x), qz(v.y), qz(v.z), qz(v.w));
+      word = qz.pack(v);
     }
     *reinterpret_cast<uint32_t*>(q + (size_t)w.pix * Cpad + w.g * 4) = word;
   }
@@ -291,6 +327,20 @@ static int launch_rows(const float* x, int64_t M, int64_t K, int8_t* q, float* s
   if (!x || !q || !s) return set_error(BQ_ERR_ARG, "%s: null pointer", what);
   if (M > 0x7fffffff || K > 0x7fffffff) return set_error(BQ_ERR_ARG, "%s: size too large", what);
   const bool vec = (K % 4 == 0) && (((uintptr_t)x | (uintptr_t)q) & 15) == 0;
+  // Short rows in numbers: one wave a row (at 6304 x 768, 8.1 -> 7.0 us). Longer rows keep
+  // a block a row: a single wave then does a whole row's quantize arithmetic alone (6304 x
+  // 3072: 20.5 -> 22.2 us; one row of 4096: 3.4 -> 6.2 us as one wave).
+  const int nw = vec && K > 0 ? (int)((K + 255) / 256) : 0;  // float4 a lane
+  if (nw > 0 && nw <= 4 && M >= 1024) {
+    dim3 g((unsigned)((M + QW_WAVES - 1) / QW_WAVES)), b(QW_WAVES * 64);
+    switch (nw) {
+      case 1: quantize_rows_wave_kernel<1><<<g, b, 0, st>>>(x, (int)M, (int)K, q, s); break;
+      case 2: quantize_rows_wave_kernel<2><<<g, b, 0, st>>>(x, (int)M, (int)K, q, s); break;
+      case 3: quantize_rows_wave_kernel<3><<<g, b, 0, st>>>(x, (int)M, (int)K, q, s); break;
+      default: quantize_rows_wave_kernel<4><<<g, b, 0, st>>>(x, (int)M, (int)K, q, s); break;
+    }
+    return check_launch(what);
+  }
   const int nv = vec ? (int)((K + 1023) / 1024) : 0;
   dim3 grid((unsigned)M), block(QR_THREADS);
   switch (vec ? nv : 0) {

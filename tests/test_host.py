@@ -47,3 +47,36 @@ def test_rule_argument_checked():
         bt.quantize_for_int8(torch.nn.Sequential(), rule="fast")
     with pytest.raises(ValueError, match="rule must be"):
         Conv2d(64, 64, 3, padding=1).quantize_int8("fast")
+
+
+def test_bench_layer_work_matches_the_implicit_gemm_shapes():
+    """bench.layer_work's GEMM view of a conv: M = N·OH·OW, N = O, K = KH·KW·Cpad, with
+    ops 2·M·N·K. The ResNet-18 b16 shapes are the ones tabulated for the reference's
+    implicit-GEMM conv (kernels.ts:2084-2302): (16384, 64, 576), stride-2 (4096, 128, 576),
+    1×1 downsample (4096, 128, 64). Depthwise and dense GEMM shapes likewise."""
+    import types
+    import bench
+    import torch
+
+    def conv(n, h, c, o, k, s, p, kind="conv2d_i8_nhwc", residual=None):
+        wq = types.SimpleNamespace(KH=k, KW=k, O=o)
+        a = {"qx": torch.empty((n, h, h, c), dtype=torch.int8), "wq": wq, "stride": s, "pad": p,
+             "residual": residual}
+        return bench.layer_work(kind, a)
+
+    assert conv(16, 32, 64, 64, 3, 1, 1)[0] == (16384, 64, 576)
+    assert conv(16, 32, 64, 128, 3, 2, 1)[0] == (4096, 128, 576)
+    assert conv(16, 32, 64, 128, 1, 2, 0)[0] == (4096, 128, 64)
+    shape, ops, byts = conv(16, 4, 512, 512, 3, 1, 1)
+    assert shape == (256, 512, 4608) and ops == 2 * 256 * 512 * 4608
+    assert byts == 16 * 4 * 4 * 512 + 512 * 4608 + 4 * 256 * 512
+    # the int8 twin adds a byte per output, a residual four
+    r = torch.empty(1)
+    assert conv(16, 4, 512, 512, 3, 1, 1, "conv2d_i8_nhwc_q", r)[2] == byts + 4 * 256 * 512 + 256 * 512
+    # depthwise 3x3 stride 2 on 112² x 96 at b64: 2·9 ops per output
+    shape, ops, byts = conv(64, 112, 96, 96, 3, 2, 1, "dwconv_i8_nhwc")
+    assert shape == (64 * 56 * 56, 96, 9) and ops == 2 * 9 * 64 * 56 * 56 * 96
+    assert byts == 64 * 112 * 112 * 96 + 4 * 64 * 56 * 56 * 96 + 9 * 96
+    a = {"qa": torch.empty((6304, 768), dtype=torch.int8), "qw": torch.empty((2304, 768), dtype=torch.int8),
+         "residual": None}
+    assert bench.layer_work("gemm_i8", a)[:2] == ((6304, 2304, 768), 2 * 6304 * 2304 * 768)
