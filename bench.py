@@ -73,41 +73,6 @@ def time_graph(g, calls, replays, stream):
     return time_events(lambda i: g.replay(), replays, stream) / calls
 
 
-# the borch_amd.int8 wrappers that launch a model layer's int8 kernel (the input already int8)
-_LAYER_KERNELS = ("conv2d_i8_nhwc", "conv2d_i8_nhwc_q", "dwconv_i8_nhwc", "gemm_i8")
-
-
-def record_layers(model, x):
-    """One eager forward of the int8 ``model`` with the wrappers that launch the conv,
-    depthwise and GEMM kernels recording their bound arguments. Returns
-    ``[(layer name, wrapper name, wrapper, arguments)]`` in launch order."""
-    import inspect
-    import torch
-    from borch_amd import int8 as I8, nn as bnn
-    calls, current, saved, hooks = [], [""], {}, []
-    for name, m in model.named_modules():
-        if isinstance(m, (bnn.Conv2d, bnn.Linear)):
-            hooks.append(m.register_forward_pre_hook(lambda mod, inp, _n=name: current.__setitem__(0, _n)))
-    for n in _LAYER_KERNELS:
-        f = saved[n] = getattr(I8, n)
-
-        def rec(*a, _f=f, _n=n, **k):
-            bound = inspect.signature(_f).bind(*a, **k)
-            bound.apply_defaults()
-            calls.append((current[0], _n, _f, dict(bound.arguments)))
-            return _f(*a, **k)
-        setattr(I8, n, rec)
-    try:
-        with torch.no_grad():
-            model(x)
-    finally:
-        for n, f in saved.items():
-            setattr(I8, n, f)
-        for h in hooks:
-            h.remove()
-    return calls
-
-
 def layer_work(kind, a):
     """(GEMM view (M, N, K), int8 ops, algorithmic bytes) of one recorded launch. Convs are
     implicit GEMMs: M = N·OH·OW pixels, N = output channels, K = KH·KW·Cpad; bytes = the
@@ -135,7 +100,8 @@ def layer_table(model, x, stream, calls=10, replays=5):
     has just written them), HIP events around ``replays`` replays. One row per layer."""
     import torch
     rows = []
-    for name, kind, f, a in record_layers(model, x):
+    from borch_amd.tune import record_launches
+    for name, kind, f, a in record_launches(model, x):
         g = capture(lambda i: f(**a), calls)
         ms = time_graph(g, calls, replays, stream)
         del g

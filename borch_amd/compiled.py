@@ -8,19 +8,28 @@ timing is never quoted for an "int8" forward that was mostly f32.
 Run: eager, or with ``graph=True`` a HIP graph captured on the first call for that
 input shape and replayed afterwards (the reference's record/replay, device.ts:634-660):
 the int8 forward is many small launches, and a replay issues them as one.
+
+Tune (``tune=True``, the default, as the reference's, compile.ts:55-62): before a shape's
+first run on a GPU, the int8 GEMM / conv kernel of every distinct layer problem is chosen
+by measurement (``borch_amd.tune``); ``tuned`` keeps the decisions, one list per shape.
+The choice changes time only: every candidate computes the same result.
 """
 from __future__ import annotations
 
 import torch
 
 from .nn import quantize_for_int8
+from .tune import tune as _tune
 
 
 class Compiled:
-    def __init__(self, model, int8: bool = False, graph: bool = False, fuse: bool = True):
+    def __init__(self, model, int8: bool = False, graph: bool = False, fuse: bool = True, tune: bool = True):
         self.model = model
         self.int8 = int8
         self.graph = graph
+        self.tune = tune
+        self.tuned = []  # the tuner's decisions, one list per input shape (borch_amd.tune.tune)
+        self._tuned_keys = set()
         self.int8_layers = 0
         model.eval()
         if fuse and callable(getattr(model, "fuse", None)):
@@ -31,9 +40,12 @@ class Compiled:
 
     @torch.no_grad()
     def __call__(self, x):
+        key = (tuple(x.shape), x.dtype, x.device)
+        if self.tune and x.device.type == "cuda" and key not in self._tuned_keys:
+            self._tuned_keys.add(key)
+            self.tuned.append(_tune(self.model, x))
         if not self.graph or x.device.type != "cuda":
             return self.model(x)
-        key = (tuple(x.shape), x.dtype, x.device)
         entry = self._graphs.get(key)
         if entry is None:
             static_in = x.clone()
@@ -54,6 +66,6 @@ class Compiled:
         return static_out
 
 
-def compiled(model, int8: bool = False, graph: bool = False, fuse: bool = True) -> Compiled:
-    """``torch.compiled(model, {int8})`` of borch-ts (compile.ts:570-578)."""
-    return Compiled(model, int8=int8, graph=graph, fuse=fuse)
+def compiled(model, int8: bool = False, graph: bool = False, fuse: bool = True, tune: bool = True) -> Compiled:
+    """``torch.compiled(model, {int8, tune})`` of borch-ts (compile.ts:55-62, 570-578)."""
+    return Compiled(model, int8=int8, graph=graph, fuse=fuse, tune=tune)

@@ -20,6 +20,9 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <array>
+#include <map>
+#include <mutex>
 #include <utility>
 
 #include "bq_common.h"
@@ -58,6 +61,9 @@ struct GemmP {
   // residual and activation), one float per tile at bm * tiles_n + bn — the partial maxima
   // from which the next layer's per-tensor quantizer takes its scale without a max pass.
   float* amax;
+  // Host-side selection only (the kernels ignore them): a tuned plan's configuration id
+  // (0: the shape rule) and K split (0: the split rule).
+  int plan_cfg, plan_split;
 };
 
 constexpr int BK = 128;  // bytes of K per LDS stage: one cache line per row
@@ -987,10 +993,12 @@ static int forced_split() {
 // costs a fixed 2-3 us (partials written through to the device-coherent level, the counter
 // round trip, the last workgroup's reads); measured on 64x64 tiles it pays from 16 stages
 // for a conv (whose loader makes a stage dearer) and from 32 for a dense GEMM.
-static int pick_split(long long tiles, int KT, bool conv) {
+static int pick_split(long long tiles, int KT, bool conv, int planned = 0) {
   int S;
   if (forced_split() > 0) {
     S = forced_split();
+  } else if (planned > 0) {
+    S = planned;
   } else {
     if (tiles >= SPLIT_MAX_TILES || KT < (conv ? 16 : 32)) return 1;
     S = (int)std::min<long long>((256 + tiles - 1) / tiles, KT / 4);
@@ -1003,7 +1011,7 @@ static int pick_split(long long tiles, int KT, bool conv) {
 template <int BM, int BN, int WAVES_M, int WAVES_N, bool CONV, int NBUF, int FD>
 static void launch_tiled(GemmP p, hipStream_t st, const Ws& ws) {
   const long long tiles = (long long)((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
-  int S = BM * BN <= SPLIT_MAX_TILE ? pick_split(tiles, (p.K + BK - 1) / BK, CONV) : 1;
+  int S = BM * BN <= SPLIT_MAX_TILE ? pick_split(tiles, (p.K + BK - 1) / BK, CONV, p.plan_split) : 1;
   if (S > 1) {
     const size_t need = SPLIT_CNT_BYTES + (size_t)tiles * S * BM * BN * 4;
     if (!ws.ptr || ws.bytes < need || tiles * 4 > (long long)SPLIT_CNT_BYTES || tiles * S > 0x7fffffffll) {
@@ -1049,6 +1057,7 @@ constexpr TileDims CFG_TILES[15] = {{0, 0},    {256, 256}, {256, 256}, {256, 256
 // K slices ahead (short MFMA runs).
 static int choose_cfg(const GemmP& p) {
   if (forced_cfg() >= 1 && forced_cfg() <= 14) return forced_cfg();
+  if (p.plan_cfg >= 1 && p.plan_cfg <= 14) return p.plan_cfg;
   const long long t256 = (long long)((p.M + 255) / 256) * ((p.N + 255) / 256);
   const long long t128 = (long long)((p.M + 127) / 128) * ((p.N + 127) / 128);
   const long long t128x32 = (long long)((p.M + 127) / 128) * ((p.N + 31) / 32);
@@ -1087,6 +1096,77 @@ static void launch_gemm(const GemmP& p, hipStream_t st, const Ws& ws) {
 }
 
 static bool aligned16(const void* q) { return ((uintptr_t)q & 15) == 0; }
+
+// ---------------------------------------------------------------- kernel choice by measurement
+//
+// A plan fixes, for one problem, the tiled kernel's configuration and K split that the
+// rules above would otherwise pick. Every configuration and split computes the same exact
+// int32 sums and the same epilogue, so a plan changes time only, never a result. Problems
+// are keyed by their full geometry: a dense GEMM (0, M, N, K) or a convolution (1, N, H, W,
+// C, O, KH, KW, stride, pad). The host tuner times the candidates (bq_plan_candidates, the
+// rules' pick first) and records the fastest (bq_plan_set).
+using PlanKey = std::array<int64_t, 10>;
+struct Plan {
+  int cfg, split;
+};
+static std::mutex g_plan_mu;
+static std::map<PlanKey, Plan> g_plans;
+
+static PlanKey dense_key(int64_t M, int64_t N, int64_t K) { return PlanKey{0, M, N, K, 0, 0, 0, 0, 0, 0}; }
+static PlanKey conv_key(int64_t N, int64_t H, int64_t W, int64_t C, int64_t O, int64_t KH, int64_t KW,
+                        int64_t stride, int64_t pad) {
+  return PlanKey{1, N, H, W, C, O, KH, KW, stride, pad};
+}
+
+static void apply_plan(GemmP& p, const PlanKey& k) {
+  std::lock_guard<std::mutex> lock(g_plan_mu);
+  if (g_plans.empty()) return;
+  const auto it = g_plans.find(k);
+  if (it != g_plans.end()) {
+    p.plan_cfg = it->second.cfg;
+    p.plan_split = it->second.split;
+  }
+}
+
+// The GEMM view of a problem given as (M, N, K) or (N, H, W, C, O, KH, KW, stride, pad);
+// false for a bad geometry. `tiled`: whether the tiled kernel runs it (a dense GEMM of at
+// most 64 rows takes the GEMV / skinny kernels: nothing to choose).
+static bool problem_view(const int64_t* pr, int n, PlanKey& key, GemmP& p, bool& conv, bool& tiled) {
+  if (!pr) return false;
+  p = GemmP{};
+  if (n == 3) {
+    const int64_t M = pr[0], N = pr[1], K = pr[2];
+    if (M < 1 || N < 1 || K < 16 || K % 16 || M > 0x7fffffff || N > 0x7fffffff || K > KMAX_EXACT) return false;
+    key = dense_key(M, N, K);
+    p.M = (int)M; p.N = (int)N; p.K = (int)K;
+    conv = false;
+    tiled = M > 64;
+    return true;
+  }
+  if (n != 9) return false;
+  const int64_t N = pr[0], H = pr[1], W = pr[2], C = pr[3], O = pr[4], KH = pr[5], KW = pr[6], st = pr[7], pad = pr[8];
+  if (N < 1 || H < 1 || W < 1 || C < 16 || C % 16 || O < 1 || KH < 1 || KW < 1 || st < 1 || pad < 0 ||
+      H + 2 * pad < KH || W + 2 * pad < KW)
+    return false;
+  const int64_t OH = (H + 2 * pad - KH) / st + 1, OW = (W + 2 * pad - KW) / st + 1;
+  const int64_t M = N * OH * OW, K = KH * KW * C;
+  if (M > 0x7fffffff || O > 0x7fffffff || K > KMAX_EXACT) return false;
+  key = conv_key(N, H, W, C, O, KH, KW, st, pad);
+  p.M = (int)M; p.N = (int)O; p.K = (int)K;
+  conv = !(KH == 1 && KW == 1 && st == 1 && pad == 0);  // a 1x1 conv runs the dense loader
+  tiled = true;
+  return true;
+}
+
+// The K split configuration `cfg` runs for this problem with a full-size workspace.
+static int split_of(const GemmP& p, int cfg, bool conv, int planned) {
+  const TileDims d = CFG_TILES[cfg];
+  if (d.bm * d.bn > SPLIT_MAX_TILE) return 1;
+  const long long tiles = (long long)((p.M + d.bm - 1) / d.bm) * ((p.N + d.bn - 1) / d.bn);
+  const int S = pick_split(tiles, (p.K + BK - 1) / BK, conv, planned);
+  const size_t need = SPLIT_CNT_BYTES + (size_t)tiles * S * d.bm * d.bn * 4;
+  return (S > 1 && (need > SPLIT_WS_BYTES || tiles * 4 > (long long)SPLIT_CNT_BYTES)) ? 1 : S;
+}
 
 }  // namespace bq
 
@@ -1136,6 +1216,7 @@ int bq_gemm_i8(const int8_t* A, const int8_t* W, int64_t M, int64_t N, int64_t K
       default: skinny_i8_kernel<4, 8, 1><<<grid, 8 * 64, 0, st>>>(p); break;
     }
   } else {
+    apply_plan(p, dense_key(M, N, K));
     launch_gemm<false>(p, st, Ws{ws, ws_bytes});
   }
   return check_launch(what);
@@ -1176,6 +1257,7 @@ static int conv_impl(const char* what, const int8_t* x, int64_t N, int64_t H, in
   p.s_out = s_out;
   p.q_out = q_out;
   p.amax = amax;
+  apply_plan(p, conv_key(N, H, W, C, O, KH, KW, stride, pad));
   hipStream_t st = (hipStream_t)stream;
   if (KH == 1 && KW == 1 && stride == 1 && pad == 0)
     launch_gemm<false>(p, st, Ws{ws, ws_bytes});  // a 1x1 conv is the dense GEMM on [N*H*W, C]
@@ -1195,7 +1277,65 @@ int64_t bq_conv2d_absmax_parts(int64_t N, int64_t H, int64_t W, int64_t C, int64
   GemmP p{};
   p.M = (int)(N * OH * OW);
   p.N = (int)O;
+  apply_plan(p, conv_key(N, H, W, C, O, KH, KW, stride, pad));
   return p.M == 0 ? 0 : out_tiles(p);
+}
+
+int bq_plan_candidates(const int64_t* problem, int n, int32_t* cfgs, int32_t* splits, int cap) {
+  PlanKey key;
+  GemmP p;
+  bool conv, tiled;
+  if (!problem_view(problem, n, key, p, conv, tiled))
+    return set_error(BQ_ERR_ARG, "bq_plan_candidates: bad problem (3 dense or 9 conv dimensions)");
+  if (!tiled) return 0;
+  std::pair<int, int> out[64];
+  int cnt = 0;
+  const int rule = choose_cfg(p);
+  out[cnt++] = {rule, split_of(p, rule, conv, 0)};
+  // 3 (four waves on 256x256) and 9 (64x64 with an 8-deep ring) never won a measurement
+  static const int ids[] = {1, 2, 4, 5, 6, 7, 8, 10, 11, 12, 13, 14};
+  for (int cfg : ids) {
+    const TileDims d = CFG_TILES[cfg];
+    const int KT = (p.K + BK - 1) / BK;
+    const int tries[] = {1, 2, 4, 8};
+    for (int want : tries) {
+      if (want > 1 && (d.bm * d.bn > SPLIT_MAX_TILE || KT < 2 * want)) break;
+      const std::pair<int, int> c{cfg, split_of(p, cfg, conv, want)};
+      if (c.second != want) continue;  // the workspace cannot hold this split
+      bool dup = false;
+      for (int i = 0; i < cnt; ++i) dup |= out[i] == c;
+      if (!dup && cnt < 64) out[cnt++] = c;
+    }
+  }
+  for (int i = 0; i < cnt && i < cap; ++i) {
+    if (cfgs) cfgs[i] = out[i].first;
+    if (splits) splits[i] = out[i].second;
+  }
+  return cnt;
+}
+
+int bq_plan_set(const int64_t* problem, int n, int32_t cfg, int32_t split) {
+  PlanKey key;
+  GemmP p;
+  bool conv, tiled;
+  if (!problem_view(problem, n, key, p, conv, tiled))
+    return set_error(BQ_ERR_ARG, "bq_plan_set: bad problem (3 dense or 9 conv dimensions)");
+  std::lock_guard<std::mutex> lock(g_plan_mu);
+  if (cfg == 0) {
+    g_plans.erase(key);
+    return BQ_OK;
+  }
+  if (cfg < 1 || cfg > 14 || cfg == 3 || cfg == 9 || split < 1 || split > 64)
+    return set_error(BQ_ERR_ARG, "bq_plan_set: bad configuration %d / split %d", cfg, split);
+  if (!tiled) return set_error(BQ_ERR_ARG, "bq_plan_set: a GEMM of at most 64 rows has no tiled kernel to plan");
+  g_plans[key] = Plan{cfg, split};
+  return BQ_OK;
+}
+
+int bq_plan_clear(void) {
+  std::lock_guard<std::mutex> lock(g_plan_mu);
+  g_plans.clear();
+  return BQ_OK;
 }
 
 int bq_conv2d_i8_nhwc(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t C, const int8_t* w,

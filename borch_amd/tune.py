@@ -1,0 +1,163 @@
+"""Kernel choice by measurement for the int8 GEMM / conv kernels.
+
+The library picks the tiled kernel's configuration (tile, ring depth) and K split per
+problem by rule. ``tune(model, x)`` records the int8 launches of one forward, times every
+candidate of each distinct problem on the device (HIP graphs of back-to-back launches,
+HIP events), and records the fastest as the problem's plan (``bq_plan_set``) when it beats
+the rule's pick by more than ``min_gain``; otherwise the rule stays. All candidates compute
+the same exact int32 sums and the same epilogue, so tuning changes time only, never a
+result.
+
+Mirrors the reference's ``Device.choose`` / ``runTuning`` (borch-ts/src/device.ts:2686-2700,
+2834-2846: the rule's pick first, the fastest cached per key) and ``compiled``'s ``tune``
+option (borch-ts/src/compile.ts:55-62), with one report per decision like its
+``TuneReport`` (device.ts:532-536).
+"""
+from __future__ import annotations
+
+import ctypes
+import inspect
+
+import torch
+
+from . import int8 as _i8
+from ._lib import check, lib
+
+# the borch_amd.int8 wrappers that launch a layer's int8 kernel on an int8 input
+LAYER_KERNELS = ("conv2d_i8_nhwc", "conv2d_i8_nhwc_q", "dwconv_i8_nhwc", "gemm_i8")
+
+
+def record_launches(model, x):
+    """One eager forward of ``model`` with the wrappers in ``LAYER_KERNELS`` recording their
+    bound arguments: ``[(layer name, wrapper name, wrapper, arguments)]`` in launch order."""
+    from . import nn as bnn
+    calls, current, saved, hooks = [], [""], {}, []
+    for name, m in model.named_modules():
+        if isinstance(m, (bnn.Conv2d, bnn.Linear)):
+            hooks.append(m.register_forward_pre_hook(lambda mod, inp, _n=name: current.__setitem__(0, _n)))
+    for n in LAYER_KERNELS:
+        f = saved[n] = getattr(_i8, n)
+
+        def rec(*a, _f=f, _n=n, **k):
+            bound = inspect.signature(_f).bind(*a, **k)
+            bound.apply_defaults()
+            calls.append((current[0], _n, _f, dict(bound.arguments)))
+            return _f(*a, **k)
+        setattr(_i8, n, rec)
+    try:
+        with torch.no_grad():
+            model(x)
+    finally:
+        for n, f in saved.items():
+            setattr(_i8, n, f)
+        for h in hooks:
+            h.remove()
+    return calls
+
+
+def problem_of(kind: str, a: dict):
+    """The plan key of a recorded launch: (M, N, K) for a dense GEMM, (N, H, W, Cpad, O, KH,
+    KW, stride, pad) for a conv; None where there is no tiled kernel to choose."""
+    if kind == "gemm_i8":
+        M, K = a["qa"].shape
+        return (int(M), int(a["qw"].shape[0]), int(K)) if M > 64 else None
+    if kind in ("conv2d_i8_nhwc", "conv2d_i8_nhwc_q"):
+        n, h, w, c = a["qx"].shape
+        wq = a["wq"]
+        return (int(n), int(h), int(w), int(c), int(wq.O), int(wq.KH), int(wq.KW), int(a["stride"]), int(a["pad"]))
+    return None
+
+
+def _arr(problem):
+    return (ctypes.c_int64 * len(problem))(*problem)
+
+
+def candidates(problem) -> list[tuple[int, int]]:
+    """(configuration id, K split) pairs the library offers for ``problem``; the rule's pick first."""
+    n = lib().bq_plan_candidates(_arr(problem), len(problem), None, None, 0)
+    if n < 0:
+        check(n)
+    if n == 0:
+        return []
+    cfgs, splits = (ctypes.c_int32 * n)(), (ctypes.c_int32 * n)()
+    lib().bq_plan_candidates(_arr(problem), len(problem), cfgs, splits, n)
+    return list(zip(cfgs, splits))
+
+
+def set_plan(problem, cfg: int, split: int) -> None:
+    """Records the plan for ``problem``; ``cfg == 0`` returns it to the rule."""
+    check(lib().bq_plan_set(_arr(problem), len(problem), int(cfg), int(split)))
+
+
+def clear_plans() -> None:
+    check(lib().bq_plan_clear())
+
+
+def _time_us(fn, a, stream, calls: int, rounds: int) -> float:
+    """Microseconds per launch of ``fn(**a)``: a HIP graph of ``calls`` launches, the
+    minimum over ``rounds`` timed replays."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn(**a)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(calls):
+            fn(**a)
+    g.replay()
+    best = float("inf")
+    for _ in range(rounds):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        g.replay()
+        e1.record(stream)
+        e1.synchronize()
+        best = min(best, e0.elapsed_time(e1) * 1e3 / calls)
+    del g
+    return best
+
+
+def _label(c) -> str:
+    return f"cfg{c[0]}/split{c[1]}"
+
+
+def tune(model, x, min_gain: float = 0.03, calls: int = 8, rounds: int = 3) -> list[dict]:
+    """Times every candidate of each distinct int8 problem in one forward of ``model`` on
+    ``x`` and keeps the fastest when it is more than ``min_gain`` faster than the rule's
+    pick. Returns one report per decision: key, prior, prior_us, chosen, chosen_us,
+    candidates."""
+    if x.device.type != "cuda":
+        return []
+    _i8.split_workspace(x.device)  # the splits timed here are the splits that run later
+    stream = torch.cuda.current_stream(x.device)
+    reports, seen = [], set()
+    for layer, kind, fn, a in record_launches(model, x):
+        problem = problem_of(kind, a)
+        if problem is None or problem in seen:
+            continue
+        seen.add(problem)
+        cands = candidates(problem)
+        if len(cands) < 2:
+            continue
+        set_plan(problem, 0, 0)
+        times = []
+        for c in cands:
+            set_plan(problem, *c)
+            times.append(_time_us(fn, a, stream, calls, rounds))
+        best = min(range(len(cands)), key=times.__getitem__)
+        if best != 0:  # confirm against the rule's pick, back to back
+            set_plan(problem, *cands[0])
+            times[0] = min(times[0], _time_us(fn, a, stream, calls, rounds))
+            set_plan(problem, *cands[best])
+            times[best] = min(times[best], _time_us(fn, a, stream, calls, rounds))
+        chosen = best if times[best] < times[0] * (1.0 - min_gain) else 0
+        if chosen:
+            set_plan(problem, *cands[chosen])
+        else:
+            set_plan(problem, 0, 0)
+        reports.append({"key": problem, "layer": layer, "prior": _label(cands[0]), "prior_us": round(times[0], 2),
+                        "chosen": _label(cands[chosen]), "chosen_us": round(times[chosen], 2),
+                        "candidates": len(cands)})
+    torch.cuda.synchronize(x.device)
+    return reports

@@ -160,6 +160,25 @@ int bq_conv2d_i8_nhwc(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t 
 int64_t bq_conv2d_absmax_parts(int64_t N, int64_t H, int64_t W, int64_t C, int64_t O, int64_t KH, int64_t KW,
                                int64_t stride, int64_t pad);
 
+/* Kernel choice by measurement. The GEMM and conv entry points pick a tiled-kernel
+ * configuration (tile, ring depth) and a K split by rule; a plan overrides both for one
+ * problem. Every configuration and split computes the same exact int32 sums and the same
+ * epilogue, so a plan changes the time only, never a result. A problem is
+ *   n == 3: a dense bq_gemm_i8 (M, N, K), or
+ *   n == 9: a bq_conv2d_i8_nhwc(_q) (N, H, W, C, O, KH, KW, stride, pad), C the padded count.
+ * bq_plan_candidates writes up to `cap` (configuration id, K split) pairs, the rules' pick
+ * first, and returns how many there are (0: nothing to choose, as for a dense GEMM of at
+ * most 64 rows; negative: a bad problem). bq_plan_set records one (cfg == 0 removes the
+ * problem's plan); bq_plan_clear removes all. A plan in force when bq_conv2d_absmax_parts
+ * sizes a buffer must stay in force for the conv that fills it. Plans are process-wide;
+ * set them before a graph capture (a captured launch keeps the choice it was made with).
+ * Replaces Device.choose / runTuning (borch-ts/src/device.ts:2686-2700, 2834-2846), the
+ * rule's pick first and the fastest cached per key, that compiled(..., {tune}) drives
+ * (borch-ts/src/compile.ts:55-62). */
+int bq_plan_candidates(const int64_t* problem, int n, int32_t* cfgs, int32_t* splits, int cap);
+int bq_plan_set(const int64_t* problem, int n, int32_t cfg, int32_t split);
+int bq_plan_clear(void);
+
 /* bq_conv2d_i8_nhwc that also writes the output's int8 twin with a calibrated scale:
  * q_out int8 [N, OH, OW, O] = clip(rint(y / s_out[0]), +-127) (exact quotient, half to even) of the final f32 y
  * (after residual and activation), the next conv's input with no quantize pass.

@@ -126,3 +126,73 @@ def test_ctypes_signatures_match_the_header():
         params = params.strip()
         n = 0 if params in ("", "void") else params.count(",") + 1
         assert n == len(_lib.SIGNATURES[name][1]), (name, n, len(_lib.SIGNATURES[name][1]))
+
+
+def _candidates(lib, problem):
+    arr = (ctypes.c_int64 * len(problem))(*problem)
+    n = lib.bq_plan_candidates(arr, len(problem), None, None, 0)
+    if n <= 0:
+        return n
+    cfgs, splits = (ctypes.c_int32 * n)(), (ctypes.c_int32 * n)()
+    assert lib.bq_plan_candidates(arr, len(problem), cfgs, splits, n) == n
+    return list(zip(cfgs, splits))
+
+
+@pytest.mark.parametrize("problem", [(4096, 4096, 4096), (6304, 768, 3072), (256, 512, 4608), (65, 64, 8192),
+                                     (16, 32, 32, 64, 64, 3, 3, 1, 1), (16, 4, 4, 512, 512, 3, 3, 1, 1),
+                                     (64, 112, 112, 32, 96, 1, 1, 1, 0), (2, 13, 13, 16, 24, 3, 3, 2, 1)])
+def test_plan_candidates(problem):
+    """The kernel-choice candidates (host code, no GPU): the rules' pick first, no pair twice,
+    configuration ids of the tiled kernel only (3 and 9 are never offered), K splits only on
+    tiles of at most 4096 outputs, and never more splits than K stages."""
+    from borch_amd import _lib
+    lib = _lib.lib()
+    cands = _candidates(lib, problem)
+    assert isinstance(cands, list) and len(cands) >= 2
+    assert len(set(cands)) == len(cands)
+    small = {7, 9, 10, 12}  # tiles of 64 x 64 and 128 x 32 outputs
+    for cfg, split in cands:
+        assert 1 <= cfg <= 14 and split >= 1
+        assert cfg not in (3, 9) or (cfg, split) == cands[0]
+        if split > 1:
+            assert cfg in small
+    K = problem[2] if len(problem) == 3 else problem[3] * problem[5] * problem[6]
+    assert all(split <= (K + 127) // 128 for _, split in cands)
+
+
+def test_plan_rejects_bad_problems_and_small_gemms():
+    from borch_amd import _lib
+    lib = _lib.lib()
+    assert _candidates(lib, (64, 4096, 4096)) == 0  # the GEMV / skinny kernels: nothing to choose
+    assert _candidates(lib, (100, 100, 100)) < 0  # K % 16
+    assert _candidates(lib, (1, 2, 3, 4)) < 0  # neither 3 nor 9 dimensions
+    assert _candidates(lib, (1, 4, 4, 16, 8, 5, 5, 1, 0)) < 0  # the filter is larger than the input
+    arr = (ctypes.c_int64 * 3)(4096, 4096, 4096)
+    assert lib.bq_plan_set(arr, 3, 3, 1) < 0 and lib.bq_plan_set(arr, 3, 15, 1) < 0
+    assert lib.bq_plan_set(arr, 3, 1, 0) < 0
+    small = (ctypes.c_int64 * 3)(16, 512, 512)
+    assert lib.bq_plan_set(small, 3, 1, 1) < 0
+
+
+def test_plan_sets_the_conv_tile_count():
+    """A plan changes the tiled kernel's configuration, so the per-tile maxima a conv writes
+    (bq_conv2d_absmax_parts) follow it; removing the plan restores the rule."""
+    from borch_amd import _lib
+    lib = _lib.lib()
+    geom = (16, 32, 32, 64, 128, 3, 3, 1, 1)  # M = 16384 pixels, 128 output channels
+    arr = (ctypes.c_int64 * 9)(*geom)
+    try:
+        rule = lib.bq_conv2d_absmax_parts(*geom)
+        assert rule > 0
+        assert lib.bq_plan_set(arr, 9, 1, 1) == 0  # 256 x 256 tiles
+        assert lib.bq_conv2d_absmax_parts(*geom) == (16384 // 256) * 1
+        assert lib.bq_plan_set(arr, 9, 12, 1) == 0  # 128 x 32 tiles
+        assert lib.bq_conv2d_absmax_parts(*geom) == (16384 // 128) * 4
+        assert _candidates(lib, geom)[0][0] == _candidates(lib, geom)[0][0]  # the rule's pick stays first
+        assert lib.bq_plan_set(arr, 9, 0, 0) == 0
+        assert lib.bq_conv2d_absmax_parts(*geom) == rule
+        assert lib.bq_plan_set(arr, 9, 1, 1) == 0
+        assert lib.bq_plan_clear() == 0
+        assert lib.bq_conv2d_absmax_parts(*geom) == rule
+    finally:
+        lib.bq_plan_clear()

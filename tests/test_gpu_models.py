@@ -299,3 +299,27 @@ def test_c3_resnet18_static_calibrated(dev):
 def O_quant():
     from oracle import quant
     return quant
+
+
+def test_tuned_compiled_matches_untuned(dev):
+    """compiled(tune=True) chooses each int8 conv's kernel by measurement before its first
+    capture; the tuned forward equals the untuned one bit for bit, and every decision kept
+    a candidate no slower than the rule's pick."""
+    from borch_amd import tune as T
+    say("tuned vs untuned compiled (ResNet-18 b4, ViT encoder b2)")
+    T.clear_plans()
+    try:
+        for name, x in (("resnet18", WL.c3_input(4, 3)), ("vit_b16", WL.c5_input(2, 197, 768, 3))):
+            model = nets.build(name, seed=3, device=dev)
+            xt = torch.from_numpy(x).to(dev)
+            c0 = bt.compiled(model, int8=True, graph=True, fuse=False, tune=False)
+            ref = n(c0(xt))
+            c1 = bt.compiled(model, int8=True, graph=True, fuse=False, tune=True)
+            got = n(c1(xt))
+            assert np.array_equal(got, ref), name
+            assert len(c1.tuned) == 1 and len(c1.tuned[0]) > 0, name
+            for rep in c1.tuned[0]:
+                assert rep["chosen"] == rep["prior"] or rep["chosen_us"] < rep["prior_us"], rep
+            assert np.array_equal(n(c1(xt)), ref), name  # a replay, with the plans in force
+    finally:
+        T.clear_plans()

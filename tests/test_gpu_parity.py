@@ -518,3 +518,72 @@ def test_probe_stream_read_folds_every_byte(dev):
         pad[:n16] = chunk_x
         want = np.bitwise_xor.reduce(pad.reshape(nblk, per), axis=1)
         np.testing.assert_array_equal(sink.cpu().numpy(), want)
+
+
+# ------------------------------------------------------------ kernel choice by measurement
+
+@pytest.fixture
+def no_plans():
+    from borch_amd import tune as T
+    T.clear_plans()
+    yield T
+    T.clear_plans()
+
+
+@pytest.mark.parametrize("M,N,K,res,act", [(6304, 768, 768, True, 0), (300, 200, 4112, False, 1),
+                                           (1000, 40, 96, False, 2), (257, 2304, 768, True, 3)])
+def test_every_gemm_plan_gives_the_same_result(dev, no_plans, M, N, K, res, act):
+    """Every (configuration, K split) the library offers for a dense GEMM gives the rule's
+    output and int32 accumulators bit for bit (bias, residual and activation included)."""
+    T = no_plans
+    say(f"plans gemm M={M} N={N} K={K}")
+    rng = np.random.default_rng(M + N + K)
+    qa = t(rng.integers(-127, 128, size=(M, K)).astype(np.int8), dev)
+    qw = t(rng.integers(-127, 128, size=(N, K)).astype(np.int8), dev)
+    sa = t(rng.uniform(1e-4, 1e-3, M).astype(np.float32), dev)
+    sw = t(rng.uniform(1e-4, 1e-3, N).astype(np.float32), dev)
+    b = t(rng.normal(size=N).astype(np.float32), dev)
+    r = t(rng.normal(size=(M, N)).astype(np.float32), dev) if res else None
+    I.split_workspace(dev)
+    want, want_acc = I.gemm_i8(qa, qw, sa, sw, b, act, want_acc=True, residual=r)
+    cands = T.candidates((M, N, K))
+    assert len(cands) >= 8
+    for cfg, split in cands:
+        T.set_plan((M, N, K), cfg, split)
+        got, acc = I.gemm_i8(qa, qw, sa, sw, b, act, want_acc=True, residual=r)
+        assert torch.equal(acc, want_acc), (cfg, split)
+        assert torch.equal(got, want), (cfg, split)
+
+
+@pytest.mark.parametrize("N,C,H,O_,k,stride,pad,res", [(16, 64, 32, 64, 3, 1, 1, True), (16, 512, 4, 512, 3, 1, 1, True),
+                                                     (4, 32, 28, 240, 1, 1, 0, False), (2, 48, 15, 96, 5, 2, 2, False)])
+def test_every_conv_plan_gives_the_same_result(dev, no_plans, N, C, H, O_, k, stride, pad, res):
+    """Every candidate for a conv gives the rule's f32 output, int32 accumulators, int8 twin
+    and per-tensor maximum bit for bit (its per-tile maxima follow the plan's tile count)."""
+    T = no_plans
+    say(f"plans conv N={N} C={C} H={H} O={O_} k={k} s={stride}")
+    rng = np.random.default_rng(N * C + H + O_)
+    x = rng.normal(size=(N, C, H, H)).astype(np.float32)
+    w = (rng.normal(size=(O_, C, k, k)) * np.sqrt(2.0 / (C * k * k))).astype(np.float32)
+    b = t((rng.normal(size=O_) * 0.1).astype(np.float32), dev)
+    OH = (H + 2 * pad - k) // stride + 1
+    r = t(rng.normal(size=(N, O_, OH, OH)).astype(np.float32), dev) if res else None
+    w8 = I.pack_conv_weight(t(w, dev))
+    qx, sa = I.quantize_nhwc(t(x, dev), w8.cpad)
+    s_out = torch.tensor([0.05], dtype=torch.float32, device=dev)
+    I.split_workspace(dev)
+    want, want_acc = I.conv2d_i8_nhwc(qx, sa, w8, stride, pad, b, r, I.ACT_RELU, want_acc=True)
+    want_max = want._bq_absmax[0][: want._bq_absmax[1]].max()
+    _, want_q = I.conv2d_i8_nhwc_q(qx, sa, w8, s_out, stride, pad, b, r, I.ACT_RELU)
+    problem = (N, H, H, w8.cpad, O_, k, k, stride, pad)
+    cands = T.candidates(problem)
+    assert len(cands) >= 8
+    for cfg, split in cands:
+        T.set_plan(problem, cfg, split)
+        got, acc = I.conv2d_i8_nhwc(qx, sa, w8, stride, pad, b, r, I.ACT_RELU, want_acc=True)
+        assert torch.equal(acc, want_acc), (cfg, split)
+        assert torch.equal(got, want), (cfg, split)
+        parts, nparts, _ = got._bq_absmax
+        assert torch.equal(parts[:nparts].max(), want_max), (cfg, split)
+        _, q = I.conv2d_i8_nhwc_q(qx, sa, w8, s_out, stride, pad, b, r, I.ACT_RELU)
+        assert torch.equal(q, want_q), (cfg, split)
