@@ -312,6 +312,12 @@ def bench_models(dev, stream, steps, layers_out=None):
         out[key] = {"int8_graph_ms": round(g_ms, 4), "int8_eager_ms": round(eager_ms, 4),
                     "f32_ms": round(f32_ms, 4), "int8_layers": c.int8_layers,
                     "max_abs_diff_vs_f32_rel": round(gap, 5)}
+        dec = c.tuned[0] if c.tuned else []
+        out[key]["tuned"] = {"problems": len(dec), "changed": sum(d["chosen"] != d["prior"] for d in dec),
+                             "rule_us": round(sum(d["prior_us"] for d in dec), 1),
+                             "tuned_us": round(sum(d["chosen_us"] for d in dec), 1)}
+        if layers_out is not None:
+            layers_out[key + "_tuning"] = dec
         rows = layer_table(model, x, stream)
         out[key]["layers_alone"] = layer_summary(rows)
         if name == "resnet18":  # per-layer MFMA fraction: [layer, M, N, K, us, fraction of 5.0 POP/s]
@@ -350,6 +356,8 @@ def bench_models(dev, stream, steps, layers_out=None):
 def print_layer_tables(models, tables):
     """Markdown: per model, the forward times and one row per int8 layer timed alone."""
     for key, rows in tables.items():
+        if key.endswith("_tuning"):
+            continue
         m = models[key]
         print(f"## {key}\n")
         print(f"int8 forward (HIP graph, dynamic scales): {m['int8_graph_ms']} ms; "
@@ -361,6 +369,15 @@ def print_layer_tables(models, tables):
             print(f"| {r['layer']} | {r['kernel']} | {r['M']} | {r['N']} | {r['K']} | {r['ops']} | {r['bytes']} | "
                   f"{r['us']} | {r['TOPS']} | {r['mfma_frac']} | {r['GBps']} |")
         print()
+        dec = tables.get(key + "_tuning", [])
+        if dec:
+            print(f"Kernel choice by measurement (compiled(tune=True)): {json.dumps(m['tuned'])}\n")
+            print("| first layer of the problem | problem | candidates | rule's pick | us | chosen | us |")
+            print("|---|---|---|---|---|---|---|")
+            for d in dec:
+                print(f"| {d['layer']} | {d['key']} | {d['candidates']} | {d['prior']} | {d['prior_us']} | "
+                      f"{d['chosen']} | {d['chosen_us']} |")
+            print()
 
 
 def main():
