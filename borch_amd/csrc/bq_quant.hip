@@ -449,8 +449,8 @@ int bq_quantize_nhwc_parts(const float* x, int64_t P, int64_t C, int64_t Cpad, c
 }
 
 int bq_quantize_nhwc_chscale(const float* x, int64_t N, int64_t HW, int64_t C, int64_t Cpad, const float* cs,
-                             int8_t* q, float* s, const float* s_given, void* ws, size_t ws_bytes,
-                             bq_stream_t stream) {
+                             int8_t* q, float* s, const float* s_given, const float* absmax_parts, int64_t nparts,
+                             void* ws, size_t ws_bytes, bq_stream_t stream) {
   const char* what = "bq_quantize_nhwc_chscale";
   if (N < 0 || HW < 1 || C < 1 || Cpad < C) return set_error(BQ_ERR_ARG, "%s: bad sizes", what);
   if (C % 4 || Cpad % 4) return set_error(BQ_ERR_UNSUPPORTED, "%s: C and Cpad must be multiples of 4", what);
@@ -465,13 +465,17 @@ int bq_quantize_nhwc_chscale(const float* x, int64_t N, int64_t HW, int64_t C, i
   hipStream_t st = (hipStream_t)stream;
   const FastDiv dhw = fast_div((uint32_t)HW);
   int np = 0;
-  float* parts = nullptr;
-  if (!s_given) {
+  const float* parts = nullptr;
+  if (!s_given && absmax_parts) {  // the maxima of the product, from the gate's producer
+    if (nparts < 1 || nparts > 0x7fffffff) return set_error(BQ_ERR_ARG, "%s: bad nparts %lld", what, (long long)nparts);
+    parts = absmax_parts;
+    np = (int)nparts;
+  } else if (!s_given) {
     np = nparts_for(P * C);
     if (!ws || ws_bytes < (size_t)np * sizeof(float))
       return set_error(BQ_ERR_ARG, "%s: workspace %zu bytes, need %zu", what, ws_bytes, (size_t)np * sizeof(float));
     parts = (float*)ws;
-    absmax_chscale_kernel<<<np, QT_THREADS, 0, st>>>(x, cs, (int)P, (int)C, dhw.mul, dhw.shift, parts);
+    absmax_chscale_kernel<<<np, QT_THREADS, 0, st>>>(x, cs, (int)P, (int)C, dhw.mul, dhw.shift, (float*)ws);
     if (int r = check_launch(what)) return r;
   }
   int64_t blocks = (P * (Cpad / 4) + QT_THREADS - 1) / QT_THREADS;

@@ -5,17 +5,22 @@
 // the operation of borch's CPU runner "se" node (borch-ts/src/cpu/runner.ts:256-268:
 // meanRows, gemmBiasAct(swish), gemmBiasAct(sigmoid); lib.rs:222-244 mean_rows). The gate
 // multiplies the activation inside the next conv's quantizer (bq_quantize_nhwc_chscale)
-// instead of the runner's scaleRows pass. Two kernels: partial sums over row chunks (the
-// bandwidth pass), then one workgroup per image finishes the mean and runs the small MLP.
-// Every sum has a fixed order: results do not depend on scheduling.
+// instead of the runner's scaleRows pass. Two kernels: partial sums (and maxima) over row
+// chunks (the bandwidth pass), then one workgroup per image finishes the mean and runs the
+// small MLP. Every sum has a fixed order: results do not depend on scheduling.
+//
+// The excite also gives the quantizer of the product its dynamic scale without a pass over
+// x: the gate is positive and f32 rounding is monotonic, so over the pixels of (n, c)
+// max |fl(x * g)| = fl(max |x| * g). The partial pass keeps max |x| per chunk and channel;
+// the gate workgroup of each image writes the maximum of fl(max|x| * g) over its channels.
 #include <algorithm>
 
 #include "bq_common.h"
 
 namespace bq {
 
-constexpr int SE_THREADS = 256;    // the partial-sum pass
-constexpr int GATE_THREADS = 1024; // the per-image pass: 16 waves cover the squeeze outputs and channels
+constexpr int SE_THREADS = 256;     // the partial-sum pass
+constexpr int GATE_THREADS = 1024;  // the per-image pass: 16 waves cover the squeeze outputs and channels
 
 __device__ __forceinline__ float sigmoid_f(float v) {
   return __builtin_amdgcn_rcpf(__fadd_rn(1.0f, __builtin_amdgcn_exp2f(__fmul_rn(v, -1.4426950408889634f))));
@@ -25,11 +30,14 @@ __device__ __forceinline__ float sigmoid_f(float v) {
 // g = t % G (4 channels) over the rows r = t / G, t / G + TR, ... of the chunk (TR = 256 / G
 // row lanes, G >= 1 groups a pass, more passes when C / 4 > 256), eight rows' loads issued
 // before they are added in row order; the TR row-lane sums of a group are then added in
-// lane order through LDS. partial[(n * chunks + chunk) * C + c].
+// lane order through LDS. partial[(n * chunks + chunk) * C + c]; with `pmax`, max |x| of the
+// same rows at the same index.
 __global__ __launch_bounds__(SE_THREADS) void se_partial_kernel(const float* __restrict__ x, int HW, int C,
                                                                 int chunks, int rows_per,
-                                                                float* __restrict__ partial) {
+                                                                float* __restrict__ partial,
+                                                                float* __restrict__ pmax) {
   __shared__ float4 red[SE_THREADS];
+  __shared__ float4 redm[SE_THREADS];
   const int n = blockIdx.x / chunks, chunk = blockIdx.x - n * chunks;
   const int r0 = chunk * rows_per, r1 = min(HW, r0 + rows_per);
   const int groups = C / 4;
@@ -41,7 +49,7 @@ __global__ __launch_bounds__(SE_THREADS) void se_partial_kernel(const float* __r
   constexpr int U = 8;
   for (int gb = 0; gb < groups; gb += G) {
     const int g = gb + g0;
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f), mx = acc;
     if (lane_r < TR && g < groups) {
       const float* xg = xn + g * 4;
       for (int r = r0 + lane_r; r < r1; r += U * TR) {
@@ -55,48 +63,68 @@ __global__ __launch_bounds__(SE_THREADS) void se_partial_kernel(const float* __r
         for (int u = 0; u < U; ++u) {
           acc.x = __fadd_rn(acc.x, v[u].x); acc.y = __fadd_rn(acc.y, v[u].y);
           acc.z = __fadd_rn(acc.z, v[u].z); acc.w = __fadd_rn(acc.w, v[u].w);
+          mx.x = fmaxf(mx.x, fabsf(v[u].x)); mx.y = fmaxf(mx.y, fabsf(v[u].y));
+          mx.z = fmaxf(mx.z, fabsf(v[u].z)); mx.w = fmaxf(mx.w, fabsf(v[u].w));
         }
       }
     }
     red[t] = acc;
+    redm[t] = mx;
     __syncthreads();
     if (t < G && gb + t < groups) {
-      float4 s = red[t];
+      float4 s = red[t], m = redm[t];
       for (int k = 1; k < TR; ++k) {
-        const float4 v = red[k * G + t];
+        const float4 v = red[k * G + t], w = redm[k * G + t];
         s.x = __fadd_rn(s.x, v.x); s.y = __fadd_rn(s.y, v.y);
         s.z = __fadd_rn(s.z, v.z); s.w = __fadd_rn(s.w, v.w);
+        m.x = fmaxf(m.x, w.x); m.y = fmaxf(m.y, w.y); m.z = fmaxf(m.z, w.z); m.w = fmaxf(m.w, w.w);
       }
-      *reinterpret_cast<float4*>(partial + ((size_t)n * chunks + chunk) * C + (gb + t) * 4) = s;
+      const size_t o = ((size_t)n * chunks + chunk) * C + (gb + t) * 4;
+      *reinterpret_cast<float4*>(partial + o) = s;
+      if (pmax) *reinterpret_cast<float4*>(pmax + o) = m;
     }
     __syncthreads();
   }
 }
 
-// One block per image: pooled (in LDS), z = silu(W1 pooled + b1) (one wave per output
-// j, its lanes over c, a wave tree), gate = sigmoid(W2 z + b2) (one thread per channel,
-// reading the transposed expand weight w2t [S, C] so a wave's loads are contiguous).
-__global__ __launch_bounds__(GATE_THREADS) void se_gate_kernel(const float* __restrict__ partial, int chunks, int HW,
+// One block per image: pooled and max |x| per channel (in LDS), z = silu(W1 pooled + b1)
+// (one wave per output j, its lanes over c, a wave tree), gate = sigmoid(W2 z + b2) (one
+// thread per channel, reading the transposed expand weight w2t [S, C] so a wave's loads are
+// contiguous). With `amax`: max over c of fl(max|x[n, :, c]| * gate[n, c]) into amax[n].
+// (Splitting the squeeze and the excite into two wider kernels was slower on every B0
+// layer: 9-18 us against 5.5-18 us, each small launch paying its own latency chain.)
+__global__ __launch_bounds__(GATE_THREADS) void se_gate_kernel(const float* __restrict__ partial,
+                                                             const float* __restrict__ pmax, int chunks, int HW,
                                                              int C, int S, const float* __restrict__ w1,
                                                              const float* __restrict__ b1,
                                                              const float* __restrict__ w2t,
-                                                             const float* __restrict__ b2, float* __restrict__ gate) {
-  extern __shared__ float sm[];  // pooled [C], z [S]
+                                                             const float* __restrict__ b2, float* __restrict__ gate,
+                                                             float* __restrict__ amax) {
+  extern __shared__ float sm[];  // pooled [C], z [S], xmax [C] (with amax)
+  __shared__ float wmax[GATE_THREADS / 64];
   float* pooled = sm;
   float* z = sm + C;
+  float* xmax = sm + C + S;
   const int n = blockIdx.x;
   const float inv = __fdiv_rn(1.0f, (float)HW);
   for (int c = threadIdx.x; c < C; c += GATE_THREADS) {
-    float s = 0.f;
+    float s = 0.f, m = 0.f;
     for (int k0 = 0; k0 < chunks; k0 += 8) {  // eight loads in flight, added in chunk order
-      float v[8];
+      float v[8], w[8];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) v[k] = k0 + k < chunks ? partial[((size_t)n * chunks + k0 + k) * C + c] : 0.f;
+      for (int k = 0; k < 8; ++k) {
+        const size_t o = ((size_t)n * chunks + k0 + k) * C + c;
+        v[k] = k0 + k < chunks ? partial[o] : 0.f;
+        w[k] = (amax && k0 + k < chunks) ? pmax[o] : 0.f;
+      }
 #pragma unroll
-      for (int k = 0; k < 8; ++k)
+      for (int k = 0; k < 8; ++k) {
         if (k0 + k < chunks) s = __fadd_rn(s, v[k]);
+        m = fmaxf(m, w[k]);
+      }
     }
     pooled[c] = __fmul_rn(s, inv);
+    if (amax) xmax[c] = m;
   }
   __syncthreads();
   // z: each wave builds JW outputs at once, its lanes over c (c = lane, lane + 64, ... in
@@ -130,9 +158,10 @@ __global__ __launch_bounds__(GATE_THREADS) void se_gate_kernel(const float* __re
     }
   }
   __syncthreads();
-  // gate: each thread CW channels at once (c0, c0 + 256, ...), j in order, JU loads of w2t a
-  // channel issued before their FMAs.
+  // gate: each thread CW channels at once (c0, c0 + 1024, ...), j in order, JU loads of w2t
+  // a channel issued before their FMAs.
   constexpr int CW = 4, JU = 8;
+  float m = 0.f;
   for (int c0 = threadIdx.x; c0 < C; c0 += GATE_THREADS * CW) {
     float acc[CW];
 #pragma unroll
@@ -159,7 +188,22 @@ __global__ __launch_bounds__(GATE_THREADS) void se_gate_kernel(const float* __re
 #pragma unroll
     for (int u = 0; u < CW; ++u) {
       const int c = c0 + GATE_THREADS * u;
-      if (c < C) gate[(size_t)n * C + c] = sigmoid_f(acc[u]);
+      if (c < C) {
+        const float g = sigmoid_f(acc[u]);
+        gate[(size_t)n * C + c] = g;
+        if (amax) m = fmaxf(m, __fmul_rn(xmax[c], g));
+      }
+    }
+  }
+  if (amax) {  // uniform
+    m = wave_max(m);
+    if (lane == 0) wmax[wave] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float r = wmax[0];
+#pragma unroll
+      for (int w = 1; w < GATE_THREADS / 64; ++w) r = fmaxf(r, wmax[w]);
+      amax[n] = r;
     }
   }
 }
@@ -178,11 +222,17 @@ extern "C" {
 
 size_t bq_se_gate_ws_bytes(int64_t N, int64_t HW, int64_t C) {
   if (N < 0 || HW < 1 || C < 0) return 0;
-  return (size_t)N * se_chunks(HW, C) * C * sizeof(float);
+  return 2 * (size_t)N * se_chunks(HW, C) * C * sizeof(float);  // partial sums, then partial maxima
+}
+
+int64_t bq_se_gate_absmax_parts(int64_t N, int64_t C) {
+  if (N < 0 || C < 1) return set_error(BQ_ERR_ARG, "bq_se_gate_absmax_parts: bad sizes");
+  return N;
 }
 
 int bq_se_gate_nhwc(const float* x, int64_t N, int64_t HW, int64_t C, const float* w1, const float* b1, int64_t S,
-                    const float* w2t, const float* b2, float* gate, void* ws, size_t ws_bytes, bq_stream_t stream) {
+                    const float* w2t, const float* b2, float* gate, float* absmax_parts, void* ws, size_t ws_bytes,
+                    bq_stream_t stream) {
   const char* what = "bq_se_gate_nhwc";
   if (N < 0 || HW < 1 || C < 4 || S < 1) return set_error(BQ_ERR_ARG, "%s: bad sizes", what);
   if (C % 4) return set_error(BQ_ERR_UNSUPPORTED, "%s: C=%lld is not a multiple of 4", what, (long long)C);
@@ -192,16 +242,20 @@ int bq_se_gate_nhwc(const float* x, int64_t N, int64_t HW, int64_t C, const floa
   if (!x || !w1 || !w2t || !gate) return set_error(BQ_ERR_ARG, "%s: null pointer", what);
   if ((uintptr_t)x & 15) return set_error(BQ_ERR_ARG, "%s: x must be 16-byte aligned", what);
   const int chunks = se_chunks(HW, C);
-  const size_t need = (size_t)N * chunks * C * sizeof(float);
+  const size_t need = bq_se_gate_ws_bytes(N, HW, C);
   if (!ws || ws_bytes < need) return set_error(BQ_ERR_ARG, "%s: workspace %zu bytes, need %zu", what, ws_bytes, need);
   if ((uintptr_t)ws & 15) return set_error(BQ_ERR_ARG, "%s: workspace must be 16-byte aligned", what);
-  if ((C + S) * sizeof(float) > 64 * 1024) return set_error(BQ_ERR_UNSUPPORTED, "%s: C + S too large", what);
+  if ((2 * C + S) * sizeof(float) > 64 * 1024) return set_error(BQ_ERR_UNSUPPORTED, "%s: 2 C + S too large", what);
+  float* partial = (float*)ws;
+  float* pmax = partial + (size_t)N * chunks * C;
   hipStream_t st = (hipStream_t)stream;
   const int rows_per = (int)((HW + chunks - 1) / chunks);
-  se_partial_kernel<<<(unsigned)(N * chunks), SE_THREADS, 0, st>>>(x, (int)HW, (int)C, chunks, rows_per, (float*)ws);
+  se_partial_kernel<<<(unsigned)(N * chunks), SE_THREADS, 0, st>>>(x, (int)HW, (int)C, chunks, rows_per, partial,
+                                                                   absmax_parts ? pmax : nullptr);
   if (int r = check_launch(what)) return r;
-  se_gate_kernel<<<(unsigned)N, GATE_THREADS, (size_t)(C + S) * sizeof(float), st>>>(
-      (const float*)ws, chunks, (int)HW, (int)C, (int)S, w1, b1, w2t, b2, gate);
+  const size_t lds = (size_t)(C + S + (absmax_parts ? C : 0)) * sizeof(float);
+  se_gate_kernel<<<(unsigned)N, GATE_THREADS, lds, st>>>(partial, pmax, chunks, (int)HW, (int)C, (int)S, w1, b1, w2t,
+                                                         b2, gate, absmax_parts);
   return check_launch(what);
 }
 

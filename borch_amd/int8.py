@@ -148,7 +148,9 @@ def quantize_nhwc_chscale(x: torch.Tensor, cs: torch.Tensor, cpad: int | None = 
     """Per-tensor int8 of ``x * cs[:, :, None, None]`` (x NCHW f32, cs [N, C] f32: a
     squeeze-excite gate) into NHWC int8 ``[N, H, W, cpad]`` without storing the product
     (bq_quantize_nhwc_chscale): ``(q, s [1])``, the same bytes as quantizing the product.
-    With ``scale`` (a calibrated [1] tensor) one pass and that scale."""
+    With ``scale`` (a calibrated [1] tensor) one pass and that scale; else, when ``cs`` is
+    the gate ``se_gate_nhwc`` made from this same, unchanged ``x``, one pass with the maxima
+    it wrote; else two passes."""
     if x.dtype != torch.float32 or cs.dtype != torch.float32:
         raise TypeError("int8 path takes float32 activations and gates")
     require_device(x.device)
@@ -161,12 +163,17 @@ def quantize_nhwc_chscale(x: torch.Tensor, cs: torch.Tensor, cpad: int | None = 
     q = torch.empty((N, H, W, cpad), dtype=torch.int8, device=x.device)
     if scale is not None:
         check(lib().bq_quantize_nhwc_chscale(xl.data_ptr(), N, H * W, C, cpad, csc.data_ptr(), q.data_ptr(), None,
-                                             scale.data_ptr(), None, 0, _stream(x)))
+                                             scale.data_ptr(), None, 0, None, 0, _stream(x)))
         return q, scale
     s = torch.empty((1,), dtype=torch.float32, device=x.device)
+    made = getattr(cs, "_bq_product_absmax", None)
+    if made is not None and made[2] is x and made[3] == x._version and made[4] == cs._version and csc is cs:
+        check(lib().bq_quantize_nhwc_chscale(xl.data_ptr(), N, H * W, C, cpad, csc.data_ptr(), q.data_ptr(),
+                                             s.data_ptr(), None, made[0].data_ptr(), made[1], None, 0, _stream(x)))
+        return q, s
     ws = _ws(N * H * W * C, x.device)
     check(lib().bq_quantize_nhwc_chscale(xl.data_ptr(), N, H * W, C, cpad, csc.data_ptr(), q.data_ptr(),
-                                         s.data_ptr(), None, ws.data_ptr(), ws.numel(), _stream(x)))
+                                         s.data_ptr(), None, None, 0, ws.data_ptr(), ws.numel(), _stream(x)))
     return q, s
 
 
@@ -174,7 +181,9 @@ def se_gate_nhwc(x: torch.Tensor, w1: torch.Tensor, b1, w2: torch.Tensor, b2, w2
     """Squeeze-excite gates ``sigmoid(w2 · silu(w1 · mean_hw(x) + b1) + b2)`` in f32 for an
     NCHW activation (channels-last memory is read in place): ``[N, C]`` (bq_se_gate_nhwc;
     borch's CPU runner "se" node, runner.ts:256-268). ``w1 [S, C]``, ``w2 [C, S]``; ``w2t``
-    (optional) is ``w2`` already transposed to ``[S, C]`` contiguous, as the kernel reads it."""
+    (optional) is ``w2`` already transposed to ``[S, C]`` contiguous, as the kernel reads it.
+    The gate carries the partial maxima of ``|x * gate|`` the kernel also writes, for
+    ``quantize_nhwc_chscale`` of the same ``x`` (its dynamic scale without a max pass)."""
     if x.dtype != torch.float32:
         raise TypeError(f"squeeze-excite takes float32 activations, got {x.dtype}")
     require_device(x.device)
@@ -190,8 +199,14 @@ def se_gate_nhwc(x: torch.Tensor, w1: torch.Tensor, b1, w2: torch.Tensor, b2, w2
     gate = torch.empty((N, C), dtype=torch.float32, device=x.device)
     nb = int(lib().bq_se_gate_ws_bytes(N, H * W, C))
     ws = torch.empty((max(nb // 4, 4),), dtype=torch.float32, device=x.device)
+    nparts = int(lib().bq_se_gate_absmax_parts(N, C))
+    if nparts < 0:
+        check(nparts)
+    parts = torch.empty((max(nparts, 1),), dtype=torch.float32, device=x.device)
     check(lib().bq_se_gate_nhwc(xl.data_ptr(), N, H * W, C, w1c.data_ptr(), _ptr(b1c), S, w2c.data_ptr(), _ptr(b2c),
-                                gate.data_ptr(), ws.data_ptr(), ws.numel() * 4, _stream(x)))
+                                gate.data_ptr(), parts.data_ptr(), ws.data_ptr(), ws.numel() * 4, _stream(x)))
+    if xl is x:  # the maxima describe x itself (a channels-last x is read in place)
+        gate._bq_product_absmax = (parts, nparts, x, x._version, gate._version)
     return gate
 
 

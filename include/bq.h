@@ -99,12 +99,14 @@ int bq_quantize_nhwc_parts(const float* x, int64_t P, int64_t C, int64_t Cpad, c
  * is fl(x[n, p, c] * cs[n, c]) (one f32 multiply, never stored), x f32 [N*HW, C]
  * channels-last, cs f32 [N, C] (a squeeze-excite's sigmoid gates), into q int8
  * [N*HW, Cpad] (channels C..Cpad-1 zero). The scale is s_given[0] when s_given is non-null
- * (calibrated; one pass), else float32(max|fl(x*cs)| / 127) into s[0] (two passes, partial
- * maxima in ws, bq_quantize_tensor_ws_bytes(N*HW*C) bytes). The same bytes as quantizing
- * the stored product. C and Cpad multiples of 4; x, cs 16-byte aligned. */
+ * (calibrated; one pass), else float32(max|fl(x*cs)| / 127) into s[0]: from absmax_parts
+ * f32 [nparts] whose maximum is max|fl(x*cs)| when given (one pass; bq_se_gate_nhwc writes
+ * them), else two passes with partial maxima in ws (bq_quantize_tensor_ws_bytes(N*HW*C)
+ * bytes). The same bytes as quantizing the stored product. C and Cpad multiples of 4; x, cs
+ * 16-byte aligned. */
 int bq_quantize_nhwc_chscale(const float* x, int64_t N, int64_t HW, int64_t C, int64_t Cpad, const float* cs,
-                             int8_t* q, float* s, const float* s_given, void* ws, size_t ws_bytes,
-                             bq_stream_t stream);
+                             int8_t* q, float* s, const float* s_given, const float* absmax_parts, int64_t nparts,
+                             void* ws, size_t ws_bytes, bq_stream_t stream);
 
 /* The same quantization with a given (calibrated) scale s f32 [1]: one pass, no maximum.
  * The static-scale input of borch-ts (int8.inMax, tensor.ts:11912-11913; calibrateInt8
@@ -201,17 +203,25 @@ int bq_dwconv_i8_nhwc(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t 
                       const float* sA, const float* sW, const float* bias, int act,
                       float* out, int32_t* acc, bq_stream_t stream);
 
-/* Bytes of `ws` bq_se_gate_nhwc needs (the per-chunk partial sums). */
+/* Workspace bytes of bq_se_gate_nhwc for this size (per-chunk partial sums and maxima). */
 size_t bq_se_gate_ws_bytes(int64_t N, int64_t HW, int64_t C);
+
+/* The number of floats bq_se_gate_nhwc writes to a non-null `absmax_parts` (one per image). */
+int64_t bq_se_gate_absmax_parts(int64_t N, int64_t C);
 
 /* Squeeze-excite gates in f32 of a channels-last activation x f32 [N, HW, C] (C % 4 == 0):
  *   pooled = mean over HW (sum in a fixed order, then * f32(1/HW)),
  *   z = silu(w1 [S, C] . pooled + b1),  gate f32 [N, C] = sigmoid(w2 . z + b2)
- * with the expand weight w2 [C, S] passed transposed as w2t [S, C] (b1, b2 nullable). The gate is then folded into the next conv's input quantization
- * (bq_quantize_nhwc_chscale). Replaces the CPU runner's "se" node (meanRows, gemmBiasAct
- * swish and sigmoid; borch-ts/src/cpu/runner.ts:256-268, wasm/src/lib.rs:222-244). */
+ * with the expand weight w2 [C, S] passed transposed as w2t [S, C] (b1, b2 nullable). The
+ * gate is then folded into the next conv's input quantization (bq_quantize_nhwc_chscale).
+ * absmax_parts (nullable, bq_se_gate_absmax_parts floats) receives partial maxima of
+ * |fl(x * gate)| (exact: the gate is positive and rounding monotonic, so per image and
+ * channel it is fl(max|x| * gate)), the dynamic scale of that quantization without a pass
+ * over x. Replaces the CPU runner's "se" node (meanRows, gemmBiasAct swish and sigmoid;
+ * borch-ts/src/cpu/runner.ts:256-268, wasm/src/lib.rs:222-244). */
 int bq_se_gate_nhwc(const float* x, int64_t N, int64_t HW, int64_t C, const float* w1, const float* b1, int64_t S,
-                    const float* w2t, const float* b2, float* gate, void* ws, size_t ws_bytes, bq_stream_t stream);
+                    const float* w2t, const float* b2, float* gate, float* absmax_parts, void* ws, size_t ws_bytes,
+                    bq_stream_t stream);
 
 /* Weight-only int8 (W8A32) GEMV for the decode shape, M <= 8: f32 x [M, K] against int8
  * W [N, K] with per-channel sW [N]; out f32 [M, N] = sum_k x * f32(f32(q) * sW[n]) (f32 FMA

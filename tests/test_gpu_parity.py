@@ -126,6 +126,32 @@ def test_se_gate(dev, N, C, H, S):
     assert torch.equal(g, I.se_gate_nhwc(xt, t(w1, dev), t(b1, dev), t(w2, dev), t(b2, dev)))
 
 
+@pytest.mark.parametrize("N,C,H,S,cpad", [(64, 32, 112, 8, 32), (8, 144, 56, 6, 144), (4, 1152, 7, 48, 1152),
+                                         (3, 1200, 5, 50, 1216), (2, 36, 9, 9, 48)])
+def test_se_gate_maxima_give_the_product_scale(dev, N, C, H, S, cpad):
+    """The partial maxima the squeeze-excite writes (max over pixels of |x| times the gate,
+    per channel) give quantize_nhwc_chscale the same scale and bytes in one pass as its two
+    passes over x * gate and as quantizing the stored product; an x changed in place after
+    the gate falls back to the two passes."""
+    say(f"se_gate maxima N={N} C={C} H={H} S={S}")
+    rng = np.random.default_rng(N * C + H + S)
+    xt = t(rng.normal(size=(N, C, H, H)).astype(np.float32), dev).contiguous(memory_format=torch.channels_last)
+    w1 = t((rng.normal(size=(S, C)) / np.sqrt(C)).astype(np.float32), dev)
+    w2 = t((rng.normal(size=(C, S)) / np.sqrt(S)).astype(np.float32), dev)
+    b1, b2 = t(rng.normal(size=S).astype(np.float32), dev), t(rng.normal(size=C).astype(np.float32), dev)
+    g = I.se_gate_nhwc(xt, w1, b1, w2, b2)
+    assert getattr(g, "_bq_product_absmax", None) is not None
+    q1, s1 = I.quantize_nhwc_chscale(xt, g, cpad)  # one pass, the gate's maxima
+    q2, s2 = I.quantize_nhwc_chscale(xt, g.clone(), cpad)  # two passes
+    prod = (xt * g[:, :, None, None]).contiguous(memory_format=torch.channels_last)
+    q3, s3 = I.quantize_nhwc(prod, cpad)
+    assert torch.equal(s1, s2) and torch.equal(s1, s3)
+    assert torch.equal(q1, q2) and torch.equal(q1, q3)
+    xt.mul_(2.0)  # in place: the maxima no longer describe x
+    q4, s4 = I.quantize_nhwc_chscale(xt, g, cpad)
+    assert torch.equal(s4, s1 * 2) and torch.equal(q4, q1)
+
+
 def test_quantize_tensor(dev):
     say("quantize_tensor")
     rng = np.random.default_rng(11)
