@@ -525,7 +525,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
           } else if (p.act == BQ_ACT_GELU) {
             o = gelu4(o);
           }
-          *reinterpret_cast<float4*>(p.out + idx) = o;
+          if (p.out) *reinterpret_cast<float4*>(p.out + idx) = o;  // null: the twin alone
           if (p.acc) *reinterpret_cast<int4*>(p.acc + idx) = a;
           if (p.q_out)
             *reinterpret_cast<uint32_t*>(p.q_out + idx) =
@@ -567,7 +567,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
             const size_t idx = (size_t)m * p.N + n + q;
             const float rv = has_r ? p.res[idx] : 0.f;
             const float o = dequant_one(a, s_sa[mloc], s_sw[ncol + q], s_b[ncol + q], true, rv, has_r, p.act);
-            p.out[idx] = o;
+            if (p.out) p.out[idx] = o;
             if (p.acc) p.acc[idx] = a;
             if (p.q_out) p.q_out[idx] = (int8_t)qz_out(o);
             amax = fmaxf(amax, fabsf(o));
@@ -1241,7 +1241,7 @@ static int conv_impl(const char* what, const int8_t* x, int64_t N, int64_t H, in
     return set_error(BQ_ERR_UNSUPPORTED, "%s: KH*KW*C=%lld > %d: int32 accumulators could overflow", what,
                      (long long)K, KMAX_EXACT);
   if (M == 0) return BQ_OK;
-  if (!x || !w || !sA || !sW || !out) return set_error(BQ_ERR_ARG, "%s: null pointer", what);
+  if (!x || !w || !sA || !sW || (!out && !q_out)) return set_error(BQ_ERR_ARG, "%s: null pointer", what);
   if (!aligned16(x) || !aligned16(w)) return set_error(BQ_ERR_ARG, "%s: x and w must be 16-byte aligned", what);
   if (act < BQ_ACT_NONE || act > BQ_ACT_GELU) return set_error(BQ_ERR_ARG, "%s: bad activation %d", what, act);
   GemmP p{};

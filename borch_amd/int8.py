@@ -402,9 +402,11 @@ def _absmax_parts(N, H, W, C, wq, stride, pad, device):
     return torch.empty((max(n, 1),), dtype=torch.float32, device=device), max(n, 1)
 
 
-def conv2d_i8_nhwc_q(qx, sa, wq: Int8ConvWeight, s_out, stride=1, pad=0, bias=None, residual=None, act=ACT_NONE):
+def conv2d_i8_nhwc_q(qx, sa, wq: Int8ConvWeight, s_out, stride=1, pad=0, bias=None, residual=None, act=ACT_NONE,
+                     f32_out=True):
     """``conv2d_i8_nhwc`` that also returns the output's int8 twin ``[N, OH, OW, O]``
-    quantized with the calibrated scale ``s_out [1]`` (bq_conv2d_i8_nhwc_q; O % 16 == 0)."""
+    quantized with the calibrated scale ``s_out [1]`` (bq_conv2d_i8_nhwc_q; O % 16 == 0).
+    ``f32_out=False``: the twin alone is written and returned as ``(None, q)``."""
     _need(qx, "x", torch.int8)
     N, H, W, C = qx.shape
     if C != wq.cpad:
@@ -413,7 +415,8 @@ def conv2d_i8_nhwc_q(qx, sa, wq: Int8ConvWeight, s_out, stride=1, pad=0, bias=No
     OW = (W + 2 * pad - wq.KW) // stride + 1
     if OH < 1 or OW < 1:
         raise RuntimeError("the filter is larger than the input.")
-    out = torch.empty((N, wq.O, OH, OW), dtype=torch.float32, device=qx.device, memory_format=torch.channels_last)
+    out = (torch.empty((N, wq.O, OH, OW), dtype=torch.float32, device=qx.device, memory_format=torch.channels_last)
+           if f32_out else None)
     q = torch.empty((N, OH, OW, wq.O), dtype=torch.int8, device=qx.device)
     res = None
     if residual is not None:
@@ -424,7 +427,7 @@ def conv2d_i8_nhwc_q(qx, sa, wq: Int8ConvWeight, s_out, stride=1, pad=0, bias=No
     # no per-tile maxima: a calibrated layer's consumer takes the twin or its own static scale
     check(lib().bq_conv2d_i8_nhwc_q(qx.contiguous().data_ptr(), N, H, W, C, wq.q.data_ptr(), wq.O, wq.KH, wq.KW,
                                     stride, pad, sa.data_ptr(), wq.s.data_ptr(), _ptr(b), _ptr(res), act,
-                                    out.data_ptr(), None, s_out.data_ptr(), q.data_ptr(), None,
+                                    _ptr(out), None, s_out.data_ptr(), q.data_ptr(), None,
                                     *_ws_args(qx.device), _stream(qx)))
     return out, q
 

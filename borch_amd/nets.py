@@ -179,12 +179,21 @@ class MBConv(tnn.Module):
     def _se(self, h):
         return h * self._se_gate(h)[:, :, None, None]
 
+    # With calibrated scales the depthwise conv reads the expand conv's int8 twin, so the
+    # expand conv writes that twin alone (no f32 output: 866 MB a B0 b64 forward).
+    twin_path = True
+
     def forward(self, x):
         if self.fused:
             # the gate multiplies the projection's input inside its int8 quantization
             # (f32: a plain product): the gated tensor is never stored
-            h = self.expand(x) if self.expand is not None else x
-            h = self.dw(h)
+            ex = self.expand.conv if self.expand is not None else None
+            dw = self.dw.conv
+            if self.twin_path and ex is not None and ex.twin_only() and dw.takes_twin_of(ex):
+                h = dw.forward_int8(*ex.twin_forward(x))
+            else:
+                h = self.expand(x) if self.expand is not None else x
+                h = self.dw(h)
             g = self._se_gate(h)
             return self.project(h, x, channel_scale=g) if self.residual else self.project(h, channel_scale=g)
         h = torch.nn.functional.silu(self.bn0(self.expand(x))) if self.has_expand else x

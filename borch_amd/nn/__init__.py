@@ -225,32 +225,64 @@ class Conv2d(_tnn.Module):
                                                                    torch.maximum(self._calib[1], cout)]
             return out
         if self.int8 is not None:
-            stride, pad = self._geometry()
             if x.dim() != 4 or x.shape[1] != self.in_channels:
                 raise RuntimeError(f"channels do not match: input {x.shape[1] if x.dim() > 1 else x.shape}, "
                                    f"filter {self.in_channels}")
             qx, sa = self._int8_input(x, channel_scale)
-            if isinstance(self.int8, _i8.Int8DwWeight):
-                out = _i8.dwconv_i8_nhwc(qx, sa, self.int8, stride, pad, self.bias,
-                                         self.act if residual is None else _i8.ACT_NONE)
-                if self.int8.cpad != self.int8.C:
-                    out = out[:, : self.int8.C]
-                if residual is not None:
-                    out = out + residual
-                    if self.act == _i8.ACT_RELU:
-                        out = torch.relu(out)
-                return out
-            if self.out_scale is not None and self.int8.O % 16 == 0:
-                out, q = _i8.conv2d_i8_nhwc_q(qx, sa, self.int8, self.out_scale, stride, pad, self.bias, residual,
-                                              self.act)
-                out._int8_twin = (q, self.out_scale, self.out_scale_v, out._version)
-                return out
-            return _i8.conv2d_i8_nhwc(qx, sa, self.int8, stride, pad, self.bias, residual, self.act)
+            return self.forward_int8(qx, sa, residual)
         out = functional._f32_conv2d(x, self.weight, self.bias, self.stride, self.padding, self.dilation,
                                      self.groups, self.padding_mode)
         if residual is not None:
             out = out + residual
         return _i8._act_f32(out, self.act)
+
+    def twin_only(self) -> bool:
+        """Whether ``twin_forward`` applies: int8, calibrated output scale, O % 16 == 0."""
+        return (self.int8 is not None and not _CALIBRATING and self.out_scale is not None
+                and isinstance(self.int8, _i8.Int8ConvWeight) and self.int8.O % 16 == 0)
+
+    def takes_twin_of(self, producer) -> bool:
+        """Whether this layer reads ``producer``'s int8 twin as its input as it stands
+        (int8, its calibrated input scale is the producer's output scale, same channels)."""
+        return (self.int8 is not None and not _CALIBRATING and self.in_scale is not None
+                and producer.out_scale is not None and self.in_scale_v == producer.out_scale_v
+                and self.int8.cpad == producer.out_channels)
+
+    def twin_forward(self, x, residual=None):
+        """``self(x, residual)`` as its int8 twin alone, ``(q [N, OH, OW, O], out_scale)``, the
+        f32 output never written: for a consumer that reads only the twin (``forward_int8``
+        of a layer that ``takes_twin_of`` this one). Requires ``twin_only()``."""
+        if not self.twin_only():
+            raise RuntimeError("twin_forward needs an int8 layer with a calibrated output scale and O % 16 == 0")
+        if x.dim() != 4 or x.shape[1] != self.in_channels:
+            raise RuntimeError(f"channels do not match: input {x.shape[1] if x.dim() > 1 else x.shape}, "
+                               f"filter {self.in_channels}")
+        qx, sa = self._int8_input(x)
+        stride, pad = self._geometry()
+        _, q = _i8.conv2d_i8_nhwc_q(qx, sa, self.int8, self.out_scale, stride, pad, self.bias, residual, self.act,
+                                    f32_out=False)
+        return q, self.out_scale
+
+    def forward_int8(self, qx, sa, residual=None):
+        """The int8 layer on an already quantized NHWC input ``qx [N, H, W, cpad]`` with its
+        per-tensor scale ``sa [1]``: the conv (or depthwise) kernel and its epilogue."""
+        stride, pad = self._geometry()
+        if isinstance(self.int8, _i8.Int8DwWeight):
+            out = _i8.dwconv_i8_nhwc(qx, sa, self.int8, stride, pad, self.bias,
+                                     self.act if residual is None else _i8.ACT_NONE)
+            if self.int8.cpad != self.int8.C:
+                out = out[:, : self.int8.C]
+            if residual is not None:
+                out = out + residual
+                if self.act == _i8.ACT_RELU:
+                    out = torch.relu(out)
+            return out
+        if self.out_scale is not None and self.int8.O % 16 == 0:
+            out, q = _i8.conv2d_i8_nhwc_q(qx, sa, self.int8, self.out_scale, stride, pad, self.bias, residual,
+                                          self.act)
+            out._int8_twin = (q, self.out_scale, self.out_scale_v, out._version)
+            return out
+        return _i8.conv2d_i8_nhwc(qx, sa, self.int8, stride, pad, self.bias, residual, self.act)
 
     def extra_repr(self):
         s = (f"{self.in_channels}, {self.out_channels}, kernel_size={self.kernel_size}, "

@@ -184,7 +184,8 @@ int bq_plan_clear(void);
 /* bq_conv2d_i8_nhwc that also writes the output's int8 twin with a calibrated scale:
  * q_out int8 [N, OH, OW, O] = clip(rint(y / s_out[0]), +-127) (exact quotient, half to even) of the final f32 y
  * (after residual and activation), the next conv's input with no quantize pass.
- * O % 16 == 0 (the twin is then the next layer's padded NHWC layout). Replaces the
+ * O % 16 == 0 (the twin is then the next layer's padded NHWC layout). `out` may be NULL
+ * here: the twin alone is written (a consumer that reads nothing else). Replaces the
  * quantOut store of convForwardInt8 / sumSplitsConv (borch-ts/src/kernels.ts:2177-2190,
  * 5866-5898) and the Int8Twin hand-off (tensor.ts:11909-11910, 11954-11955). */
 int bq_conv2d_i8_nhwc_q(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t C, const int8_t* w,

@@ -323,3 +323,39 @@ def test_tuned_compiled_matches_untuned(dev):
             assert np.array_equal(n(c1(xt)), ref), name  # a replay, with the plans in force
     finally:
         T.clear_plans()
+
+
+def test_c4_efficientnet_b0_static_twin_only(dev):
+    """EfficientNet-B0 with calibrated scales: each MBConv's expand conv writes its int8
+    twin alone (no f32 output) and the depthwise conv reads it. The forward equals the one
+    that writes and passes the f32 expand output (whose depthwise conv took the same twin),
+    bit for bit, eagerly and as a HIP-graph replay."""
+    say("C4 EfficientNet-B0 b2 at 128^2, calibrated: twin-only expand outputs")
+    model = nets.build("efficientnet_b0", seed=5, device=dev)
+    bt.compiled(model, int8=True, graph=False, fuse=False, tune=False)
+    calib = [torch.from_numpy(WL.c4_input(2, s, side=128)).to(dev) for s in (21, 22)]
+    bt.calibrate_int8(model, calib)
+    x = torch.from_numpy(WL.c4_input(2, 23, side=128)).to(dev)
+    twin_only = {"n": 0}
+    real = I.conv2d_i8_nhwc_q
+
+    def counting(*a, **k):
+        twin_only["n"] += k.get("f32_out", True) is False
+        return real(*a, **k)
+    I.conv2d_i8_nhwc_q = counting
+    try:
+        with torch.no_grad():
+            y_twin = n(model(x))
+    finally:
+        I.conv2d_i8_nhwc_q = real
+    assert twin_only["n"] == 15, twin_only  # every MBConv with an expand conv (blocks 1-15)
+    nets.MBConv.twin_path = False
+    try:
+        with torch.no_grad():
+            y_f32 = n(model(x))
+    finally:
+        nets.MBConv.twin_path = True
+    assert np.array_equal(y_twin, y_f32)
+    c = bt.compiled(model, int8=False, graph=True, fuse=False, tune=False)
+    for _ in range(2):
+        assert np.array_equal(n(c(x)), y_twin)
