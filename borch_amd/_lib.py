@@ -36,6 +36,9 @@ SIGNATURES = {
     "bq_last_error": (ctypes.c_char_p, []),
     "bq_device_ok": (_c_int, [_c_int]),
     "bq_quantize_rows": (_c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_p]),
+    "bq_quantize_rows_act": (_c_int, [_c_p, _c_i64, _c_i64, _c_int, _c_p, _c_p, _c_p, _c_p]),
+    "bq_layernorm_quantize_rows": (_c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_p, ctypes.c_float, _c_p, _c_p, _c_p,
+                                            _c_p]),
     "bq_quantize_weight_per_channel": (_c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_p]),
     "bq_quantize_tensor_ws_bytes": (_c_size, [_c_i64]),
     "bq_quantize_tensor": (_c_int, [_c_p, _c_i64, _c_p, _c_p, _c_p, _c_size, _c_p]),

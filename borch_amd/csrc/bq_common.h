@@ -52,6 +52,21 @@ __device__ __forceinline__ float wave_max(float v) {
   return fmaxf(fmaxf(a, b), fmaxf(c, d));
 }
 
+// Wave64 sum in a fixed order (deterministic), every lane active: the same DPP butterfly
+// within rows of 16 (each lane of a row ends with the row's sum), then
+// (row0 + row1) + (row2 + row3) from lanes 0, 16, 32, 48.
+__device__ __forceinline__ float wave_sum_fixed(float v) {
+  v = __fadd_rn(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false)));
+  v = __fadd_rn(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false)));
+  v = __fadd_rn(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false)));
+  v = __fadd_rn(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false)));
+  const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return __fadd_rn(__fadd_rn(a, b), __fadd_rn(c, d));
+}
+
 // The scale rule: float32(peak / 127), correctly rounded (HIP's f32 division is the IEEE
 // correctly rounded one; __fdiv_rn makes that explicit).
 __device__ __forceinline__ float scale_of(float peak) { return __fdiv_rn(peak, 127.0f); }
@@ -147,6 +162,21 @@ __device__ __attribute__((noinline)) float gelu(float v) {
 
 __device__ __attribute__((noinline)) float4 gelu4(float4 v) {
   return make_float4(gelu(v.x), gelu(v.y), gelu(v.z), gelu(v.w));
+}
+
+// The same GELU inline, for a kernel whose whole job is the per-element work (the
+// activation-then-quantize pass): the same operations, so the same bits as gelu().
+__device__ __forceinline__ float gelu_inline(float v) {
+  return __fmul_rn(__fmul_rn(v, 0.5f), __fadd_rn(1.0f, erff(__fmul_rn(v, 0.70710678118654752f))));
+}
+
+// act (uniform across the launch) applied to four values; BQ_ACT_NONE leaves them.
+__device__ __forceinline__ float4 activate4_inline(float4 v, int act) {
+  if (act == BQ_ACT_GELU) return make_float4(gelu_inline(v.x), gelu_inline(v.y), gelu_inline(v.z), gelu_inline(v.w));
+  if (act == BQ_ACT_SILU) return make_float4(silu(v.x), silu(v.y), silu(v.z), silu(v.w));
+  if (act == BQ_ACT_RELU)
+    return make_float4(v.x > 0.f ? v.x : 0.f, v.y > 0.f ? v.y : 0.f, v.z > 0.f ? v.z : 0.f, v.w > 0.f ? v.w : 0.f);
+  return v;
 }
 
 __device__ __forceinline__ float activate(float v, int act) {

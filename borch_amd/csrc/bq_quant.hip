@@ -43,10 +43,13 @@ __device__ __forceinline__ float block_max(float v, float* red) {
 }
 
 // NV float4 per thread kept in registers (K <= NV * 1024); NV == 0: any K, two reads.
-template <int NV>
+// ACT: the activation applied to x first (BQ_ACT_*; compile-time in the vector kernels,
+// run time in the scalar one, NV == 0).
+template <int NV, int ACT>
 __global__ __launch_bounds__(QR_THREADS) void quantize_rows_kernel(const float* __restrict__ x,
                                                                   int K, int8_t* __restrict__ q,
-                                                                  float* __restrict__ s) {
+                                                                  float* __restrict__ s, int act,
+                                                                  float* __restrict__ y_out) {
   __shared__ float red[QR_THREADS / 64];
   const size_t row = blockIdx.x;
   const float* xr = x + row * (size_t)K;
@@ -59,7 +62,8 @@ __global__ __launch_bounds__(QR_THREADS) void quantize_rows_kernel(const float* 
     for (int i = 0; i < NV; ++i) {
       const int k = (t + i * QR_THREADS) * 4;
       if (k < K) {
-        v[i] = *reinterpret_cast<const float4*>(xr + k);
+        v[i] = activate4_inline(*reinterpret_cast<const float4*>(xr + k), ACT);
+        if (ACT != BQ_ACT_NONE && y_out) *reinterpret_cast<float4*>(y_out + row * (size_t)K + k) = v[i];
         m = fmaxf(m, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
       } else {
         v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -76,11 +80,15 @@ __global__ __launch_bounds__(QR_THREADS) void quantize_rows_kernel(const float* 
     }
   } else {
     float m = 0.f;
-    for (int k = t; k < K; k += QR_THREADS) m = fmaxf(m, fabsf(xr[k]));
+    for (int k = t; k < K; k += QR_THREADS) {
+      const float a = activate(xr[k], act);
+      if (act != BQ_ACT_NONE && y_out) y_out[row * (size_t)K + k] = a;
+      m = fmaxf(m, fabsf(a));
+    }
     const float sc = scale_of(block_max(m, red));
     if (t == 0) s[row] = sc;
     const Quantizer qz(sc);
-    for (int k = t; k < K; k += QR_THREADS) qr[k] = (int8_t)qz(xr[k]);
+    for (int k = t; k < K; k += QR_THREADS) qr[k] = (int8_t)qz(activate(xr[k], act));
   }
 }
 
@@ -90,10 +98,11 @@ __global__ __launch_bounds__(QR_THREADS) void quantize_rows_kernel(const float* 
 // LDS, no barrier). The same max, scale and rounding as the block-per-row kernel.
 constexpr int QW_WAVES = 4;
 
-template <int NV>
+template <int NV, int ACT>
 __global__ __launch_bounds__(QW_WAVES * 64) void quantize_rows_wave_kernel(const float* __restrict__ x, int M,
                                                                           int K, int8_t* __restrict__ q,
-                                                                          float* __restrict__ s) {
+                                                                          float* __restrict__ s,
+                                                                          float* __restrict__ y_out) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * QW_WAVES + (threadIdx.x >> 6);
   if (row >= M) return;
@@ -107,11 +116,82 @@ __global__ __launch_bounds__(QW_WAVES * 64) void quantize_rows_wave_kernel(const
   }
   float m = 0.f;
 #pragma unroll
-  for (int i = 0; i < NV; ++i)
+  for (int i = 0; i < NV; ++i) {
+    if (ACT != BQ_ACT_NONE && (lane + i * 64) * 4 < K) {
+      v[i] = activate4_inline(v[i], ACT);
+      if (y_out) *reinterpret_cast<float4*>(y_out + (size_t)row * K + (lane + i * 64) * 4) = v[i];
+    }
     m = fmaxf(m, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+  }
   const float sc = scale_of(wave_max(m));  // the whole wave is here: rows are per wave
   if (lane == 0) s[row] = sc;
   const Quantizer qz(sc);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int k = (lane + i * 64) * 4;
+    if (k < K) *reinterpret_cast<uint32_t*>(qr + k) = qz.pack(v[i]);
+  }
+}
+
+// LayerNorm over each row, then the per-row quantization of the result, in one pass: the
+// normalised row is never stored (unless y is given). The reference's layerNormRows
+// (borch-ts/src/kernels.ts:2935-2986): mean = sum / K, var = sum((x - mean)^2) / K (biased,
+// centred in a second pass over the row), rstd = 1 / sqrt(var + eps), y = ((x - mean) *
+// rstd) * gamma + beta, one f32 rounding per operation; here the row stays in registers
+// (one wave a row, four rows a block) and both sums are fixed-order wave reductions. Then
+// max |y|, the scale rule and the quantizer of quantize_rows_kernel.
+template <int NV>
+__global__ __launch_bounds__(QW_WAVES * 64) void ln_quantize_rows_kernel(const float* __restrict__ x, int M, int K,
+                                                                        const float* __restrict__ gamma,
+                                                                        const float* __restrict__ beta, float eps,
+                                                                        int8_t* __restrict__ q, float* __restrict__ s,
+                                                                        float* __restrict__ y_out) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * QW_WAVES + (threadIdx.x >> 6);
+  if (row >= M) return;  // whole waves
+  const float* xr = x + (size_t)row * K;
+  float4 v[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int k = (lane + i * 64) * 4;
+    v[i] = k < K ? *reinterpret_cast<const float4*>(xr + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+    sum = __fadd_rn(__fadd_rn(sum, __fadd_rn(v[i].x, v[i].y)), __fadd_rn(v[i].z, v[i].w));
+  const float mean = __fdiv_rn(wave_sum_fixed(sum), (float)K);
+  float sq = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    if ((lane + i * 64) * 4 < K) {  // the padding lanes hold zeros, not centred values
+      const float a = __fsub_rn(v[i].x, mean), b = __fsub_rn(v[i].y, mean);
+      const float c = __fsub_rn(v[i].z, mean), d = __fsub_rn(v[i].w, mean);
+      sq = __fadd_rn(sq, __fadd_rn(__fadd_rn(__fmul_rn(a, a), __fmul_rn(b, b)),
+                                   __fadd_rn(__fmul_rn(c, c), __fmul_rn(d, d))));
+    }
+  }
+  const float var = __fdiv_rn(wave_sum_fixed(sq), (float)K);
+  const float rstd = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(var, eps)));
+  float m = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int k = (lane + i * 64) * 4;
+    if (k < K) {
+      const float4 g = gamma ? *reinterpret_cast<const float4*>(gamma + k) : make_float4(1.f, 1.f, 1.f, 1.f);
+      const float4 b = beta ? *reinterpret_cast<const float4*>(beta + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+      v[i].x = __fadd_rn(__fmul_rn(__fmul_rn(__fsub_rn(v[i].x, mean), rstd), g.x), b.x);
+      v[i].y = __fadd_rn(__fmul_rn(__fmul_rn(__fsub_rn(v[i].y, mean), rstd), g.y), b.y);
+      v[i].z = __fadd_rn(__fmul_rn(__fmul_rn(__fsub_rn(v[i].z, mean), rstd), g.z), b.z);
+      v[i].w = __fadd_rn(__fmul_rn(__fmul_rn(__fsub_rn(v[i].w, mean), rstd), g.w), b.w);
+      m = fmaxf(m, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+      if (y_out) *reinterpret_cast<float4*>(y_out + (size_t)row * K + k) = v[i];
+    }
+  }
+  const float sc = scale_of(wave_max(m));
+  if (lane == 0) s[row] = sc;
+  const Quantizer qz(sc);
+  int8_t* qr = q + (size_t)row * K;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int k = (lane + i * 64) * 4;
@@ -321,38 +401,48 @@ static int nparts_for(int64_t n) {
 }
 
 static int launch_rows(const float* x, int64_t M, int64_t K, int8_t* q, float* s, hipStream_t st,
-                       const char* what) {
+                       const char* what, int act = BQ_ACT_NONE, float* y = nullptr) {
   if (M < 0 || K < 0) return set_error(BQ_ERR_ARG, "%s: negative size (%lld x %lld)", what, (long long)M, (long long)K);
   if (M == 0) return BQ_OK;
   if (!x || !q || !s) return set_error(BQ_ERR_ARG, "%s: null pointer", what);
   if (M > 0x7fffffff || K > 0x7fffffff) return set_error(BQ_ERR_ARG, "%s: size too large", what);
-  const bool vec = (K % 4 == 0) && (((uintptr_t)x | (uintptr_t)q) & 15) == 0;
+  if (act < BQ_ACT_NONE || act > BQ_ACT_GELU) return set_error(BQ_ERR_ARG, "%s: bad activation %d", what, act);
+  const bool vec = (K % 4 == 0) && (((uintptr_t)x | (uintptr_t)q | (uintptr_t)y) & 15) == 0;
+  // the vector kernels are built plain and with GELU (a transformer MLP's second input);
+  // ReLU / SiLU inputs take the scalar kernel
+  const bool vact = act == BQ_ACT_NONE || act == BQ_ACT_GELU;
   // Short rows in numbers: one wave a row (at 6304 x 768, 8.1 -> 7.0 us). Longer rows keep
   // a block a row: a single wave then does a whole row's quantize arithmetic alone (6304 x
   // 3072: 20.5 -> 22.2 us; one row of 4096: 3.4 -> 6.2 us as one wave).
-  const int nw = vec && K > 0 ? (int)((K + 255) / 256) : 0;  // float4 a lane
+  const int nw = vec && vact && K > 0 ? (int)((K + 255) / 256) : 0;  // float4 a lane
   if (nw > 0 && nw <= 4 && M >= 1024) {
     dim3 g((unsigned)((M + QW_WAVES - 1) / QW_WAVES)), b(QW_WAVES * 64);
+    auto wave = [&](auto k0, auto kg) {
+      (act == BQ_ACT_GELU ? kg : k0)<<<g, b, 0, st>>>(x, (int)M, (int)K, q, s, y);
+    };
     switch (nw) {
-      case 1: quantize_rows_wave_kernel<1><<<g, b, 0, st>>>(x, (int)M, (int)K, q, s); break;
-      case 2: quantize_rows_wave_kernel<2><<<g, b, 0, st>>>(x, (int)M, (int)K, q, s); break;
-      case 3: quantize_rows_wave_kernel<3><<<g, b, 0, st>>>(x, (int)M, (int)K, q, s); break;
-      default: quantize_rows_wave_kernel<4><<<g, b, 0, st>>>(x, (int)M, (int)K, q, s); break;
+      case 1: wave(quantize_rows_wave_kernel<1, 0>, quantize_rows_wave_kernel<1, BQ_ACT_GELU>); break;
+      case 2: wave(quantize_rows_wave_kernel<2, 0>, quantize_rows_wave_kernel<2, BQ_ACT_GELU>); break;
+      case 3: wave(quantize_rows_wave_kernel<3, 0>, quantize_rows_wave_kernel<3, BQ_ACT_GELU>); break;
+      default: wave(quantize_rows_wave_kernel<4, 0>, quantize_rows_wave_kernel<4, BQ_ACT_GELU>); break;
     }
     return check_launch(what);
   }
-  const int nv = vec ? (int)((K + 1023) / 1024) : 0;
+  const int nv = vec && vact ? (int)((K + 1023) / 1024) : 0;
   dim3 grid((unsigned)M), block(QR_THREADS);
-  switch (vec ? nv : 0) {
-    case 1: quantize_rows_kernel<1><<<grid, block, 0, st>>>(x, (int)K, q, s); break;
-    case 2: quantize_rows_kernel<2><<<grid, block, 0, st>>>(x, (int)K, q, s); break;
-    case 3: quantize_rows_kernel<3><<<grid, block, 0, st>>>(x, (int)K, q, s); break;
-    case 4: quantize_rows_kernel<4><<<grid, block, 0, st>>>(x, (int)K, q, s); break;
+  auto blk = [&](auto k0, auto kg) {
+    (act == BQ_ACT_GELU ? kg : k0)<<<grid, block, 0, st>>>(x, (int)K, q, s, act, y);
+  };
+  switch (nv) {
+    case 1: blk(quantize_rows_kernel<1, 0>, quantize_rows_kernel<1, BQ_ACT_GELU>); break;
+    case 2: blk(quantize_rows_kernel<2, 0>, quantize_rows_kernel<2, BQ_ACT_GELU>); break;
+    case 3: blk(quantize_rows_kernel<3, 0>, quantize_rows_kernel<3, BQ_ACT_GELU>); break;
+    case 4: blk(quantize_rows_kernel<4, 0>, quantize_rows_kernel<4, BQ_ACT_GELU>); break;
     case 5:
-    case 6: quantize_rows_kernel<6><<<grid, block, 0, st>>>(x, (int)K, q, s); break;
+    case 6: blk(quantize_rows_kernel<6, 0>, quantize_rows_kernel<6, BQ_ACT_GELU>); break;
     case 7:
-    case 8: quantize_rows_kernel<8><<<grid, block, 0, st>>>(x, (int)K, q, s); break;
-    default: quantize_rows_kernel<0><<<grid, block, 0, st>>>(x, (int)K, q, s); break;
+    case 8: blk(quantize_rows_kernel<8, 0>, quantize_rows_kernel<8, BQ_ACT_GELU>); break;
+    default: quantize_rows_kernel<0, 0><<<grid, block, 0, st>>>(x, (int)K, q, s, act, y); break;
   }
   return check_launch(what);
 }
@@ -384,6 +474,11 @@ int bq_device_ok(int device) {
 
 int bq_quantize_rows(const float* x, int64_t M, int64_t K, int8_t* q, float* s, bq_stream_t stream) {
   return launch_rows(x, M, K, q, s, (hipStream_t)stream, "bq_quantize_rows");
+}
+
+int bq_quantize_rows_act(const float* x, int64_t M, int64_t K, int act, int8_t* q, float* s, float* y,
+                         bq_stream_t stream) {
+  return launch_rows(x, M, K, q, s, (hipStream_t)stream, "bq_quantize_rows_act", act, y);
 }
 
 int bq_quantize_weight_per_channel(const float* w, int64_t N, int64_t K, int8_t* q, float* s,
@@ -489,6 +584,33 @@ int bq_quantize_nhwc_scaled(const float* x, int64_t P, int64_t C, int64_t Cpad, 
                             bq_stream_t stream) {
   if (!s) return set_error(BQ_ERR_ARG, "bq_quantize_nhwc_scaled: null scale");
   return quantize_nhwc_impl("bq_quantize_nhwc_scaled", x, P, C, Cpad, q, nullptr, s, nullptr, 0, (hipStream_t)stream);
+}
+
+int bq_layernorm_quantize_rows(const float* x, int64_t M, int64_t K, const float* gamma, const float* beta, float eps,
+                               int8_t* q, float* s, float* y, bq_stream_t stream) {
+  const char* what = "bq_layernorm_quantize_rows";
+  if (M < 0 || K < 1) return set_error(BQ_ERR_ARG, "%s: bad sizes (%lld x %lld)", what, (long long)M, (long long)K);
+  if (M == 0) return BQ_OK;
+  if (M > 0x7fffffff) return set_error(BQ_ERR_ARG, "%s: size too large", what);
+  if (K % 4 || K > 4096)
+    return set_error(BQ_ERR_UNSUPPORTED, "%s: K=%lld (a multiple of 4, at most 4096)", what, (long long)K);
+  if (!x || !q || !s) return set_error(BQ_ERR_ARG, "%s: null pointer", what);
+  if (((uintptr_t)x | (uintptr_t)gamma | (uintptr_t)beta | (uintptr_t)y) & 15 || (uintptr_t)q & 3)
+    return set_error(BQ_ERR_ARG, "%s: x, gamma, beta, y must be 16-byte aligned, q 4-byte aligned", what);
+  if (!(eps >= 0.f)) return set_error(BQ_ERR_ARG, "%s: eps must be >= 0", what);
+  hipStream_t st = (hipStream_t)stream;
+  dim3 g((unsigned)((M + QW_WAVES - 1) / QW_WAVES)), b(QW_WAVES * 64);
+  const int nw = (int)((K + 255) / 256);
+  auto go = [&](auto kern) { kern<<<g, b, 0, st>>>(x, (int)M, (int)K, gamma, beta, eps, q, s, y); };
+  if (nw == 1) go(ln_quantize_rows_kernel<1>);
+  else if (nw == 2) go(ln_quantize_rows_kernel<2>);
+  else if (nw == 3) go(ln_quantize_rows_kernel<3>);
+  else if (nw == 4) go(ln_quantize_rows_kernel<4>);
+  else if (nw <= 6) go(ln_quantize_rows_kernel<6>);
+  else if (nw <= 8) go(ln_quantize_rows_kernel<8>);
+  else if (nw <= 12) go(ln_quantize_rows_kernel<12>);
+  else go(ln_quantize_rows_kernel<16>);
+  return check_launch(what);
 }
 
 int bq_quantize_tensor(const float* x, int64_t n, int8_t* q, float* s, void* ws, size_t ws_bytes,

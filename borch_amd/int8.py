@@ -77,8 +77,10 @@ def _f32c(x: torch.Tensor) -> torch.Tensor:
 
 # --------------------------------------------------------------------------- quantizers
 
-def quantize_rows(x: torch.Tensor):
-    """Per-row int8 of f32 ``[M, K]`` → ``(q int8 [M, K], s f32 [M])`` (bq_quantize_rows)."""
+def quantize_rows(x: torch.Tensor, act: int = ACT_NONE, want_y: bool = False):
+    """Per-row int8 of f32 ``[M, K]`` → ``(q int8 [M, K], s f32 [M])`` (bq_quantize_rows); of
+    ``act(x)`` without storing it when ``act`` is given (bq_quantize_rows_act), and with
+    ``want_y`` also the f32 ``act(x)`` the kernel quantized: ``(q, s, y)``."""
     x = _f32c(x)
     require_device(x.device)
     if x.dim() != 2:
@@ -86,7 +88,13 @@ def quantize_rows(x: torch.Tensor):
     M, K = x.shape
     q = torch.empty((M, K), dtype=torch.int8, device=x.device)
     s = torch.empty((M,), dtype=torch.float32, device=x.device)
-    check(lib().bq_quantize_rows(x.data_ptr(), M, K, q.data_ptr(), s.data_ptr(), _stream(x)))
+    if act == ACT_NONE and not want_y:
+        check(lib().bq_quantize_rows(x.data_ptr(), M, K, q.data_ptr(), s.data_ptr(), _stream(x)))
+        return q, s
+    y = torch.empty((M, K), dtype=torch.float32, device=x.device) if want_y else None
+    check(lib().bq_quantize_rows_act(x.data_ptr(), M, K, int(act), q.data_ptr(), s.data_ptr(), _ptr(y), _stream(x)))
+    if want_y:
+        return q, s, (x if act == ACT_NONE else y)
     return q, s
 
 
@@ -458,11 +466,16 @@ def dwconv_i8_nhwc(qx, sa, wq: Int8DwWeight, stride=1, pad=0, bias=None, act=ACT
 
 # ----------------------------------------------------------------- float-in, float-out
 
-def linear(x: torch.Tensor, w8: Int8Weight, bias=None, act=ACT_NONE, residual=None) -> torch.Tensor:
+def linear(x: torch.Tensor, w8: Int8Weight, bias=None, act=ACT_NONE, residual=None,
+           pre_act=ACT_NONE) -> torch.Tensor:
     """Dynamic-quant int8 Linear: per-row activations, per-channel weights, f32 out
     ``[..., N]`` (the numpy core's ``x @ W.T + b``, borch/_nn.py:413-415, in W8A8), with an
-    optional ``residual [..., N]`` added in the epilogue before ``act``. A weight-only
-    packing runs ``linear_w8a32`` instead."""
+    optional ``residual [..., N]`` added in the epilogue before ``act``. ``pre_act`` applies
+    an activation to ``x`` first, inside the input quantizer. A weight-only packing runs
+    ``linear_w8a32`` instead."""
+    if pre_act != ACT_NONE and (w8.weight_only or w8.kpad != w8.in_features):
+        x = _act_f32(x, pre_act)
+        pre_act = ACT_NONE
     if w8.weight_only:
         out = linear_w8a32(x, w8, bias, ACT_NONE if residual is not None else act)
         if residual is not None:
@@ -476,9 +489,46 @@ def linear(x: torch.Tensor, w8: Int8Weight, bias=None, act=ACT_NONE, residual=No
     x2 = x.reshape(-1, x.shape[-1])
     if w8.kpad != w8.in_features:
         x2 = torch.nn.functional.pad(x2, (0, w8.kpad - w8.in_features))
-    qa, sa = quantize_rows(x2)
+    qa, sa = quantize_rows(x2, pre_act)
     r = None if residual is None else residual.reshape(-1, w8.out_features)
     out = gemm_i8(qa, w8.q, sa, w8.s, bias, act, residual=r)
+    return out.reshape(*lead, w8.out_features)
+
+
+def layernorm_quantize_rows(x: torch.Tensor, weight, bias, eps: float, want_y: bool = False):
+    """LayerNorm over the last axis of ``x [M, K]`` then per-row int8 of the result, in one
+    pass (bq_layernorm_quantize_rows): ``(q int8 [M, K], s [M])``, and the normalised f32
+    rows too with ``want_y``. The reference's layerNormRows order (kernels.ts:2935-2986)."""
+    _need(x, "x", torch.float32)
+    if x.dim() != 2:
+        raise ValueError("layernorm_quantize_rows takes [M, K]")
+    x = x.contiguous()
+    M, K = x.shape
+    g = None if weight is None else weight.detach().float().contiguous()
+    b = None if bias is None else bias.detach().float().contiguous()
+    q = torch.empty((M, K), dtype=torch.int8, device=x.device)
+    s = torch.empty((M,), dtype=torch.float32, device=x.device)
+    y = torch.empty((M, K), dtype=torch.float32, device=x.device) if want_y else None
+    check(lib().bq_layernorm_quantize_rows(x.data_ptr(), M, K, _ptr(g), _ptr(b), float(eps), q.data_ptr(),
+                                           s.data_ptr(), _ptr(y), _stream(x)))
+    return (q, s, y) if want_y else (q, s)
+
+
+def fusable_layernorm(ln, x: torch.Tensor, w8: Int8Weight) -> bool:
+    """Whether ``ln`` (a torch LayerNorm) can run inside the W8A8 Linear's input quantizer."""
+    K = x.shape[-1] if x.dim() else 0
+    return (isinstance(ln, torch.nn.LayerNorm) and tuple(ln.normalized_shape) == (K,) and x.is_cuda
+            and x.dtype == torch.float32 and not w8.weight_only and K % 4 == 0 and K <= 4096
+            and w8.kpad == K == w8.in_features)
+
+
+def layernorm_linear(x: torch.Tensor, ln, w8: Int8Weight, bias=None, act=ACT_NONE, residual=None) -> torch.Tensor:
+    """``linear(ln(x))`` in W8A8 with the LayerNorm in the input quantizer: the normalised
+    activation is never stored (``fusable_layernorm`` must hold)."""
+    lead = x.shape[:-1]
+    q, s = layernorm_quantize_rows(x.reshape(-1, x.shape[-1]), ln.weight, ln.bias, ln.eps)
+    r = None if residual is None else residual.reshape(-1, w8.out_features)
+    out = gemm_i8(q, w8.q, s, w8.s, bias, act, residual=r)
     return out.reshape(*lead, w8.out_features)
 
 

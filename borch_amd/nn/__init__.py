@@ -75,9 +75,20 @@ class Linear(_tnn.Module):
             self.int8 = _i8.pack_linear_weight(self.weight.detach(), weight_only)
         return True
 
-    def forward(self, x, residual=None):
+    def forward(self, x, residual=None, pre_norm=None, pre_act=None):
         """``x @ W.T + b``; the fused modules (``LinearReLU``, ``LinearGELU``, ``LinearAdd``)
-        add ``residual`` and apply the activation in the same epilogue."""
+        add ``residual`` and apply the activation in the same epilogue. ``pre_norm`` (a
+        LayerNorm) or ``pre_act`` (an activation id, e.g. GELU) is applied to ``x`` first; on
+        the W8A8 path it runs inside the input quantizer, so the normalised or activated
+        input is never stored."""
+        if pre_norm is not None:
+            if self.int8 is not None and _i8.fusable_layernorm(pre_norm, x, self.int8):
+                return _i8.layernorm_linear(x, pre_norm, self.int8, self.bias, self.act, residual)
+            x = pre_norm(x)
+        if pre_act is not None and pre_act != _i8.ACT_NONE:
+            if self.int8 is not None:
+                return _i8.linear(x, self.int8, self.bias, self.act, residual, pre_act=pre_act)
+            x = _i8._act_f32(x, pre_act)
         if self.int8 is not None:
             return _i8.linear(x, self.int8, self.bias, self.act, residual)
         out = functional._f32_linear(x, self.weight, self.bias)

@@ -107,7 +107,7 @@ class LinearAdd(_tnn.Module):
         self.linear.act = _i8.ACT_NONE
         self.training = False
 
-    def forward(self, x, residual=None):
+    def forward(self, x, residual=None, pre_act=None):
         if residual is None:
             raise TypeError("LinearAdd.forward takes (x1, x2)")
-        return self.linear(x, residual)
+        return self.linear(x, residual, pre_act=pre_act)

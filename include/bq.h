@@ -66,6 +66,24 @@ int bq_device_ok(int device);
 int bq_quantize_rows(const float* x, int64_t M, int64_t K, int8_t* q, float* s,
                      bq_stream_t stream);
 
+/* bq_quantize_rows of act(x) (BQ_ACT_*, one f32 evaluation per element, the epilogue's
+ * operation order) without storing act(x): a transformer MLP's second input, where the
+ * reference runs the activation pass and then the quantize (kernels.ts:2024-2081). y
+ * (nullable) f32 [M, K] also receives act(x) (16-byte aligned). */
+int bq_quantize_rows_act(const float* x, int64_t M, int64_t K, int act, int8_t* q, float* s, float* y,
+                         bq_stream_t stream);
+
+/* LayerNorm over each row, then bq_quantize_rows of the result, in one pass (the
+ * normalised row is not stored):
+ *   y = ((x - mean) * rstd) * gamma + beta, mean = sum(x) / K, var = sum((x - mean)^2) / K,
+ *   rstd = 1 / sqrt(var + eps), f32, one rounding per operation (gamma, beta f32 [K],
+ *   nullable: 1 and 0); q int8 [M, K], s f32 [M] = the per-row scales of y.
+ * y (nullable) f32 [M, K] also receives the normalised rows. K % 4 == 0, K <= 4096; x,
+ * gamma, beta, y 16-byte aligned. Replaces layerNormRows (borch-ts/src/kernels.ts:2935-2986)
+ * followed by the activation quantize of the next Linear (kernels.ts:2024-2081). */
+int bq_layernorm_quantize_rows(const float* x, int64_t M, int64_t K, const float* gamma, const float* beta, float eps,
+                               int8_t* q, float* s, float* y, bq_stream_t stream);
+
 /* Per-output-channel weight quantization of a Linear weight W f32 [N, K] -> q int8
  * [N, K], s f32 [N]. Replaces quantizeInt8PerChannel (borch-ts/src/quant.ts:23-53); the
  * same kernel and rule as bq_quantize_rows. */

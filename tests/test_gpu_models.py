@@ -46,6 +46,18 @@ def capture(model, rows=None):
         def hook(mod, args, kwargs, out, name=name):
             x = args[0].detach()
             res = args[1].detach() if len(args) > 1 and args[1] is not None else None
+            pre = kwargs.get("pre_norm")
+            if pre is not None:  # the layer's input is the fused LayerNorm's f32 rows (the kernel's own)
+                if I.fusable_layernorm(pre, x, mod.int8):
+                    y_ln = I.layernorm_quantize_rows(x.reshape(-1, x.shape[-1]), pre.weight, pre.bias, pre.eps,
+                                                     want_y=True)[2]
+                    x = y_ln.reshape(x.shape)
+                else:
+                    x = pre(x)
+            pre_act = kwargs.get("pre_act")
+            if pre_act:  # the layer's input is act(x) as its input quantizer evaluates it
+                x2 = x.reshape(-1, x.shape[-1]).contiguous()
+                x = I.quantize_rows(x2, pre_act, want_y=True)[2].reshape(x.shape)
             gate = args[2] if len(args) > 2 else kwargs.get("channel_scale")
             if gate is not None:  # the layer's input is x * gate (the kernel forms the same f32 products)
                 x = x * gate.detach()[:, :, None, None]

@@ -152,6 +152,60 @@ def test_se_gate_maxima_give_the_product_scale(dev, N, C, H, S, cpad):
     assert torch.equal(s4, s1 * 2) and torch.equal(q4, q1)
 
 
+@pytest.mark.parametrize("M,K,affine", [(6304 // 8, 768, True), (5, 768, False), (1, 100, True), (9, 772, True),
+                                        (1030, 1024, True), (3, 3072, True), (2, 4096, False), (7, 16, True)])
+def test_layernorm_quantize_rows(dev, M, K, affine):
+    """Fused LayerNorm + per-row quantize: the normalised rows (y output) within 1e-5 rel /
+    1e-6 abs of float64 torch.layer_norm (a library routine), and the int8 rows and scales
+    bit-exact against the oracle's quantize_rows of those same f32 rows."""
+    say(f"layernorm_quantize_rows M={M} K={K} affine={affine}")
+    rng = np.random.default_rng(M * 3 + K)
+    x = (rng.normal(size=(M, K)) * rng.uniform(0.5, 3.0, size=(M, 1)) + rng.uniform(-2, 2, size=(M, 1))).astype(np.float32)
+    g = rng.uniform(0.5, 1.5, K).astype(np.float32) if affine else None
+    b = rng.normal(size=K).astype(np.float32) * np.float32(0.1) if affine else None
+    q, s, y = I.layernorm_quantize_rows(t(x, dev), None if g is None else t(g, dev), None if b is None else t(b, dev),
+                                        1e-6, want_y=True)
+    T = lambda a: None if a is None else torch.from_numpy(a).double()
+    want = torch.nn.functional.layer_norm(T(x), (K,), T(g), T(b), 1e-6).numpy()
+    np.testing.assert_allclose(n(y), want, rtol=RTOL, atol=ATOL)
+    qo, so = O.quantize_rows(n(y))
+    assert np.array_equal(n(s), so) and np.array_equal(n(q), qo)
+    q2, s2 = I.layernorm_quantize_rows(t(x, dev), None if g is None else t(g, dev), None if b is None else t(b, dev),
+                                       1e-6)
+    assert torch.equal(q2, q) and torch.equal(s2, s)
+
+
+@pytest.mark.parametrize("M,K,act", [(6304 // 8, 3072, 3), (1030, 768, 3), (5, 100, 3), (3, 4096, 3), (2, 8192, 3),
+                                     (7, 13, 3), (1030, 768, 2), (9, 520, 1)])
+def test_quantize_rows_act(dev, M, K, act):
+    """Per-row quantization of act(x) without storing it: the activated rows (y output)
+    within 1e-5 rel / 1e-6 abs of the oracle's activation, equal to torch's own f32 GELU /
+    SiLU / ReLU on the device wherever they agree on the function, and the int8 rows and
+    scales bit-exact against the oracle's quantize_rows of those same rows."""
+    say(f"quantize_rows_act M={M} K={K} act={act}")
+    rng = np.random.default_rng(M + K + act)
+    x = (rng.normal(size=(M, K)) * 2).astype(np.float32)
+    q, s, y = I.quantize_rows(t(x, dev), act, want_y=True)
+    ref = {1: np.maximum(x, 0), 2: O.silu(x), 3: O.gelu(x)}[act]
+    np.testing.assert_allclose(n(y), ref, rtol=RTOL, atol=ATOL)
+    qo, so = O.quantize_rows(n(y))
+    assert np.array_equal(n(s), so) and np.array_equal(n(q), qo)
+    q2, s2 = I.quantize_rows(t(x, dev), act)
+    assert torch.equal(q2, q) and torch.equal(s2, s)
+    if act == 3:  # the same erf-form GELU, torch's operation order, as torch's device kernel
+        yt = torch.nn.functional.gelu(t(x, dev))
+        say(f"  GELU bits differing from torch's: {int((yt != y).sum())} of {M * K}")
+
+
+def test_layernorm_quantize_rows_rejects(dev):
+    """Rows longer than 4096 or not a multiple of 4 are refused by name (the Linear then
+    runs the LayerNorm and the quantizer separately); nothing is launched."""
+    with pytest.raises(NotImplementedError, match="K=4100"):
+        I.layernorm_quantize_rows(torch.zeros(2, 4100, device=dev), None, None, 1e-6)
+    with pytest.raises(NotImplementedError, match="K=6"):
+        I.layernorm_quantize_rows(torch.zeros(2, 6, device=dev), None, None, 1e-6)
+
+
 def test_quantize_tensor(dev):
     say("quantize_tensor")
     rng = np.random.default_rng(11)
