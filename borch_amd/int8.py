@@ -8,6 +8,7 @@ its conv input). There is no CPU path: a tensor that is not on a gfx950 device r
 """
 from __future__ import annotations
 
+import contextlib
 from dataclasses import dataclass
 
 import torch
@@ -58,8 +59,27 @@ def split_workspace(device: torch.device):
     return ws
 
 
+# A workspace that replaces the device's for the calls made inside ``workspace_scope``:
+# launches on concurrent streams must not share one (the tile counters and partials).
+_WS_SCOPE: list = []
+
+
+@contextlib.contextmanager
+def workspace_scope(ws: torch.Tensor):
+    """The GEMM / conv calls made inside use ``ws`` (``bq_gemm_ws_bytes()`` zero-filled bytes,
+    on the device they run on) as their split-K workspace instead of the device's."""
+    _WS_SCOPE.append(ws)
+    try:
+        yield
+    finally:
+        _WS_SCOPE.pop()
+
+
 def _ws_args(device):
-    ws = split_workspace(device)
+    if _WS_SCOPE and _WS_SCOPE[-1].device == torch.device(device):
+        ws = _WS_SCOPE[-1]
+    else:
+        ws = split_workspace(device)
     return (None, 0) if ws is None else (ws.data_ptr(), ws.numel())
 
 

@@ -371,3 +371,28 @@ def test_c4_efficientnet_b0_static_twin_only(dev):
     c = bt.compiled(model, int8=False, graph=True, fuse=False, tune=False)
     for _ in range(2):
         assert np.array_equal(n(c(x)), y_twin)
+
+
+def test_split_batch_graph_matches_whole(dev):
+    """compiled(split=2): the batch runs as two chunks on parallel streams inside the graph
+    (each with its own split-K workspace). Where every quantization is per row or uses a
+    calibrated scale the result equals the whole-batch graph bit for bit, on every replay;
+    a model whose convs take dynamic per-tensor scales (a maximum over the whole batch) is
+    refused."""
+    say("split batch graphs (ViT encoder b4, calibrated EfficientNet-B0 b4 at 96^2)")
+    vit = nets.build("vit_b16", seed=7, device=dev)
+    x = torch.from_numpy(WL.c5_input(4, 197, 768, 7)).to(dev)
+    whole = n(bt.compiled(vit, int8=True, graph=True, fuse=False, tune=False)(x))
+    c = bt.compiled(vit, int8=False, graph=True, fuse=False, tune=False, split=2)
+    for _ in range(3):
+        assert np.array_equal(n(c(x)), whole)
+    b0 = nets.build("efficientnet_b0", seed=7, device=dev)
+    bt.compiled(b0, int8=True, graph=False, fuse=False, tune=False)
+    xb = torch.from_numpy(WL.c4_input(4, 8, side=96)).to(dev)
+    with pytest.raises(ValueError, match="calibrated"):
+        bt.compiled(b0, int8=False, graph=True, fuse=False, tune=False, split=2)(xb)
+    bt.calibrate_int8(b0, [torch.from_numpy(WL.c4_input(4, s, side=96)).to(dev) for s in (9, 10)])
+    whole = n(bt.compiled(b0, int8=False, graph=True, fuse=False, tune=False)(xb))
+    c = bt.compiled(b0, int8=False, graph=True, fuse=False, tune=True, split=2)
+    for _ in range(3):
+        assert np.array_equal(n(c(xb)), whole)
