@@ -44,7 +44,7 @@ def assert_f32(got, want):
 
 @pytest.mark.parametrize("M,K", [(1, 16), (16, 512), (7, 1000), (3, 4096), (6304 // 16, 768), (5, 10000),
                                  (4, 13), (2, 8192), (1, 3072), (9, 2052), (5, 1284), (6, 4100), (1029, 772), (1024, 256), (2048, 1024),
-                                 (1500, 100)])
+                                 (1500, 100), (5, 2048), (130, 6144)])
 def test_quantize_rows(dev, M, K):
     say(f"quantize_rows M={M} K={K}")
     rng = np.random.default_rng(M * 131 + K)
