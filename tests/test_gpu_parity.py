@@ -506,7 +506,8 @@ def test_dwconv(dev, N, C, H, k, stride, pad):
 # ------------------------------------------------------------------- weight-only W8A32
 
 @pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (2, 17, 16), (5, 300, 1040), (8, 64, 8192), (1, 33, 2048),
-                                   (64, 96, 768), (3, 4100, 4096), (4, 256, 4096), (5, 64, 3072)])
+                                   (64, 96, 768), (3, 4100, 4096), (4, 256, 4096), (5, 64, 3072),
+                                   (8, 512, 4096), (7, 130, 2064)])
 def test_w8a32_linear(dev, M, N, K):
     say(f"w8a32 M={M} N={N} K={K}")
     rng = np.random.default_rng(M * 7 + N + K)
