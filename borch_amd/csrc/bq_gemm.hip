@@ -687,10 +687,16 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_i8_kernel(const GemmP p) {
 // Each wave keeps RPW rows (RPW * KC loads) in flight.
 constexpr int GV_WAVES = 8;
 
+// Wave64 integer sum, every lane active: a DPP butterfly within rows of 16 (quad_perm
+// [1,0,3,2], [2,3,0,1], row_half_mirror, row_mirror), then the four row sums read out of
+// lanes 0, 16, 32, 48 (no LDS permutes; integer addition is exact in any order).
 __device__ __forceinline__ int wave_sum(int v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
+  v += __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);
+  v += __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);
+  v += __builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, false);
+  v += __builtin_amdgcn_mov_dpp(v, 0x140, 0xF, 0xF, false);
+  return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16) + __builtin_amdgcn_readlane(v, 32) +
+         __builtin_amdgcn_readlane(v, 48);
 }
 
 template <int MR, int KC, int RPW, int WAVES = GV_WAVES>

@@ -19,12 +19,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t w_rsrc(const void* base, uint3
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
 
-__device__ __forceinline__ float wave_fsum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = __fadd_rn(v, __shfl_xor(v, off, 64));
-  return v;
-}
-
 constexpr int WA_WAVES = 8;
 constexpr int WA_XLDS = 16384;       // f32 activations staged through registers (64 KB of LDS)
 constexpr int WA_XLDS_BIG = 32768;   // staged by a load loop after the weights (128 KB of LDS)
@@ -125,7 +119,7 @@ __global__ __launch_bounds__(WA_WAVES * 64) void gemv_w8a32_kernel(const float* 
     }
 #pragma unroll
     for (int j = 0; j < RPW; ++j) {
-      const float s = wave_fsum(acc[j]);
+      const float s = wave_sum_fixed(acc[j]);  // every lane is here
       const int n = row0 + j;
       if (lane == 0 && j < nrows) {
         float v = bias ? __fadd_rn(s, bias[n]) : s;
