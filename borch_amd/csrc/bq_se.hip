@@ -128,7 +128,8 @@ __global__ __launch_bounds__(GATE_THREADS) void se_gate_kernel(const float* __re
   }
   __syncthreads();
   // z: each wave builds JW outputs at once, its lanes over c (c = lane, lane + 64, ... in
-  // order for every output), all loads of a batch issued before its FMAs; then a wave tree.
+  // order for every output), all loads of a batch issued before its FMAs; then a fixed-order
+  // DPP wave sum.
   constexpr int JW = 4, CU = 4;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   for (int j0 = wave * JW; j0 < S; j0 += (GATE_THREADS / 64) * JW) {
@@ -151,9 +152,7 @@ __global__ __launch_bounds__(GATE_THREADS) void se_gate_kernel(const float* __re
     }
 #pragma unroll
     for (int q = 0; q < JW; ++q) {
-      float v = acc[q];
-#pragma unroll
-      for (int off = 32; off > 0; off >>= 1) v = __fadd_rn(v, __shfl_xor(v, off, 64));
+      const float v = wave_sum_fixed(acc[q]);  // the whole wave is here (the loop is per wave)
       if (lane == 0 && j0 + q < S) z[j0 + q] = silu(__fadd_rn(v, b1 ? b1[j0 + q] : 0.f));
     }
   }
