@@ -320,6 +320,8 @@ def bench_models(dev, stream, steps, layers_out=None):
                              "tuned_us": round(sum(d["chosen_us"] for d in dec), 1)}
         if layers_out is not None:
             layers_out[key + "_tuning"] = dec
+        from borch_amd.tune import tune as _tune
+        _tune(model, x)  # the whole batch's problems too (a split graph tuned its chunks')
         rows = layer_table(model, x, stream)
         out[key]["layers_alone"] = layer_summary(rows)
         if name == "resnet18":  # per-layer MFMA fraction: [layer, M, N, K, us, fraction of 5.0 POP/s]
