@@ -41,7 +41,7 @@ class Compiled:
         self.split = int(split)
         if self.split < 1:
             raise ValueError(f"split must be >= 1, got {split}")
-        self._streams = None  # (streams, split-K workspaces), made on the first split call
+        self._streams = {}  # device -> [(stream, split-K workspace)], made on its first split call
         self.tuned = []  # the tuner's decisions, one list per input shape (borch_amd.tune.tune)
         self._tuned_keys = set()
         self.int8_layers = 0
@@ -66,17 +66,19 @@ class Compiled:
         """The model on ``x``: whole, or as ``split`` chunks on parallel streams."""
         if not self._split_ok(x):
             return self.model(x)
-        if self._streams is None:
+        streams = self._streams.get(x.device)
+        if streams is None:  # the warm-up runs come first, outside any capture
             nb = int(_i8.lib().bq_gemm_ws_bytes())
-            self._streams = [(torch.cuda.Stream(device=x.device),
-                              torch.zeros(nb, dtype=torch.uint8, device=x.device)) for _ in range(self.split)]
+            streams = self._streams[x.device] = [(torch.cuda.Stream(device=x.device),
+                                                  torch.zeros(nb, dtype=torch.uint8, device=x.device))
+                                                 for _ in range(self.split)]
         cur = torch.cuda.current_stream(x.device)
         outs = []
-        for (s, ws), xc in zip(self._streams, x.chunk(self.split)):
+        for (s, ws), xc in zip(streams, x.chunk(self.split)):
             s.wait_stream(cur)
             with torch.cuda.stream(s), _i8.workspace_scope(ws):
                 outs.append(self.model(xc))
-        for s, _ in self._streams:
+        for s, _ in streams:
             cur.wait_stream(s)
         return torch.cat(outs)
 
