@@ -23,6 +23,7 @@
 #include <array>
 #include <map>
 #include <mutex>
+#include <type_traits>
 #include <utility>
 
 #include "bq_common.h"
@@ -170,10 +171,9 @@ __device__ __forceinline__ void wait_dma() {
 // Stage kt+NBUF is fetched into the buffer stage kt just left, right after the barrier that
 // ends stage kt, and must land by the barrier that ends stage kt+NBUF-1: NBUF-1 stages of
 // MFMAs cover its latency (small tiles, whose stages are short, take deep rings).
-template <int BM, int BN, int WAVES_M, int WAVES_N, bool CONV, int NBUF, int FD>
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool CONV, int NBUF, int FD, bool MF16, typename Acc>
 __device__ __forceinline__ void mainloop_dma(const GemmP& p, int m0, int n0, int kt0, int KT, int8_t* lds,
-                                             float* s_sa, float* s_sw, float* s_b,
-                                             v16i (&c)[BM / WAVES_M / 32][BN / WAVES_N / 32]) {
+                                             float* s_sa, float* s_sw, float* s_b, Acc& c) {
   constexpr int WAVES = WAVES_M * WAVES_N;
   constexpr int T = WAVES * 64;
   constexpr int WTM = BM / WAVES_M;
@@ -274,7 +274,7 @@ __device__ __forceinline__ void mainloop_dma(const GemmP& p, int m0, int n0, int
 #pragma unroll
     for (int j = 0; j < TN; ++j) bf[j] = *reinterpret_cast<const v4i*>(bs + lds_off(wn * WTN + j * 32 + fr, ks * 2 + fh));
   };
-  auto mma = [&](const v4i (&a)[TM], const v4i (&b)[TN]) {
+  auto mma = [&](const auto (&a)[TM], const auto (&b)[TN]) {  // generic: instantiated by the 32x32 loops only
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -294,7 +294,50 @@ __device__ __forceinline__ void mainloop_dma(const GemmP& p, int m0, int n0, int
   for (int st = 0; st < NBUF; ++st) dma_stage(st, st);
   wait_dma<(NBUF - 1) * PER>();
   __syncthreads();
-  if constexpr (FD == 2) {
+  if constexpr (MF16) {
+    // v_mfma_i32_16x16x64_i8: the wave tile as (2 TM) x (2 TN) blocks of 16 x 16, a stage as
+    // two 64-byte K slices. The same MACs and LDS bytes as the 32x32x32 form, in twice as
+    // many half-size MFMAs, which sustain a higher rate at the power limit on random int8
+    // operands (3.66 against 3.21 POP/s, the same operand bytes, no memory traffic).
+    // Lane l reads row l % 16 of a 16-row block and 16-byte K chunk l / 16 of the slice; its
+    // result register r is row 4 (l / 16) + r, column l % 16.
+    constexpr int TM2 = 2 * TM, TN2 = 2 * TN;
+    constexpr int NM16 = TM2 * TN2, NR16 = TM2 + TN2;
+    const int gr = lane & 15, gc = lane >> 4;
+    auto frags16 = [&](int buf, int ks, v4i (&af)[TM2], v4i (&bf)[TN2]) {
+      const int8_t* as = lds + buf * (BM + BN) * BK;
+      const int8_t* bs = as + BM * BK;
+#pragma unroll
+      for (int i = 0; i < TM2; ++i) af[i] = *reinterpret_cast<const v4i*>(as + lds_off(wm * WTM + i * 16 + gr, ks * 4 + gc));
+#pragma unroll
+      for (int j = 0; j < TN2; ++j) bf[j] = *reinterpret_cast<const v4i*>(bs + lds_off(wn * WTN + j * 16 + gr, ks * 4 + gc));
+    };
+    auto mma16 = [&](const v4i (&a)[TM2], const v4i (&b)[TN2]) {
+#pragma unroll
+      for (int i = 0; i < TM2; ++i)
+#pragma unroll
+        for (int j = 0; j < TN2; ++j) c[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], b[j], c[i][j], 0, 0, 0);
+    };
+    v4i af[2][TM2], bf[2][TN2];
+    frags16(0, 0, af[0], bf[0]);
+    int cur = 0;
+    for (int kt = 0; kt < KT; ++kt) {
+      const int nxt = cur + 1 == NBUF ? 0 : cur + 1;
+      frags16(cur, 1, af[1], bf[1]);
+      mma16(af[0], bf[0]);
+      interleave_front<0x100, NR16, NM16, (NM16 + 1) / 2>();
+      __builtin_amdgcn_sched_barrier(0);
+      wait_dma<(NBUF - 2) * PER>();
+      wait_lds();  // this wave's reads of the buffer about to be refilled have returned
+      __syncthreads();
+      frags16(nxt, 0, af[0], bf[0]);  // past the last stage: data no one uses
+      dma_stage(cur, kt + NBUF);
+      mma16(af[1], bf[1]);
+      interleave<true, 0x100, NR16, NM16>();
+      __builtin_amdgcn_sched_barrier(0);
+      cur = nxt;
+    }
+  } else if constexpr (FD == 2) {
     // Fragments two slices ahead (four register sets, one per slice); the barrier sits
     // after slice 1 so that slices 0 and 1 of stage kt+1 are read under slices 2 and 3.
     v4i af[4][TM], bf[4][TN];
@@ -363,7 +406,7 @@ __device__ __forceinline__ void mainloop_dma(const GemmP& p, int m0, int n0, int
   __syncthreads();
 }
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, bool CONV, int NBUF, int FD>
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool CONV, int NBUF, int FD, bool MF16 = false>
 __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const GemmP p) {
   constexpr int T = WAVES_M * WAVES_N * 64;
   constexpr int WTM = BM / WAVES_M;  // wave tile rows
@@ -402,12 +445,21 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
   const int kt0 = split * per;
 
   const Quantizer qz_out(p.q_out ? p.s_out[0] : 0.f);
-  v16i c[TM][TN];
+  // the accumulators: TM x TN blocks of 32 x 32 (16 registers each), or with MF16
+  // (2 TM) x (2 TN) blocks of 16 x 16 (4 registers each): the same registers either way
+  std::conditional_t<MF16, v4i[2 * TM][2 * TN], v16i[TM][TN]> c;
+  if constexpr (MF16) {
 #pragma unroll
-  for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < 2 * TM; ++i)
 #pragma unroll
-    for (int j = 0; j < TN; ++j) c[i][j] = v16i{};
-  mainloop_dma<BM, BN, WAVES_M, WAVES_N, CONV, NBUF, FD>(p, m0, n0, kt0, min(per, KT - kt0), lds, s_sa, s_sw,
+      for (int j = 0; j < 2 * TN; ++j) c[i][j] = v4i{};
+  } else {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) c[i][j] = v16i{};
+  }
+  mainloop_dma<BM, BN, WAVES_M, WAVES_N, CONV, NBUF, FD, MF16>(p, m0, n0, kt0, min(per, KT - kt0), lds, s_sa, s_sw,
                                                          s_b, c);
   if (CAN_SPLIT && S > 1) {
     // Exact split-K reduction in the same launch. Partials are int32, so the sum is exact
@@ -425,16 +477,30 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
     const int tile = bm * tiles_n + bn;
     uint64_t* const part = reinterpret_cast<uint64_t*>(p.part);
     uint64_t* mine = part + ((size_t)(tile * S + split) * NV) * T + tid;
+    // chunk e of a lane: two consecutive accumulator registers, in the order of c
+    auto chunk = [&](int e) -> uint64_t {
+      int lo, hi;
+      if constexpr (MF16) {
+        lo = c[e / (4 * TN)][(e / 2) % (2 * TN)][2 * (e % 2)];
+        hi = c[e / (4 * TN)][(e / 2) % (2 * TN)][2 * (e % 2) + 1];
+      } else {
+        lo = c[e / (8 * TN)][(e / 8) % TN][2 * (e % 8)];
+        hi = c[e / (8 * TN)][(e / 8) % TN][2 * (e % 8) + 1];
+      }
+      return (uint64_t)(uint32_t)lo | ((uint64_t)(uint32_t)hi << 32);
+    };
+    auto add_chunk = [&](int e, uint64_t w) {
+      if constexpr (MF16) {
+        c[e / (4 * TN)][(e / 2) % (2 * TN)][2 * (e % 2)] += (int)(uint32_t)w;
+        c[e / (4 * TN)][(e / 2) % (2 * TN)][2 * (e % 2) + 1] += (int)(uint32_t)(w >> 32);
+      } else {
+        c[e / (8 * TN)][(e / 8) % TN][2 * (e % 8)] += (int)(uint32_t)w;
+        c[e / (8 * TN)][(e / 8) % TN][2 * (e % 8) + 1] += (int)(uint32_t)(w >> 32);
+      }
+    };
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-#pragma unroll
-        for (int g = 0; g < 8; ++g) {
-          const uint64_t v = (uint64_t)(uint32_t)c[i][j][2 * g] | ((uint64_t)(uint32_t)c[i][j][2 * g + 1] << 32);
-          __hip_atomic_store(mine + (size_t)((i * TN + j) * 8 + g) * T, v, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-        }
+    for (int e = 0; e < NV; ++e)
+      __hip_atomic_store(mine + (size_t)e * T, chunk(e), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     wait_dma_all();  // every partial store of this lane has completed
     __syncthreads();
     if (tid == 0)
@@ -457,15 +523,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
 #pragma unroll
       for (int u = 0; u < BATCH; ++u)
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-          for (int j = 0; j < TN; ++j)
-#pragma unroll
-            for (int g = 0; g < 8; ++g) {
-              const uint64_t w = v[u][(i * TN + j) * 8 + g];
-              c[i][j][2 * g] += (int)(uint32_t)w;
-              c[i][j][2 * g + 1] += (int)(uint32_t)(w >> 32);
-            }
+        for (int e = 0; e < NV; ++e) add_chunk(e, v[u][e]);
     }
     if (tid == 0) __hip_atomic_store(p.cnt + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
@@ -486,11 +544,21 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
   // and send them to scratch memory).
   auto slice = [&](auto ic) {
     constexpr int i = decltype(ic)::value;
+    if constexpr (MF16) {  // blocks 2i and 2i + 1 of 16 rows: lane l, register r is row 4 (l / 16) + r
 #pragma unroll
-    for (int j = 0; j < TN; ++j)
+      for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        patch[((r >> 2) * 8 + (lane >> 5) * 4 + (r & 3)) * PITCH + j * 32 + (lane & 31)] = c[i][j][r];
+        for (int j = 0; j < 2 * TN; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            patch[(sub * 16 + (lane >> 4) * 4 + r) * PITCH + j * 16 + (lane & 15)] = c[2 * i + sub][j][r];
+    } else {
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          patch[((r >> 2) * 8 + (lane >> 5) * 4 + (r & 3)) * PITCH + j * 32 + (lane & 31)] = c[i][j][r];
+    }
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's patch is written
     __builtin_amdgcn_wave_barrier();
     const int col4 = lane % C4;
@@ -1016,7 +1084,7 @@ static int pick_split(long long tiles, int KT, bool conv, int planned = 0) {
   return (KT + per - 1) / per;
 }
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, bool CONV, int NBUF, int FD>
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool CONV, int NBUF, int FD, bool MF16 = false>
 static void launch_tiled(GemmP p, hipStream_t st, const Ws& ws) {
   const long long tiles = (long long)((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
   int S = BM * BN <= SPLIT_MAX_TILE ? pick_split(tiles, (p.K + BK - 1) / BK, CONV, p.plan_split) : 1;
@@ -1030,7 +1098,7 @@ static void launch_tiled(GemmP p, hipStream_t st, const Ws& ws) {
     }
   }
   p.ksplit = S;
-  gemm_i8_kernel<BM, BN, WAVES_M, WAVES_N, CONV, NBUF, FD><<<(unsigned)(tiles * S), WAVES_M * WAVES_N * 64, 0, st>>>(p);
+  gemm_i8_kernel<BM, BN, WAVES_M, WAVES_N, CONV, NBUF, FD, MF16><<<(unsigned)(tiles * S), WAVES_M * WAVES_N * 64, 0, st>>>(p);
 }
 
 // BQ_GEMM_CFG forces one tile configuration (tuning sweeps); unset = the shape rule.
@@ -1047,12 +1115,15 @@ static int forced_cfg() {
 //   5 <128,128,2,2,2,2>  6 <256,128,2,2,3,1>  7 <64,64,2,2,4,2>    8 <256,64,4,1,3,1>
 //   9 <64,64,2,2,8,1>   10 <64,64,2,2,2,2>   11 <128,64,4,1,2,1>  12 <128,32,4,1,2,1>
 //  13 <256,64,4,1,2,1>  14 <128,64,4,1,3,1>
+//  15 <256,256,2,4,2,1> on 16x16x64 MFMAs (the same form measured 4-13% slower than 5 and
+//     6 on 128x128 and 256x128 tiles, so those stay on 32x32x32)
 struct TileDims {
   int bm, bn;
 };
-constexpr TileDims CFG_TILES[15] = {{0, 0},    {256, 256}, {256, 256}, {256, 256}, {128, 128},
-                                    {128, 128}, {256, 128}, {64, 64},   {256, 64},  {64, 64},
-                                    {64, 64},   {128, 64},  {128, 32},  {256, 64},  {128, 64}};
+constexpr int NCFG = 16;  // ids 1 .. NCFG - 1
+constexpr TileDims CFG_TILES[NCFG] = {{0, 0},    {256, 256}, {256, 256}, {256, 256}, {128, 128}, {128, 128},
+                                      {256, 128}, {64, 64},   {256, 64},  {64, 64},   {64, 64},   {128, 64},
+                                      {128, 32},  {256, 64},  {128, 64},  {256, 256}};
 
 // The configuration the tiled kernel runs for M x N x K. Narrow outputs (N <= 64: 1x1 convs
 // of mobile networks, the stem, early ResNet layers) take small-LDS tiles that fit several
@@ -1062,30 +1133,33 @@ constexpr TileDims CFG_TILES[15] = {{0, 0},    {256, 256}, {256, 256}, {256, 256
 // stages of a small tile's operands in flight; when there are more tiles than CUs, a small
 // tile takes the 2-deep ring instead so that several workgroups share a CU. The 256x256
 // tile's 64 KB stages leave room for two buffers only. Small tiles read their fragments two
-// K slices ahead (short MFMA runs).
-static int choose_cfg(const GemmP& p) {
-  if (forced_cfg() >= 1 && forced_cfg() <= 14) return forced_cfg();
-  if (p.plan_cfg >= 1 && p.plan_cfg <= 14) return p.plan_cfg;
+// K slices ahead (short MFMA runs). The dense 256x256 tile runs on 16x16x64 MFMAs, which
+// sustain a higher rate than 32x32x32 at the power limit (4096^3: 67-69 against 73-75 us);
+// its convolution form keeps 32x32x32, which needs fewer fragment registers next to the
+// implicit-GEMM addressing (the 16x16 form spills there).
+static int choose_cfg(const GemmP& p, bool conv) {
+  if (forced_cfg() >= 1 && forced_cfg() < NCFG) return forced_cfg();
+  if (p.plan_cfg >= 1 && p.plan_cfg < NCFG) return p.plan_cfg;
   const long long t256 = (long long)((p.M + 255) / 256) * ((p.N + 255) / 256);
   const long long t128 = (long long)((p.M + 127) / 128) * ((p.N + 127) / 128);
   const long long t128x32 = (long long)((p.M + 127) / 128) * ((p.N + 31) / 32);
   const long long t64 = (long long)((p.M + 63) / 64) * ((p.N + 63) / 64);
   if (p.N <= 32 && t128x32 >= 128) return 12;
   if (p.N <= 64 && t64 > 256) return 10;
-  if (t256 >= 192 && p.N >= 192) return 1;
+  if (t256 >= 192 && p.N >= 192) return conv ? 1 : 15;
   if (t128 >= 128 && p.N >= 96) return t128 > 256 ? 5 : 4;
   return 7;
 }
 
 // Output tiles of the tiled kernel for this problem (the length of its absmax output).
-static long long out_tiles(const GemmP& p) {
-  const TileDims d = CFG_TILES[choose_cfg(p)];
+static long long out_tiles(const GemmP& p, bool conv) {
+  const TileDims d = CFG_TILES[choose_cfg(p, conv)];
   return (long long)((p.M + d.bm - 1) / d.bm) * ((p.N + d.bn - 1) / d.bn);
 }
 
 template <bool CONV>
 static void launch_gemm(const GemmP& p, hipStream_t st, const Ws& ws) {
-  switch (choose_cfg(p)) {
+  switch (choose_cfg(p, CONV)) {
     case 1: return launch_tiled<256, 256, 2, 4, CONV, 2, 1>(p, st, ws);
     case 2: return launch_tiled<256, 256, 2, 4, CONV, 2, 2>(p, st, ws);
     case 3: return launch_tiled<256, 256, 2, 2, CONV, 2, 2>(p, st, ws);
@@ -1099,6 +1173,7 @@ static void launch_gemm(const GemmP& p, hipStream_t st, const Ws& ws) {
     case 12: return launch_tiled<128, 32, 4, 1, CONV, 2, 1>(p, st, ws);
     case 13: return launch_tiled<256, 64, 4, 1, CONV, 2, 1>(p, st, ws);
     case 14: return launch_tiled<128, 64, 4, 1, CONV, 3, 1>(p, st, ws);
+    case 15: return launch_tiled<256, 256, 2, 4, CONV, 2, 1, true>(p, st, ws);
     default: return launch_tiled<64, 64, 2, 2, CONV, 4, 2>(p, st, ws);
   }
 }
@@ -1286,7 +1361,7 @@ int64_t bq_conv2d_absmax_parts(int64_t N, int64_t H, int64_t W, int64_t C, int64
   p.M = (int)(N * OH * OW);
   p.N = (int)O;
   apply_plan(p, conv_key(N, H, W, C, O, KH, KW, stride, pad));
-  return p.M == 0 ? 0 : out_tiles(p);
+  return p.M == 0 ? 0 : out_tiles(p, !(KH == 1 && KW == 1 && stride == 1 && pad == 0));
 }
 
 int bq_plan_candidates(const int64_t* problem, int n, int32_t* cfgs, int32_t* splits, int cap) {
@@ -1298,10 +1373,10 @@ int bq_plan_candidates(const int64_t* problem, int n, int32_t* cfgs, int32_t* sp
   if (!tiled) return 0;
   std::pair<int, int> out[64];
   int cnt = 0;
-  const int rule = choose_cfg(p);
+  const int rule = choose_cfg(p, conv);
   out[cnt++] = {rule, split_of(p, rule, conv, 0)};
   // 3 (four waves on 256x256) and 9 (64x64 with an 8-deep ring) never won a measurement
-  static const int ids[] = {1, 2, 4, 5, 6, 7, 8, 10, 11, 12, 13, 14};
+  static const int ids[] = {1, 2, 4, 5, 6, 7, 8, 10, 11, 12, 13, 14, 15};
   for (int cfg : ids) {
     const TileDims d = CFG_TILES[cfg];
     const int KT = (p.K + BK - 1) / BK;
@@ -1333,7 +1408,7 @@ int bq_plan_set(const int64_t* problem, int n, int32_t cfg, int32_t split) {
     g_plans.erase(key);
     return BQ_OK;
   }
-  if (cfg < 1 || cfg > 14 || cfg == 3 || cfg == 9 || split < 1 || split > 64)
+  if (cfg < 1 || cfg >= NCFG || cfg == 3 || cfg == 9 || split < 1 || split > 64)
     return set_error(BQ_ERR_ARG, "bq_plan_set: bad configuration %d / split %d", cfg, split);
   if (!tiled) return set_error(BQ_ERR_ARG, "bq_plan_set: a GEMM of at most 64 rows has no tiled kernel to plan");
   g_plans[key] = Plan{cfg, split};

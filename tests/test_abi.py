@@ -105,11 +105,13 @@ def test_probe_library_exports_its_header():
     for n in names:
         assert hasattr(lib, n), n
     i64, p = ctypes.c_int64, ctypes.c_void_p
-    lib.bqp_mfma_rate.argtypes = [p, i64, p, i64, ctypes.c_int, ctypes.c_int, p, p]
+    lib.bqp_mfma_rate.argtypes = [p, i64, p, i64, ctypes.c_int, ctypes.c_int, ctypes.c_int, p, p]
     lib.bqp_stream_read.argtypes = [p, i64, ctypes.c_int, p, p]
-    assert lib.bqp_mfma_rate(None, 4096, None, 4096, 1, 1, None, None) == -1
+    assert lib.bqp_mfma_rate(None, 4096, None, 4096, 16, 1, 1, None, None) == -1
     assert b"null" in lib.bqp_last_error()
-    assert lib.bqp_mfma_rate(16, 4000, 16, 4096, 1, 1, 16, None) == -1
+    assert lib.bqp_mfma_rate(16, 4000, 16, 4096, 16, 1, 1, 16, None) == -1
+    assert lib.bqp_mfma_rate(16, 4096, 16, 4096, 8, 1, 1, 16, None) == -1
+    assert b"form" in lib.bqp_last_error()
     assert lib.bqp_stream_read(16, 24, 1, 16, None) == -1
     assert lib.bqp_stream_read(16, 32, 3, 16, None) == -1
     assert b"chunks" in lib.bqp_last_error()
@@ -152,7 +154,7 @@ def test_plan_candidates(problem):
     assert len(set(cands)) == len(cands)
     small = {7, 9, 10, 12}  # tiles of 64 x 64 and 128 x 32 outputs
     for cfg, split in cands:
-        assert 1 <= cfg <= 14 and split >= 1
+        assert 1 <= cfg <= 15 and split >= 1
         assert cfg not in (3, 9) or (cfg, split) == cands[0]
         if split > 1:
             assert cfg in small
@@ -168,7 +170,7 @@ def test_plan_rejects_bad_problems_and_small_gemms():
     assert _candidates(lib, (1, 2, 3, 4)) < 0  # neither 3 nor 9 dimensions
     assert _candidates(lib, (1, 4, 4, 16, 8, 5, 5, 1, 0)) < 0  # the filter is larger than the input
     arr = (ctypes.c_int64 * 3)(4096, 4096, 4096)
-    assert lib.bq_plan_set(arr, 3, 3, 1) < 0 and lib.bq_plan_set(arr, 3, 15, 1) < 0
+    assert lib.bq_plan_set(arr, 3, 3, 1) < 0 and lib.bq_plan_set(arr, 3, 16, 1) < 0
     assert lib.bq_plan_set(arr, 3, 1, 0) < 0
     small = (ctypes.c_int64 * 3)(16, 512, 512)
     assert lib.bq_plan_set(small, 3, 1, 1) < 0
