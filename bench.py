@@ -137,7 +137,8 @@ def probes(dev, stream, qa, qw, wcopies):
     run as the kernels they bound:
     * the int8 MFMA rate with no memory traffic, on fragments of the 4096^3 GEMM's own
       quantized operands (the MFMA clock falls with the power the operand bits draw), in the
-      GEMM tile's per-wave shape and occupancy (8 waves a CU); best of 3;
+      GEMM tile's per-wave shape and occupancy (8 waves a CU); best of 3; in the 16x16x64 form
+      the 256x256 tile runs (the ceiling) and in the 32x32x32 form beside it;
     * the plain streaming read of the GEMV's cache-cold 16 MiB weight copies: best of four
       load depths per lane; the floor of any kernel that reads those bytes once."""
     import ctypes
@@ -145,7 +146,7 @@ def probes(dev, stream, qa, qw, wcopies):
     lib = ctypes.CDLL(str(ROOT / "borch_amd" / "lib" / "libbqprobe.so"))
     lib.bqp_mfma_rate.restype = ctypes.c_int
     lib.bqp_mfma_rate.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int,
-                                  ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+                                  ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
     lib.bqp_stream_read.restype = ctypes.c_int
     lib.bqp_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
     lib.bqp_last_error.restype = ctypes.c_char_p
@@ -158,11 +159,13 @@ def probes(dev, stream, qa, qw, wcopies):
     sink = torch.empty(cus * 512, dtype=torch.int32, device=dev)
     iters = 400
     st = stream.cuda_stream
-    ok(lib.bqp_mfma_rate(qa.data_ptr(), qa.numel(), qw.data_ptr(), qw.numel(), cus, 8, sink.data_ptr(), st))
-    best = min(time_events(lambda i: ok(lib.bqp_mfma_rate(qa.data_ptr(), qa.numel(), qw.data_ptr(), qw.numel(),
-                                                          cus, iters, sink.data_ptr(), st)), 1, stream)
-               for _ in range(3))
-    mfma_tops = cus * 8 * iters * 32 * 65536 / (best * 1e-3) / 1e12
+    rate, took = {}, {}
+    for form in (32, 16):
+        ok(lib.bqp_mfma_rate(qa.data_ptr(), qa.numel(), qw.data_ptr(), qw.numel(), form, cus, 8, sink.data_ptr(), st))
+        took[form] = min(time_events(lambda i: ok(lib.bqp_mfma_rate(qa.data_ptr(), qa.numel(), qw.data_ptr(), qw.numel(),
+                                                                    form, cus, iters, sink.data_ptr(), st)), 1, stream)
+                         for _ in range(3))
+        rate[form] = cus * 8 * iters * 2097152 / (took[form] * 1e-3) / 1e12
     nbytes = wcopies[0].numel()
     rsink = torch.empty(nbytes // 4096 + 1, dtype=torch.int32, device=dev)
     read_us = {}
@@ -172,8 +175,10 @@ def probes(dev, stream, qa, qw, wcopies):
         read_us[ch] = time_graph(g, len(wcopies), 8, stream) * 1e3
         del g
     ch = min(read_us, key=read_us.get)
-    return {"mfma_int8_TOPS_no_memory": round(mfma_tops, 1), "mfma_probe": f"{cus} CUs x 8 waves, "
-            f"{iters * 32} v_mfma_i32_32x32x32_i8 a wave on the 4096^3 operands' bytes, {best:.3f} ms",
+    return {"mfma_int8_TOPS_no_memory": round(rate[16], 1), "mfma_32x32x32_TOPS_no_memory": round(rate[32], 1),
+            "mfma_probe": f"{cus} CUs x 8 waves on the 4096^3 operands' bytes: {iters * 64} v_mfma_i32_16x16x64_i8 "
+                          f"a wave (the GEMM's form) {took[16]:.3f} ms, {iters * 32} v_mfma_i32_32x32x32_i8 a wave "
+                          f"{took[32]:.3f} ms",
             "read_16MiB_cold_us": round(read_us[ch], 3), "read_GBps": round(nbytes / (read_us[ch] * 1e-6) / 1e9, 1),
             "read_probe": f"plain streaming read of {nbytes} B over {len(wcopies)} rotated copies, "
                           f"{ch} x 16 B loads a lane (best of 1/2/4/8)"}

@@ -532,9 +532,13 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
   // per-wave LDS patch (exact), come back as four consecutive columns of one row per lane,
   // and leave as 16-byte stores of whole 256-byte row segments. 32x32 result layout:
   // lane l, register r holds row 8*(r/4) + 4*(l/32) + r%4, column l%32.
-  constexpr int PITCH = WTN + 8;  // ints; 4*PITCH % 64 == 32 keeps both half-waves' rows apart
+  // Patch pitch (ints) for conflict-free ds_write_b32 of a whole wave (64 banks): the 32x32
+  // layout writes two 32-column rows 4 apart (4 PITCH % 64 == 32 keeps them apart), the
+  // 16x16 layout four 16-column rows 4 apart (4 PITCH % 64 == 16). The read-back takes one
+  // 256-byte row per 16 lanes, conflict-free at any 16-byte-aligned pitch.
+  constexpr int PITCH = WTN + (MF16 ? 4 : 8);
   static_assert(WAVES_M * WAVES_N * 32 * PITCH * 4 <= NBUF * (BM + BN) * BK, "epilogue patch");
-  static_assert((PITCH * 4) % 16 == 0 && (4 * PITCH) % 64 == 32, "patch pitch");
+  static_assert((PITCH * 4) % 16 == 0 && (4 * PITCH) % 64 == (MF16 ? 16 : 32), "patch pitch");
   int* patch = reinterpret_cast<int*>(lds) + wave * 32 * PITCH;
   constexpr int C4 = WTN / 4;                 // float4 columns per row
   constexpr int ROWS_PER_STORE = 64 / C4;     // rows one 64-lane store covers

@@ -74,6 +74,43 @@ __global__ __launch_bounds__(512) void mfma_rate_kernel(const int8_t* A, uint32_
   sink[g] = r;
 }
 
+// The same with v_mfma_i32_16x16x64_i8 in the 256x256 tile's 16x16 form: 8 x 4 accumulators
+// per wave, two fragment sets (the two 64-byte K slices of a stage).
+constexpr int SETS16 = 2, TM16 = 8, TN16 = 4;
+__global__ __launch_bounds__(512) void mfma_rate16_kernel(const int8_t* A, uint32_t a_chunks, const int8_t* W,
+                                                          uint32_t w_chunks, int iters, int32_t* sink) {
+  const uint32_t g = blockIdx.x * 512u + threadIdx.x;
+  v4i af[SETS16][TM16], bf[SETS16][TN16];
+#pragma unroll
+  for (int s = 0; s < SETS16; ++s) {
+#pragma unroll
+    for (int i = 0; i < TM16; ++i) af[s][i] = frag(A, a_chunks, g * 64u + s * TM16 + i);
+#pragma unroll
+    for (int j = 0; j < TN16; ++j) bf[s][j] = frag(W, w_chunks, g * 64u + 32u + s * TN16 + j);
+  }
+  v4i c[TM16][TN16];
+#pragma unroll
+  for (int i = 0; i < TM16; ++i)
+#pragma unroll
+    for (int j = 0; j < TN16; ++j) c[i][j] = v4i{};
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int s = 0; s < SETS16; ++s)
+#pragma unroll
+      for (int i = 0; i < TM16; ++i)
+#pragma unroll
+        for (int j = 0; j < TN16; ++j) c[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[s][i], bf[s][j], c[i][j], 0, 0, 0);
+  }
+  int r = 0;
+#pragma unroll
+  for (int i = 0; i < TM16; ++i)
+#pragma unroll
+    for (int j = 0; j < TN16; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) r ^= c[i][j][e];
+  sink[g] = r;
+}
+
 template <int CH>
 __global__ __launch_bounds__(256) void stream_read_kernel(const v4i* src, uint32_t n16, int32_t* sink) {
   const uint32_t base = blockIdx.x * (256u * CH) + threadIdx.x;
@@ -100,16 +137,21 @@ extern "C" {
 
 const char* bqp_last_error(void) { return g_err; }
 
-int bqp_mfma_rate(const int8_t* A, int64_t a_bytes, const int8_t* W, int64_t w_bytes, int blocks, int iters,
-                  int32_t* sink, void* stream) {
+int bqp_mfma_rate(const int8_t* A, int64_t a_bytes, const int8_t* W, int64_t w_bytes, int form, int blocks,
+                  int iters, int32_t* sink, void* stream) {
+  if (form != 32 && form != 16) return fail(BQ_ERR_ARG, "bqp_mfma_rate: form must be 32 or 16");
   if (!A || !W || !sink) return fail(BQ_ERR_ARG, "bqp_mfma_rate: null pointer");
   if (a_bytes < 4096 || w_bytes < 4096 || a_bytes % 16 || w_bytes % 16 || a_bytes / 16 > 0xffffffffll ||
       w_bytes / 16 > 0xffffffffll)
     return fail(BQ_ERR_ARG, "bqp_mfma_rate: operand sizes must be multiples of 16, >= 4096 and < 64 GiB");
   if (((uintptr_t)A & 15) || ((uintptr_t)W & 15)) return fail(BQ_ERR_ARG, "bqp_mfma_rate: unaligned operands");
   if (blocks < 1 || blocks > 65536 || iters < 1) return fail(BQ_ERR_ARG, "bqp_mfma_rate: bad blocks/iters");
-  mfma_rate_kernel<<<blocks, 512, 0, (hipStream_t)stream>>>(A, (uint32_t)(a_bytes / 16), W, (uint32_t)(w_bytes / 16),
-                                                            iters, sink);
+  if (form == 16)
+    mfma_rate16_kernel<<<blocks, 512, 0, (hipStream_t)stream>>>(A, (uint32_t)(a_bytes / 16), W,
+                                                                (uint32_t)(w_bytes / 16), iters, sink);
+  else
+    mfma_rate_kernel<<<blocks, 512, 0, (hipStream_t)stream>>>(A, (uint32_t)(a_bytes / 16), W,
+                                                              (uint32_t)(w_bytes / 16), iters, sink);
   return launched("bqp_mfma_rate");
 }
 
