@@ -90,7 +90,10 @@ def layer_work(kind, a):
     if kind == "dwconv_i8_nhwc":
         return (m, c, wq.KH * wq.KW), 2 * m * c * wq.KH * wq.KW, n * h * w * c + 4 * m * c + wq.KH * wq.KW * c
     k = wq.KH * wq.KW * c
-    out_b = 4 * m * wq.O * (2 if a.get("residual") is not None else 1) + (m * wq.O if kind.endswith("_q") else 0)
+    # the f32 output unless the launch writes the twin alone
+    f32_out = kind == "conv2d_i8_nhwc" or (kind == "conv2d_i8_nhwc_q" and a.get("f32_out", True))
+    out_b = (4 * m * wq.O * f32_out + 4 * m * wq.O * (a.get("residual") is not None)
+             + (m * wq.O if kind.endswith("_q") else 0))
     return (m, wq.O, k), 2 * m * wq.O * k, n * h * w * c + wq.O * k + out_b
 
 

@@ -73,6 +73,11 @@ def test_bench_layer_work_matches_the_implicit_gemm_shapes():
     # the int8 twin adds a byte per output, a residual four
     r = torch.empty(1)
     assert conv(16, 4, 512, 512, 3, 1, 1, "conv2d_i8_nhwc_q", r)[2] == byts + 4 * 256 * 512 + 256 * 512
+    # the twin alone: no f32 output
+    wq = types.SimpleNamespace(KH=3, KW=3, O=512)
+    a = {"qx": torch.empty((16, 4, 4, 512), dtype=torch.int8), "wq": wq, "stride": 1, "pad": 1, "residual": None,
+         "f32_out": False}
+    assert bench.layer_work("conv2d_i8_nhwc_q", a)[2] == byts - 4 * 256 * 512 + 256 * 512
     # depthwise 3x3 stride 2 on 112² x 96 at b64: 2·9 ops per output
     shape, ops, byts = conv(64, 112, 96, 96, 3, 2, 1, "dwconv_i8_nhwc")
     assert shape == (64 * 56 * 56, 96, 9) and ops == 2 * 9 * 64 * 56 * 56 * 96
