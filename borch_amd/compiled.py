@@ -7,15 +7,17 @@ timing is never quoted for an "int8" forward that was mostly f32.
 
 Run: eager, or with ``graph=True`` a HIP graph captured on the first call for that
 input shape and replayed afterwards (the reference's record/replay, device.ts:634-660):
-the int8 forward is many small launches, and a replay issues them as one.
+the int8 forward is many small launches, and a replay issues them as one. As with any
+captured graph, the returned tensor is the graph's own output buffer: the next call with
+the same input shape overwrites it (clone it to keep it).
 
 Split (``split=n``, graph mode): the batch runs as ``n`` chunks on parallel streams inside
 the one graph, so one chunk's store- or latency-bound kernels overlap another's MFMA work
 (each stream with its own split-K workspace). Refused where it would change the result:
 a conv with a dynamic per-tensor input scale takes the maximum over the whole batch, so the
 model needs calibrated scales (``calibrate_int8``) or per-row (Linear) quantization only.
-Measured: EfficientNet-B0 b64 calibrated 1.55 -> 1.42 ms, ViT-B/16 b32 2.92 -> 2.76 ms at
-n = 2; ResNet-18 b16 (small launch-bound layers) is slower split.
+Measured at n = 2: EfficientNet-B0 b64 calibrated 1.55 -> 1.41 ms, ViT-B/16 b32 3.09 ->
+2.87 ms; ResNet-18 b16 (small launch-bound layers) is slower split.
 
 Tune (``tune=True``, the default, as the reference's, compile.ts:55-62): before a shape's
 first run on a GPU, the int8 GEMM / conv kernel of every distinct layer problem is chosen
