@@ -4,8 +4,8 @@
 // kernels.ts:2695-2708) for streamed/windowed weights, and its `dequantInt8` unpack pass
 // (kernels.ts:1264-1274).
 //
-// gemv_w8a32_kernel (M <= 8, the decode shape): HBM-bound on the int8 weight — a quarter
-// of the f32 bytes. Each wave owns RPW weight rows; a row is read as contiguous 1 KB
+// gemv_w8a32_kernel (M <= 6, the decode shape; gemv_w8a32_mfma_kernel below for M = 7, 8):
+// HBM-bound on the int8 weight — a quarter of the f32 bytes. Each wave owns RPW weight rows; a row is read as contiguous 1 KB
 // wave-loads (64 lanes x 16 bytes) and every load of the wave's rows is issued before any
 // arithmetic; each lane multiplies its 16 weights against the matching 16 activations
 // (L1/L2-resident, reused across the wave's rows) and the wave reduces the lane sums.
@@ -20,6 +20,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t w_rsrc(const void* base, uint3
 }
 
 constexpr int WA_WAVES = 8;
+constexpr int WA_MMAX = 8;  // activation rows a launch takes (the decode shapes)
+// From this many activation rows the MFMA kernel runs (4096 x 4096, us, per-wave / MFMA:
+// M=5 12.9 / 12.9, M=6 14.0 / 13.1, M=7 15.6 / 13.4, M=8 17.3 / 13.9; M=2 7.9 / 12.3).
+constexpr int WA_MFMA_MIN_M = 7;
 constexpr int WA_XLDS = 16384;       // f32 activations staged through registers (64 KB of LDS)
 constexpr int WA_XLDS_BIG = 32768;   // staged by a load loop after the weights (128 KB of LDS)
 
@@ -130,6 +134,87 @@ __global__ __launch_bounds__(WA_WAVES * 64) void gemv_w8a32_kernel(const float* 
   }
 }
 
+// gemv_w8a32_mfma_kernel (2 <= M <= 8): the products on v_mfma_f32_16x16x4_f32. A
+// workgroup owns 16 weight rows; its waves split K into 64-byte chunks (wave w takes
+// chunks w, w + 8, ...). Lane l holds 16 bytes of weight row l % 16 at K offset
+// 64 c + 16 (l / 16) and the 16 matching floats of activation row l % 16 (zero for rows
+// >= M); MFMA j of a chunk multiplies byte j of every lane's piece, so the MFMA's K index
+// l / 16 stands for K offset 64 c + 16 (l / 16) + j in both operands. The effective weight
+// is f32(q) * scale (one rounding, as in the kernel above); the f32 sums take another
+// order, within the same f32-accumulation bound. The per-wave kernel above reads every
+// activation row in every wave and does M FMAs a weight on the VALU: at M = 8, 17.3 us for
+// a 4096 x 4096 weight. Partial 16 x 16 blocks meet through LDS in wave order.
+constexpr int WM_ROWS = 16;
+template <int CPW>  // 64-byte chunks a wave: K <= CPW * 8 * 64
+__global__ __launch_bounds__(WA_WAVES * 64) void gemv_w8a32_mfma_kernel(const float* __restrict__ x, const int8_t* W,
+                                                                        int M, int N, int K,
+                                                                        const float* __restrict__ sW,
+                                                                        const float* __restrict__ bias, int act,
+                                                                        float* __restrict__ out) {
+  typedef float v4f __attribute__((ext_vector_type(4)));
+  __shared__ float red[WA_WAVES][WM_ROWS][16];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int n0 = blockIdx.x * WM_ROWS;
+  const int nrows = min(WM_ROWS, N - n0);
+  const int r = lane & 15;        // weight row (A operand) and activation row (B operand) of this lane
+  const int kq = (lane >> 4) * 16;  // this lane's 16-byte piece of a 64-byte chunk
+  const __amdgpu_buffer_rsrc_t rw = w_rsrc(W + (size_t)n0 * K, (uint32_t)(nrows * K));  // rows past N read 0
+  const bool xrow = r < M;
+  v4i w[CPW];
+#pragma unroll
+  for (int c = 0; c < CPW; ++c) {
+    const int k = (wave + WA_WAVES * c) * 64 + kq;
+    w[c] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rw, k < K ? (uint32_t)(r * K + k) : W_OOB, 0, 0));
+  }
+  const float sc = r < nrows ? sW[n0 + r] : 0.f;
+  v4f acc = {0.f, 0.f, 0.f, 0.f};
+  // the activations in batches of up to 8 chunks (64 floats a lane in registers), every
+  // load of a batch issued before its first MFMA
+  constexpr int XB = CPW < 8 ? CPW : 8;
+#pragma unroll
+  for (int b0 = 0; b0 < CPW; b0 += XB) {
+    if ((wave + WA_WAVES * b0) * 64 >= K) break;  // uniform across the wave
+    float4 xv[XB][4];
+#pragma unroll
+    for (int c = 0; c < XB; ++c) {
+      const int k = (wave + WA_WAVES * (b0 + c)) * 64 + kq;
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        xv[c][t] = xrow && k < K ? *reinterpret_cast<const float4*>(x + (size_t)r * K + k + 4 * t)
+                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int c = 0; c < XB; ++c) {
+      if ((wave + WA_WAVES * (b0 + c)) * 64 >= K) break;  // uniform across the wave
+      const float xs[16] = {xv[c][0].x, xv[c][0].y, xv[c][0].z, xv[c][0].w, xv[c][1].x, xv[c][1].y,
+                            xv[c][1].z, xv[c][1].w, xv[c][2].x, xv[c][2].y, xv[c][2].z, xv[c][2].w,
+                            xv[c][3].x, xv[c][3].y, xv[c][3].z, xv[c][3].w};
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const float wf = __fmul_rn((float)(int)(int8_t)((uint32_t)w[b0 + c][j >> 2] >> ((j & 3) * 8)), sc);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(wf, xs[j], acc, 0, 0, 0);
+      }
+    }
+  }
+  // result register i of lane l: weight row 4 (l / 16) + i, activation row l % 16
+#pragma unroll
+  for (int i = 0; i < 4; ++i) red[wave][(lane >> 4) * 4 + i][lane & 15] = acc[i];
+  __syncthreads();
+  if (tid < WM_ROWS * 16) {
+    const int row = tid >> 4;
+    const int m = tid & 15;
+    if (m < M && row < nrows) {
+      float s = red[0][row][m];
+#pragma unroll
+      for (int wv = 1; wv < WA_WAVES; ++wv) s = __fadd_rn(s, red[wv][row][m]);
+      const float v = bias ? __fadd_rn(s, bias[n0 + row]) : s;
+      out[(size_t)m * N + n0 + row] = activate(v, act);
+    }
+  }
+}
+
 // w[n, k] = f32(q[n, k]) * s[n] (one rounding), four elements a thread.
 __global__ __launch_bounds__(256) void dequant_i8_kernel(const int8_t* __restrict__ q, int64_t N, int64_t K,
                                                          const float* __restrict__ s, float* __restrict__ w) {
@@ -158,7 +243,7 @@ int bq_gemv_w8a32(const float* x, const int8_t* W, int64_t M, int64_t N, int64_t
   const char* what = "bq_gemv_w8a32";
   if (M < 0 || N < 0 || K < 0) return set_error(BQ_ERR_ARG, "%s: negative size", what);
   if (M == 0 || N == 0) return BQ_OK;
-  if (M > 8) return set_error(BQ_ERR_UNSUPPORTED, "%s: M=%lld > 8 (dequantize and use an f32 GEMM)", what, (long long)M);
+  if (M > WA_MMAX) return set_error(BQ_ERR_UNSUPPORTED, "%s: M=%lld > %d (dequantize and use an f32 GEMM)", what, (long long)M, WA_MMAX);
   if (K % 16 || K > 8192) return set_error(BQ_ERR_UNSUPPORTED, "%s: K=%lld (needs K %% 16 == 0 and K <= 8192)", what, (long long)K);
   if (N > 0x7fffffff || (int64_t)N * K >= ((int64_t)1 << 31)) return set_error(BQ_ERR_ARG, "%s: size too large", what);
   if (!x || !W || !sW || !out) return set_error(BQ_ERR_ARG, "%s: null pointer", what);
@@ -168,6 +253,13 @@ int bq_gemv_w8a32(const float* x, const int8_t* W, int64_t M, int64_t N, int64_t
   const unsigned grid = (unsigned)((N + WA_WAVES * RPW - 1) / (WA_WAVES * RPW));
   hipStream_t st = (hipStream_t)stream;
   const int m = (int)M, n = (int)N, k = (int)K;
+  if (M >= WA_MFMA_MIN_M) {
+    const unsigned g2 = (unsigned)((N + WM_ROWS - 1) / WM_ROWS);
+    if (K <= 2048) gemv_w8a32_mfma_kernel<4><<<g2, WA_WAVES * 64, 0, st>>>(x, W, m, n, k, sW, bias, act, out);
+    else if (K <= 4096) gemv_w8a32_mfma_kernel<8><<<g2, WA_WAVES * 64, 0, st>>>(x, W, m, n, k, sW, bias, act, out);
+    else gemv_w8a32_mfma_kernel<16><<<g2, WA_WAVES * 64, 0, st>>>(x, W, m, n, k, sW, bias, act, out);
+    return check_launch(what);
+  }
   const int64_t kc = K <= 1024 ? 1 : K <= 2048 ? 2 : K <= 4096 ? 4 : 8;  // the kernel's KC
   if (M * kc * 1024 <= WA_XLDS) {
     if (K <= 1024) gemv_w8a32_kernel<1, RPW, true><<<grid, WA_WAVES * 64, 0, st>>>(x, W, m, n, k, sW, bias, act, out);
