@@ -162,9 +162,16 @@ def quantize_nhwc(x: torch.Tensor, cpad: int | None = None):
     P = N * H * W
     parts = getattr(xl, "_bq_absmax", None)
     if parts is not None and parts[2] == xl._version:
+        # A conv output read by two int8 convs (a residual block's first conv and its
+        # downsampling shortcut) is quantized once. Only such outputs are cached: they are
+        # new tensors in every forward, so a graph capture never finds a warm-up's bytes.
+        done = getattr(xl, "_bq_q8", None)
+        if done is not None and done[2] == xl._version and done[3] == cpad:
+            return done[0], done[1]
         # the producing conv's per-tile max |y| (bq_conv2d_i8_nhwc): no max pass over x
         check(lib().bq_quantize_nhwc_parts(xl.data_ptr(), P, C, cpad, parts[0].data_ptr(), parts[1], q.data_ptr(),
                                            s.data_ptr(), _stream(x)))
+        xl._bq_q8 = (q, s, xl._version, cpad)
         return q, s
     ws = _ws(P * C, x.device)
     check(lib().bq_quantize_nhwc(xl.data_ptr(), P, C, cpad, q.data_ptr(), s.data_ptr(), ws.data_ptr(),

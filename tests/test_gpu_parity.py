@@ -464,6 +464,8 @@ def test_conv_absmax_parts_feed_the_next_quantizer(dev, N, C, H, O_, k, stride, 
         assert nparts > 4096, nparts
     cpad = I.round_up(O_, 16)
     q1, s1 = I.quantize_nhwc(y, cpad)            # from the epilogue's partial maxima
+    q1b, s1b = I.quantize_nhwc(y, cpad)          # a second consumer: the same bytes, not quantized again
+    assert q1b is q1 and s1b is s1
     y2 = y.clone(memory_format=torch.channels_last)  # a copy carries no maxima
     assert getattr(y2, "_bq_absmax", None) is None
     q2, s2 = I.quantize_nhwc(y2, cpad)           # two passes
