@@ -99,6 +99,16 @@ def _need(t: torch.Tensor, name: str, dtype: torch.dtype) -> None:
     require_device(t.device)
 
 
+def _vec(t, n: int, name: str):
+    """``t`` as a contiguous float32 vector of exactly ``n`` values (None stays None): the
+    kernels read n values from the pointer, so a shorter vector must never reach them."""
+    if t is None:
+        return None
+    if t.numel() != n:
+        raise ValueError(f"{name}: expected {n} values, got {t.numel()}")
+    return t.detach().reshape(-1).float().contiguous()
+
+
 def _f32c(x: torch.Tensor) -> torch.Tensor:
     if x.dtype != torch.float32:
         raise TypeError(f"int8 path takes float32 activations, got {x.dtype}")
@@ -348,7 +358,7 @@ def linear_w8a32(x: torch.Tensor, w8: Int8Weight, bias=None, act=ACT_NONE) -> to
     N = w8.out_features
     if M <= 8 and K <= 8192:
         out = torch.empty((M, N), dtype=torch.float32, device=x.device)
-        b = None if bias is None else bias.contiguous().float()
+        b = _vec(bias, N, "bias")
         check(lib().bq_gemv_w8a32(x2.data_ptr(), w8.q.data_ptr(), M, N, K, w8.s.data_ptr(), _ptr(b), act,
                                   out.data_ptr(), _stream(x2)))
     else:
@@ -397,7 +407,7 @@ def gemm_i8(qa, qw, sa, sw, bias=None, act=ACT_NONE, want_acc=False, residual=No
     sa, sw = sa.contiguous().float(), sw.contiguous().float()
     if sa.numel() != M or sw.numel() != N:
         raise ValueError("scale sizes do not match the operands")
-    b = None if bias is None else bias.contiguous().float()
+    b = _vec(bias, N, "bias")
     r = None
     if residual is not None:
         if tuple(residual.shape) != (M, N):
@@ -430,7 +440,7 @@ def conv2d_i8_nhwc(qx, sa, wq: Int8ConvWeight, stride=1, pad=0, bias=None, resid
             raise RuntimeError(f"residual shape {tuple(residual.shape)} != output {(N, wq.O, OH, OW)}")
         res = residual.float().contiguous(memory_format=torch.channels_last)
     acc = torch.empty((N * OH * OW, wq.O), dtype=torch.int32, device=qx.device) if want_acc else None
-    b = None if bias is None else bias.contiguous().float()
+    b = _vec(bias, wq.O, "bias")
     parts, nparts = _absmax_parts(N, H, W, C, wq, stride, pad, qx.device)
     check(lib().bq_conv2d_i8_nhwc(qx.contiguous().data_ptr(), N, H, W, C, wq.q.data_ptr(), wq.O, wq.KH, wq.KW,
                                   stride, pad, sa.data_ptr(), wq.s.data_ptr(), _ptr(b), _ptr(res), act,
@@ -468,7 +478,7 @@ def conv2d_i8_nhwc_q(qx, sa, wq: Int8ConvWeight, s_out, stride=1, pad=0, bias=No
         if tuple(residual.shape) != (N, wq.O, OH, OW):
             raise RuntimeError(f"residual shape {tuple(residual.shape)} != output {(N, wq.O, OH, OW)}")
         res = residual.float().contiguous(memory_format=torch.channels_last)
-    b = None if bias is None else bias.contiguous().float()
+    b = _vec(bias, wq.O, "bias")
     # no per-tile maxima: a calibrated layer's consumer takes the twin or its own static scale
     check(lib().bq_conv2d_i8_nhwc_q(qx.contiguous().data_ptr(), N, H, W, C, wq.q.data_ptr(), wq.O, wq.KH, wq.KW,
                                     stride, pad, sa.data_ptr(), wq.s.data_ptr(), _ptr(b), _ptr(res), act,
@@ -492,6 +502,8 @@ def dwconv_i8_nhwc(qx, sa, wq: Int8DwWeight, stride=1, pad=0, bias=None, act=ACT
     acc = torch.empty((N, OH, OW, C), dtype=torch.int32, device=qx.device) if want_acc else None
     b = None
     if bias is not None:
+        if bias.numel() not in (wq.C, C):
+            raise ValueError(f"bias: expected {wq.C} values, got {bias.numel()}")
         b = bias.contiguous().float()
         if b.numel() != C:
             b = torch.nn.functional.pad(b, (0, C - b.numel()))
@@ -541,8 +553,8 @@ def layernorm_quantize_rows(x: torch.Tensor, weight, bias, eps: float, want_y: b
         raise ValueError("layernorm_quantize_rows takes [M, K]")
     x = x.contiguous()
     M, K = x.shape
-    g = None if weight is None else weight.detach().float().contiguous()
-    b = None if bias is None else bias.detach().float().contiguous()
+    g = _vec(weight, K, "weight")
+    b = _vec(bias, K, "bias")
     q = torch.empty((M, K), dtype=torch.int8, device=x.device)
     s = torch.empty((M,), dtype=torch.float32, device=x.device)
     y = torch.empty((M, K), dtype=torch.float32, device=x.device) if want_y else None

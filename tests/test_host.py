@@ -101,3 +101,16 @@ def test_workspace_scope_is_per_thread():
         th.start()
         th.join()
     assert seen == [[]] and I._scopes() == []
+
+
+def test_vectors_reaching_the_kernels_have_their_full_length():
+    """Bias / scale vectors are passed to the kernels as bare pointers: a short one is
+    refused on the host instead of being read past its end."""
+    import pytest
+    import torch
+    from borch_amd import int8 as I
+    assert I._vec(None, 4, "bias") is None
+    v = I._vec(torch.arange(4, dtype=torch.float64), 4, "bias")
+    assert v.dtype == torch.float32 and v.is_contiguous() and v.tolist() == [0.0, 1.0, 2.0, 3.0]
+    with pytest.raises(ValueError, match="expected 5 values, got 4"):
+        I._vec(torch.zeros(4), 5, "bias")
