@@ -198,3 +198,15 @@ def test_plan_sets_the_conv_tile_count():
         assert lib.bq_conv2d_absmax_parts(*geom) == rule
     finally:
         lib.bq_plan_clear()
+
+
+def test_rule_picks_the_16x16x64_tile_for_large_dense_gemms():
+    """The rule's first pick (host code, no GPU): the 256x256 tile on 16x16x64 MFMAs
+    (configuration 15) for a large dense GEMM, ragged or not; the same tile size stays on
+    32x32x32 (configuration 1) for an implicit-GEMM conv."""
+    from borch_amd import _lib
+    lib = _lib.lib()
+    assert _candidates(lib, (4096, 4096, 4096))[0] == (15, 1)
+    assert _candidates(lib, (3900, 3300, 32))[0] == (15, 1)
+    assert _candidates(lib, (64, 32, 32, 64, 256, 3, 3, 1, 1))[0] == (1, 1)
+    assert _candidates(lib, (64, 32, 32, 64, 256, 1, 1, 1, 0))[0] == (15, 1)  # a 1x1 conv is the dense GEMM

@@ -275,7 +275,8 @@ def test_c2_gemm_4096(dev):
 @pytest.mark.parametrize("M,N,K", [(17, 33, 16), (65, 100, 48), (100, 1, 272), (300, 130, 4096 + 16),
                                    (64, 64, 128), (129, 257, 1152), (6304, 768, 768), (2, 4100, 64),
                                    (1, 33, 8208), (3, 257, 2048), (4, 100, 1040), (1, 4096, 8192),
-                                   (2, 17, 16), (4, 4096, 4096), (5, 300, 3072), (33, 70, 4096)])
+                                   (2, 17, 16), (4, 4096, 4096), (5, 300, 3072), (33, 70, 4096),
+                                   (3900, 3300, 32)])  # the 256x256 16x16x64 tile by rule, ragged on both edges
 @pytest.mark.parametrize("act", [0, 1])
 def test_gemm_shapes(dev, M, N, K, act):
     say(f"gemm shape M={M} N={N} K={K} act={act}")
