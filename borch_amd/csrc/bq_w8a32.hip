@@ -4,7 +4,7 @@
 // kernels.ts:2695-2708) for streamed/windowed weights, and its `dequantInt8` unpack pass
 // (kernels.ts:1264-1274).
 //
-// gemv_w8a32_kernel (M <= 6, the decode shape; gemv_w8a32_mfma_kernel below for M = 7, 8):
+// gemv_w8a32_kernel (M <= 4, the decode shape; gemv_w8a32_mfma_kernel below for M = 5..8):
 // HBM-bound on the int8 weight — a quarter of the f32 bytes. Each wave owns RPW weight rows; a row is read as contiguous 1 KB
 // wave-loads (64 lanes x 16 bytes) and every load of the wave's rows is issued before any
 // arithmetic; each lane multiplies its 16 weights against the matching 16 activations
@@ -22,8 +22,8 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t w_rsrc(const void* base, uint3
 constexpr int WA_WAVES = 8;
 constexpr int WA_MMAX = 8;  // activation rows a launch takes (the decode shapes)
 // From this many activation rows the MFMA kernel runs (4096 x 4096, us, per-wave / MFMA:
-// M=5 12.9 / 12.9, M=6 14.0 / 13.1, M=7 15.6 / 13.4, M=8 17.3 / 13.9; M=2 7.9 / 12.3).
-constexpr int WA_MFMA_MIN_M = 7;
+// M=2 7.9 / 11.4, M=4 10.5 / 11.7, M=5 13.0 / 11.7, M=6 14.4 / 11.9, M=8 17.3 / 12.8).
+constexpr int WA_MFMA_MIN_M = 5;
 constexpr int WA_XLDS = 16384;       // f32 activations staged through registers (64 KB of LDS)
 constexpr int WA_XLDS_BIG = 32768;   // staged by a load loop after the weights (128 KB of LDS)
 
@@ -162,21 +162,12 @@ __global__ __launch_bounds__(WA_WAVES * 64) void gemv_w8a32_mfma_kernel(const fl
   const int kq = (lane >> 4) * 16;  // this lane's 16-byte piece of a 64-byte chunk
   const __amdgpu_buffer_rsrc_t rw = w_rsrc(W + (size_t)n0 * K, (uint32_t)(nrows * K));  // rows past N read 0
   const bool xrow = r < M;
-  v4i w[CPW];
-#pragma unroll
-  for (int c = 0; c < CPW; ++c) {
-    const int k = (wave + WA_WAVES * c) * 64 + kq;
-    w[c] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rw, k < K ? (uint32_t)(r * K + k) : W_OOB, 0, 0));
-  }
-  const float sc = r < nrows ? sW[n0 + r] : 0.f;
-  v4f acc = {0.f, 0.f, 0.f, 0.f};
-  // the activations in batches of up to 8 chunks (64 floats a lane in registers), every
-  // load of a batch issued before its first MFMA
+  // The activations in batches of up to 8 chunks (64 floats a lane in registers). The scale
+  // and the first batch are issued before the weights, so that chunk c's MFMAs wait for
+  // weight chunk c only (the counter drains in issue order), not for the whole stream.
   constexpr int XB = CPW < 8 ? CPW : 8;
-#pragma unroll
-  for (int b0 = 0; b0 < CPW; b0 += XB) {
-    if ((wave + WA_WAVES * b0) * 64 >= K) break;  // uniform across the wave
-    float4 xv[XB][4];
+  float4 xv[XB][4];
+  auto load_x = [&](int b0) {
 #pragma unroll
     for (int c = 0; c < XB; ++c) {
       const int k = (wave + WA_WAVES * (b0 + c)) * 64 + kq;
@@ -185,6 +176,21 @@ __global__ __launch_bounds__(WA_WAVES * 64) void gemv_w8a32_mfma_kernel(const fl
         xv[c][t] = xrow && k < K ? *reinterpret_cast<const float4*>(x + (size_t)r * K + k + 4 * t)
                                  : make_float4(0.f, 0.f, 0.f, 0.f);
     }
+  };
+  const float sc = r < nrows ? sW[n0 + r] : 0.f;
+  load_x(0);
+  v4i w[CPW];
+#pragma unroll
+  for (int c = 0; c < CPW; ++c) {
+    const int k = (wave + WA_WAVES * c) * 64 + kq;
+    w[c] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rw, k < K ? (uint32_t)(r * K + k) : W_OOB, 0, 0));
+  }
+  __builtin_amdgcn_sched_barrier(0);  // every load above is issued before the first MFMA
+  v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int b0 = 0; b0 < CPW; b0 += XB) {
+    if ((wave + WA_WAVES * b0) * 64 >= K) break;  // uniform across the wave
+    if (b0 > 0) load_x(b0);
 #pragma unroll
     for (int c = 0; c < XB; ++c) {
       if ((wave + WA_WAVES * (b0 + c)) * 64 >= K) break;  // uniform across the wave
