@@ -24,6 +24,7 @@ constexpr int WA_MMAX = 8;  // activation rows a launch takes (the decode shapes
 // From this many activation rows the MFMA kernel runs (4096 x 4096, us, per-wave / MFMA:
 // M=2 7.9 / 11.4, M=4 10.5 / 11.7, M=5 13.0 / 11.7, M=6 14.4 / 11.9, M=8 17.3 / 12.8).
 constexpr int WA_MFMA_MIN_M = 5;
+constexpr int WA_MPW = WA_MFMA_MIN_M - 1;  // activation rows the per-wave kernel takes
 constexpr int WA_XLDS = 16384;       // f32 activations staged through registers (64 KB of LDS)
 constexpr int WA_XLDS_BIG = 32768;   // staged by a load loop after the weights (128 KB of LDS)
 
@@ -33,7 +34,10 @@ constexpr int WA_XLDS_BIG = 32768;   // staged by a load loop after the weights 
 // the wait for them is not a wait for the weights; up to WA_XLDS_BIG, by a loop after the
 // weight loads: 8 rows of 4096 at 23.8 -> 19.1 us instead of every wave reading them from
 // L2). The register staging: one row of 4096 at 7.6 -> 7.3 us, four at 12.3 -> 11.5 us.
-template <int KC, int RPW, bool XL, int XN = WA_XLDS>
+// CO: the products chunk by chunk as each weight chunk lands (M = 1: one row of 4096 at
+// 7.0 -> 6.5 us); else row by row once every chunk has landed (M = 2..4: 8.0 / 9.0 / 10.1
+// us, 0.1-0.8 us less than chunk by chunk).
+template <int KC, int RPW, bool XL, int XN = WA_XLDS, bool CO = false>
 __global__ __launch_bounds__(WA_WAVES * 64) void gemv_w8a32_kernel(const float* __restrict__ x, const int8_t* W,
                                                                    int M, int N, int K, const float* __restrict__ sW,
                                                                    const float* __restrict__ bias, int act,
@@ -60,17 +64,18 @@ __global__ __launch_bounds__(WA_WAVES * 64) void gemv_w8a32_kernel(const float* 
       xr[r] = i < n4 ? reinterpret_cast<const float4*>(x)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
   }
+  float sc[RPW];  // before the weights: the first products then wait for chunk 0 only
+#pragma unroll
+  for (int j = 0; j < RPW; ++j) sc[j] = j < nrows ? sW[row0 + j] : 0.f;
   v4i w[RPW][KC];
+  // chunk-major, the order the products use them: chunk c waits for its own loads only
 #pragma unroll
-  for (int j = 0; j < RPW; ++j)
+  for (int c = 0; c < KC; ++c)
 #pragma unroll
-    for (int c = 0; c < KC; ++c) {
+    for (int j = 0; j < RPW; ++j) {
       const int k = c * 1024 + lane * 16;
       w[j][c] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rw, k < K ? (uint32_t)(j * K + k) : W_OOB, 0, 0));
     }
-  float sc[RPW];
-#pragma unroll
-  for (int j = 0; j < RPW; ++j) sc[j] = j < nrows ? sW[row0 + j] : 0.f;
   __builtin_amdgcn_sched_barrier(0);
   if constexpr (XL) {
     // Row m's float4 number c*256 + l*4 + t (the t-th of lane l's four in 1 KB chunk c) is
@@ -97,38 +102,89 @@ __global__ __launch_bounds__(WA_WAVES * 64) void gemv_w8a32_kernel(const float* 
     }
     __syncthreads();
   }
-  for (int m = 0; m < M; ++m) {
-    float acc[RPW];
+  if constexpr (CO) {
+    // Chunk by chunk, as the loads arrive: the chunk's effective weights f32(q) * scale, then
+    // every row's FMAs against them (each output accumulates chunk by chunk, byte by byte).
+    float acc[WA_MPW][RPW];
 #pragma unroll
-    for (int j = 0; j < RPW; ++j) acc[j] = 0.f;
+    for (int m = 0; m < WA_MPW; ++m)
+#pragma unroll
+      for (int j = 0; j < RPW; ++j) acc[m][j] = 0.f;
 #pragma unroll
     for (int c = 0; c < KC; ++c) {
       const int k = c * 1024 + lane * 16;
-      if (k >= K) break;
-      const float4* xp = XL ? reinterpret_cast<const float4*>(xs) + (m * KC + c) * 256 + lane
-                            : reinterpret_cast<const float4*>(x + (size_t)m * K + k);
-      float xv[16];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const float4 v = xp[XL ? t * 64 : t];
-        xv[t * 4] = v.x; xv[t * 4 + 1] = v.y; xv[t * 4 + 2] = v.z; xv[t * 4 + 3] = v.w;
-      }
+      if (c * 1024 >= K) break;  // uniform
+      float wf[RPW][16];
 #pragma unroll
       for (int j = 0; j < RPW; ++j)
 #pragma unroll
-        for (int q = 0; q < 16; ++q) {
-          const int b = (int)(int8_t)((uint32_t)w[j][c][q >> 2] >> ((q & 3) * 8));
-          acc[j] = __fmaf_rn(xv[q], __fmul_rn((float)b, sc[j]), acc[j]);
+        for (int q = 0; q < 16; ++q)
+          wf[j][q] = __fmul_rn((float)(int)(int8_t)((uint32_t)w[j][c][q >> 2] >> ((q & 3) * 8)), sc[j]);
+#pragma unroll
+      for (int m = 0; m < WA_MPW; ++m) {
+        if (m >= M) break;  // uniform
+        const float4* xp = XL ? reinterpret_cast<const float4*>(xs) + (m * KC + c) * 256 + lane
+                              : reinterpret_cast<const float4*>(x + (size_t)m * K + k);
+        float xv[16];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const float4 v = k < K ? xp[XL ? t * 64 : t] : make_float4(0.f, 0.f, 0.f, 0.f);
+          xv[t * 4] = v.x; xv[t * 4 + 1] = v.y; xv[t * 4 + 2] = v.z; xv[t * 4 + 3] = v.w;
         }
+#pragma unroll
+        for (int j = 0; j < RPW; ++j)
+#pragma unroll
+          for (int q = 0; q < 16; ++q) acc[m][j] = __fmaf_rn(xv[q], wf[j][q], acc[m][j]);
+      }
     }
 #pragma unroll
-    for (int j = 0; j < RPW; ++j) {
-      const float s = wave_sum_fixed(acc[j]);  // every lane is here
-      const int n = row0 + j;
-      if (lane == 0 && j < nrows) {
-        float v = bias ? __fadd_rn(s, bias[n]) : s;
-        v = activate(v, act);
-        out[(size_t)m * N + n] = v;
+    for (int m = 0; m < WA_MPW; ++m) {
+      if (m >= M) break;
+#pragma unroll
+      for (int j = 0; j < RPW; ++j) {
+        const float s = wave_sum_fixed(acc[m][j]);  // every lane is here
+        const int n = row0 + j;
+        if (lane == 0 && j < nrows) {
+          float v = bias ? __fadd_rn(s, bias[n]) : s;
+          v = activate(v, act);
+          out[(size_t)m * N + n] = v;
+        }
+      }
+    }
+  } else {
+    for (int m = 0; m < M; ++m) {
+      float acc[RPW];
+#pragma unroll
+      for (int j = 0; j < RPW; ++j) acc[j] = 0.f;
+#pragma unroll
+      for (int c = 0; c < KC; ++c) {
+        const int k = c * 1024 + lane * 16;
+        if (k >= K) break;
+        const float4* xp = XL ? reinterpret_cast<const float4*>(xs) + (m * KC + c) * 256 + lane
+                              : reinterpret_cast<const float4*>(x + (size_t)m * K + k);
+        float xv[16];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const float4 v = xp[XL ? t * 64 : t];
+          xv[t * 4] = v.x; xv[t * 4 + 1] = v.y; xv[t * 4 + 2] = v.z; xv[t * 4 + 3] = v.w;
+        }
+#pragma unroll
+        for (int j = 0; j < RPW; ++j)
+#pragma unroll
+          for (int q = 0; q < 16; ++q) {
+            const int b = (int)(int8_t)((uint32_t)w[j][c][q >> 2] >> ((q & 3) * 8));
+            acc[j] = __fmaf_rn(xv[q], __fmul_rn((float)b, sc[j]), acc[j]);
+          }
+      }
+#pragma unroll
+      for (int j = 0; j < RPW; ++j) {
+        const float s = wave_sum_fixed(acc[j]);  // every lane is here
+        const int n = row0 + j;
+        if (lane == 0 && j < nrows) {
+          float v = bias ? __fadd_rn(s, bias[n]) : s;
+          v = activate(v, act);
+          out[(size_t)m * N + n] = v;
+        }
       }
     }
   }
@@ -268,10 +324,10 @@ int bq_gemv_w8a32(const float* x, const int8_t* W, int64_t M, int64_t N, int64_t
   }
   const int64_t kc = K <= 1024 ? 1 : K <= 2048 ? 2 : K <= 4096 ? 4 : 8;  // the kernel's KC
   if (M * kc * 1024 <= WA_XLDS) {
-    if (K <= 1024) gemv_w8a32_kernel<1, RPW, true><<<grid, WA_WAVES * 64, 0, st>>>(x, W, m, n, k, sW, bias, act, out);
-    else if (K <= 2048) gemv_w8a32_kernel<2, RPW, true><<<grid, WA_WAVES * 64, 0, st>>>(x, W, m, n, k, sW, bias, act, out);
-    else if (K <= 4096) gemv_w8a32_kernel<4, RPW, true><<<grid, WA_WAVES * 64, 0, st>>>(x, W, m, n, k, sW, bias, act, out);
-    else gemv_w8a32_kernel<8, RPW, true><<<grid, WA_WAVES * 64, 0, st>>>(x, W, m, n, k, sW, bias, act, out);
+    if (K <= 1024) (M == 1 ? gemv_w8a32_kernel<1, RPW, true, WA_XLDS, true> : gemv_w8a32_kernel<1, RPW, true>)<<<grid, WA_WAVES * 64, 0, st>>>(x, W, m, n, k, sW, bias, act, out);
+    else if (K <= 2048) (M == 1 ? gemv_w8a32_kernel<2, RPW, true, WA_XLDS, true> : gemv_w8a32_kernel<2, RPW, true>)<<<grid, WA_WAVES * 64, 0, st>>>(x, W, m, n, k, sW, bias, act, out);
+    else if (K <= 4096) (M == 1 ? gemv_w8a32_kernel<4, RPW, true, WA_XLDS, true> : gemv_w8a32_kernel<4, RPW, true>)<<<grid, WA_WAVES * 64, 0, st>>>(x, W, m, n, k, sW, bias, act, out);
+    else (M == 1 ? gemv_w8a32_kernel<8, RPW, true, WA_XLDS, true> : gemv_w8a32_kernel<8, RPW, true>)<<<grid, WA_WAVES * 64, 0, st>>>(x, W, m, n, k, sW, bias, act, out);
   } else if (M * kc * 1024 <= WA_XLDS_BIG) {
     constexpr int B = WA_XLDS_BIG;
     if (K <= 1024) gemv_w8a32_kernel<1, RPW, true, B><<<grid, WA_WAVES * 64, 0, st>>>(x, W, m, n, k, sW, bias, act, out);
