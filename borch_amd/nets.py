@@ -97,10 +97,13 @@ class Block(tnn.Module):
         return torch.relu(out + side)
 
     def fuse(self):
+        if self.c1 is not None:  # already folded: the unfolded layers are gone
+            return self
         self.c1 = I.ConvReLU2d(fuse_conv_bn_eval(self.conv1, self.bn1))
         self.c2 = I.ConvAddReLU2d(fuse_conv_bn_eval(self.conv2, self.bn2))
         self.down = fuse_conv_bn_eval(self.downConv, self.downBn) if self.downConv is not None else None
         self.conv1 = self.bn1 = self.conv2 = self.bn2 = self.downConv = self.downBn = None
+        return self
 
 
 class ResNet18(tnn.Module):
@@ -129,6 +132,8 @@ class ResNet18(tnn.Module):
 
     def fuse(self):
         self.eval()
+        if self.stem_f is not None:  # already folded
+            return self
         self.stem_f = I.ConvReLU2d(fuse_conv_bn_eval(self.stem, self.bn))
         self.stem = self.bn = None
         for b in self.body:
@@ -202,6 +207,8 @@ class MBConv(tnn.Module):
         return h + x if self.residual else h
 
     def fuse(self):
+        if self.fused:  # already folded: the BNs are gone
+            return self
         if self.has_expand:
             self.expand = I.ConvSiLU2d(fuse_conv_bn_eval(self.expand, self.bn0))
         self.dw = I.ConvSiLU2d(fuse_conv_bn_eval(self.dw, self.bn1))
@@ -209,6 +216,7 @@ class MBConv(tnn.Module):
         self.project = I.ConvAdd2d(p) if self.residual else p
         self.bn0 = self.bn1 = self.bn2 = None
         self.fused = True
+        return self
 
 
 class EfficientNetB0(tnn.Module):
@@ -237,6 +245,8 @@ class EfficientNetB0(tnn.Module):
 
     def fuse(self):
         self.eval()
+        if self.fused:  # already folded
+            return self
         self.stem = I.ConvSiLU2d(fuse_conv_bn_eval(self.stem, self.bn))
         self.head = I.ConvSiLU2d(fuse_conv_bn_eval(self.head, self.bn_head))
         self.bn = self.bn_head = None
@@ -294,8 +304,9 @@ class EncoderLayer(tnn.Module):
         input quantizers (``Linear(x, pre_norm=ln)``) and the GELU in fc2's
         (``pre_act``): fc1 writes its f32 output once and fc2 reads it once. (The GELU in
         fc1's epilogue instead cost the GEMM what the separate pass cost: measured.)"""
-        self.proj_f = I.LinearAdd(self.proj)
-        self.fc2_f = I.LinearAdd(self.fc2)
+        if self.proj_f is None:
+            self.proj_f = I.LinearAdd(self.proj)
+            self.fc2_f = I.LinearAdd(self.fc2)
         return self
 
 

@@ -34,4 +34,13 @@ def fuse_conv_bn_eval(conv, bn, transpose=False):
     fused = copy.deepcopy(conv)
     fused.weight, fused.bias = fuse_conv_bn_weights(
         fused.weight, fused.bias, bn.running_mean, bn.running_var, bn.eps, bn.weight, bn.bias, transpose)
+    # An int8 packing (and calibrated scales) describe the unfolded weights: the copy must
+    # not keep running them. It is re-packed from the folded weights when the original was
+    # packed, and its scales are dropped (they measured the unfolded layer's output).
+    packed = getattr(fused, "int8", None) is not None
+    for attr in ("int8", "in_scale", "out_scale", "in_scale_v", "out_scale_v", "_calib"):
+        if hasattr(fused, attr):
+            setattr(fused, attr, None)
+    if packed:
+        fused.quantize_int8()
     return fused

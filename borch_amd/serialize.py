@@ -62,6 +62,18 @@ def _expected(mod) -> dict:
     return {"kind": "dw", "C": O, "cpad": _i8.round_up(O, 4), "KH": KH, "KW": KW}
 
 
+def _packed_shapes(rec: dict):
+    """(q shape, scale shape) of the packing a geometry record describes: a Linear's
+    ``[out, Kpad]`` (Kpad = in rounded up to 16, at least 16) and ``[out]``; a conv's
+    ``[O, KH*KW*cpad]`` and ``[O]``; a depthwise conv's ``[KH*KW, cpad]`` and ``[cpad]``."""
+    kind = rec["kind"]
+    if kind == "linear":
+        return (rec["out_features"], _i8.round_up(max(rec["in_features"], 16), 16)), (rec["out_features"],)
+    if kind == "conv":
+        return (rec["O"], rec["KH"] * rec["KW"] * rec["cpad"]), (rec["O"],)
+    return (rec["KH"] * rec["KW"], rec["cpad"]), (rec["cpad"],)
+
+
 def _i8_nn_linear():
     from .nn import Linear
     return Linear
@@ -93,6 +105,12 @@ def load_int8(model, path, device=None) -> int:
         if q.dtype != torch.int8 or s.dtype != torch.float32:
             raise ValueError(f"{path}: layer {name!r} has dtypes {q.dtype}/{s.dtype}")
         kind = rec["kind"]
+        # The kernels take their sizes from the record, not from the tensors: a tensor of
+        # any other shape would be read past its end.
+        want_q, want_s = _packed_shapes(rec)
+        if tuple(q.shape) != want_q or tuple(s.shape) != want_s:
+            raise ValueError(f"{path}: layer {name!r} has q {tuple(q.shape)} / scale {tuple(s.shape)}, "
+                             f"its geometry needs {want_q} / {want_s}")
         if kind == "linear":
             mod.int8 = _i8.Int8Weight(q, s, rec["in_features"], rec["out_features"], rec.get("weight_only", False))
         elif kind == "conv":

@@ -75,3 +75,29 @@ def test_loaded_model_matches_quantized_gpu(dev, tmp_path):
     x = torch.from_numpy(WL.c3_input(4, 5)).to(dev)
     with torch.no_grad():
         assert torch.equal(model(x), fresh(x))
+
+
+@pytest.mark.parametrize("layer,bad_q,bad_s", [
+    ("0", (2, 16), (1,)),      # conv: O=24, KH*KW*cpad=144 expected
+    ("0", (24, 144), (23,)),
+    ("2", (9, 20), (24,)),     # depthwise: [9, 24] / [24] expected
+    ("4", (10, 368), (10,)),   # linear: [10, 384] / [10] expected (a shorter q.shape[1] changes Kpad)
+])
+def test_truncated_tensor_raises(tmp_path, layer, bad_q, bad_s):
+    """The kernels size their reads from the geometry record: a packed tensor of any other
+    shape is refused on load instead of being read past its end."""
+    from safetensors.torch import load_file, save_file
+    from safetensors import safe_open
+    m = _small()
+    _pack_on_cpu(m)
+    f = tmp_path / "m.safetensors"
+    bt.save_int8(m, f)
+    with safe_open(str(f), framework="pt") as h:
+        meta = h.metadata()
+    t = load_file(str(f))
+    t[f"{layer}.q"] = torch.zeros(bad_q, dtype=torch.int8)
+    t[f"{layer}.scale"] = torch.ones(bad_s, dtype=torch.float32)
+    g = tmp_path / "bad.safetensors"
+    save_file(t, str(g), metadata=meta)
+    with pytest.raises(ValueError, match=f"layer '{layer}' has q"):
+        bt.load_int8(_small(), g, device="cpu")
