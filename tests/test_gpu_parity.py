@@ -513,7 +513,9 @@ def test_dwconv(dev, N, C, H, k, stride, pad):
 
 @pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (2, 17, 16), (5, 300, 1040), (8, 64, 8192), (1, 33, 2048),
                                    (64, 96, 768), (3, 4100, 4096), (4, 256, 4096), (5, 64, 3072),
-                                   (8, 512, 4096), (7, 130, 2064)])
+                                   (8, 512, 4096), (7, 130, 2064),
+                                   # the per-wave kernel's 128 KB LDS staging (M * K in (16384, 32768])
+                                   (3, 130, 8192), (4, 257, 6144)])
 def test_w8a32_linear(dev, M, N, K):
     say(f"w8a32 M={M} N={N} K={K}")
     rng = np.random.default_rng(M * 7 + N + K)
@@ -526,8 +528,42 @@ def test_w8a32_linear(dev, M, N, K):
     assert np.array_equal(n(I.dequant_weight(w8)), O.dequant_weight(qw_o, sw_o))
     y = n(I.linear_w8a32(t(x, dev), w8, t(b, dev)))
     y_o, bound = O.linear_w8a32(x, qw_o, sw_o, b)
+    _check_w8a32(y, y_o, bound, x, qw_o, sw_o)
+
+
+def _check_w8a32(y, y_o, bound, x, qw_o, sw_o):
+    """Every output within the f32-accumulation bound of the float64 result on the same
+    effective weights; the achieved error is printed relative to sum |x * w| (the scale
+    the bound is proportional to) and to |y| where |y| is not tiny."""
+    N = y_o.shape[-1]
     err = np.abs(y.astype(np.float64) - y_o)
     assert np.all(err <= bound + 1e-30), f"max err {err.max()} vs bound {bound[err.argmax() // N, err.argmax() % N]}"
+    mag = np.abs(x.astype(np.float64)) @ np.abs(O.dequant_weight(qw_o, sw_o).astype(np.float64)).T
+    big = np.abs(y_o) > 1e-3 * np.abs(y_o).max()
+    say(f"  max err / sum|x*w| = {(err / np.maximum(mag, 1e-30)).max():.3g}, "
+        f"max rel err (|y| > 1e-3 max) = {(err[big] / np.abs(y_o[big])).max():.3g}, "
+        f"max err / bound = {(err / bound).max():.3g}")
+
+
+@pytest.mark.parametrize("act", [I.ACT_RELU, I.ACT_GELU, I.ACT_SILU])
+@pytest.mark.parametrize("M", [1, 3, 6])
+def test_w8a32_activation(dev, M, act):
+    """The W8A32 epilogue's activation after the bias: ReLU exactly on the kernel's own f32
+    sum, SiLU / GELU within 1e-5 rel / 1e-6 abs of the closed form of that sum."""
+    say(f"w8a32 act={act} M={M}")
+    rng = np.random.default_rng(40 + M + act)
+    N, K = 200, 1024
+    x = rng.normal(size=(M, K)).astype(np.float32)
+    w = rng.normal(size=(N, K)).astype(np.float32) * np.float32(0.05)
+    b = rng.normal(size=N).astype(np.float32)
+    w8 = I.pack_linear_weight(t(w, dev), weight_only=True)
+    plain = n(I.linear_w8a32(t(x, dev), w8, t(b, dev)))
+    got = n(I.linear_w8a32(t(x, dev), w8, t(b, dev), act))
+    if act == I.ACT_RELU:
+        assert np.array_equal(got, np.where(plain > 0, plain, np.float32(0)))
+    else:
+        want = O.silu(plain) if act == I.ACT_SILU else O.gelu(plain)
+        np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
 
 
 def test_w8a32_module(dev):
