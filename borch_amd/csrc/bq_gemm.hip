@@ -1255,18 +1255,49 @@ static int split_of(const GemmP& p, int cfg, bool conv, int planned) {
   return (S > 1 && (need > SPLIT_WS_BYTES || tiles * 4 > (long long)SPLIT_CNT_BYTES)) ? 1 : S;
 }
 
-}  // namespace bq
+// The split-K workspace of bq_gemm_i8_noalloc: SPLIT_WS_BYTES of the library's own device
+// memory, one copy on every GPU the library runs on, held until the process ends. In host
+// code `scratch` names a host-side stand-in, never the device memory: the device address
+// of each GPU's copy comes from hipGetSymbolAddress with that GPU current, and only that
+// address is passed to kernels.
+static __device__ __align__(256) unsigned char scratch[SPLIT_WS_BYTES];
 
-using namespace bq;
+constexpr int SCRATCH_MAX_DEVICES = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[SCRATCH_MAX_DEVICES];  // per device ordinal; null until set up
 
-extern "C" {
+__global__ void zero_words_kernel(uint32_t* __restrict__ p, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
+}
 
-size_t bq_gemm_ws_bytes(void) { return SPLIT_WS_BYTES; }
+// The current device's scratch address, set up on its first call: the symbol's address
+// looked up once, with that device current, and the tile counters (the part that must
+// start at zero; every launch leaves them zero again) cleared by a kernel on `st`.
+static int noalloc_scratch(const char* what, hipStream_t st, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return set_error(BQ_ERR_DEVICE, "%s: hipGetDevice: %s", what, hipGetErrorString(e));
+  if (dev < 0 || dev >= SCRATCH_MAX_DEVICES)
+    return set_error(BQ_ERR_DEVICE, "%s: device %d beyond the %d this library keeps scratch for", what, dev,
+                     SCRATCH_MAX_DEVICES);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return set_error(BQ_ERR_DEVICE, "%s: hipGetSymbolAddress(scratch): %s", what, hipGetErrorString(e));
+    zero_words_kernel<<<1, 256, 0, st>>>(static_cast<uint32_t*>(ptr), (int)(SPLIT_CNT_BYTES / 4));
+    const int rc = check_launch(what);
+    if (rc != BQ_OK) return rc;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return BQ_OK;
+}
 
-int bq_gemm_i8(const int8_t* A, const int8_t* W, int64_t M, int64_t N, int64_t K, const float* sA,
-               const float* sW, const float* bias, const float* residual, int act, float* out, int32_t* acc,
-               void* ws, size_t ws_bytes, bq_stream_t stream) {
-  const char* what = "bq_gemm_i8";
+static int gemm_impl(const char* what, const int8_t* A, const int8_t* W, int64_t M, int64_t N, int64_t K,
+                     const float* sA, const float* sW, const float* bias, const float* residual, int act,
+                     float* out, int32_t* acc, void* ws, size_t ws_bytes, bool noalloc, bq_stream_t stream) {
   if (M < 0 || N < 0 || K < 0) return set_error(BQ_ERR_ARG, "%s: negative size", what);
   if (M > 0x7fffffff || N > 0x7fffffff || M * N > ((int64_t)1 << 40))
     return set_error(BQ_ERR_ARG, "%s: size too large", what);
@@ -1303,10 +1334,37 @@ int bq_gemm_i8(const int8_t* A, const int8_t* W, int64_t M, int64_t N, int64_t K
       default: skinny_i8_kernel<4, 8, 1><<<grid, 8 * 64, 0, st>>>(p); break;
     }
   } else {
+    if (noalloc) {
+      const int rc = noalloc_scratch(what, st, &ws);
+      if (rc != BQ_OK) return rc;
+      ws_bytes = SPLIT_WS_BYTES;
+    }
     apply_plan(p, dense_key(M, N, K));
     launch_gemm<false>(p, st, Ws{ws, ws_bytes});
   }
   return check_launch(what);
+}
+
+}  // namespace bq
+
+using namespace bq;
+
+extern "C" {
+
+size_t bq_gemm_ws_bytes(void) { return SPLIT_WS_BYTES; }
+
+int bq_gemm_i8(const int8_t* A, const int8_t* W, int64_t M, int64_t N, int64_t K, const float* sA,
+               const float* sW, const float* bias, const float* residual, int act, float* out, int32_t* acc,
+               void* ws, size_t ws_bytes, bq_stream_t stream) {
+  return gemm_impl("bq_gemm_i8", A, W, M, N, K, sA, sW, bias, residual, act, out, acc, ws, ws_bytes, false,
+                   stream);
+}
+
+int bq_gemm_i8_noalloc(const int8_t* A, const int8_t* W, int64_t M, int64_t N, int64_t K, const float* sA,
+                       const float* sW, const float* bias, const float* residual, int act, float* out,
+                       int32_t* acc, bq_stream_t stream) {
+  return gemm_impl("bq_gemm_i8_noalloc", A, W, M, N, K, sA, sW, bias, residual, act, out, acc, nullptr, 0, true,
+                   stream);
 }
 
 static int conv_impl(const char* what, const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t C,

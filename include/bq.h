@@ -157,6 +157,21 @@ int bq_gemm_i8(const int8_t* A, const int8_t* W, int64_t M, int64_t N, int64_t K
                const float* sA, const float* sW, const float* bias, const float* residual, int act,
                float* out, int32_t* acc, void* ws, size_t ws_bytes, bq_stream_t stream);
 
+/* bq_gemm_i8 that allocates nothing and takes no workspace: the same arguments without
+ * ws / ws_bytes, the same kernels and bit-identical results. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). Its split-K workspace is
+ * the library's own static device array of bq_gemm_ws_bytes() bytes (about 6.5 MiB), one
+ * copy per GPU, held until the process ends. That size covers the K split the rule picks
+ * for every shape, so no shape is refused for its size; every other limit is
+ * bq_gemm_i8's. The first call on a device looks up that device's copy and enqueues one
+ * small kernel on `stream` that zeroes its tile counters (every launch leaves them zero
+ * again). All calls on one GPU share that GPU's copy: calls that overlap on one GPU (two
+ * streams, or two threads) race and give wrong results. */
+int bq_gemm_i8_noalloc(const int8_t* A, const int8_t* W, int64_t M, int64_t N, int64_t K, const float* sA,
+                       const float* sW, const float* bias, const float* residual, int act, float* out,
+                       int32_t* acc, bq_stream_t stream);
+
 /* Implicit-GEMM int8 convolution, NHWC, groups 1, dilation 1:
  *   x int8 [N, H, W, C] (C % 16 == 0, per-tensor scale sA f32 [1]),
  *   w int8 [O, KH, KW, C] (per-channel scale sW f32 [O]),
