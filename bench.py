@@ -369,6 +369,44 @@ def bench_models(dev, stream, steps, layers_out=None):
     return out
 
 
+def w8a32_rows(dev, stream):
+    """Weight-only W8A32 Linear (bq_linear_w8a32: the int8 weight read inside the kernel)
+    beside the unpack-then-f32-GEMM path it replaces (bq_dequant_i8 writes the f32 weight,
+    torch-ROCm's f32 GEMM reads it): M = 16 and 256 on the 4096 x 4096 weight (24 rotated
+    copies, cache-cold), M = 6304 on ViT-B/16 b32's MLP shapes. Also the f32 GEMM alone on a
+    weight unpacked beforehand (what a resident f32 weight would cost)."""
+    import torch
+    from borch_amd import int8 as I
+    from borch_amd import workloads as WL
+    rows = {}
+    for M, N, K, copies in ((16, 4096, 4096, 24), (256, 4096, 4096, 24), (6304, 3072, 768, 4), (6304, 768, 3072, 4)):
+        rng = np.random.default_rng(M + N + K)
+        X = torch.from_numpy(rng.normal(size=(M, K)).astype(np.float32)).to(dev)
+        Wt = torch.from_numpy((rng.normal(size=(N, K)) / np.sqrt(K)).astype(np.float32)).to(dev)
+        Bv = torch.from_numpy((0.1 * rng.normal(size=N)).astype(np.float32)).to(dev)
+        w8 = I.pack_linear_weight(Wt, weight_only=True)
+        del Wt
+        ws = [I.Int8Weight(w8.q.clone(), w8.s, K, N, True) for _ in range(copies)]
+        g = capture(lambda i: I.linear_w8a32(X, ws[i], Bv), copies)
+        t_ours = time_graph(g, copies, 6, stream)
+        del g
+        g = capture(lambda i: torch.nn.functional.linear(X, I.dequant_weight(ws[i]), Bv), copies)
+        t_old = time_graph(g, copies, 6, stream)
+        del g
+        wf = [I.dequant_weight(w) for w in ws[:4]]
+        g = capture(lambda i: torch.nn.functional.linear(X, wf[i % 4], Bv), copies)
+        t_f32 = time_graph(g, copies, 6, stream)
+        del g, wf, ws
+        flops = 2 * M * N * K
+        rows[f"M{M}_N{N}_K{K}"] = {"us": round(t_ours * 1e3, 2), "dequant_then_f32_gemm_us": round(t_old * 1e3, 2),
+                                   "f32_gemm_on_unpacked_weight_us": round(t_f32 * 1e3, 2),
+                                   "TFLOPs": round(flops / (t_ours * 1e-3) / 1e12, 1),
+                                   "weight_GBps": round(N * K / (t_ours * 1e-3) / 1e9, 1)}
+        log(f"W8A32 M={M} N={N} K={K}: {rows[f'M{M}_N{N}_K{K}']}")
+        torch.cuda.empty_cache()
+    return rows
+
+
 def print_layer_tables(models, tables):
     """Markdown: per model, the forward times and one row per int8 layer timed alone."""
     for key, rows in tables.items():
@@ -541,6 +579,7 @@ def main():
                          "hbm_frac": round(wbytes / (t_w * 1e-3) / 1e9 / PEAK_HBM_GBS, 4), "bytes": wbytes}
     log(f"W8A32 M=1: {sweep['W8A32_M1']}")
     del g_w, qws, w8v, w8s
+    sweep["W8A32"] = w8a32_rows(dev, stream)
     # C1: the Linear 16x512x512 through nn.Linear (per-row quantize + GEMM), latency
     from borch_amd import nn as bnn
     x_c1, w_c1, b_c1 = WL.c1_linear(0)

@@ -36,6 +36,27 @@ __device__ __forceinline__ int fdiv(int n, uint32_t mul, int shift) {
   return (int)((__umulhi((uint32_t)n, mul) + (uint32_t)n) >> shift);
 }
 
+// Workgroup -> output tile. Workgroups are dispatched round-robin over the 8 XCDs (each
+// with its own L2), so workgroup id is first regrouped by XCD (xcd_order: consecutive
+// regrouped ids run on one XCD; the K splits of a tile are consecutive), then tiles are handed out
+// in bands of 8 tile columns walking down M: the 32 workgroups of one XCD at a 4096^2
+// problem cover a 4 x 8 block of tiles, and each K step's A and W slabs are fetched into
+// that XCD's L2 once and then shared.
+__device__ __forceinline__ int xcd_order(int id, int G) {
+  constexpr int XCDS = 8;
+  return G % XCDS == 0 ? (id % XCDS) * (G / XCDS) + id / XCDS : id;
+}
+__device__ __forceinline__ void tile_of(int id, int tiles_m, int tiles_n, int& bm, int& bn) {
+  constexpr int GROUP = 8;
+  const int per_group = GROUP * tiles_m;
+  const int g = id / per_group;
+  const int first_n = g * GROUP;
+  const int gsize = min(tiles_n - first_n, GROUP);
+  const int in = id - g * per_group;
+  bm = in / gsize;
+  bn = first_n + in % gsize;
+}
+
 // Wave64 max of a non-negative float; every lane of the wave must be active (each caller
 // reaches it with the whole workgroup, before a barrier or a per-wave store). Within each
 // row of 16 lanes by DPP (quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror, row_mirror),

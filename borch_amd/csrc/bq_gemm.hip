@@ -93,27 +93,6 @@ __device__ __forceinline__ v4i buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off
 // two 128-byte halves of the 256-byte bank line). Measured: zero LDS bank conflicts.
 __device__ __forceinline__ int lds_off(int r, int c) { return r * BK + ((c ^ ((r >> 1) & 7)) << 4); }
 
-// Workgroup -> output tile. Workgroups are dispatched round-robin over the 8 XCDs (each
-// with its own L2), so workgroup id is first regrouped by XCD (xcd_order: consecutive
-// regrouped ids run on one XCD; the K splits of a tile are consecutive), then tiles are handed out
-// in bands of 8 tile columns walking down M: the 32 workgroups of one XCD at a 4096^2
-// problem cover a 4 x 8 block of tiles, and each K step's A and W slabs are fetched into
-// that XCD's L2 once and then shared.
-__device__ __forceinline__ int xcd_order(int id, int G) {
-  constexpr int XCDS = 8;
-  return G % XCDS == 0 ? (id % XCDS) * (G / XCDS) + id / XCDS : id;
-}
-__device__ __forceinline__ void tile_of(int id, int tiles_m, int tiles_n, int& bm, int& bn) {
-  constexpr int GROUP = 8;
-  const int per_group = GROUP * tiles_m;
-  const int g = id / per_group;
-  const int first_n = g * GROUP;
-  const int gsize = min(tiles_n - first_n, GROUP);
-  const int in = id - g * per_group;
-  bm = in / gsize;
-  bn = first_n + in % gsize;
-}
-
 // Scheduling hints: NMMA MFMAs, each followed by up to ceil(COUNT/NMMA) instructions of
 // class MASK (0x008 MFMA, 0x020 VMEM read, 0x100 DS read, 0x200 DS write), so memory
 // instructions issue between MFMAs instead of in one block.

@@ -285,8 +285,7 @@ def quantize_nhwc_scaled(x: torch.Tensor, scale: torch.Tensor, cpad: int | None 
 @dataclass
 class Int8Weight:
     """A Linear weight packed for ``bq_gemm_i8``: ``q int8 [N, Kpad]``, ``s f32 [N]``.
-    ``weight_only`` selects W8A32 (f32 activations, ``bq_gemv_w8a32`` / dequant + f32 GEMM)
-    instead of W8A8."""
+    ``weight_only`` selects W8A32 (f32 activations, ``bq_linear_w8a32``) instead of W8A8."""
     q: torch.Tensor
     s: torch.Tensor
     in_features: int
@@ -341,10 +340,11 @@ def dequant_weight(w8: Int8Weight) -> torch.Tensor:
     return out
 
 
-def linear_w8a32(x: torch.Tensor, w8: Int8Weight, bias=None, act=ACT_NONE) -> torch.Tensor:
-    """Weight-only int8 Linear (W8A32, matmul(..., weightInt8), kernels.ts:2695-2708):
-    effective weight f32(q)·s, f32 accumulation. M <= 8: the streaming GEMV kernel; larger
-    M: the dequant pass, then torch-ROCm's f32 GEMM (the reference's fallback)."""
+def linear_w8a32(x: torch.Tensor, w8: Int8Weight, bias=None, act=ACT_NONE, residual=None) -> torch.Tensor:
+    """Weight-only int8 Linear (W8A32, matmul(..., weightInt8), kernels.ts:2661-2753): f32
+    activations against the int8 weight read inside the kernel (bq_linear_w8a32; no f32 copy
+    of the weight is made), effective weight f32(q)·s, f32 accumulation; ``residual [..., N]``
+    is added after the bias and before ``act``."""
     if x.shape[-1] != w8.in_features:
         raise RuntimeError(f"mat1 and mat2 shapes cannot be multiplied "
                            f"({'x'.join(str(n) for n in x.reshape(-1, x.shape[-1]).shape)} and "
@@ -356,13 +356,15 @@ def linear_w8a32(x: torch.Tensor, w8: Int8Weight, bias=None, act=ACT_NONE) -> to
         x2 = torch.nn.functional.pad(x2, (0, w8.kpad - w8.in_features))
     M, K = x2.shape
     N = w8.out_features
-    if M <= 8 and K <= 8192:
-        out = torch.empty((M, N), dtype=torch.float32, device=x.device)
-        b = _vec(bias, N, "bias")
-        check(lib().bq_gemv_w8a32(x2.data_ptr(), w8.q.data_ptr(), M, N, K, w8.s.data_ptr(), _ptr(b), act,
-                                  out.data_ptr(), _stream(x2)))
-    else:
-        out = _act_f32(torch.nn.functional.linear(x2, dequant_weight(w8), bias), act)
+    out = torch.empty((M, N), dtype=torch.float32, device=x.device)
+    b = _vec(bias, N, "bias")
+    r = None
+    if residual is not None:
+        if tuple(residual.shape[:-1]) != tuple(lead) or residual.shape[-1] != N:
+            raise RuntimeError(f"residual shape {tuple(residual.shape)} != output {(*lead, N)}")
+        r = residual.reshape(M, N).float().contiguous()
+    check(lib().bq_linear_w8a32(x2.data_ptr(), w8.q.data_ptr(), M, N, K, w8.s.data_ptr(), _ptr(b), _ptr(r), act,
+                                out.data_ptr(), _stream(x2)))
     return out.reshape(*lead, N)
 
 
@@ -526,10 +528,7 @@ def linear(x: torch.Tensor, w8: Int8Weight, bias=None, act=ACT_NONE, residual=No
         x = _act_f32(x, pre_act)
         pre_act = ACT_NONE
     if w8.weight_only:
-        out = linear_w8a32(x, w8, bias, ACT_NONE if residual is not None else act)
-        if residual is not None:
-            out = _act_f32(out + residual, act)
-        return out
+        return linear_w8a32(x, w8, bias, act, residual)
     if x.shape[-1] != w8.in_features:
         a = "x".join(str(n) for n in (x.reshape(-1, x.shape[-1]).shape if x.dim() else ()))
         raise RuntimeError(

@@ -257,17 +257,31 @@ int bq_se_gate_nhwc(const float* x, int64_t N, int64_t HW, int64_t C, const floa
                     const float* w2t, const float* b2, float* gate, float* absmax_parts, void* ws, size_t ws_bytes,
                     bq_stream_t stream);
 
-/* Weight-only int8 (W8A32) GEMV for the decode shape, M <= 8: f32 x [M, K] against int8
- * W [N, K] with per-channel sW [N]; out f32 [M, N] = sum_k x * f32(f32(q) * sW[n]) (f32 FMA
- * accumulation, wave-tree reduction) + bias, then act. K % 16 == 0, K <= 8192.
- * Replaces matmul(..., weightInt8) (borch-ts/src/kernels.ts:2695-2708) for streamed weights
+/* Weight-only int8 (W8A32) Linear, any M: f32 x [M, K] against int8 W [N, K] with
+ * per-channel sW [N]; out f32 [M, N] = act(y + bias[n] + residual[m, n]) with y the f32 sum
+ * over k of x * f32(q) * sW[n] (bias, residual nullable; residual f32 [M, N]). M <= 16 (K <=
+ * 8192): wave-reduction GEMV kernels, the effective weight f32(f32(q) * sW[n]) per element
+ * and f32 FMA / f32-MFMA accumulation, as the reference. Otherwise a tiled bf16-MFMA kernel:
+ * q is exact in bf16 and each x is split exactly into three bf16 pieces, so every product is
+ * exact; the f32 accumulation is the only rounding before y = fl(sum * sW[n]). Either way
+ * every output is within (K + 2) 2^-24 sum_k |x * w| + 2^-24 |y| of the exact result on the
+ * effective weights w = f32(q) * sW. The int8 weight is read inside the kernel: no f32 copy
+ * of it is written. K % 16 == 0; x and W 16-byte aligned; x and W each < 2 GiB.
+ * Replaces matmul(..., weightInt8) (borch-ts/src/kernels.ts:2661-2753, the int8 read at
+ * 2695-2708) and its routing (tensor.ts:2553-2575) for streamed / windowed weights
  * (Tensor.inWindowInt8, tensor.ts:1681-1705; stream_sequential(int8=True),
  * borch_webgpu/_stream.py:61-66). */
+int bq_linear_w8a32(const float* x, const int8_t* W, int64_t M, int64_t N, int64_t K, const float* sW,
+                    const float* bias, const float* residual, int act, float* out, bq_stream_t stream);
+
+/* bq_linear_w8a32's decode-shape kernels alone (M <= 16, K <= 8192, no residual); the same
+ * results. Kept for callers bound to it. */
 int bq_gemv_w8a32(const float* x, const int8_t* W, int64_t M, int64_t N, int64_t K, const float* sW,
                   const float* bias, int act, float* out, bq_stream_t stream);
 
-/* w f32 [N, K] = f32(q[n, k]) * s[n] (one rounding): the weight-only fallback's unpack pass
- * for larger M. Replaces dequantInt8 (borch-ts/src/kernels.ts:1264-1274). */
+/* w f32 [N, K] = f32(q[n, k]) * s[n] (one rounding): the effective weights of a weight-only
+ * packing, unpacked (a consumer that needs them in f32). Replaces dequantInt8
+ * (borch-ts/src/kernels.ts:1264-1274). */
 int bq_dequant_i8(const int8_t* q, int64_t N, int64_t K, const float* s, float* w, bq_stream_t stream);
 
 #ifdef __cplusplus

@@ -57,6 +57,12 @@ def test_argument_checks_run_on_host():
     assert lib.bq_dwconv_i8_nhwc(None, 1, 4, 4, 6, None, 3, 3, 1, 1, None, None, None, 0, None, None,
                                  None) == _lib.BQ_ERR_UNSUPPORTED
     assert lib.bq_quantize_nhwc(None, 4, 3, 2, None, None, None, 0, None) == _lib.BQ_ERR_ARG
+    # the weight-only Linear: K % 16, sizes, and the decode-only entry's M and K limits
+    assert lib.bq_linear_w8a32(None, None, 4, 4, 20, None, None, None, 0, None, None) == _lib.BQ_ERR_UNSUPPORTED
+    assert lib.bq_linear_w8a32(None, None, -1, 4, 16, None, None, None, 0, None, None) == _lib.BQ_ERR_ARG
+    assert lib.bq_linear_w8a32(None, None, 40, 4, 16, None, None, None, 0, None, None) == _lib.BQ_ERR_ARG  # null
+    assert lib.bq_gemv_w8a32(None, None, 17, 4, 16, None, None, 0, None, None) == _lib.BQ_ERR_UNSUPPORTED
+    assert lib.bq_gemv_w8a32(None, None, 2, 4, 8208, None, None, 0, None, None) == _lib.BQ_ERR_UNSUPPORTED
     # past K = 133152 an int32 sum of int8 products could wrap: refused, not computed
     assert lib.bq_gemm_i8(None, None, 4, 4, 133168, None, None, None, None, 0, None, None, None, 0, None) == _lib.BQ_ERR_UNSUPPORTED
     assert "overflow" in _lib.last_error()

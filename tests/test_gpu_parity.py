@@ -515,7 +515,16 @@ def test_dwconv(dev, N, C, H, k, stride, pad):
                                    (64, 96, 768), (3, 4100, 4096), (4, 256, 4096), (5, 64, 3072),
                                    (8, 512, 4096), (7, 130, 2064),
                                    # the per-wave kernel's 128 KB LDS staging (M * K in (16384, 32768])
-                                   (3, 130, 8192), (4, 257, 6144)])
+                                   (3, 130, 8192), (4, 257, 6144),
+                                   # the f32-MFMA GEMV up to 16 rows
+                                   (16, 4096, 4096), (12, 70, 1040),
+                                   # the tiled bf16-MFMA kernel: 32 x 64 tiles (M <= 256), ragged
+                                   # edges, a K tail inside a 128-deep stage, K > 8192 at small M
+                                   (17, 300, 1040), (256, 4096, 4096), (100, 33, 2064), (5, 130, 8208),
+                                   # 64 x 64 tiles (M > 256, fewer than 256 128 x 128 tiles)
+                                   (300, 200, 2064), (1000, 520, 784),
+                                   # 128 x 128 tiles, and ViT-B/16's MLP shapes at b32
+                                   (1100, 4100, 1024), (6304, 3072, 768), (6304, 768, 3072)])
 def test_w8a32_linear(dev, M, N, K):
     say(f"w8a32 M={M} N={N} K={K}")
     rng = np.random.default_rng(M * 7 + N + K)
@@ -545,8 +554,27 @@ def _check_w8a32(y, y_o, bound, x, qw_o, sw_o):
         f"max err / bound = {(err / bound).max():.3g}")
 
 
+@pytest.mark.parametrize("M", [3, 10, 100, 700])
+def test_w8a32_residual(dev, M):
+    """The residual is added after the bias and before the activation (the W8A8 epilogue's
+    order), in every W8A32 kernel: the result equals the plain output plus the residual,
+    then ReLU, one f32 rounding each."""
+    say(f"w8a32 residual M={M}")
+    rng = np.random.default_rng(60 + M)
+    N, K = 136, 1040
+    x = rng.normal(size=(M, K)).astype(np.float32)
+    w = rng.normal(size=(N, K)).astype(np.float32) * np.float32(0.05)
+    b = rng.normal(size=N).astype(np.float32)
+    r = rng.normal(size=(M, N)).astype(np.float32)
+    w8 = I.pack_linear_weight(t(w, dev), weight_only=True)
+    plain = n(I.linear_w8a32(t(x, dev), w8, t(b, dev)))
+    got = n(I.linear_w8a32(t(x, dev), w8, t(b, dev), I.ACT_RELU, residual=t(r, dev)))
+    want = (plain + r).astype(np.float32)
+    assert np.array_equal(got, np.where(want > 0, want, np.float32(0)))
+
+
 @pytest.mark.parametrize("act", [I.ACT_RELU, I.ACT_GELU, I.ACT_SILU])
-@pytest.mark.parametrize("M", [1, 3, 6])
+@pytest.mark.parametrize("M", [1, 3, 6, 40])
 def test_w8a32_activation(dev, M, act):
     """The W8A32 epilogue's activation after the bias: ReLU exactly on the kernel's own f32
     sum, SiLU / GELU within 1e-5 rel / 1e-6 abs of the closed form of that sum."""
@@ -572,10 +600,20 @@ def test_w8a32_module(dev):
     torch.manual_seed(0)
     lin = bt.nn.Linear(768, 3072).to(dev)
     assert bt.quantize_for_int8(lin, weight_only=True) == 1
-    x = torch.randn(1, 768, device=dev)
-    y = n(lin(x))
-    y_o, bound = O.linear_w8a32(n(x), n(lin.int8.q), n(lin.int8.s), n(lin.bias))
-    assert np.all(np.abs(y - y_o) <= bound)
+    for rows in (1, 64):
+        x = torch.randn(rows, 768, device=dev)
+        y = n(lin(x))
+        y_o, bound = O.linear_w8a32(n(x), n(lin.int8.q), n(lin.int8.s), n(lin.bias))
+        assert np.all(np.abs(y - y_o) <= bound)
+    # the skip connection of a transformer layer (LinearAdd) rides in the W8A32 epilogue
+    from borch_amd.nn.intrinsic import LinearAdd
+    fused = LinearAdd(lin)
+    x = torch.randn(2, 33, 768, device=dev)
+    r = torch.randn(2, 33, 3072, device=dev)
+    y = n(fused(x, r))
+    y_o, bound = O.linear_w8a32(n(x).reshape(-1, 768), n(lin.int8.q), n(lin.int8.s), n(lin.bias))
+    y_o = y_o.reshape(2, 33, 3072) + n(r).astype(np.float64)
+    assert np.all(np.abs(y - y_o) <= bound.reshape(2, 33, 3072) + 2.0 ** -24 * np.abs(y_o))
 
 
 def _false_ties(count=512, seed=21):
