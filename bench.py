@@ -369,6 +369,44 @@ def bench_models(dev, stream, steps, layers_out=None):
     return out
 
 
+# The reference's published matmulInt8 points (docs/INT8.md:176, 222-225; RTX 5080, WebGPU):
+# context for the rows below, not a target (different hardware).
+MMI8_PUBLISHED = {1024: {"ms": 0.038, "TOPS": 56.6}, 2048: {"ms": 0.273, "TOPS": 62.9}}
+
+
+def mmi8_rows(dev, stream):
+    """The reference's int8 GEMM gate ``mmi8`` (tests/browser/kernel_bench.html:294-337) at its
+    published shapes 1024^3 and 2048^3: its LCG operands in [-8, 8), the int32 result checked
+    on every entry before anything is timed (against an exact float64 product on the device:
+    every partial sum is an integer below 2^53), then the dequantising store timed with a
+    per-tensor activation scale, per-channel weight scales and a bias (matmulInt8(scaled))."""
+    import torch
+    from borch_amd import int8 as I
+    from borch_amd import workloads as WL
+    rows = {}
+    for size in (1024, 2048):
+        A, W = WL.mmi8_operands(size, size, size)
+        At, Wt = torch.from_numpy(A).to(dev), torch.from_numpy(W).to(dev)
+        g = torch.Generator().manual_seed(size)
+        s0 = (0.5 + torch.rand(1, generator=g)).to(dev)
+        sw = (0.5 + torch.rand(size, generator=g)).to(dev)
+        bv = torch.randn(size, generator=g).to(dev)
+        out, acc = I.gemm_i8(At, Wt, s0, sw, bv, want_acc=True)
+        exact = (At.double() @ Wt.double().t()).to(torch.int32)
+        wrong = int((acc != exact).sum())
+        gk = capture(lambda i: I.gemm_i8(At, Wt, s0, sw, bv), 10)
+        t = time_graph(gk, 10, 8, stream)
+        del gk
+        ops = 2 * size ** 3
+        rows[f"{size}^3"] = {"kernel_us": round(t * 1e3, 3), "TOPS": round(ops / (t * 1e-3) / 1e12, 1),
+                             "mfma_frac": round(ops / (t * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4),
+                             "i32_wrong_entries": wrong, "entries": size * size,
+                             "reference_published_rtx5080": MMI8_PUBLISHED[size]}
+        log(f"mmi8 {size}^3: {rows[f'{size}^3']}")
+        del At, Wt, out, acc, exact
+    return rows
+
+
 def w8a32_rows(dev, stream):
     """Weight-only W8A32 Linear (bq_linear_w8a32: the int8 weight read inside the kernel)
     beside the unpack-then-f32-GEMM path it replaces (bq_dequant_i8 writes the f32 weight,
@@ -599,6 +637,7 @@ def main():
                                      "ops": 2 * 16 * 512 * 512,
                                      "bytes": 16 * 512 + 512 * 512 + 4 * 16 + 8 * 512 + 4 * 16 * 512}
     log(f"C1: {sweep['C1_linear_16x512x512']}")
+    sweep["mmi8"] = mmi8_rows(dev, stream)
     sweep["M4096"] = {"kernel_us": round(gemm_ms * 1e3, 3), "TOPS": round(gemm_tops, 1),
                       "mfma_frac": round(gemm_tops / PEAK_INT8_TOPS, 4),
                       "quantize_us": round(quant_ms * 1e3, 3),

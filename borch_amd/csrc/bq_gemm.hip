@@ -1287,10 +1287,12 @@ static int gemm_impl(const char* what, const int8_t* A, const int8_t* W, int64_t
   if (K % 16) return set_error(BQ_ERR_UNSUPPORTED, "%s: K=%lld is not a multiple of 16", what, (long long)K);
   if (!A || !W || !sA || !sW || !out) return set_error(BQ_ERR_ARG, "%s: null pointer", what);
   if (!aligned16(A) || !aligned16(W)) return set_error(BQ_ERR_ARG, "%s: A and W must be 16-byte aligned", what);
+  const bool sa_per_tensor = (act & BQ_SCALE_A_PER_TENSOR) != 0;
+  act &= ~BQ_SCALE_A_PER_TENSOR;
   if (act < BQ_ACT_NONE || act > BQ_ACT_GELU) return set_error(BQ_ERR_ARG, "%s: bad activation %d", what, act);
   GemmP p{};
   p.A = A; p.W = W; p.M = (int)M; p.N = (int)N; p.K = (int)K;
-  p.sA = sA; p.sa_per_row = 1; p.sW = sW; p.bias = bias; p.res = residual; p.act = act;
+  p.sA = sA; p.sa_per_row = sa_per_tensor ? 0 : 1; p.sW = sW; p.bias = bias; p.res = residual; p.act = act;
   p.out = out; p.acc = acc;
   p.vec_ok = (N % 4 == 0) && aligned16(out) && aligned16(acc) && aligned16(residual);
   hipStream_t st = (hipStream_t)stream;

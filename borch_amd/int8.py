@@ -15,7 +15,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from ._lib import ACT_GELU, ACT_NONE, ACT_RELU, ACT_SILU, check, lib, require_device
+from ._lib import ACT_GELU, ACT_NONE, ACT_RELU, ACT_SILU, SCALE_A_PER_TENSOR, check, lib, require_device
 
 __all__ = [
     "ACT_NONE", "ACT_RELU", "ACT_SILU", "ACT_GELU", "Int8Weight", "Int8ConvWeight", "Int8DwWeight",
@@ -285,12 +285,15 @@ def quantize_nhwc_scaled(x: torch.Tensor, scale: torch.Tensor, cpad: int | None 
 @dataclass
 class Int8Weight:
     """A Linear weight packed for ``bq_gemm_i8``: ``q int8 [N, Kpad]``, ``s f32 [N]``.
-    ``weight_only`` selects W8A32 (f32 activations, ``bq_linear_w8a32``) instead of W8A8."""
+    ``weight_only`` selects W8A32 (f32 activations, ``bq_linear_w8a32``) instead of W8A8;
+    ``per_tensor`` quantizes the W8A8 activations with one scale for the whole input (the
+    reference's ``matmulInt8(scaled)``, kernels.ts:1818-1827) instead of one per row."""
     q: torch.Tensor
     s: torch.Tensor
     in_features: int
     out_features: int
     weight_only: bool = False
+    per_tensor: bool = False  # W8A8 with one activation scale per call (the reference's matmulInt8)
 
     @property
     def kpad(self) -> int:
@@ -322,13 +325,15 @@ class Int8DwWeight:
     KW: int
 
 
-def pack_linear_weight(w: torch.Tensor, weight_only: bool = False) -> Int8Weight:
+def pack_linear_weight(w: torch.Tensor, weight_only: bool = False, per_tensor: bool = False) -> Int8Weight:
     """Quantize once (quant.ts:23-53); K padded to a multiple of 16 with zeros (exact)."""
+    if weight_only and per_tensor:
+        raise ValueError("per_tensor is an activation quantization: a weight-only Linear has none")
     N, K = w.shape
     kp = round_up(max(K, 16), 16)
     wp = w if kp == K else torch.nn.functional.pad(w, (0, kp - K))
     q, s = quantize_weight_per_channel(wp.float())
-    return Int8Weight(q, s, K, N, weight_only)
+    return Int8Weight(q, s, K, N, weight_only, per_tensor)
 
 
 def dequant_weight(w8: Int8Weight) -> torch.Tensor:
@@ -398,7 +403,8 @@ def pack_dw_weight(w: torch.Tensor) -> Int8DwWeight:
 
 def gemm_i8(qa, qw, sa, sw, bias=None, act=ACT_NONE, want_acc=False, residual=None):
     """``out = ((f32(qa @ qw.T) * sa[m]) * sw[n]) + bias[n]`` (+ ``residual [M, N]``) then
-    act (bq_gemm_i8). Returns ``out`` or ``(out, acc int32)``."""
+    act (bq_gemm_i8). ``sa`` holds one scale per row of ``qa``, or one for the whole of it
+    (a per-tensor quantization: ``sa.numel() == 1``). Returns ``out`` or ``(out, acc int32)``."""
     _need(qa, "A", torch.int8)
     _need(qw, "W", torch.int8)
     M, K = qa.shape
@@ -407,8 +413,10 @@ def gemm_i8(qa, qw, sa, sw, bias=None, act=ACT_NONE, want_acc=False, residual=No
         raise RuntimeError(f"mat1 and mat2 shapes cannot be multiplied ({M}x{K} and {K2}x{N})")
     qa, qw = qa.contiguous(), qw.contiguous()
     sa, sw = sa.contiguous().float(), sw.contiguous().float()
-    if sa.numel() != M or sw.numel() != N:
+    if sa.numel() not in (M, 1) or sw.numel() != N:
         raise ValueError("scale sizes do not match the operands")
+    if sa.numel() == 1:  # one activation scale (for M == 1 both readings are the same)
+        act = act | SCALE_A_PER_TENSOR
     b = _vec(bias, N, "bias")
     r = None
     if residual is not None:
@@ -524,7 +532,7 @@ def linear(x: torch.Tensor, w8: Int8Weight, bias=None, act=ACT_NONE, residual=No
     optional ``residual [..., N]`` added in the epilogue before ``act``. ``pre_act`` applies
     an activation to ``x`` first, inside the input quantizer. A weight-only packing runs
     ``linear_w8a32`` instead."""
-    if pre_act != ACT_NONE and (w8.weight_only or w8.kpad != w8.in_features):
+    if pre_act != ACT_NONE and (w8.weight_only or w8.per_tensor or w8.kpad != w8.in_features):
         x = _act_f32(x, pre_act)
         pre_act = ACT_NONE
     if w8.weight_only:
@@ -537,7 +545,7 @@ def linear(x: torch.Tensor, w8: Int8Weight, bias=None, act=ACT_NONE, residual=No
     x2 = x.reshape(-1, x.shape[-1])
     if w8.kpad != w8.in_features:
         x2 = torch.nn.functional.pad(x2, (0, w8.kpad - w8.in_features))
-    qa, sa = quantize_rows(x2, pre_act)
+    qa, sa = quantize_tensor(x2) if w8.per_tensor else quantize_rows(x2, pre_act)
     r = None if residual is None else residual.reshape(-1, w8.out_features)
     out = gemm_i8(qa, w8.q, sa, w8.s, bias, act, residual=r)
     return out.reshape(*lead, w8.out_features)
@@ -566,7 +574,7 @@ def fusable_layernorm(ln, x: torch.Tensor, w8: Int8Weight) -> bool:
     """Whether ``ln`` (a torch LayerNorm) can run inside the W8A8 Linear's input quantizer."""
     K = x.shape[-1] if x.dim() else 0
     return (isinstance(ln, torch.nn.LayerNorm) and tuple(ln.normalized_shape) == (K,) and x.is_cuda
-            and x.dtype == torch.float32 and not w8.weight_only and K % 4 == 0 and K <= 4096
+            and x.dtype == torch.float32 and not w8.weight_only and not w8.per_tensor and K % 4 == 0 and K <= 4096
             and w8.kpad == K == w8.in_features)
 
 

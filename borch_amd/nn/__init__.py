@@ -66,13 +66,16 @@ class Linear(_tnn.Module):
         self.int8 = None  # Int8Weight once quantize_int8() has run
         self.act = _i8.ACT_NONE  # fused epilogue activation (LinearReLU sets RELU)
 
-    def quantize_int8(self, weight_only: bool = False) -> bool:
+    def quantize_int8(self, weight_only: bool = False, per_tensor: bool = False) -> bool:
         """Packs the weight once per output channel (quant.ts:23-53). Any shape is taken
         (K is zero-padded to a multiple of 16). ``weight_only`` keeps activations f32
-        (W8A32, the reference's int8 window weight, tensor.ts:1681-1705). Returns True."""
+        (W8A32, the reference's int8 window weight, tensor.ts:1681-1705); ``per_tensor``
+        quantizes the activations with one scale for the whole input, as the reference's
+        ``matmulInt8(scaled)`` takes them (kernels.ts:1818-1827), instead of one per row.
+        Returns True."""
         require_device(self.weight.device)
         with torch.no_grad():
-            self.int8 = _i8.pack_linear_weight(self.weight.detach(), weight_only)
+            self.int8 = _i8.pack_linear_weight(self.weight.detach(), weight_only, per_tensor)
         return True
 
     def forward(self, x, residual=None, pre_norm=None, pre_act=None):
@@ -312,13 +315,15 @@ def _int8_layers(model):
 
 
 def quantize_for_int8(model, linear: bool = True, conv: bool = True, weight_only: bool = False,
-                      rule: str = "all") -> int:
+                      rule: str = "all", per_tensor: bool = False) -> int:
     """Every Linear / Conv2d of ``model`` the int8 kernels take, quantized once; returns
     how many took it (borch-ts/src/nn.ts:6770-6780). Refused by name where the device has
     no int8 kernels (nn.ts:6771-6773): the path is an accuracy trade a caller asks for and
     must not silently become the f32 forward. ``rule="reference"`` restricts convs to the
     shapes the reference's int8 conv takes (13 of CIFAR ResNet-18's 20), for comparison
-    with its published numbers; the default takes every conv this library can."""
+    with its published numbers; the default takes every conv this library can.
+    ``per_tensor`` gives W8A8 Linears one activation scale per call (the reference's
+    matmulInt8) instead of one per row."""
     if rule not in ("all", "reference"):
         raise ValueError(f"rule must be 'all' or 'reference', not {rule!r}")
     layers = list(_int8_layers(model))
@@ -332,7 +337,7 @@ def quantize_for_int8(model, linear: bool = True, conv: bool = True, weight_only
     taken = 0
     for _, mod in layers:
         if isinstance(mod, Linear) and linear:
-            taken += bool(mod.quantize_int8(weight_only))
+            taken += bool(mod.quantize_int8(weight_only, per_tensor))
         elif isinstance(mod, Conv2d) and conv:
             taken += bool(mod.quantize_int8(rule))
     return taken

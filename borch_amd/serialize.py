@@ -29,8 +29,11 @@ FORMAT = "borch_amd-int8/1"
 
 def _record(w8) -> dict:
     if isinstance(w8, _i8.Int8Weight):
-        return {"kind": "linear", "in_features": w8.in_features, "out_features": w8.out_features,
-                "weight_only": bool(w8.weight_only)}
+        rec = {"kind": "linear", "in_features": w8.in_features, "out_features": w8.out_features,
+               "weight_only": bool(w8.weight_only)}
+        if w8.per_tensor:
+            rec["per_tensor"] = True
+        return rec
     if isinstance(w8, _i8.Int8ConvWeight):
         return {"kind": "conv", "O": w8.O, "C": w8.C, "cpad": w8.cpad, "KH": w8.KH, "KW": w8.KW}
     if isinstance(w8, _i8.Int8DwWeight):
@@ -97,6 +100,8 @@ def load_int8(model, path, device=None) -> int:
         want = _expected(mod)
         if rec.get("kind") == "linear":
             want["weight_only"] = bool(rec.get("weight_only", False))
+            if rec.get("per_tensor"):
+                want["per_tensor"] = True
         if rec != want:
             raise ValueError(f"{path}: layer {name!r} is {rec}, the model has {want}")
         dev = device if device is not None else mod.weight.device
@@ -112,7 +117,8 @@ def load_int8(model, path, device=None) -> int:
             raise ValueError(f"{path}: layer {name!r} has q {tuple(q.shape)} / scale {tuple(s.shape)}, "
                              f"its geometry needs {want_q} / {want_s}")
         if kind == "linear":
-            mod.int8 = _i8.Int8Weight(q, s, rec["in_features"], rec["out_features"], rec.get("weight_only", False))
+            mod.int8 = _i8.Int8Weight(q, s, rec["in_features"], rec["out_features"], rec.get("weight_only", False),
+                                      bool(rec.get("per_tensor", False)))
         elif kind == "conv":
             mod.int8 = _i8.Int8ConvWeight(q, s, rec["O"], rec["C"], rec["cpad"], rec["KH"], rec["KW"])
         else:

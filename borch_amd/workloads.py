@@ -58,6 +58,39 @@ def c5_input(batch: int = 32, tokens: int = 197, dim: int = 768, seed: int = 0):
     return _normal(rng, (batch, tokens, dim), 1.0)
 
 
+def lcg_int8(n: int, seed: int) -> np.ndarray:
+    """The int8 operands of the reference's exactness gate ``mmi8``
+    (tests/browser/kernel_bench.html:300-301): ``st = st * 1664525 + 1013904223`` (mod 2^32)
+    from ``st = seed``, each value ``(st >> 28) - 8``, in [-8, 7]. Vectorised by jumping
+    ahead: within a block of B steps, ``st_{j} = a^j st_0 + c (a^{j-1} + ... + 1)``."""
+    a, c, B = 1664525, 1013904223, 4096
+    mask = np.uint64(0xFFFFFFFF)
+    aj = np.empty(B, np.uint64)
+    cj = np.empty(B, np.uint64)
+    x, y = 1, 0
+    for j in range(B):  # aj[j] = a^(j+1), cj[j] = c (a^j + ... + 1), mod 2^32
+        x = (x * a) & 0xFFFFFFFF
+        y = (y * a + c) & 0xFFFFFFFF
+        aj[j], cj[j] = x, y
+    out = np.empty(n, np.int8)
+    st = np.uint64(seed & 0xFFFFFFFF)
+    for i in range(0, n, B):
+        blk = (aj * st + cj) & mask
+        k = min(B, n - i)
+        out[i:i + k] = ((blk[:k] >> np.uint64(28)).astype(np.int16) - 8).astype(np.int8)
+        st = blk[B - 1]
+    return out
+
+
+def mmi8_operands(M: int, K: int, N: int):
+    """``mmi8``'s shape ``M x K x N``: A int8 [M, K] = lcg(seed 7), B int8 [K, N] = lcg(seed 11),
+    as that procedure draws them (kernel_bench.html:301), returned in the Linear layout this
+    library takes: A [M, K] and W = B^T [N, K] (so A @ W.T is the reference's A @ B)."""
+    A = lcg_int8(M * K, 7).reshape(M, K)
+    B = lcg_int8(K * N, 11).reshape(K, N)
+    return A, np.ascontiguousarray(B.T)
+
+
 def gemm_bytes(M: int, N: int = GEMM_N, K: int = GEMM_K) -> int:
     """Algorithmic HBM bytes of one W8A8 GEMM launch: A int8 + W int8 + sA + sW + bias +
     f32 out."""

@@ -49,6 +49,11 @@ typedef void* bq_stream_t; /* a hipStream_t; NULL = the null stream */
 #define BQ_ACT_SILU 2
 #define BQ_ACT_GELU 3 /* erf form, f32: (y * 0.5) * (1 + erf(y * sqrt(1/2))) */
 
+/* OR-ed into bq_gemm_i8's `act`: sA is one activation scale for the whole A (f32 [1])
+ * instead of one per row, as the reference's matmulInt8(scaled) takes it (Scale[0],
+ * borch-ts/src/kernels.ts:1818-1827) after a per-tensor quantize (bq_quantize_tensor). */
+#define BQ_SCALE_A_PER_TENSOR 0x100
+
 /* Library version, (major << 16) | minor. */
 int bq_version(void);
 
@@ -145,7 +150,8 @@ int bq_quantize_nhwc_scaled(const float* x, int64_t P, int64_t C, int64_t Cpad, 
 size_t bq_gemm_ws_bytes(void);
 
 /* W8A8 GEMM with the fused dequant epilogue, Linear layout (x @ W.T):
- *   A int8 [M, K] (per-row scales sA f32 [M]), W int8 [N, K] (per-channel sW f32 [N]),
+ *   A int8 [M, K] (per-row scales sA f32 [M], or one sA f32 [1] for the whole A with
+ *   act | BQ_SCALE_A_PER_TENSOR), W int8 [N, K] (per-channel sW f32 [N]),
  *   out f32 [M, N] = ((f32(A @ W.T) * sA[m]) * sW[n]) + bias[n] (bias nullable), then
  *   + residual[m, n] (f32 [M, N], nullable: a transformer's skip connection), then the
  *   activation `act` (BQ_ACT_*). `acc` (nullable) receives the exact int32 [M, N].

@@ -748,3 +748,55 @@ def test_every_conv_plan_gives_the_same_result(dev, no_plans, N, C, H, O_, k, st
         assert torch.equal(parts[:nparts].max(), want_max), (cfg, split)
         _, q = I.conv2d_i8_nhwc_q(qx, sa, w8, s_out, stride, pad, b, r, I.ACT_RELU)
         assert torch.equal(q, want_q), (cfg, split)
+
+
+# ------------------------------------------------- per-tensor activation scale (matmulInt8)
+
+@pytest.mark.parametrize("M,N,K", [(1, 96, 512), (3, 300, 1040), (16, 512, 512), (40, 200, 768), (256, 512, 4608),
+                                   (1000, 520, 784), (4096, 1024, 512)])
+def test_gemm_per_tensor_activation_scale(dev, M, N, K):
+    """bq_gemm_i8 with act | BQ_SCALE_A_PER_TENSOR: one activation scale sA[0] for every row,
+    the reference's matmulInt8(scaled) arithmetic fround(fround(fround(acc*s0)*s[n])+b[n])
+    (kernels.ts:1818-1827; kernel_bench.html:321), after a per-tensor quantize
+    (bq_quantize_tensor). int32 and f32 bit-exact against the oracle, in every kernel family
+    (GEMV, skinny, tiled, split-K), and through nn.Linear(per_tensor)."""
+    say(f"per-tensor activation scale M={M} N={N} K={K}")
+    rng = np.random.default_rng(M + 3 * N + K)
+    x = rng.normal(size=(M, K)).astype(np.float32)
+    w = (rng.normal(size=(N, K)) / np.sqrt(K)).astype(np.float32)
+    b = (0.1 * rng.normal(size=N)).astype(np.float32)
+    qa, sa = I.quantize_tensor(t(x, dev))
+    qa_o, sa_o = O.quantize_tensor(x)
+    assert np.array_equal(n(qa), qa_o) and n(sa)[0] == sa_o[0]
+    qw, sw = I.quantize_weight_per_channel(t(w, dev))
+    out, acc = I.gemm_i8(qa, qw, sa, sw, t(b, dev), want_acc=True)
+    acc_o = O.gemm_i8_i32(qa_o, n(qw))
+    assert np.array_equal(n(acc), acc_o)
+    assert_f32(n(out), O.dequant(acc_o, sa_o[0], n(sw), b))
+    import borch_amd as bt
+    lin = bt.nn.Linear(K, N).to(dev)
+    with torch.no_grad():
+        lin.weight.copy_(t(w, dev))
+        lin.bias.copy_(t(b, dev))
+    assert bt.quantize_for_int8(lin, per_tensor=True) == 1 and lin.int8.per_tensor
+    assert_f32(n(lin(t(x, dev))), O.dequant(acc_o, sa_o[0], n(sw), b))
+
+
+@pytest.mark.parametrize("size", [1024, 2048])
+def test_mmi8_lcg_procedure(dev, size):
+    """The reference's exactness gate mmi8 (kernel_bench.html:294-337) at its published
+    shapes: LCG int8 operands in [-8, 8), the raw int32 result held to the exact integer
+    reference on EVERY entry, then the dequantising store (per-tensor activation scale,
+    per-channel weight scales and bias, all in [0.5, 1.5) / N(0, 1)) bit for bit."""
+    say(f"mmi8 {size}^3 on the LCG operands")
+    from borch_amd import workloads as WL
+    A, W = WL.mmi8_operands(size, size, size)
+    rng = np.random.default_rng(size)
+    s0 = np.float32(0.5 + rng.random())
+    sw = (0.5 + rng.random(size)).astype(np.float32)
+    b = rng.normal(size=size).astype(np.float32)
+    out, acc = I.gemm_i8(t(A, dev), t(W, dev), torch.tensor([s0], device=dev), t(sw, dev), t(b, dev), want_acc=True)
+    ref = O.gemm_i8_i32(A, W)
+    wrong = int((n(acc) != ref).sum())
+    assert wrong == 0, f"{wrong} of {size * size} entries differ from the int32 reference"
+    assert_f32(n(out), O.dequant(ref, s0, sw, b))

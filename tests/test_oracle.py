@@ -431,3 +431,22 @@ def test_se_gate_against_torch_float64():
     z = torch.nn.functional.silu(torch.nn.functional.linear(p, T(w1), T(b1)))
     want = torch.sigmoid(torch.nn.functional.linear(z, T(w2), T(b2))).float().numpy()
     np.testing.assert_allclose(OM.se_gate(x, w1, b1, w2, b2), want, rtol=1e-7, atol=1e-9)
+
+
+@pytest.mark.parametrize("n,seed", [(1, 7), (4095, 11), (4096, 7), (10001, 11), (3 * 4096 + 5, 3)])
+def test_vectorised_lcg_is_the_reference_generator(n, seed):
+    """workloads.lcg_int8 (jump-ahead blocks) draws exactly kernel_bench.html:300-301's
+    sequence, restated step by step in _lcg_int8."""
+    from borch_amd import workloads as WL
+    assert np.array_equal(WL.lcg_int8(n, seed), _lcg_int8(n, seed))
+
+
+def test_mmi8_operands_layout():
+    """A @ W.T of the Linear layout equals the reference's A @ B on its own operands."""
+    from borch_amd import workloads as WL
+    A, W = WL.mmi8_operands(32, 48, 16)
+    assert np.array_equal(A.reshape(-1), _lcg_int8(32 * 48, 7))
+    B = _lcg_int8(48 * 16, 11).reshape(48, 16)
+    assert np.array_equal(W, B.T)
+    ref = A.astype(np.int64) @ B.astype(np.int64)
+    assert np.array_equal(O.gemm_i8_i32(A, W), ref.astype(np.int32))
