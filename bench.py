@@ -60,7 +60,7 @@ def capture(fn, calls):
             fn(i)
     torch.cuda.current_stream().wait_stream(s)
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    with torch.cuda.graph(g, stream=s):  # the warm-up stream: its split-K workspace is recorded
         for i in range(calls):
             fn(i)
     return g

@@ -22,7 +22,10 @@ Measured at n = 2: EfficientNet-B0 b64 calibrated 1.55 -> 1.41 ms, ViT-B/16 b32 
 Tune (``tune=True``, the default, as the reference's, compile.ts:55-62): before a shape's
 first run on a GPU, the int8 GEMM / conv kernel of every distinct layer problem is chosen
 by measurement (``borch_amd.tune``); ``tuned`` keeps the decisions, one list per shape.
-The choice changes time only: every candidate computes the same result.
+The choice changes time only: every candidate computes the same result. Decisions persist
+in a plan table on disk (``plan_cache``: a path, or by default ``tune.default_cache_path()``;
+False keeps them in the process only), so a later process with the same device and library
+times nothing (the reference's localStorage cache, device.ts:2689-2697, 2810-2831).
 """
 from __future__ import annotations
 
@@ -30,13 +33,15 @@ import torch
 
 from . import int8 as _i8
 from .nn import Conv2d, _int8_layers, quantize_for_int8
+from .tune import PlanCache
 from .tune import tune as _tune
 
 
 class Compiled:
     def __init__(self, model, int8: bool = False, graph: bool = False, fuse: bool = True, tune: bool = True,
-                 split: int = 1):
+                 split: int = 1, plan_cache=None):
         self.model = model
+        self.plan_cache = None if plan_cache is False else PlanCache(plan_cache)
         self.int8 = int8
         self.graph = graph
         self.tune = tune
@@ -89,7 +94,8 @@ class Compiled:
         key = (tuple(x.shape), x.dtype, x.device)
         if self.tune and x.device.type == "cuda" and key not in self._tuned_keys:
             self._tuned_keys.add(key)
-            self.tuned.append(_tune(self.model, x.chunk(self.split)[0] if self._split_ok(x) else x))
+            self.tuned.append(_tune(self.model, x.chunk(self.split)[0] if self._split_ok(x) else x,
+                                    cache=self.plan_cache))
         if not self.graph or x.device.type != "cuda":
             return self.model(x)
         entry = self._graphs.get(key)
@@ -102,7 +108,9 @@ class Compiled:
                     self._run(static_in)
             torch.cuda.current_stream(x.device).wait_stream(s)
             g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g):
+            # captured on the warm-up stream: the split-K workspace made for it is the one
+            # the graph records
+            with torch.cuda.graph(g, stream=s):
                 static_out = self._run(static_in)
             entry = (g, static_in, static_out)
             self._graphs[key] = entry
@@ -113,7 +121,8 @@ class Compiled:
 
 
 def compiled(model, int8: bool = False, graph: bool = False, fuse: bool = True, tune: bool = True,
-             split: int = 1) -> Compiled:
+             split: int = 1, plan_cache=None) -> Compiled:
     """``torch.compiled(model, {int8, tune})`` of borch-ts (compile.ts:55-62, 570-578); ``split``
-    runs the batch as parallel chunks inside the graph."""
-    return Compiled(model, int8=int8, graph=graph, fuse=fuse, tune=tune, split=split)
+    runs the batch as parallel chunks inside the graph; ``plan_cache`` is where tuning
+    decisions persist (None: the default table, False: none)."""
+    return Compiled(model, int8=int8, graph=graph, fuse=fuse, tune=tune, split=split, plan_cache=plan_cache)

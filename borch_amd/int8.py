@@ -38,25 +38,31 @@ def _stream(t: torch.Tensor):
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
-# The split-K workspace of bq_gemm_i8 / bq_conv2d_i8_nhwc(_q) (bq_gemm_ws_bytes): one
-# zero-filled buffer per device, made outside any graph capture and kept for the life of
-# the process, since a captured HIP graph keeps using the pointer it recorded. The kernels
-# leave its counters zero after every call. Calls issued through this module on one device
-# share it, so they must not overlap on two streams.
+# The split-K workspaces of bq_gemm_i8 / bq_conv2d_i8_nhwc(_q) (bq_gemm_ws_bytes): one
+# zero-filled buffer per (device, stream), made outside any graph capture (on the stream
+# it serves) and kept for the life of the process, since a captured HIP graph keeps using
+# the pointer it recorded. The kernels leave its counters zero after every call; calls on
+# one stream run in order, so they may share it, while launches on two streams at once
+# each have their own tile counters and partials. (torch hands out streams from a fixed
+# pool per device, so the table stays small.)
 _SPLIT_WS: dict = {}
 
 
-def split_workspace(device: torch.device):
-    """The device's split-K workspace, or None while a graph is being captured before one
-    exists (the calls then run unsplit: same results)."""
+def split_workspace(device: torch.device, stream=None):
+    """The split-K workspace of ``stream`` (default: the current stream) on ``device``, or
+    None while a graph is being captured on a stream that has none yet (those calls then
+    run unsplit: the same results). Capture on the stream the warm-up ran on to keep it."""
     idx = torch.device(device).index
     idx = torch.cuda.current_device() if idx is None else idx
-    ws = _SPLIT_WS.get(idx)
+    st = torch.cuda.current_stream(idx) if stream is None else stream
+    key = (idx, st.cuda_stream)
+    ws = _SPLIT_WS.get(key)
     if ws is None:
         if torch.cuda.is_current_stream_capturing():
             return None
-        ws = torch.zeros(int(lib().bq_gemm_ws_bytes()), dtype=torch.uint8, device=torch.device("cuda", idx))
-        _SPLIT_WS[idx] = ws
+        with torch.cuda.stream(st):
+            ws = torch.zeros(int(lib().bq_gemm_ws_bytes()), dtype=torch.uint8, device=torch.device("cuda", idx))
+        _SPLIT_WS[key] = ws
     return ws
 
 

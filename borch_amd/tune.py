@@ -12,11 +12,23 @@ Mirrors the reference's ``Device.choose`` / ``runTuning`` (borch-ts/src/device.t
 2834-2846: the rule's pick first, the fastest cached per key) and ``compiled``'s ``tune``
 option (borch-ts/src/compile.ts:55-62), with one report per decision like its
 ``TuneReport`` (device.ts:532-536).
+
+Decisions persist in a JSON table (``PlanCache``), as the reference keeps them per adapter
+in memory and in ``localStorage`` (device.ts:2689-2697, 2810-2831): keyed by the device
+(architecture and compute-unit count), the built library (a hash of ``libbq.so``: a rebuild
+may change what is fastest) and the problem. A later ``tune`` (a later process) takes a
+stored decision without timing anything; a stored plan the library no longer offers is
+ignored and the problem is timed again.
 """
 from __future__ import annotations
 
 import ctypes
+import hashlib
 import inspect
+import json
+import os
+import tempfile
+from pathlib import Path
 
 import torch
 
@@ -102,7 +114,7 @@ def _time_us(fn, a, stream, calls: int, rounds: int) -> float:
         fn(**a)
     torch.cuda.current_stream().wait_stream(s)
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    with torch.cuda.graph(g, stream=s):  # the warm-up stream: the splits timed are the splits that run
         for _ in range(calls):
             fn(**a)
     g.replay()
@@ -122,15 +134,96 @@ def _label(c) -> str:
     return f"cfg{c[0]}/split{c[1]}"
 
 
-def tune(model, x, min_gain: float = 0.03, calls: int = 8, rounds: int = 3) -> list[dict]:
+PLAN_FORMAT = "borch_amd-plans/1"
+_LIB_ID = None
+
+
+def library_id() -> str:
+    """The built library's identity: the first 16 hex digits of the SHA-256 of libbq.so."""
+    global _LIB_ID
+    if _LIB_ID is None:
+        from ._lib import LIB_PATH
+        _LIB_ID = hashlib.sha256(Path(LIB_PATH).read_bytes()).hexdigest()[:16]
+    return _LIB_ID
+
+
+def device_id(device) -> str:
+    props = torch.cuda.get_device_properties(device)
+    return f"{getattr(props, 'gcnArchName', props.name)}/{props.multi_processor_count}cu"
+
+
+def default_cache_path() -> Path:
+    """``$BORCH_AMD_PLAN_CACHE``, else ``~/.cache/borch_amd/plans.json``."""
+    env = os.environ.get("BORCH_AMD_PLAN_CACHE")
+    return Path(env) if env else Path.home() / ".cache" / "borch_amd" / "plans.json"
+
+
+class PlanCache:
+    """Tuning decisions on disk: ``{"format", "tables": {"<device>|<library>": {"<problem>":
+    {"cfg", "split", "rule_us", "chosen_us"}}}}``. ``cfg == 0`` records that the rule's
+    pick stays. Writes merge with what is on disk and replace the file atomically."""
+
+    def __init__(self, path=None):
+        self.path = Path(path) if path is not None else default_cache_path()
+
+    def _read(self) -> dict:
+        try:
+            data = json.loads(self.path.read_text())
+        except (OSError, ValueError):
+            return {"format": PLAN_FORMAT, "tables": {}}
+        if not isinstance(data, dict) or data.get("format") != PLAN_FORMAT or not isinstance(data.get("tables"), dict):
+            return {"format": PLAN_FORMAT, "tables": {}}
+        return data
+
+    @staticmethod
+    def _table_key(device) -> str:
+        return f"{device_id(device)}|{library_id()}"
+
+    def load(self, device) -> dict:
+        """{problem tuple: entry} stored for this device and library."""
+        table = self._read()["tables"].get(self._table_key(device), {})
+        out = {}
+        for k, v in table.items():
+            try:
+                out[tuple(int(t) for t in k.split(","))] = {"cfg": int(v["cfg"]), "split": int(v["split"]),
+                                                            "rule_us": float(v["rule_us"]),
+                                                            "chosen_us": float(v["chosen_us"])}
+            except (KeyError, TypeError, ValueError):
+                continue
+        return out
+
+    def store(self, device, entries: dict) -> bool:
+        """Adds ``{problem: entry}`` to the table; False (and nothing written) if the file
+        cannot be written."""
+        if not entries:
+            return True
+        data = self._read()
+        table = data["tables"].setdefault(self._table_key(device), {})
+        for problem, e in entries.items():
+            table[",".join(str(int(t)) for t in problem)] = e
+        try:
+            self.path.parent.mkdir(parents=True, exist_ok=True)
+            fd, tmp = tempfile.mkstemp(dir=str(self.path.parent), prefix=".plans-", suffix=".json")
+            with os.fdopen(fd, "w") as f:
+                json.dump(data, f, indent=1, sort_keys=True)
+            os.replace(tmp, self.path)
+        except OSError:
+            return False
+        return True
+
+
+def tune(model, x, min_gain: float = 0.03, calls: int = 8, rounds: int = 3, cache: PlanCache | None = None) -> list[dict]:
     """Times every candidate of each distinct int8 problem in one forward of ``model`` on
     ``x`` and keeps the fastest when it is more than ``min_gain`` faster than the rule's
-    pick. Returns one report per decision: key, prior, prior_us, chosen, chosen_us,
-    candidates."""
+    pick. With ``cache``, a decision stored for this device and library is taken as it
+    stands (nothing timed) and new decisions are stored. Returns one report per decision:
+    key, prior, prior_us, chosen, chosen_us, candidates, cached."""
     if x.device.type != "cuda":
         return []
     _i8.split_workspace(x.device)  # the splits timed here are the splits that run later
     stream = torch.cuda.current_stream(x.device)
+    stored = cache.load(x.device) if cache is not None else {}
+    new_entries = {}
     reports, seen = [], set()
     for layer, kind, fn, a in record_launches(model, x):
         problem = problem_of(kind, a)
@@ -139,6 +232,14 @@ def tune(model, x, min_gain: float = 0.03, calls: int = 8, rounds: int = 3) -> l
         seen.add(problem)
         cands = candidates(problem)
         if len(cands) < 2:
+            continue
+        e = stored.get(problem)
+        if e is not None and (e["cfg"] == 0 or (e["cfg"], e["split"]) in cands):
+            chosen = (e["cfg"], e["split"]) if e["cfg"] else cands[0]
+            set_plan(problem, *(chosen if e["cfg"] else (0, 0)))
+            reports.append({"key": problem, "layer": layer, "prior": _label(cands[0]), "prior_us": e["rule_us"],
+                            "chosen": _label(chosen), "chosen_us": e["chosen_us"], "candidates": len(cands),
+                            "cached": True})
             continue
         set_plan(problem, 0, 0)
         times = []
@@ -158,6 +259,11 @@ def tune(model, x, min_gain: float = 0.03, calls: int = 8, rounds: int = 3) -> l
             set_plan(problem, 0, 0)
         reports.append({"key": problem, "layer": layer, "prior": _label(cands[0]), "prior_us": round(times[0], 2),
                         "chosen": _label(cands[chosen]), "chosen_us": round(times[chosen], 2),
-                        "candidates": len(cands)})
+                        "candidates": len(cands), "cached": False})
+        new_entries[problem] = {"cfg": int(cands[chosen][0]) if chosen else 0,
+                                "split": int(cands[chosen][1]) if chosen else 0,
+                                "rule_us": round(times[0], 2), "chosen_us": round(times[chosen], 2)}
     torch.cuda.synchronize(x.device)
+    if cache is not None:
+        cache.store(x.device, new_entries)
     return reports

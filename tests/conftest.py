@@ -10,6 +10,10 @@ if ROOT not in sys.path:
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs a gfx950 GPU (runs through the C ABI on the device)")
+    # tuning decisions of a test run persist in a table of its own, not the user's
+    if "BORCH_AMD_PLAN_CACHE" not in os.environ:
+        import tempfile
+        os.environ["BORCH_AMD_PLAN_CACHE"] = os.path.join(tempfile.mkdtemp(prefix="bq-plans-"), "plans.json")
 
 
 @pytest.fixture(scope="session")

@@ -396,3 +396,89 @@ def test_split_batch_graph_matches_whole(dev):
     c = bt.compiled(b0, int8=False, graph=True, fuse=False, tune=True, split=2)
     for _ in range(3):
         assert np.array_equal(n(c(xb)), whole)
+
+
+def test_split_workspace_per_stream(dev):
+    """Split-K GEMMs and convs issued on two streams at once each use their own split-K
+    workspace (tile counters and partials): both give the serial results, bit for bit."""
+    say("split-K on two concurrent streams")
+    rng = np.random.default_rng(5)
+    M, N, K = 256, 512, 4608  # 32 tiles of 64 x 64 over 36 stages: split 8 ways
+    ops = []
+    for _ in range(2):
+        qa = torch.from_numpy(rng.integers(-127, 128, size=(M, K)).astype(np.int8)).to(dev)
+        qw = torch.from_numpy(rng.integers(-127, 128, size=(N, K)).astype(np.int8)).to(dev)
+        sa = torch.from_numpy(rng.uniform(1e-3, 1e-2, M).astype(np.float32)).to(dev)
+        sw = torch.from_numpy(rng.uniform(1e-3, 1e-2, N).astype(np.float32)).to(dev)
+        ops.append((qa, qw, sa, sw))
+    want = [I.gemm_i8(*o) for o in ops]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(device=dev), torch.cuda.Stream(device=dev)]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream(dev))
+    ws = [I.split_workspace(dev, s) for s in streams]
+    assert ws[0].data_ptr() != ws[1].data_ptr()
+    got = [[], []]
+    for _ in range(16):
+        for i, s in enumerate(streams):
+            with torch.cuda.stream(s):
+                got[i].append(I.gemm_i8(*ops[i]))
+    torch.cuda.synchronize()
+    for i in range(2):
+        for g in got[i]:
+            assert torch.equal(g, want[i]), f"stream {i}"
+    for w in ws:
+        assert int(w[:4096].count_nonzero()) == 0
+
+
+def test_plan_cache_persists_decisions(dev, tmp_path):
+    """tune(cache=...) stores every decision (device, library hash, problem); a second tune
+    with the table, in this process after the plans are cleared and in a fresh process,
+    times nothing and sets the same plans; the forward under the loaded plans equals the
+    tuned one bit for bit."""
+    import subprocess
+    from borch_amd import tune as T
+    say("persisted tuning plans (ResNet-18 b4)")
+    T.clear_plans()
+    path = tmp_path / "plans.json"
+    cache = T.PlanCache(path)
+    try:
+        model = nets.build("resnet18", seed=3, device=dev)
+        bt.quantize_for_int8(model)
+        x = torch.from_numpy(WL.c3_input(4, 3)).to(dev)
+        first = T.tune(model, x, cache=cache)
+        assert first and not any(r["cached"] for r in first)
+        assert path.exists() and len(cache.load(dev)) == len(first)
+        with torch.no_grad():
+            y1 = model(x).clone()
+        T.clear_plans()
+        timed = {"n": 0}
+        real = T._time_us
+
+        def counting(*a, **k):
+            timed["n"] += 1
+            return real(*a, **k)
+        T._time_us = counting
+        try:
+            second = T.tune(model, x, cache=cache)
+        finally:
+            T._time_us = real
+        assert timed["n"] == 0 and all(r["cached"] for r in second)
+        assert [(r["key"], r["chosen"]) for r in second] == [(r["key"], r["chosen"]) for r in first]
+        with torch.no_grad():
+            assert torch.equal(model(x), y1)
+        # a fresh process with the same table times nothing either
+        code = ("import sys, torch; sys.path.insert(0, '.');"
+                "import borch_amd as bt; from borch_amd import nets, workloads as WL, tune as T;"
+                "m = nets.build('resnet18', seed=3, device='cuda'); bt.quantize_for_int8(m);"
+                "x = torch.from_numpy(WL.c3_input(4, 3)).cuda();"
+                f"r = T.tune(m, x, cache=T.PlanCache({str(path)!r}));"
+                "print('CACHED', sum(q['cached'] for q in r), len(r))")
+        import os
+        root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+        out = subprocess.run([sys.executable, "-c", code], cwd=root, capture_output=True, text=True, timeout=240)
+        assert out.returncode == 0, out.stderr[-2000:]
+        line = [ln for ln in out.stdout.splitlines() if ln.startswith("CACHED")][-1].split()
+        assert line[1] == line[2] == str(len(first)), line
+    finally:
+        T.clear_plans()

@@ -114,3 +114,23 @@ def test_vectors_reaching_the_kernels_have_their_full_length():
     assert v.dtype == torch.float32 and v.is_contiguous() and v.tolist() == [0.0, 1.0, 2.0, 3.0]
     with pytest.raises(ValueError, match="expected 5 values, got 4"):
         I._vec(torch.zeros(4), 5, "bias")
+
+
+def test_plan_cache_file(tmp_path, monkeypatch):
+    """The plan table on disk: decisions stored per (device, library) and problem, merged on
+    write, unreadable or foreign files read as empty, another library's table ignored."""
+    from borch_amd import tune as T
+    monkeypatch.setattr(T, "device_id", lambda device: "gfx950/256cu")
+    c = T.PlanCache(tmp_path / "sub" / "plans.json")
+    assert c.load("cuda:0") == {}
+    assert c.store("cuda:0", {(256, 512, 4608): {"cfg": 9, "split": 8, "rule_us": 10.5, "chosen_us": 9.1}})
+    assert c.store("cuda:0", {(16, 32, 32, 64, 64, 3, 3, 1, 1): {"cfg": 0, "split": 0, "rule_us": 7.0,
+                                                                  "chosen_us": 7.0}})
+    got = c.load("cuda:0")
+    assert got[(256, 512, 4608)]["cfg"] == 9 and got[(16, 32, 32, 64, 64, 3, 3, 1, 1)]["cfg"] == 0
+    monkeypatch.setattr(T, "_LIB_ID", "another-build")
+    assert c.load("cuda:0") == {}
+    (tmp_path / "bad.json").write_text("{not json")
+    assert T.PlanCache(tmp_path / "bad.json").load("cuda:0") == {}
+    monkeypatch.setenv("BORCH_AMD_PLAN_CACHE", str(tmp_path / "x.json"))
+    assert T.default_cache_path() == tmp_path / "x.json"
