@@ -591,6 +591,12 @@ def main():
         g_e = capture(lambda i: (lambda q_s: I.gemm_i8(q_s[0], qws[i], q_s[1], sw_m, Bm))(I.quantize_rows(Am)), copies)
         t_e2e = time_graph(g_e, copies, 8, stream)
         del g_k, g_e
+        t_fused = None
+        if m <= 4:  # f32 in, f32 out in one launch: the per-row quantize fused into the GEMV (bq_linear_i8)
+            w8s_m = [I.Int8Weight(q, sw_m, K, N) for q in qws]
+            g_f = capture(lambda i: I.linear_rows(Am, w8s_m[i], Bm), copies)
+            t_fused = time_graph(g_f, copies, 8, stream)
+            del g_f, w8s_m
         if m == 1:
             ceilings = probes(dev, stream, qa, qw, qws)
             log(f"ceilings: {ceilings}")
@@ -599,6 +605,9 @@ def main():
                           "hbm_frac": round(byts / (t_k * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
                           "TOPS": round(WL.gemm_ops(m) / (t_k * 1e-3) / 1e12, 2),
                           "e2e_us_with_quantize": round(t_e2e * 1e3, 3), "bytes": byts,
+                          **({"fused_quantize_e2e_us": round(t_fused * 1e3, 3),
+                              "fused_GBps": round((byts + 4 * m * K) / (t_fused * 1e-3) / 1e9, 1)}
+                             if t_fused is not None else {}),
                           "read_floor_us": ceilings["read_16MiB_cold_us"],
                           "frac_of_read_floor": round(ceilings["read_16MiB_cold_us"] / (t_k * 1e3), 4)}
         del qws, Am

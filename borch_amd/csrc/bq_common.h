@@ -128,6 +128,7 @@ __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
 // roundings clamp to the same +-127.
 struct Quantizer {
   float s, r;
+  __device__ Quantizer() : s(0.f), r(0.f) {}  // the zero scale: every value to 0
   __device__ explicit Quantizer(float s_) : s(s_), r(s_ == 0.f ? 0.f : __fdiv_rn(1.0f, s_)) {}
   static __device__ __forceinline__ bool near_half(float f, float k) {
     return !(fabsf(__fsub_rn(f, k)) < 0.49996f);

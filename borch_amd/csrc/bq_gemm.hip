@@ -65,6 +65,12 @@ struct GemmP {
   // Host-side selection only (the kernels ignore them): a tuned plan's configuration id
   // (0: the shape rule) and K split (0: the split rule).
   int plan_cfg, plan_split;
+  // GEMV with the per-row quantize fused (gemv_i8_fq_kernel): f32 activations X [M, K] in
+  // place of A / sA; the quantized rows and their scales are also written to qx [M, K] and
+  // sx [M] (nullable) by workgroup 0.
+  const float* X;
+  int8_t* qx;
+  float* sx;
 };
 
 constexpr int BK = 128;  // bytes of K per LDS stage: one cache line per row
@@ -830,12 +836,163 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_i8_kernel(const GemmP p) {
   }
 }
 
-static int forced_gemv() {
-  static int cfg = [] {
-    const char* e = getenv("BQ_GEMV_CFG");
-    return e ? atoi(e) : 0;
-  }();
-  return cfg;
+// The same GEMV on f32 activations, their per-row quantization fused (M <= 4): every
+// workgroup loads the MR rows of X (L2-resident after the first), issues its weight
+// stream, then takes each row's max|x| (wave DPP maxima, then across the waves through
+// LDS), its scale float32(max / 127) and the exact-quotient rounding of every element
+// (Quantizer: the rule bq_quantize_rows applies, so the same bytes and scales) into the
+// LDS image the dot products read, while the weight loads are in flight. One launch
+// instead of the quantize kernel and the GEMV (a 4096-float row: 2.5 us of launch and
+// kernel). Workgroup 0 also writes the quantized rows and scales (qx, sx, nullable).
+template <int MR, int KC, int RPW, int WAVES = GV_WAVES>
+__global__ __launch_bounds__(WAVES * 64) void gemv_i8_fq_kernel(const GemmP p) {
+  constexpr int T = WAVES * 64;
+  constexpr int XF4 = MR * KC * 256;        // float4s of the (padded) activation rows
+  constexpr int XPT = (XF4 + T - 1) / T;    // float4s a thread loads
+  __shared__ __attribute__((aligned(16))) int8_t xs[MR * KC * 1024];
+  __shared__ float red[WAVES][MR];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int row0 = (blockIdx.x * WAVES + wave) * RPW;
+  const int nrows = max(0, min(RPW, p.N - row0));
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.W + (size_t)min(row0, p.N) * p.K, (uint32_t)(nrows * p.K));
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.X, (uint32_t)(p.M * p.K * 4));
+  float4 xr[XPT];
+#pragma unroll
+  for (int i = 0; i < XPT; ++i) {
+    const int f = tid + i * T;
+    const int m = f / (KC * 256);
+    const int k = (f - m * (KC * 256)) * 4;
+    xr[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                           rx, (f < XF4 && m < p.M && k < p.K) ? (uint32_t)((m * p.K + k) * 4) : OOB, 0, 0));
+  }
+  const int my_j = lane / MR, my_m = lane % MR;
+  const int my_n = row0 + my_j;
+  const bool writer = lane < RPW * MR && my_j < nrows && my_m < p.M;
+  float e_sw = 0.f, e_b = 0.f;
+  if (writer) {
+    e_sw = p.sW[my_n];
+    e_b = p.bias ? p.bias[my_n] : 0.f;
+  }
+  v4i w[RPW][KC];
+#pragma unroll
+  for (int j = 0; j < RPW; ++j)
+#pragma unroll
+    for (int c = 0; c < KC; ++c) {
+      const int k = c * 1024 + lane * 16;
+      w[j][c] = buf_load16(rw, k < p.K ? (uint32_t)(j * p.K + k) : OOB);
+    }
+  __builtin_amdgcn_sched_barrier(0);  // every load in flight before anything waits
+  // row maxima (the padding and rows past M read as zeros)
+  float pm[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) pm[m] = 0.f;
+#pragma unroll
+  for (int i = 0; i < XPT; ++i) {
+    const int m = (tid + i * T) / (KC * 256);
+    const float4 v = xr[i];
+    const float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+#pragma unroll
+    for (int mm = 0; mm < MR; ++mm)
+      if (mm == m) pm[mm] = fmaxf(pm[mm], a);
+  }
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    const float v = wave_max(pm[m]);
+    if (lane == 0) red[wave][m] = v;
+  }
+  __syncthreads();
+  float sc[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    float v = red[0][m];
+#pragma unroll
+    for (int wv = 1; wv < WAVES; ++wv) v = fmaxf(v, red[wv][m]);
+    sc[m] = scale_of(v);
+  }
+  // one reciprocal per row's scale, not per element group
+  Quantizer qz[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) qz[m] = Quantizer(sc[m]);
+#pragma unroll
+  for (int i = 0; i < XPT; ++i) {
+    const int f = tid + i * T;
+    if (f < XF4) {
+      const int m = f / (KC * 256);
+      const int k = (f - m * (KC * 256)) * 4;
+      Quantizer q0 = qz[0];
+#pragma unroll
+      for (int mm = 1; mm < MR; ++mm)
+        if (mm == m) q0 = qz[mm];
+      const uint32_t packed = q0.pack(xr[i]);
+      *reinterpret_cast<uint32_t*>(xs + m * (KC * 1024) + k) = packed;
+      if (blockIdx.x == 0 && p.qx && m < p.M && k < p.K) *reinterpret_cast<uint32_t*>(p.qx + (size_t)m * p.K + k) = packed;
+    }
+  }
+  if (blockIdx.x == 0 && p.sx && tid < p.M && tid < MR) {
+    float smm = sc[0];
+#pragma unroll
+    for (int mm = 1; mm < MR; ++mm)
+      if (mm == tid) smm = sc[mm];
+    p.sx[tid] = smm;
+  }
+  __syncthreads();
+  float e_sa = sc[0];
+#pragma unroll
+  for (int mm = 1; mm < MR; ++mm)
+    if (mm == my_m) e_sa = sc[mm];
+  v4i x[MR][KC];
+#pragma unroll
+  for (int m = 0; m < MR; ++m)
+#pragma unroll
+    for (int c = 0; c < KC; ++c) x[m][c] = *reinterpret_cast<const v4i*>(xs + (m * KC + c) * 1024 + lane * 16);
+  int acc[RPW][MR];
+#pragma unroll
+  for (int j = 0; j < RPW; ++j)
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      int a = 0;
+#pragma unroll
+      for (int c = 0; c < KC; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) a = __builtin_amdgcn_sdot4(w[j][c][q], x[m][c][q], a, false);
+      acc[j][m] = wave_sum(a);
+    }
+  int mine = 0;
+#pragma unroll
+  for (int j = 0; j < RPW; ++j)
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+      if (lane == j * MR + m) mine = acc[j][m];
+  if (writer) {
+    const size_t idx = (size_t)my_m * p.N + my_n;
+    const float rv = p.res ? p.res[idx] : 0.f;
+    p.out[idx] = dequant_one(mine, e_sa, e_sw, e_b, p.bias != nullptr, rv, p.res != nullptr, p.act);
+    if (p.acc) p.acc[idx] = mine;
+  }
+}
+
+template <int MR, int RPW, int WAVES>
+static bool launch_gemv_fq_cfg(const GemmP& p, hipStream_t st) {
+  const unsigned grid = (unsigned)((p.N + WAVES * RPW - 1) / (WAVES * RPW));
+  if (p.K <= 1024) gemv_i8_fq_kernel<MR, 1, RPW, WAVES><<<grid, WAVES * 64, 0, st>>>(p);
+  else if (p.K <= 2048) gemv_i8_fq_kernel<MR, 2, RPW, WAVES><<<grid, WAVES * 64, 0, st>>>(p);
+  else if (p.K <= 4096) gemv_i8_fq_kernel<MR, 4, RPW, WAVES><<<grid, WAVES * 64, 0, st>>>(p);
+  else if (p.K <= 8192) gemv_i8_fq_kernel<MR, 8, RPW, WAVES><<<grid, WAVES * 64, 0, st>>>(p);
+  else return false;
+  return true;
+}
+
+// Eight waves a workgroup (the f32 rows are loaded and quantized once per workgroup, so
+// more weight rows a workgroup spend less of the L2 -> CU traffic on them): one weight row
+// a wave for one activation row, two for two to four. Measured, 4096 x 4096, cache-cold,
+// one launch against quantize + GEMV: M = 1 5.37 against 7.75 us, M = 2 6.6 against 8.0,
+// M = 4 8.4 against 8.4 (four waves a workgroup: 6.1 / 8.3 / 10.1 us).
+template <int MR>
+static bool launch_gemv_fq(const GemmP& p, hipStream_t st) {
+  if constexpr (MR == 1) return launch_gemv_fq_cfg<MR, 1, 8>(p, st);
+  else return launch_gemv_fq_cfg<MR, 2, 8>(p, st);
 }
 
 template <int MR, int RPW, int WAVES>
@@ -853,15 +1010,8 @@ static bool launch_gemv_cfg(const GemmP& p, hipStream_t st) {
 // workgroup for one or two activation rows, eight for three or four (measured).
 template <int MR>
 static bool launch_gemv(const GemmP& p, hipStream_t st) {
-  switch (forced_gemv()) {
-    case 1: return launch_gemv_cfg<MR, 1, 8>(p, st);
-    case 2: return launch_gemv_cfg<MR, 2, 8>(p, st);
-    case 3: return launch_gemv_cfg<MR, 2, 4>(p, st);
-    case 4: return launch_gemv_cfg<MR, 1, 4>(p, st);
-    default:
-      if constexpr (MR <= 2) return launch_gemv_cfg<MR, 1, 4>(p, st);
-      else return launch_gemv_cfg<MR, 1, 8>(p, st);
-  }
+  if constexpr (MR <= 2) return launch_gemv_cfg<MR, 1, 4>(p, st);
+  else return launch_gemv_cfg<MR, 1, 8>(p, st);
 }
 
 // -------------------------------------------------------------------------- depthwise
@@ -1037,16 +1187,6 @@ struct Ws {
   size_t bytes;
 };
 
-// BQ_GEMM_SPLIT forces the number of K splits of the tiled kernel (tuning sweeps; still
-// subject to the workspace); unset = the rule below.
-static int forced_split() {
-  static int v = [] {
-    const char* e = getenv("BQ_GEMM_SPLIT");
-    return e ? atoi(e) : 0;
-  }();
-  return v;
-}
-
 // K splits for a grid of `tiles` tiles of `KT` stages: enough workgroups to cover the
 // chip's 256 CUs, each split at least 4 stages long, and no split left empty. The split
 // costs a fixed 2-3 us (partials written through to the device-coherent level, the counter
@@ -1054,9 +1194,7 @@ static int forced_split() {
 // for a conv (whose loader makes a stage dearer) and from 32 for a dense GEMM.
 static int pick_split(long long tiles, int KT, bool conv, int planned = 0) {
   int S;
-  if (forced_split() > 0) {
-    S = forced_split();
-  } else if (planned > 0) {
+  if (planned > 0) {
     S = planned;
   } else {
     if (tiles >= SPLIT_MAX_TILES || KT < (conv ? 16 : 32)) return 1;
@@ -1082,15 +1220,6 @@ static void launch_tiled(GemmP p, hipStream_t st, const Ws& ws) {
   }
   p.ksplit = S;
   gemm_i8_kernel<BM, BN, WAVES_M, WAVES_N, CONV, NBUF, FD, MF16><<<(unsigned)(tiles * S), WAVES_M * WAVES_N * 64, 0, st>>>(p);
-}
-
-// BQ_GEMM_CFG forces one tile configuration (tuning sweeps); unset = the shape rule.
-static int forced_cfg() {
-  static int cfg = [] {
-    const char* e = getenv("BQ_GEMM_CFG");
-    return e ? atoi(e) : 0;
-  }();
-  return cfg;
 }
 
 // Tiled-kernel configurations, by id: <BM, BN, waves M x N, ring depth, fragment distance>.
@@ -1121,7 +1250,6 @@ constexpr TileDims CFG_TILES[NCFG] = {{0, 0},    {256, 256}, {256, 256}, {256, 2
 // its convolution form keeps 32x32x32, which needs fewer fragment registers next to the
 // implicit-GEMM addressing (the 16x16 form spills there).
 static int choose_cfg(const GemmP& p, bool conv) {
-  if (forced_cfg() >= 1 && forced_cfg() < NCFG) return forced_cfg();
   if (p.plan_cfg >= 1 && p.plan_cfg < NCFG) return p.plan_cfg;
   const long long t256 = (long long)((p.M + 255) / 256) * ((p.N + 255) / 256);
   const long long t128 = (long long)((p.M + 127) / 128) * ((p.N + 127) / 128);
@@ -1346,6 +1474,37 @@ int bq_gemm_i8_noalloc(const int8_t* A, const int8_t* W, int64_t M, int64_t N, i
                        int32_t* acc, bq_stream_t stream) {
   return gemm_impl("bq_gemm_i8_noalloc", A, W, M, N, K, sA, sW, bias, residual, act, out, acc, nullptr, 0, true,
                    stream);
+}
+
+int bq_linear_i8(const float* x, const int8_t* W, int64_t M, int64_t N, int64_t K, const float* sW,
+                 const float* bias, const float* residual, int act, float* out, int8_t* qx, float* sx, void* ws,
+                 size_t ws_bytes, bq_stream_t stream) {
+  const char* what = "bq_linear_i8";
+  if (M < 0 || N < 0 || K < 0) return set_error(BQ_ERR_ARG, "%s: negative size", what);
+  if (M == 0 || N == 0) return BQ_OK;
+  if (K % 16) return set_error(BQ_ERR_UNSUPPORTED, "%s: K=%lld is not a multiple of 16", what, (long long)K);
+  if (!x || !W || !sW || !out) return set_error(BQ_ERR_ARG, "%s: null pointer", what);
+  if (!aligned16(x) || !aligned16(W)) return set_error(BQ_ERR_ARG, "%s: x and W must be 16-byte aligned", what);
+  if (act < BQ_ACT_NONE || act > BQ_ACT_GELU) return set_error(BQ_ERR_ARG, "%s: bad activation %d", what, act);
+  if (M <= 4 && K <= 8192 && M * K * 4 < ((int64_t)1 << 31) && N <= 0x7fffffff && N * K < ((int64_t)1 << 31)) {
+    if (qx && !aligned16(qx)) return set_error(BQ_ERR_ARG, "%s: qx must be 16-byte aligned", what);
+    GemmP p{};
+    p.X = x; p.qx = qx; p.sx = sx; p.W = W; p.M = (int)M; p.N = (int)N; p.K = (int)K;
+    p.sa_per_row = 1; p.sW = sW; p.bias = bias; p.res = residual; p.act = act; p.out = out;
+    hipStream_t st = (hipStream_t)stream;
+    switch (M) {
+      case 1: launch_gemv_fq<1>(p, st); break;
+      case 2: launch_gemv_fq<2>(p, st); break;
+      case 3: launch_gemv_fq<3>(p, st); break;
+      default: launch_gemv_fq<4>(p, st); break;
+    }
+    return check_launch(what);
+  }
+  if (!qx || !sx) return set_error(BQ_ERR_ARG, "%s: qx and sx are needed (M=%lld > 4 quantizes into them)", what,
+                                   (long long)M);
+  const int rc = bq_quantize_rows(x, M, K, qx, sx, stream);
+  if (rc != BQ_OK) return rc;
+  return gemm_impl(what, qx, W, M, N, K, sx, sW, bias, residual, act, out, nullptr, ws, ws_bytes, false, stream);
 }
 
 static int conv_impl(const char* what, const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t C,

@@ -22,7 +22,7 @@ __all__ = [
     "quantize_rows", "quantize_weight_per_channel", "quantize_tensor", "quantize_nhwc",
     "gemm_i8", "conv2d_i8_nhwc", "conv2d_i8_nhwc_q", "dwconv_i8_nhwc", "pack_linear_weight", "pack_conv_weight",
     "quantize_nhwc_scaled", "quantize_nhwc_chscale", "se_gate_nhwc", "linear_w8a32", "dequant_weight",
-    "pack_dw_weight", "linear", "conv2d", "depthwise_conv2d", "round_up", "split_workspace",
+    "pack_dw_weight", "linear", "linear_rows", "conv2d", "depthwise_conv2d", "round_up", "split_workspace",
 ]
 
 
@@ -551,10 +551,37 @@ def linear(x: torch.Tensor, w8: Int8Weight, bias=None, act=ACT_NONE, residual=No
     x2 = x.reshape(-1, x.shape[-1])
     if w8.kpad != w8.in_features:
         x2 = torch.nn.functional.pad(x2, (0, w8.kpad - w8.in_features))
-    qa, sa = quantize_tensor(x2) if w8.per_tensor else quantize_rows(x2, pre_act)
     r = None if residual is None else residual.reshape(-1, w8.out_features)
+    if x2.shape[0] <= 4 and pre_act == ACT_NONE and not w8.per_tensor:
+        return linear_rows(x2, w8, bias, act, r).reshape(*lead, w8.out_features)
+    qa, sa = quantize_tensor(x2) if w8.per_tensor else quantize_rows(x2, pre_act)
     out = gemm_i8(qa, w8.q, sa, w8.s, bias, act, residual=r)
     return out.reshape(*lead, w8.out_features)
+
+
+def linear_rows(x2: torch.Tensor, w8: Int8Weight, bias=None, act=ACT_NONE, residual=None, want_q: bool = False):
+    """The dynamic-quant W8A8 Linear on f32 ``x2 [M, Kpad]`` in one call (bq_linear_i8: for
+    M <= 4 one launch, the per-row quantization fused into the GEMV). Returns ``out [M, N]``,
+    or ``(out, q int8 [M, Kpad], s [M])`` with ``want_q``."""
+    x2 = _f32c(x2)
+    require_device(x2.device)
+    M, K = x2.shape
+    N = w8.out_features
+    if K != w8.kpad:
+        raise RuntimeError(f"mat1 and mat2 shapes cannot be multiplied ({M}x{K} and {w8.kpad}x{N})")
+    b = _vec(bias, N, "bias")
+    r = None
+    if residual is not None:
+        if tuple(residual.shape) != (M, N):
+            raise RuntimeError(f"residual shape {tuple(residual.shape)} != output {(M, N)}")
+        r = residual.float().contiguous()
+    out = torch.empty((M, N), dtype=torch.float32, device=x2.device)
+    need_q = want_q or M > 4 or K > 8192
+    q = torch.empty((M, K), dtype=torch.int8, device=x2.device) if need_q else None
+    s = torch.empty((M,), dtype=torch.float32, device=x2.device) if need_q else None
+    check(lib().bq_linear_i8(x2.data_ptr(), w8.q.data_ptr(), M, N, K, w8.s.data_ptr(), _ptr(b), _ptr(r), act,
+                             out.data_ptr(), _ptr(q), _ptr(s), *_ws_args(x2.device), _stream(x2)))
+    return (out, q, s) if want_q else out
 
 
 def layernorm_quantize_rows(x: torch.Tensor, weight, bias, eps: float, want_y: bool = False):

@@ -163,6 +163,19 @@ int bq_gemm_i8(const int8_t* A, const int8_t* W, int64_t M, int64_t N, int64_t K
                const float* sA, const float* sW, const float* bias, const float* residual, int act,
                float* out, int32_t* acc, void* ws, size_t ws_bytes, bq_stream_t stream);
 
+/* The dynamic-quant W8A8 Linear: out f32 [M, N] = bq_gemm_i8 of the per-row quantization of
+ * x f32 [M, K] (bq_quantize_rows' rule and bytes) against W int8 [N, K] / sW, with bias,
+ * residual and act as bq_gemm_i8. The quantized rows and scales are written to qx int8
+ * [M, K] and sx f32 [M]. M <= 4, K <= 8192: one launch, the quantization fused into the
+ * GEMV (every workgroup quantizes the rows into its own LDS while its weight loads are in
+ * flight; qx and sx are then optional, nullable). Otherwise bq_quantize_rows into qx / sx,
+ * then bq_gemm_i8 (ws: its split-K workspace). K % 16 == 0; x, W, qx 16-byte aligned.
+ * Replaces the reference's Linear forward: the activation quantize (kernels.ts:2024-2081)
+ * followed by matmulInt8(scaled) (kernels.ts:1808-1852), here with per-row scales. */
+int bq_linear_i8(const float* x, const int8_t* W, int64_t M, int64_t N, int64_t K, const float* sW,
+                 const float* bias, const float* residual, int act, float* out, int8_t* qx, float* sx, void* ws,
+                 size_t ws_bytes, bq_stream_t stream);
+
 /* bq_gemm_i8 that allocates nothing and takes no workspace: the same arguments without
  * ws / ws_bytes, the same kernels and bit-identical results. No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under HIP graph

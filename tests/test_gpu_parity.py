@@ -800,3 +800,34 @@ def test_mmi8_lcg_procedure(dev, size):
     wrong = int((n(acc) != ref).sum())
     assert wrong == 0, f"{wrong} of {size * size} entries differ from the int32 reference"
     assert_f32(n(out), O.dequant(ref, s0, sw, b))
+
+
+# ------------------------------------- the dynamic-quant Linear in one call (bq_linear_i8)
+
+@pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (2, 300, 1040), (3, 129, 8192), (4, 64, 16), (1, 33, 2064),
+                                   (4, 4100, 4096), (5, 256, 1024), (17, 96, 784), (300, 520, 4608)])
+@pytest.mark.parametrize("extras", [False, True])
+def test_linear_rows_fused_quantize(dev, M, N, K, extras):
+    """bq_linear_i8: for M <= 4 the per-row quantization runs inside the GEMV. Its quantized
+    rows and scales equal the oracle's (bytes and bits), its int32 / f32 result equals
+    bq_quantize_rows + bq_gemm_i8 bit for bit and the oracle's epilogue, with a residual and
+    an activation too; larger M quantizes into the caller's buffers, then the GEMM."""
+    say(f"bq_linear_i8 M={M} N={N} K={K} extras={extras}")
+    rng = np.random.default_rng(M * 11 + N + K)
+    x = rng.normal(size=(M, K)).astype(np.float32)
+    x[0, : min(K, 8)] = [2.5, -2.5, 0.0, 1e-30, -7.25, 3.0, 0.5, -0.5][: min(K, 8)]
+    w = (rng.normal(size=(N, K)) / np.sqrt(K)).astype(np.float32)
+    b = (0.1 * rng.normal(size=N)).astype(np.float32)
+    r = rng.normal(size=(M, N)).astype(np.float32) if extras else None
+    act = I.ACT_RELU if extras else I.ACT_NONE
+    w8 = I.pack_linear_weight(t(w, dev))
+    out, q, s = I.linear_rows(t(x, dev), w8, t(b, dev), act, None if r is None else t(r, dev), want_q=True)
+    q_o, s_o = O.quantize_rows(x)
+    assert np.array_equal(n(q), q_o) and np.array_equal(n(s), s_o)
+    qa, sa = I.quantize_rows(t(x, dev))
+    want = I.gemm_i8(qa, w8.q, sa, w8.s, t(b, dev), act, residual=None if r is None else t(r, dev))
+    assert torch.equal(out, want)
+    y_o = O.dequant(O.gemm_i8_i32(q_o, n(w8.q)), s_o, n(w8.s), b, act == I.ACT_RELU, r)
+    assert_f32(n(out), y_o)
+    if M <= 4:  # without the optional quantized-row outputs: the same result
+        assert torch.equal(I.linear_rows(t(x, dev), w8, t(b, dev), act, None if r is None else t(r, dev)), out)
