@@ -445,6 +445,34 @@ def w8a32_rows(dev, stream):
     return rows
 
 
+def model_trace(dev, stream, name, steps):
+    """One configuration's int8 forward for a kernel trace: the compiled HIP graph replayed
+    ``steps`` times with dynamic scales (and, for the conv nets, ``steps`` times with calibrated
+    scales), each replay timed with HIP events. The trace's per-kernel durations against these
+    replay times split each forward into time inside kernels and the gaps between them."""
+    import torch
+    import borch_amd as bt
+    from borch_amd import nets, workloads as WL
+    make = {"resnet18": lambda s: WL.c3_input(16, s), "efficientnet_b0": lambda s: WL.c4_input(64, s),
+            "vit_b16": lambda s: WL.c5_input(32, 197, 768, s)}[name]
+    model = nets.build(name, seed=0, device=dev)
+    x = torch.from_numpy(make(0)).to(dev)
+    out = {"model": name, "steps": steps}
+    c = bt.compiled(model, int8=True, graph=True, fuse=False, plan_cache=False)
+    with torch.no_grad():
+        c(x)
+        torch.cuda.synchronize()
+        out["dynamic_replay_ms"] = [round(time_events(lambda i: c(x), 1, stream), 4) for _ in range(steps)]
+    if name != "vit_b16":
+        bt.calibrate_int8(model, [torch.from_numpy(make(s)).to(dev) for s in (11, 12)])
+        c2 = bt.compiled(model, int8=False, graph=True, fuse=False, plan_cache=False)
+        with torch.no_grad():
+            c2(x)
+            torch.cuda.synchronize()
+            out["static_replay_ms"] = [round(time_events(lambda i: c2(x), 1, stream), 4) for _ in range(steps)]
+    print(json.dumps(out), flush=True)
+
+
 def print_layer_tables(models, tables):
     """Markdown: per model, the forward times and one row per int8 layer timed alone."""
     for key, rows in tables.items():
@@ -485,6 +513,10 @@ def main():
                     help="for counter runs: the bandwidth-bound kernels alone (GEMV M=1 and skinny M=16 over 24 "
                          "rotated weights, the 4096x4096 per-row quantize, EfficientNet-B0 b64 depthwise layers, a "
                          "per-tensor quantize) and 5 launches of a 64 MiB device copy; prints their shapes and bytes")
+    ap.add_argument("--model-trace", choices=["resnet18", "efficientnet_b0", "vit_b16"],
+                    help="for kernel traces: the model's int8 forward as a HIP graph, replayed --steps times with "
+                         "dynamic scales, then (ResNet-18, EfficientNet-B0) --steps times calibrated; prints the "
+                         "replay times")
     ap.add_argument("--layers", action="store_true",
                     help="the model configurations only, then every int8 layer's table as markdown "
                          "(GEMM shape, ops, bytes, us alone, TOPS, MFMA fraction, GB/s)")
@@ -506,6 +538,10 @@ def main():
 
     if args.hbm_kernels:
         hbm_kernels(dev)
+        return
+
+    if args.model_trace:
+        model_trace(dev, stream, args.model_trace, args.steps)
         return
 
     if args.layers:

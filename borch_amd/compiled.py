@@ -48,7 +48,7 @@ class Compiled:
         self.split = int(split)
         if self.split < 1:
             raise ValueError(f"split must be >= 1, got {split}")
-        self._streams = {}  # device -> [(stream, split-K workspace)], made on its first split call
+        self._streams = {}  # device -> [stream], made on its first split call (each with its own split-K workspace)
         self.tuned = []  # the tuner's decisions, one list per input shape (borch_amd.tune.tune)
         self._tuned_keys = set()
         self.int8_layers = 0
@@ -75,17 +75,16 @@ class Compiled:
             return self.model(x)
         streams = self._streams.get(x.device)
         if streams is None:  # the warm-up runs come first, outside any capture
-            nb = int(_i8.lib().bq_gemm_ws_bytes())
-            streams = self._streams[x.device] = [(torch.cuda.Stream(device=x.device),
-                                                  torch.zeros(nb, dtype=torch.uint8, device=x.device))
-                                                 for _ in range(self.split)]
+            streams = self._streams[x.device] = [torch.cuda.Stream(device=x.device) for _ in range(self.split)]
+            for s in streams:  # each chunk stream's split-K workspace, made now (outside any capture)
+                _i8.split_workspace(x.device, s)
         cur = torch.cuda.current_stream(x.device)
         outs = []
-        for (s, ws), xc in zip(streams, x.chunk(self.split)):
+        for s, xc in zip(streams, x.chunk(self.split)):
             s.wait_stream(cur)
-            with torch.cuda.stream(s), _i8.workspace_scope(ws):
+            with torch.cuda.stream(s):
                 outs.append(self.model(xc))
-        for s, _ in streams:
+        for s in streams:
             cur.wait_stream(s)
         return torch.cat(outs)
 

@@ -8,8 +8,6 @@ its conv input). There is no CPU path: a tensor that is not on a gfx950 device r
 """
 from __future__ import annotations
 
-import contextlib
-import threading
 from dataclasses import dataclass
 
 import torch
@@ -66,36 +64,9 @@ def split_workspace(device: torch.device, stream=None):
     return ws
 
 
-# A workspace that replaces the device's for the calls made inside ``workspace_scope``:
-# launches on concurrent streams must not share one (the tile counters and partials).
-# Per thread: a scope opened on one thread does not redirect another thread's calls.
-_WS_SCOPE = threading.local()
-
-
-def _scopes() -> list:
-    st = getattr(_WS_SCOPE, "stack", None)
-    if st is None:
-        st = _WS_SCOPE.stack = []
-    return st
-
-
-@contextlib.contextmanager
-def workspace_scope(ws: torch.Tensor):
-    """The GEMM / conv calls made inside use ``ws`` (``bq_gemm_ws_bytes()`` zero-filled bytes,
-    on the device they run on) as their split-K workspace instead of the device's."""
-    _scopes().append(ws)
-    try:
-        yield
-    finally:
-        _scopes().pop()
-
-
 def _ws_args(device):
-    st = _scopes()
-    if st and st[-1].device == torch.device(device):
-        ws = st[-1]
-    else:
-        ws = split_workspace(device)
+    """(pointer, bytes) of the current stream's split-K workspace, or (None, 0) (unsplit)."""
+    ws = split_workspace(device)
     return (None, 0) if ws is None else (ws.data_ptr(), ws.numel())
 
 

@@ -87,22 +87,6 @@ def test_bench_layer_work_matches_the_implicit_gemm_shapes():
     assert bench.layer_work("gemm_i8", a)[:2] == ((6304, 2304, 768), 2 * 6304 * 2304 * 768)
 
 
-def test_workspace_scope_is_per_thread():
-    """A split-K workspace scope (compiled(split=n) opens one per stream) redirects the
-    calls of the thread that opened it only."""
-    import threading
-    import torch
-    from borch_amd import int8 as I
-    ws = torch.zeros(16, dtype=torch.uint8)
-    seen = []
-    with I.workspace_scope(ws):
-        assert I._scopes()[-1] is ws
-        th = threading.Thread(target=lambda: seen.append(list(I._scopes())))
-        th.start()
-        th.join()
-    assert seen == [[]] and I._scopes() == []
-
-
 def test_vectors_reaching_the_kernels_have_their_full_length():
     """Bias / scale vectors are passed to the kernels as bare pointers: a short one is
     refused on the host instead of being read past its end."""
