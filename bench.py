@@ -208,6 +208,19 @@ def hbm_kernels(dev):
         for q in qws:
             I.gemm_i8(qa, q, sa, sw, B)
         ran[f"gemm M={m} (24 rotated weights)"] = WL.gemm_bytes(m)
+    a256 = WL.c2_gemm(256, 0)[0]
+    qa, sa = I.quantize_rows(torch.from_numpy(a256).to(dev))
+    for q in qws:
+        I.gemm_i8(qa, q, sa, sw, B)
+    ran["gemm M=256 (24 rotated weights)"] = WL.gemm_bytes(256)
+    w8v = [I.Int8Weight(q, sw, 4096, 4096, True) for q in qws]
+    x1 = torch.from_numpy(a1[:1]).to(dev)
+    for w8 in w8v:
+        I.linear_w8a32(x1, w8, B)
+    ran["w8a32 M=1 (24 rotated weights)"] = 4096 * 4096 + 4 * 4096 * 3 + 4 * 4096
+    for w8 in w8v:
+        I.linear_rows(x1, I.Int8Weight(w8.q, sw, 4096, 4096), B)
+    ran["linear_rows M=1, quantize fused (24 rotated weights)"] = WL.gemm_bytes(1) + 4 * 4096
     A = torch.from_numpy(WL.c2_gemm(4096, 0)[0]).to(dev)
     for _ in range(5):
         I.quantize_rows(A)
