@@ -458,6 +458,38 @@ def w8a32_rows(dev, stream):
     return rows
 
 
+VIT_GEMMS = [("qkv", 6304, 2304, 768, False), ("proj", 6304, 768, 768, True), ("fc1", 6304, 3072, 768, False),
+             ("fc2", 6304, 768, 3072, True), ("4096^3", 4096, 4096, 4096, False)]
+
+
+def gemm_shapes(dev):
+    """The MFMA GEMMs of the configurations alone, for counter runs and kernel traces: ViT-B/16
+    b32's four Linears at the full batch (the kernel the shape rule picks) and the 4096^3 GEMM,
+    five launches each, then five 64 MiB device copies (the FETCH / WRITE calibration)."""
+    import torch
+    from borch_amd import int8 as I
+    g = torch.Generator().manual_seed(0)
+    ran = {}
+    for name, M, N, K, res in VIT_GEMMS:
+        qa = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8).to(dev)
+        qw = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8).to(dev)
+        sa = (torch.rand(M, generator=g) * 1e-3).to(dev)
+        sw = (torch.rand(N, generator=g) * 1e-3).to(dev)
+        b = torch.randn(N, generator=g).to(dev)
+        r = torch.randn(M, N, generator=g).to(dev) if res else None
+        for _ in range(5):
+            I.gemm_i8(qa, qw, sa, sw, b, residual=r)
+        byts = M * K + N * K + 4 * M + 8 * N + 4 * M * N * (2 if res else 1)
+        ran[name] = {"M": M, "N": N, "K": K, "ops": 2 * M * N * K, "bytes": byts, "residual": res}
+        del qa, qw, r
+    src = torch.randn(16 << 20, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"gemm_shapes": ran, "copy_launches": 5, "copy_bytes": 64 << 20}))
+
+
 def model_trace(dev, stream, name, steps):
     """One configuration's int8 forward for a kernel trace: the compiled HIP graph replayed
     ``steps`` times with dynamic scales (and, for the conv nets, ``steps`` times with calibrated
@@ -526,6 +558,10 @@ def main():
                     help="for counter runs: the bandwidth-bound kernels alone (GEMV M=1 and skinny M=16 over 24 "
                          "rotated weights, the 4096x4096 per-row quantize, EfficientNet-B0 b64 depthwise layers, a "
                          "per-tensor quantize) and 5 launches of a 64 MiB device copy; prints their shapes and bytes")
+    ap.add_argument("--gemm-shapes", action="store_true",
+                    help="for counter runs: 5 launches each of ViT-B/16 b32's four Linear GEMMs (qkv, proj with its "
+                         "residual, fc1, fc2 with its residual; per-row scales, bias, f32 out), the 4096^3 GEMM, and a "
+                         "64 MiB device copy; prints their shapes and algorithmic bytes and ops")
     ap.add_argument("--model-trace", choices=["resnet18", "efficientnet_b0", "vit_b16"],
                     help="for kernel traces: the model's int8 forward as a HIP graph, replayed --steps times with "
                          "dynamic scales, then (ResNet-18, EfficientNet-B0) --steps times calibrated; prints the "
@@ -551,6 +587,10 @@ def main():
 
     if args.hbm_kernels:
         hbm_kernels(dev)
+        return
+
+    if args.gemm_shapes:
+        gemm_shapes(dev)
         return
 
     if args.model_trace:

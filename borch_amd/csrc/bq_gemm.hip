@@ -527,8 +527,67 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
   int* patch = reinterpret_cast<int*>(lds) + wave * 32 * PITCH;
   constexpr int C4 = WTN / 4;                 // float4 columns per row
   constexpr int ROWS_PER_STORE = 64 / C4;     // rows one 64-lane store covers
+  constexpr int NST = 32 / ROWS_PER_STORE;    // stores per slice
   const bool has_r = p.res != nullptr;
   float amax = 0.f;  // max |y| of the values this lane stores (fmaxf: a NaN is skipped)
+
+  // Fast path: f32 output only (no int32 or int8 twin), float4-aligned, and a tile's rows
+  // within 2 GB. Its stores are buffer stores through a resource that ends at row M of
+  // the tile: a lane's offset within the tile is one 32-bit VGPR, and rows past M fall out
+  // of range and are dropped by the hardware (no per-row test, no 64-bit address
+  // arithmetic per store). About 5 VALU instructions per output against 12 on the general
+  // path, whose per-row branches on every optional output stay for the other cases.
+  const bool fast = p.vec_ok && p.out && !p.acc && !p.q_out && (long long)BM * p.N * 4 < (1ll << 31);
+  const uint32_t tile_bytes = fast ? (uint32_t)((long long)min(BM, p.M - m0) * p.N * 4) : 0u;
+  const __amdgpu_buffer_rsrc_t r_out = make_rsrc(p.out + (size_t)m0 * p.N, tile_bytes);
+  const __amdgpu_buffer_rsrc_t r_res = make_rsrc(has_r ? p.res + (size_t)m0 * p.N : p.res, has_r ? tile_bytes : 0u);
+  const uint32_t row_step = (uint32_t)(ROWS_PER_STORE * p.N) * 4u;  // bytes between a lane's rows
+  // Rows rl, rl + ROWS_PER_STORE, ... of the tile (rl: this lane's first row of the slice).
+  // (always inlined: a call would take the kernel argument block's address and move its
+  // fields from SGPRs to VGPRs)
+  auto fast_rows = [&]<bool RES, bool AMAX>(int rl, int col4, int ncol) __attribute__((always_inline)) {
+    const float4 sw4 = *reinterpret_cast<const float4*>(&s_sw[ncol]);
+    const float4 b4 = *reinterpret_cast<const float4*>(&s_b[ncol]);
+    const uint32_t voff = ((uint32_t)rl * (uint32_t)p.N + (uint32_t)(n0 + ncol)) * 4u;
+    float4 rv[NST];
+    if constexpr (RES) {  // every residual row first: a load after a store waits for it
+#pragma unroll
+      for (int k = 0; k < NST; ++k)
+        rv[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r_res, voff + k * row_step, 0, 0));
+    }
+#pragma unroll
+    for (int k = 0; k < NST; ++k) {
+      const int row = k * ROWS_PER_STORE + lane / C4;  // within the slice
+      const int4 a = *reinterpret_cast<const int4*>(&patch[row * PITCH + col4 * 4]);
+      const float sa = s_sa[rl + k * ROWS_PER_STORE];
+      float4 o;
+      o.x = __fadd_rn(__fmul_rn(__fmul_rn((float)a.x, sa), sw4.x), b4.x);
+      o.y = __fadd_rn(__fmul_rn(__fmul_rn((float)a.y, sa), sw4.y), b4.y);
+      o.z = __fadd_rn(__fmul_rn(__fmul_rn((float)a.z, sa), sw4.z), b4.z);
+      o.w = __fadd_rn(__fmul_rn(__fmul_rn((float)a.w, sa), sw4.w), b4.w);
+      if constexpr (RES) {
+        o.x = __fadd_rn(o.x, rv[k].x); o.y = __fadd_rn(o.y, rv[k].y);
+        o.z = __fadd_rn(o.z, rv[k].z); o.w = __fadd_rn(o.w, rv[k].w);
+      }
+      if (p.act == BQ_ACT_RELU) {
+        o.x = o.x > 0.f ? o.x : 0.f; o.y = o.y > 0.f ? o.y : 0.f;
+        o.z = o.z > 0.f ? o.z : 0.f; o.w = o.w > 0.f ? o.w : 0.f;
+      } else if (p.act == BQ_ACT_SILU) {
+        o.x = silu(o.x); o.y = silu(o.y); o.z = silu(o.z); o.w = silu(o.w);
+      } else if (p.act == BQ_ACT_GELU) {
+        o = gelu4(o);
+      }
+      // The row step goes into the VGPR offset, the SGPR offset stays 0: these 16-byte
+      // stores with the step in an SGPR offset wrote wrong values to about 1% of the rows
+      // (the same data register set reloaded by the next LDS read), with it in the VGPR
+      // offset none.
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, o), r_out, voff + k * row_step, 0, 0);
+      if constexpr (AMAX) {  // rows past M are computed (and dropped) but must not count
+        if (m0 + rl + k * ROWS_PER_STORE < p.M)
+          amax = fmaxf(amax, fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w))));
+      }
+    }
+  };
   // One slice per compile-time i (a run-time i would index the accumulators dynamically
   // and send them to scratch memory).
   auto slice = [&](auto ic) {
@@ -548,14 +607,29 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
         for (int r = 0; r < 16; ++r)
           patch[((r >> 2) * 8 + (lane >> 5) * 4 + (r & 3)) * PITCH + j * 32 + (lane & 31)] = c[i][j][r];
     }
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's patch is written
+    // This wave's patch is written before any lane reads another lane's values. The wait is
+    // an asm statement with a memory clobber: the compiler, which sees only one lane, would
+    // otherwise move a read above a write that cannot alias within that lane (the builtin
+    // waitcnt and wave barrier do not order memory for it).
+    wait_lds();
     __builtin_amdgcn_wave_barrier();
     const int col4 = lane % C4;
     const int ncol = wn * WTN + col4 * 4;  // tile-local column of this lane's 4 values
     const int n = n0 + ncol;
-    const float4 sw4 = *reinterpret_cast<const float4*>(&s_sw[ncol]);
-    const float4 b4 = *reinterpret_cast<const float4*>(&s_b[ncol]);
-    if (p.vec_ok && n < p.N) {
+    if (fast) {
+      if (n < p.N) {
+        const int rl = wm * WTM + i * 32 + lane / C4;
+        if (has_r) {
+          if (p.amax) fast_rows.template operator()<true, true>(rl, col4, ncol);
+          else fast_rows.template operator()<true, false>(rl, col4, ncol);
+        } else {
+          if (p.amax) fast_rows.template operator()<false, true>(rl, col4, ncol);
+          else fast_rows.template operator()<false, false>(rl, col4, ncol);
+        }
+      }
+    } else if (p.vec_ok && n < p.N) {
+      const float4 sw4 = *reinterpret_cast<const float4*>(&s_sw[ncol]);
+      const float4 b4 = *reinterpret_cast<const float4*>(&s_b[ncol]);
       // Bias 0 when absent: y + 0.0f == y for every y this produces (no -0.0).
       auto store_row = [&](int rr, float4 rv, bool with_r) {
         const int row = rr + lane / C4;
@@ -632,7 +706,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
         }
       }
     }
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // this slice's patch reads are done before the next writes
+    wait_lds();  // this slice's patch reads are done before the next slice's writes
     __builtin_amdgcn_wave_barrier();
   };
   [&]<int... Is>(std::integer_sequence<int, Is...>) {
@@ -1229,6 +1303,8 @@ static void launch_tiled(GemmP p, hipStream_t st, const Ws& ws) {
 //  13 <256,64,4,1,2,1>  14 <128,64,4,1,3,1>
 //  15 <256,256,2,4,2,1> on 16x16x64 MFMAs (the same form measured 4-13% slower than 5 and
 //     6 on 128x128 and 256x128 tiles, so those stay on 32x32x32)
+// Ids 3 and 9 never won a measurement: neither the rule nor a plan selects them, and their
+// kernels are not built (the id numbering stays, for stored plans).
 struct TileDims {
   int bm, bn;
 };
@@ -1273,12 +1349,10 @@ static void launch_gemm(const GemmP& p, hipStream_t st, const Ws& ws) {
   switch (choose_cfg(p, CONV)) {
     case 1: return launch_tiled<256, 256, 2, 4, CONV, 2, 1>(p, st, ws);
     case 2: return launch_tiled<256, 256, 2, 4, CONV, 2, 2>(p, st, ws);
-    case 3: return launch_tiled<256, 256, 2, 2, CONV, 2, 2>(p, st, ws);
     case 4: return launch_tiled<128, 128, 2, 2, CONV, 4, 2>(p, st, ws);
     case 5: return launch_tiled<128, 128, 2, 2, CONV, 2, 2>(p, st, ws);
     case 6: return launch_tiled<256, 128, 2, 2, CONV, 3, 1>(p, st, ws);
     case 8: return launch_tiled<256, 64, 4, 1, CONV, 3, 1>(p, st, ws);
-    case 9: return launch_tiled<64, 64, 2, 2, CONV, 8, 1>(p, st, ws);
     case 10: return launch_tiled<64, 64, 2, 2, CONV, 2, 2>(p, st, ws);
     case 11: return launch_tiled<128, 64, 4, 1, CONV, 2, 1>(p, st, ws);
     case 12: return launch_tiled<128, 32, 4, 1, CONV, 2, 1>(p, st, ws);
