@@ -663,6 +663,20 @@ def main():
     del g_gemm, g_q
     gemm_tops = ops / (gemm_ms * 1e-3) / 1e12
     quant_bytes = 5 * M * K + 4 * M
+    # The main loop alone, by difference: the same kernel (the rule picks the same tile and
+    # no split at either K) at K = 8192, its operands the K = 4096 ones repeated along K (the
+    # same values, so the same MFMA power draw), less the K = 4096 time. Launch, the XCDs'
+    # staggered start, prologue and epilogue cancel; what remains is 32 more 128-byte stages
+    # per tile. Timed interleaved, the minimum of each.
+    qa2, qw2 = torch.cat([qa, qa], 1), torch.cat([qw, qw], 1)
+    g_2k = capture(lambda i: I.gemm_i8(qa2, qw2, sa, sw, B), 10)
+    g_1k = capture(lambda i: I.gemm_i8(qa, qw, sa, sw, B), 10)
+    t1k = t2k = float("inf")
+    for _ in range(4):
+        t1k = min(t1k, time_graph(g_1k, 10, 3, stream))
+        t2k = min(t2k, time_graph(g_2k, 10, 3, stream))
+    del g_2k, g_1k, qa2, qw2
+    main_loop_tops = ops / ((t2k - t1k) * 1e-3) / 1e12
     del A, out
 
     # ---- sweep rows (cache-cold weight rotation for the HBM-bound ones)
@@ -774,7 +788,12 @@ def main():
                      "kernel": "gemm_i8_kernel 256x256 (bq_gemm_i8)", "kernel_ms": round(gemm_ms, 5),
                      "timing": "HIP events around HIP-graph replays on the launch stream",
                      "measured_ceiling_TOPS": ceilings["mfma_int8_TOPS_no_memory"],
-                     "frac_of_measured_ceiling": round(gemm_tops / ceilings["mfma_int8_TOPS_no_memory"], 4)},
+                     "frac_of_measured_ceiling": round(gemm_tops / ceilings["mfma_int8_TOPS_no_memory"], 4),
+                     "main_loop": {"TOPS": round(main_loop_tops, 1),
+                                   "frac_of_measured_ceiling": round(main_loop_tops / ceilings["mfma_int8_TOPS_no_memory"], 4),
+                                   "us_K4096": round(t1k * 1e3, 3), "us_K8192": round(t2k * 1e3, 3),
+                                   "method": "2*4096^3 ops / (t(K=8192) - t(K=4096)), the same kernel and "
+                                             "operands repeated along K: the 32 extra 128-byte stages alone"}},
         "ceilings": ceilings,
         "sweep": sweep,
         "models": models,

@@ -532,16 +532,21 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
   float amax = 0.f;  // max |y| of the values this lane stores (fmaxf: a NaN is skipped)
 
   // Fast path: f32 output only (no int32 or int8 twin), float4-aligned, and a tile's rows
-  // within 2 GB. Its stores are buffer stores through a resource that ends at row M of
-  // the tile: a lane's offset within the tile is one 32-bit VGPR, and rows past M fall out
-  // of range and are dropped by the hardware (no per-row test, no 64-bit address
-  // arithmetic per store). About 5 VALU instructions per output against 12 on the general
-  // path, whose per-row branches on every optional output stay for the other cases.
+  // within 2 GB. Its stores are buffer stores through a resource that ends at row M of the
+  // tile: a lane's offset within the tile is one 32-bit VGPR, and rows past M fall out of
+  // range and are dropped by the hardware (no per-row test, no 64-bit address arithmetic
+  // per store). About 5 VALU instructions per output against 12 on the general path, whose
+  // per-row branches on every optional output stay for the other cases (the int8 twin's
+  // packing inlined here pushed the 256-row tiles' kernel arguments out of SGPRs). The
+  // stores write through to memory (sc1): the output does not sit dirty in the XCD's L2 to
+  // be written back at the kernel's end, which measured 4-16% faster per launch back to
+  // back (ViT qkv 23.2 -> 21.2 us, half-batch qkv 16.0 -> 13.5).
   const bool fast = p.vec_ok && p.out && !p.acc && !p.q_out && (long long)BM * p.N * 4 < (1ll << 31);
   const uint32_t tile_bytes = fast ? (uint32_t)((long long)min(BM, p.M - m0) * p.N * 4) : 0u;
   const __amdgpu_buffer_rsrc_t r_out = make_rsrc(p.out + (size_t)m0 * p.N, tile_bytes);
   const __amdgpu_buffer_rsrc_t r_res = make_rsrc(has_r ? p.res + (size_t)m0 * p.N : p.res, has_r ? tile_bytes : 0u);
   const uint32_t row_step = (uint32_t)(ROWS_PER_STORE * p.N) * 4u;  // bytes between a lane's rows
+  constexpr int WT = 16;  // cache policy of the output stores: sc1, write-through
   // Rows rl, rl + ROWS_PER_STORE, ... of the tile (rl: this lane's first row of the slice).
   // (always inlined: a call would take the kernel argument block's address and move its
   // fields from SGPRs to VGPRs)
@@ -581,7 +586,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
       // stores with the step in an SGPR offset wrote wrong values to about 1% of the rows
       // (the same data register set reloaded by the next LDS read), with it in the VGPR
       // offset none.
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, o), r_out, voff + k * row_step, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, o), r_out, voff + k * row_step, 0, WT);
       if constexpr (AMAX) {  // rows past M are computed (and dropped) but must not count
         if (m0 + rl + k * ROWS_PER_STORE < p.M)
           amax = fmaxf(amax, fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w))));
