@@ -222,4 +222,23 @@ __device__ __forceinline__ float dequant_one(int acc, float sa, float sw, float 
   return activate(v, act);
 }
 
+// Raw (stride 0) buffer resource over `bytes` bytes from `base`: a load at or past `bytes`
+// returns zeros and a store there is dropped.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// Stores at byte offset `off` of a buffer resource that write through the XCD's L2 to
+// memory (cache policy sc1): a large output then leaves no dirty lines for the L2
+// write-back at the kernel's end. The whole offset is in the VGPR (SGPR offset 0): with part
+// of it in the SGPR offset, 16-byte stores wrote wrong values to a few rows when the next
+// instruction reloaded their data registers.
+constexpr int CPOL_WT = 16;  // sc1
+__device__ __forceinline__ void store_wt16(__amdgpu_buffer_rsrc_t r, uint32_t off, float4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, v), r, off, 0, CPOL_WT);
+}
+__device__ __forceinline__ void store_wt4(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t v) {
+  __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, CPOL_WT);
+}
+
 }  // namespace bq

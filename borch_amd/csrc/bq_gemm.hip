@@ -85,13 +85,11 @@ constexpr int KMAX_EXACT = 133152;
 // padding) become zeros without a branch. OOB is the offset that is always out of range.
 constexpr uint32_t OOB = 0x80000000u;
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
 
 __device__ __forceinline__ v4i buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
+
 
 // Byte offset of 16-byte chunk `c` (0..7) of LDS row `r`. The chunk index is XORed with
 // bits 1..3 of the row: the 16 lanes that read one MFMA fragment (16 consecutive rows,
@@ -546,7 +544,6 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
   const __amdgpu_buffer_rsrc_t r_out = make_rsrc(p.out + (size_t)m0 * p.N, tile_bytes);
   const __amdgpu_buffer_rsrc_t r_res = make_rsrc(has_r ? p.res + (size_t)m0 * p.N : p.res, has_r ? tile_bytes : 0u);
   const uint32_t row_step = (uint32_t)(ROWS_PER_STORE * p.N) * 4u;  // bytes between a lane's rows
-  constexpr int WT = 16;  // cache policy of the output stores: sc1, write-through
   // Rows rl, rl + ROWS_PER_STORE, ... of the tile (rl: this lane's first row of the slice).
   // (always inlined: a call would take the kernel argument block's address and move its
   // fields from SGPRs to VGPRs)
@@ -582,11 +579,10 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
       } else if (p.act == BQ_ACT_GELU) {
         o = gelu4(o);
       }
-      // The row step goes into the VGPR offset, the SGPR offset stays 0: these 16-byte
-      // stores with the step in an SGPR offset wrote wrong values to about 1% of the rows
-      // (the same data register set reloaded by the next LDS read), with it in the VGPR
-      // offset none.
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, o), r_out, voff + k * row_step, 0, WT);
+      // The row step goes into the VGPR offset: with it in the SGPR offset these stores
+      // wrote wrong values to about 1% of the rows (each store followed by an LDS read
+      // into its data registers); with it in the VGPR offset, none.
+      store_wt16(r_out, voff + k * row_step, o);
       if constexpr (AMAX) {  // rows past M are computed (and dropped) but must not count
         if (m0 + rl + k * ROWS_PER_STORE < p.M)
           amax = fmaxf(amax, fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w))));
@@ -1174,6 +1170,8 @@ __global__ __launch_bounds__(256) void dwconv_blk_kernel(const int8_t* __restric
   const int items = ((OW + OWB - 1) / OWB) * CG;
   const int total = rows * items;
   const float sa = sA[0];
+  // the output, written through (the host keeps it under 4 GB)
+  const __amdgpu_buffer_rsrc_t r_out = make_rsrc(out, (uint32_t)((size_t)rows * OW * C * 4));
   // Consecutive output rows share input rows (KS - S of them): the blocks of a run of rows
   // are regrouped onto one XCD so those rows come from its L2 rather than once per XCD.
   const int lb = xcd_order(blockIdx.x, gridDim.x);
@@ -1242,7 +1240,7 @@ __global__ __launch_bounds__(256) void dwconv_blk_kernel(const int8_t* __restric
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           v[j] = dequant_one(a[o][q * 4 + j], sa, swv[q * 4 + j], bv[q * 4 + j], bias != nullptr, 0.f, false, act);
-        *reinterpret_cast<float4*>(out + idx + q * 4) = make_float4(v[0], v[1], v[2], v[3]);
+        store_wt16(r_out, (uint32_t)(idx + q * 4) * 4u, make_float4(v[0], v[1], v[2], v[3]));
         if (acc)
           *reinterpret_cast<int4*>(acc + idx + q * 4) =
               make_int4(a[o][q * 4], a[o][q * 4 + 1], a[o][q * 4 + 2], a[o][q * 4 + 3]);
@@ -1741,8 +1739,9 @@ int bq_dwconv_i8_nhwc(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t 
   if (act < BQ_ACT_NONE || act > BQ_ACT_GELU) return set_error(BQ_ERR_ARG, "%s: bad activation %d", what, act);
   const bool wide = (C % 8 == 0) && ((uintptr_t)x & 7) == 0 && ((uintptr_t)w & 7) == 0;
   hipStream_t st = (hipStream_t)stream;
-  // Square 3x3 / 5x5 filters at stride 1 or 2: the register-blocked kernel (32-bit indices).
-  if (KH == KW && (KH == 3 || KH == 5) && (stride == 1 || stride == 2) && N * OH * OW * C < ((int64_t)1 << 31)) {
+  // Square 3x3 / 5x5 filters at stride 1 or 2: the register-blocked kernel (32-bit indices,
+  // its output under 4 GB for the buffer stores).
+  if (KH == KW && (KH == 3 || KH == 5) && (stride == 1 || stride == 2) && N * OH * OW * C < ((int64_t)1 << 30)) {
     // 4 channels and 4 output pixels a thread (measured on EfficientNet-B0's layers at b64:
     // 8 channels a thread was 0-20% slower, 1-2 pixels a thread up to 2x slower).
     const int rows = (int)(N * OH);
