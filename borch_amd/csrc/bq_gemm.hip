@@ -1306,21 +1306,26 @@ static void launch_tiled(GemmP p, hipStream_t st, const Ws& ws) {
 //  13 <256,64,4,1,2,1>  14 <128,64,4,1,3,1>
 //  15 <256,256,2,4,2,1> on 16x16x64 MFMAs (the same form measured 4-13% slower than 5 and
 //     6 on 128x128 and 256x128 tiles, so those stay on 32x32x32)
+//  16 <320,256,2,4,2,1> dense only: 160x64 wave tiles (256 VGPRs; the 16x16 form would spill),
+//     for grids that take two rounds of 256x256 tiles but one of 320x256
 // Ids 3 and 9 never won a measurement: neither the rule nor a plan selects them, and their
 // kernels are not built (the id numbering stays, for stored plans).
 struct TileDims {
   int bm, bn;
 };
-constexpr int NCFG = 16;  // ids 1 .. NCFG - 1
+constexpr int NCFG = 17;  // ids 1 .. NCFG - 1
 constexpr TileDims CFG_TILES[NCFG] = {{0, 0},    {256, 256}, {256, 256}, {256, 256}, {128, 128}, {128, 128},
                                       {256, 128}, {64, 64},   {256, 64},  {64, 64},   {64, 64},   {128, 64},
-                                      {128, 32},  {256, 64},  {128, 64},  {256, 256}};
+                                      {128, 32},  {256, 64},  {128, 64},  {256, 256}, {320, 256}};
 
 // The configuration the tiled kernel runs for M x N x K. Narrow outputs (N <= 64: 1x1 convs
 // of mobile networks, the stem, early ResNet layers) take small-LDS tiles that fit several
 // workgroups per CU (measured 2-2.5x over a 256x64 tile at K <= 240 and 5-15% at
 // K = 2304-4096). Otherwise the largest tile that still fills the chip (>= 192 / 128
-// workgroups) without wasting most of its columns. Ring depth: deep rings keep several
+// workgroups; a dense 256x256 grid from 150) without wasting most of its columns; a dense
+// grid that would need a second round of 256x256 tiles but fits one round of 320x256 takes
+// those (ViT-B/16 b32's fc1, 6304x3072x768: 36.5 -> 26.9 us; at 156 tiles the 256x256 tile
+// beat 128x128 by 15%, at 117 it lost by 20%). Ring depth: deep rings keep several
 // stages of a small tile's operands in flight; when there are more tiles than CUs, a small
 // tile takes the 2-deep ring instead so that several workgroups share a CU. The 256x256
 // tile's 64 KB stages leave room for two buffers only. Small tiles read their fragments two
@@ -1334,9 +1339,11 @@ static int choose_cfg(const GemmP& p, bool conv) {
   const long long t128 = (long long)((p.M + 127) / 128) * ((p.N + 127) / 128);
   const long long t128x32 = (long long)((p.M + 127) / 128) * ((p.N + 31) / 32);
   const long long t64 = (long long)((p.M + 63) / 64) * ((p.N + 63) / 64);
+  const long long t320 = (long long)((p.M + 319) / 320) * ((p.N + 255) / 256);
   if (p.N <= 32 && t128x32 >= 128) return 12;
   if (p.N <= 64 && t64 > 256) return 10;
-  if (t256 >= 192 && p.N >= 192) return conv ? 1 : 15;
+  if (!conv && t256 > 256 && t320 <= 256 && p.N >= 192) return 16;
+  if (t256 >= (conv ? 192 : 150) && p.N >= 192) return conv ? 1 : 15;
   if (t128 >= 128 && p.N >= 96) return t128 > 256 ? 5 : 4;
   return 7;
 }
@@ -1362,6 +1369,9 @@ static void launch_gemm(const GemmP& p, hipStream_t st, const Ws& ws) {
     case 13: return launch_tiled<256, 64, 4, 1, CONV, 2, 1>(p, st, ws);
     case 14: return launch_tiled<128, 64, 4, 1, CONV, 3, 1>(p, st, ws);
     case 15: return launch_tiled<256, 256, 2, 4, CONV, 2, 1, true>(p, st, ws);
+    case 16:  // dense only (the implicit-GEMM loader does not fit beside its 160 accumulators)
+      if constexpr (!CONV) return launch_tiled<320, 256, 2, 4, CONV, 2, 1>(p, st, ws);
+      [[fallthrough]];
     default: return launch_tiled<64, 64, 2, 2, CONV, 4, 2>(p, st, ws);
   }
 }
@@ -1655,8 +1665,9 @@ int bq_plan_candidates(const int64_t* problem, int n, int32_t* cfgs, int32_t* sp
   const int rule = choose_cfg(p, conv);
   out[cnt++] = {rule, split_of(p, rule, conv, 0)};
   // 3 (four waves on 256x256) and 9 (64x64 with an 8-deep ring) never won a measurement
-  static const int ids[] = {1, 2, 4, 5, 6, 7, 8, 10, 11, 12, 13, 14, 15};
+  static const int ids[] = {1, 2, 4, 5, 6, 7, 8, 10, 11, 12, 13, 14, 15, 16};
   for (int cfg : ids) {
+    if (cfg == 16 && conv) continue;  // dense only
     const TileDims d = CFG_TILES[cfg];
     const int KT = (p.K + BK - 1) / BK;
     const int tries[] = {1, 2, 4, 8};
@@ -1687,7 +1698,7 @@ int bq_plan_set(const int64_t* problem, int n, int32_t cfg, int32_t split) {
     g_plans.erase(key);
     return BQ_OK;
   }
-  if (cfg < 1 || cfg >= NCFG || cfg == 3 || cfg == 9 || split < 1 || split > 64)
+  if (cfg < 1 || cfg >= NCFG || cfg == 3 || cfg == 9 || (cfg == 16 && conv) || split < 1 || split > 64)
     return set_error(BQ_ERR_ARG, "bq_plan_set: bad configuration %d / split %d", cfg, split);
   if (!tiled) return set_error(BQ_ERR_ARG, "bq_plan_set: a GEMM of at most 64 rows has no tiled kernel to plan");
   g_plans[key] = Plan{cfg, split};

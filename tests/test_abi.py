@@ -151,8 +151,9 @@ def _candidates(lib, problem):
                                      (64, 112, 112, 32, 96, 1, 1, 1, 0), (2, 13, 13, 16, 24, 3, 3, 2, 1)])
 def test_plan_candidates(problem):
     """The kernel-choice candidates (host code, no GPU): the rules' pick first, no pair twice,
-    configuration ids of the tiled kernel only (3 and 9 are never offered), K splits only on
-    tiles of at most 4096 outputs, and never more splits than K stages."""
+    configuration ids of the tiled kernel only (3 and 9 are never offered, 16 only for a dense
+    GEMM), K splits only on tiles of at most 4096 outputs, and never more splits than K
+    stages."""
     from borch_amd import _lib
     lib = _lib.lib()
     cands = _candidates(lib, problem)
@@ -160,8 +161,10 @@ def test_plan_candidates(problem):
     assert len(set(cands)) == len(cands)
     small = {7, 9, 10, 12}  # tiles of 64 x 64 and 128 x 32 outputs
     for cfg, split in cands:
-        assert 1 <= cfg <= 15 and split >= 1
+        assert 1 <= cfg <= 16 and split >= 1
         assert cfg not in (3, 9) or (cfg, split) == cands[0]
+        # 16 only where the dense loader runs: a GEMM or a 1x1 stride-1 unpadded conv
+        assert cfg != 16 or len(problem) == 3 or (problem[5:7] == (1, 1) and problem[7:] == (1, 0))
         if split > 1:
             assert cfg in small
     K = problem[2] if len(problem) == 3 else problem[3] * problem[5] * problem[6]
@@ -176,8 +179,10 @@ def test_plan_rejects_bad_problems_and_small_gemms():
     assert _candidates(lib, (1, 2, 3, 4)) < 0  # neither 3 nor 9 dimensions
     assert _candidates(lib, (1, 4, 4, 16, 8, 5, 5, 1, 0)) < 0  # the filter is larger than the input
     arr = (ctypes.c_int64 * 3)(4096, 4096, 4096)
-    assert lib.bq_plan_set(arr, 3, 3, 1) < 0 and lib.bq_plan_set(arr, 3, 16, 1) < 0
+    assert lib.bq_plan_set(arr, 3, 3, 1) < 0 and lib.bq_plan_set(arr, 3, 17, 1) < 0
     assert lib.bq_plan_set(arr, 3, 1, 0) < 0
+    conv = (ctypes.c_int64 * 9)(16, 32, 32, 64, 64, 3, 3, 1, 1)
+    assert lib.bq_plan_set(conv, 9, 16, 1) < 0  # the 320 x 256 tile is dense only
     small = (ctypes.c_int64 * 3)(16, 512, 512)
     assert lib.bq_plan_set(small, 3, 1, 1) < 0
 
