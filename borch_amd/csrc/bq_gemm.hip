@@ -1348,15 +1348,17 @@ static void launch_tiled(GemmP p, hipStream_t st, const Ws& ws) {
 //     6 on 128x128 and 256x128 tiles, so those stay on 32x32x32)
 //  16 <320,256,2,4,2,1> dense only: 160x64 wave tiles (256 VGPRs; the 16x16 form would spill),
 //     for grids that take two rounds of 256x256 tiles but one of 320x256
+//  17 <128,256,2,4,2,2> 8 waves of 64x64, for grids of more than one round of 128x128 tiles
+//     but one of 128x256 (ViT-B/16 b32's proj and fc2, N = 768: 6-8% faster than 128x128)
 // Ids 3 and 9 never won a measurement: neither the rule nor a plan selects them, and their
 // kernels are not built (the id numbering stays, for stored plans).
 struct TileDims {
   int bm, bn;
 };
-constexpr int NCFG = 17;  // ids 1 .. NCFG - 1
+constexpr int NCFG = 18;  // ids 1 .. NCFG - 1
 constexpr TileDims CFG_TILES[NCFG] = {{0, 0},    {256, 256}, {256, 256}, {256, 256}, {128, 128}, {128, 128},
                                       {256, 128}, {64, 64},   {256, 64},  {64, 64},   {64, 64},   {128, 64},
-                                      {128, 32},  {256, 64},  {128, 64},  {256, 256}, {320, 256}};
+                                      {128, 32},  {256, 64},  {128, 64},  {256, 256}, {320, 256}, {128, 256}};
 
 // The configuration the tiled kernel runs for M x N x K. Narrow outputs (N <= 64: 1x1 convs
 // of mobile networks, the stem, early ResNet layers) take small-LDS tiles that fit several
@@ -1365,7 +1367,8 @@ constexpr TileDims CFG_TILES[NCFG] = {{0, 0},    {256, 256}, {256, 256}, {256, 2
 // workgroups; a dense 256x256 grid from 150) without wasting most of its columns; a dense
 // grid that would need a second round of 256x256 tiles but fits one round of 320x256 takes
 // those (ViT-B/16 b32's fc1, 6304x3072x768: 36.5 -> 26.9 us; at 156 tiles the 256x256 tile
-// beat 128x128 by 15%, at 117 it lost by 20%). Ring depth: deep rings keep several
+// beat 128x128 by 15%, at 117 it lost by 20%); likewise a dense grid of more than one round
+// of 128x128 tiles that fits one round of 128x256 (8 waves). Ring depth: deep rings keep several
 // stages of a small tile's operands in flight; when there are more tiles than CUs, a small
 // tile takes the 2-deep ring instead so that several workgroups share a CU. The 256x256
 // tile's 64 KB stages leave room for two buffers only. Small tiles read their fragments two
@@ -1384,6 +1387,8 @@ static int choose_cfg(const GemmP& p, bool conv) {
   if (p.N <= 64 && t64 > 256) return 10;
   if (!conv && t256 > 256 && t320 <= 256 && p.N >= 192) return 16;
   if (t256 >= (conv ? 192 : 150) && p.N >= 192) return conv ? 1 : 15;
+  const long long t128x256 = (long long)((p.M + 127) / 128) * ((p.N + 255) / 256);
+  if (!conv && t128 > 256 && t128x256 <= 256 && p.N >= 512) return 17;
   if (t128 >= 128 && p.N >= 96) return t128 > 256 ? 5 : 4;
   return 7;
 }
@@ -1409,6 +1414,7 @@ static void launch_gemm(const GemmP& p, hipStream_t st, const Ws& ws) {
     case 13: return launch_tiled<256, 64, 4, 1, CONV, 2, 1>(p, st, ws);
     case 14: return launch_tiled<128, 64, 4, 1, CONV, 3, 1>(p, st, ws);
     case 15: return launch_tiled<256, 256, 2, 4, CONV, 2, 1, true>(p, st, ws);
+    case 17: return launch_tiled<128, 256, 2, 4, CONV, 2, 2>(p, st, ws);
     case 16:  // dense only (the implicit-GEMM loader does not fit beside its 160 accumulators)
       if constexpr (!CONV) return launch_tiled<320, 256, 2, 4, CONV, 2, 1>(p, st, ws);
       [[fallthrough]];
@@ -1705,7 +1711,7 @@ int bq_plan_candidates(const int64_t* problem, int n, int32_t* cfgs, int32_t* sp
   const int rule = choose_cfg(p, conv);
   out[cnt++] = {rule, split_of(p, rule, conv, 0)};
   // 3 (four waves on 256x256) and 9 (64x64 with an 8-deep ring) never won a measurement
-  static const int ids[] = {1, 2, 4, 5, 6, 7, 8, 10, 11, 12, 13, 14, 15, 16};
+  static const int ids[] = {1, 2, 4, 5, 6, 7, 8, 10, 11, 12, 13, 14, 15, 16, 17};
   for (int cfg : ids) {
     if (cfg == 16 && conv) continue;  // dense only
     const TileDims d = CFG_TILES[cfg];

@@ -161,7 +161,7 @@ def test_plan_candidates(problem):
     assert len(set(cands)) == len(cands)
     small = {7, 9, 10, 12}  # tiles of 64 x 64 and 128 x 32 outputs
     for cfg, split in cands:
-        assert 1 <= cfg <= 16 and split >= 1
+        assert 1 <= cfg <= 17 and split >= 1
         assert cfg not in (3, 9) or (cfg, split) == cands[0]
         # 16 only where the dense loader runs: a GEMM or a 1x1 stride-1 unpadded conv
         assert cfg != 16 or len(problem) == 3 or (problem[5:7] == (1, 1) and problem[7:] == (1, 0))
@@ -179,7 +179,7 @@ def test_plan_rejects_bad_problems_and_small_gemms():
     assert _candidates(lib, (1, 2, 3, 4)) < 0  # neither 3 nor 9 dimensions
     assert _candidates(lib, (1, 4, 4, 16, 8, 5, 5, 1, 0)) < 0  # the filter is larger than the input
     arr = (ctypes.c_int64 * 3)(4096, 4096, 4096)
-    assert lib.bq_plan_set(arr, 3, 3, 1) < 0 and lib.bq_plan_set(arr, 3, 17, 1) < 0
+    assert lib.bq_plan_set(arr, 3, 3, 1) < 0 and lib.bq_plan_set(arr, 3, 18, 1) < 0
     assert lib.bq_plan_set(arr, 3, 1, 0) < 0
     conv = (ctypes.c_int64 * 9)(16, 32, 32, 64, 64, 3, 3, 1, 1)
     assert lib.bq_plan_set(conv, 9, 16, 1) < 0  # the 320 x 256 tile is dense only
