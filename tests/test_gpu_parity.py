@@ -480,7 +480,10 @@ def test_conv_absmax_parts_feed_the_next_quantizer(dev, N, C, H, O_, k, stride, 
 # output widths that are not a multiple of its pixel block); 7x7 and the rest the generic one.
 DW_CASES = [(2, 32, 16, 3, 1, 1), (2, 96, 15, 3, 2, 1), (2, 144, 14, 5, 1, 2), (2, 240, 13, 5, 2, 2),
             (1, 6, 7, 3, 1, 1), (4, 1152, 7, 5, 1, 2), (2, 12, 9, 3, 2, 1), (1, 20, 11, 5, 1, 2),
-            (3, 40, 10, 3, 1, 0), (1, 16, 10, 7, 1, 3), (1, 24, 9, 5, 2, 1)]
+            (3, 40, 10, 3, 1, 0), (1, 16, 10, 7, 1, 3), (1, 24, 9, 5, 2, 1),
+            # output rows of 14, 28 and 21 pixels: the 7-pixels-a-thread form, each filter and stride
+            (2, 48, 28, 3, 2, 1), (2, 64, 28, 5, 2, 2), (1, 32, 56, 5, 2, 2), (2, 24, 28, 3, 1, 1),
+            (1, 16, 21, 3, 1, 1)]
 
 
 @pytest.mark.parametrize("N,C,H,k,stride,pad", DW_CASES)
