@@ -45,6 +45,8 @@ SIGNATURES = {
     "bq_quantize_tensor": (_c_int, [_c_p, _c_i64, _c_p, _c_p, _c_p, _c_size, _c_p]),
     "bq_quantize_nhwc": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_size, _c_p]),
     "bq_quantize_nhwc_scaled": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p]),
+    "bq_quantize_nchw": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_size, _c_p]),
+    "bq_quantize_nchw_scaled": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p]),
     "bq_gemm_ws_bytes": (_c_size, []),
     "bq_gemm_i8": (_c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_int, _c_p, _c_p, _c_p,
                             _c_size, _c_p]),

@@ -259,6 +259,22 @@ __global__ __launch_bounds__(QT_THREADS) void quantize_tensor_kernel(const float
                                                                      float* __restrict__ s,
                                                                      const float* __restrict__ s_given) {
   __shared__ float red[QT_THREADS / 64];
+  const int64_t total = P * (int64_t)Cpad;
+  const int64_t words = (total + 3) / 4;
+  const bool flat = (C == Cpad) && ((uintptr_t)x & 15) == 0 && ((uintptr_t)q & 3) == 0 && (total & 3) == 0;
+  const int64_t stride = (int64_t)gridDim.x * QT_THREADS;
+  int64_t wi = (int64_t)blockIdx.x * QT_THREADS + threadIdx.x;
+  // This thread's first words are loaded before the scale is known: their round trip
+  // overlaps the partial maxima's (the scale does not depend on them).
+  float4 pv[4];
+  const bool pre4 = flat && wi + 3 * stride < words;
+  const bool pre1 = flat && !pre4 && wi < words;
+  if (pre4) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) pv[u] = *reinterpret_cast<const float4*>(x + (wi + u * stride) * 4);
+  } else if (pre1) {
+    pv[0] = *reinterpret_cast<const float4*>(x + wi * 4);
+  }
   float m = 0.f;
   for (int i = threadIdx.x; i < nparts; i += QT_THREADS) m = fmaxf(m, parts[i]);
   m = wave_max(m);
@@ -269,11 +285,14 @@ __global__ __launch_bounds__(QT_THREADS) void quantize_tensor_kernel(const float
   const float sc = s_given ? s_given[0] : scale_of(peak);
   if (!s_given && blockIdx.x == 0 && threadIdx.x == 0) s[0] = sc;
   const Quantizer qz(sc);
-  const int64_t total = P * (int64_t)Cpad;
-  const int64_t words = (total + 3) / 4;
-  const bool flat = (C == Cpad) && ((uintptr_t)x & 15) == 0 && ((uintptr_t)q & 3) == 0 && (total & 3) == 0;
-  const int64_t stride = (int64_t)gridDim.x * QT_THREADS;
-  int64_t wi = (int64_t)blockIdx.x * QT_THREADS + threadIdx.x;
+  if (pre4) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) *reinterpret_cast<uint32_t*>(q + (wi + u * stride) * 4) = qz.pack(pv[u]);
+    wi += 4 * stride;
+  } else if (pre1) {
+    *reinterpret_cast<uint32_t*>(q + wi * 4) = qz.pack(pv[0]);
+    wi += stride;
+  }
   if (flat) {
     // four float4 loads a thread in flight before any is quantized (one at a time left
     // the pass latency-bound)
@@ -303,13 +322,15 @@ __global__ __launch_bounds__(QT_THREADS) void quantize_tensor_kernel(const float
 }
 
 // Padded-channel variant (C < Cpad, Cpad % 16 == 0): one thread per 16-byte chunk of a
-// pixel's Cpad output bytes; it reads that chunk's (up to 16) input channels, which are
-// contiguous, and stores one 16-byte word. No per-element division.
+// pixel's Cpad output bytes; it reads that chunk's (up to 16) input channels and stores one
+// 16-byte word. The input is channels-last (HW == 0: a pixel's channels contiguous) or
+// NCHW (HW = H*W: channel c of pixel n*HW + hw at (n*C + c)*HW + hw, so consecutive threads
+// read consecutive pixels of each plane) — an NCHW network input needs no permute first.
 __global__ __launch_bounds__(QT_THREADS) void quantize_pad16_kernel(const float* __restrict__ x, int64_t P,
                                                                     int C, int Cpad,
                                                                     const float* __restrict__ parts, int nparts,
                                                                     int8_t* __restrict__ q, float* __restrict__ s,
-                                                                    const float* __restrict__ s_given) {
+                                                                    const float* __restrict__ s_given, int HW) {
   __shared__ float red[QT_THREADS / 64];
   float m = 0.f;
   for (int i = threadIdx.x; i < nparts; i += QT_THREADS) m = fmaxf(m, parts[i]);
@@ -326,7 +347,16 @@ __global__ __launch_bounds__(QT_THREADS) void quantize_pad16_kernel(const float*
   for (int64_t i = (int64_t)blockIdx.x * QT_THREADS + threadIdx.x; i < total; i += (int64_t)gridDim.x * QT_THREADS) {
     const int64_t p = i / chunks;
     const int c0 = (int)(i - p * chunks) * 16;
-    const float* xp = x + p * C + c0;
+    const float* xp;  // channel 0 of pixel p
+    int64_t cs;       // elements between channels
+    if (HW) {
+      const int64_t n = p / HW;
+      xp = x + (n * C * HW + (p - n * HW));
+      cs = HW;
+    } else {
+      xp = x + p * C;
+      cs = 1;
+    }
     uint32_t wv[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -334,7 +364,7 @@ __global__ __launch_bounds__(QT_THREADS) void quantize_pad16_kernel(const float*
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const int c = c0 + j * 4 + t;
-        b[t] = c < C ? qz(xp[j * 4 + t]) : 0;
+        b[t] = c < C ? qz(xp[c * cs]) : 0;
       }
       wv[j] = pack4(b[0], b[1], b[2], b[3]);
     }
@@ -538,10 +568,13 @@ size_t bq_quantize_tensor_ws_bytes(int64_t n) { return (size_t)nparts_for(n < 0 
 // Per-tensor quantization of x [P, C] into q [P, Cpad]. The scale is, in this order of
 // precedence: s_given (calibrated); from given_parts (partial maxima a producer wrote, e.g.
 // the conv epilogue's per-tile max |y|); else from partial maxima computed here into ws.
+// HW > 0: x is NCHW with planes of HW pixels (the padded path only), else channels-last.
 static int quantize_nhwc_impl(const char* what, const float* x, int64_t P, int64_t C, int64_t Cpad, int8_t* q,
                               float* s, const float* s_given, void* ws, size_t ws_bytes, hipStream_t st,
-                              const float* given_parts = nullptr, int64_t given_np = 0) {
+                              const float* given_parts = nullptr, int64_t given_np = 0, int64_t HW = 0) {
   if (P < 0 || C < 0 || Cpad < C) return set_error(BQ_ERR_ARG, "%s: bad sizes P=%lld C=%lld Cpad=%lld", what, (long long)P, (long long)C, (long long)Cpad);
+  if (HW && (HW < 0 || HW > 0x7fffffff || P % HW || C == Cpad || Cpad % 16 || ((uintptr_t)q & 15)))
+    return set_error(BQ_ERR_UNSUPPORTED, "%s: an NCHW input needs Cpad > C, Cpad %% 16 == 0 and a 16-byte aligned q", what);
   if (!x || !q || (!s && !s_given) || (!ws && !s_given && !given_parts))
     return set_error(BQ_ERR_ARG, "%s: null pointer", what);
   if (Cpad > 0x7fffffff) return set_error(BQ_ERR_ARG, "%s: too many channels", what);
@@ -574,7 +607,8 @@ static int quantize_nhwc_impl(const char* what, const float* x, int64_t P, int64
     int64_t blocks = (chunks + QT_THREADS - 1) / QT_THREADS;
     if (blocks > 8192) blocks = 8192;
     if (blocks < 1) blocks = 1;
-    quantize_pad16_kernel<<<(unsigned)blocks, QT_THREADS, 0, st>>>(x, P, (int)C, (int)Cpad, parts, np, q, s, s_given);
+    quantize_pad16_kernel<<<(unsigned)blocks, QT_THREADS, 0, st>>>(x, P, (int)C, (int)Cpad, parts, np, q, s, s_given,
+                                                                    (int)HW);
     return check_launch(what);
   }
   const int64_t words = (P * Cpad + 3) / 4;
@@ -645,6 +679,21 @@ int bq_quantize_nhwc_scaled(const float* x, int64_t P, int64_t C, int64_t Cpad, 
                             bq_stream_t stream) {
   if (!s) return set_error(BQ_ERR_ARG, "bq_quantize_nhwc_scaled: null scale");
   return quantize_nhwc_impl("bq_quantize_nhwc_scaled", x, P, C, Cpad, q, nullptr, s, nullptr, 0, (hipStream_t)stream);
+}
+
+int bq_quantize_nchw(const float* x, int64_t N, int64_t C, int64_t HW, int64_t Cpad, int8_t* q, float* s, void* ws,
+                     size_t ws_bytes, bq_stream_t stream) {
+  if (N < 0 || HW < 1) return set_error(BQ_ERR_ARG, "bq_quantize_nchw: bad sizes");
+  return quantize_nhwc_impl("bq_quantize_nchw", x, N * HW, C, Cpad, q, s, nullptr, ws, ws_bytes, (hipStream_t)stream,
+                            nullptr, 0, HW);
+}
+
+int bq_quantize_nchw_scaled(const float* x, int64_t N, int64_t C, int64_t HW, int64_t Cpad, const float* s, int8_t* q,
+                            bq_stream_t stream) {
+  if (!s) return set_error(BQ_ERR_ARG, "bq_quantize_nchw_scaled: null scale");
+  if (N < 0 || HW < 1) return set_error(BQ_ERR_ARG, "bq_quantize_nchw_scaled: bad sizes");
+  return quantize_nhwc_impl("bq_quantize_nchw_scaled", x, N * HW, C, Cpad, q, nullptr, s, nullptr, 0,
+                            (hipStream_t)stream, nullptr, 0, HW);
 }
 
 int bq_layernorm_quantize_rows(const float* x, int64_t M, int64_t K, const float* gamma, const float* beta, float eps,

@@ -145,7 +145,8 @@ def quantize_tensor(x: torch.Tensor):
 def quantize_nhwc(x: torch.Tensor, cpad: int | None = None):
     """Per-tensor int8 of an NCHW f32 activation into NHWC int8 with channels padded to
     ``cpad`` (zeros) → ``(q int8 [N, H, W, cpad], s f32 [1])``. A channels-last input is
-    read in place; a contiguous NCHW input is converted first. An unmodified output of
+    read in place, and so is a contiguous NCHW input quantized into padded channels (a
+    network's input image: bq_quantize_nchw); other NCHW inputs are converted first. An unmodified output of
     ``conv2d_i8_nhwc`` carries its per-tile maxima, and then one pass suffices
     (bq_quantize_nhwc_parts); otherwise partial maxima are computed first (bq_quantize_nhwc)."""
     if x.dtype != torch.float32:
@@ -153,10 +154,15 @@ def quantize_nhwc(x: torch.Tensor, cpad: int | None = None):
     require_device(x.device)
     N, C, H, W = x.shape
     cpad = C if cpad is None else int(cpad)
-    xl = x.contiguous(memory_format=torch.channels_last)
     q = torch.empty((N, H, W, cpad), dtype=torch.int8, device=x.device)
     s = torch.empty((1,), dtype=torch.float32, device=x.device)
     P = N * H * W
+    if getattr(x, "_bq_absmax", None) is None and _nchw_padded(x, cpad):
+        ws = _ws(P * C, x.device)
+        check(lib().bq_quantize_nchw(x.data_ptr(), N, C, H * W, cpad, q.data_ptr(), s.data_ptr(), ws.data_ptr(),
+                                     ws.numel(), _stream(x)))
+        return q, s
+    xl = x.contiguous(memory_format=torch.channels_last)
     parts = getattr(xl, "_bq_absmax", None)
     if parts is not None and parts[2] == xl._version:
         # A conv output read by two int8 convs (a residual block's first conv and its
@@ -174,6 +180,14 @@ def quantize_nhwc(x: torch.Tensor, cpad: int | None = None):
     check(lib().bq_quantize_nhwc(xl.data_ptr(), P, C, cpad, q.data_ptr(), s.data_ptr(), ws.data_ptr(),
                                  ws.numel(), _stream(x)))
     return q, s
+
+
+def _nchw_padded(x: torch.Tensor, cpad: int) -> bool:
+    """An NCHW-contiguous activation quantized into padded channels (the stem's input): the
+    NCHW entry points read it as it is."""
+    C = x.shape[1]
+    return (cpad > C and cpad % 16 == 0 and x.is_contiguous()
+            and not x.is_contiguous(memory_format=torch.channels_last))
 
 
 def quantize_nhwc_chscale(x: torch.Tensor, cs: torch.Tensor, cpad: int | None = None, scale=None):
@@ -250,8 +264,12 @@ def quantize_nhwc_scaled(x: torch.Tensor, scale: torch.Tensor, cpad: int | None 
     require_device(x.device)
     N, C, H, W = x.shape
     cpad = C if cpad is None else int(cpad)
-    xl = x.contiguous(memory_format=torch.channels_last)
     q = torch.empty((N, H, W, cpad), dtype=torch.int8, device=x.device)
+    if _nchw_padded(x, cpad):  # a network's NCHW input: read in place, no permute
+        check(lib().bq_quantize_nchw_scaled(x.data_ptr(), N, C, H * W, cpad, scale.data_ptr(), q.data_ptr(),
+                                            _stream(x)))
+        return q
+    xl = x.contiguous(memory_format=torch.channels_last)
     check(lib().bq_quantize_nhwc_scaled(xl.data_ptr(), N * H * W, C, cpad, scale.data_ptr(), q.data_ptr(),
                                         _stream(x)))
     return q

@@ -137,6 +137,16 @@ int bq_quantize_nhwc_chscale(const float* x, int64_t N, int64_t HW, int64_t C, i
 int bq_quantize_nhwc_scaled(const float* x, int64_t P, int64_t C, int64_t Cpad, const float* s, int8_t* q,
                             bq_stream_t stream);
 
+/* bq_quantize_nhwc and bq_quantize_nhwc_scaled for an NCHW input x f32 [N, C, HW] (a
+ * network's input image, channels padded, Cpad > C, Cpad % 16 == 0, q 16-byte aligned): the
+ * same bytes and scale as permuting x to channels-last first, without the permute. The
+ * reference's conv input quantization reads its NCHW tensors directly
+ * (borch-ts/src/kernels.ts:2057-2081 from NCHW into NC/4HW4; tensor.ts:11909-11921). */
+int bq_quantize_nchw(const float* x, int64_t N, int64_t C, int64_t HW, int64_t Cpad, int8_t* q, float* s, void* ws,
+                     size_t ws_bytes, bq_stream_t stream);
+int bq_quantize_nchw_scaled(const float* x, int64_t N, int64_t C, int64_t HW, int64_t Cpad, const float* s, int8_t* q,
+                            bq_stream_t stream);
+
 /* Bytes of the split-K workspace `ws` that bq_gemm_i8 / bq_conv2d_i8_nhwc(_q) can use, for
  * any shape (about 6.5 MiB). With it, a grid that would leave most CUs idle (few output
  * tiles, long K: e.g. the late layers of a CIFAR ResNet at small batch) is split along K

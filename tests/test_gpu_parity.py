@@ -834,3 +834,26 @@ def test_linear_rows_fused_quantize(dev, M, N, K, extras):
     assert_f32(n(out), y_o)
     if M <= 4:  # without the optional quantized-row outputs: the same result
         assert torch.equal(I.linear_rows(t(x, dev), w8, t(b, dev), act, None if r is None else t(r, dev)), out)
+
+
+@pytest.mark.parametrize("shape,cpad", [((2, 3, 17, 19), 16), ((1, 5, 8, 8), 16), ((3, 20, 5, 7), 32), ((4, 3, 32, 32), 16)])
+def test_quantize_nchw_input(dev, shape, cpad):
+    """An NCHW input quantized into padded NHWC channels straight from its planes
+    (bq_quantize_nchw / bq_quantize_nchw_scaled): the same bytes and scale as the
+    channels-last path on the permuted tensor, and as the oracle."""
+    say(f"quantize NCHW input {shape} -> cpad {cpad}")
+    rng = np.random.default_rng(sum(shape) + cpad)
+    x = rng.normal(size=shape).astype(np.float32) * 3
+    xt = t(x, dev)
+    assert xt.is_contiguous() and not xt.is_contiguous(memory_format=torch.channels_last)
+    q1, s1 = I.quantize_nhwc(xt, cpad)
+    q2, s2 = I.quantize_nhwc(xt.contiguous(memory_format=torch.channels_last), cpad)
+    assert n(s1).tobytes() == n(s2).tobytes()
+    np.testing.assert_array_equal(n(q1), n(q2))
+    q_o, s_o = O.quantize_act_nhwc(x, cpad)
+    np.testing.assert_array_equal(n(q1), q_o)
+    assert np.float32(n(s1)[0]) == np.float32(s_o)
+    # calibrated: a given scale, one pass
+    sc = torch.tensor([0.0173], device=dev)
+    np.testing.assert_array_equal(n(I.quantize_nhwc_scaled(xt, sc, cpad)),
+                                  n(I.quantize_nhwc_scaled(xt.contiguous(memory_format=torch.channels_last), sc, cpad)))
