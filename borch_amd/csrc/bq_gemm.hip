@@ -1180,7 +1180,7 @@ __device__ __forceinline__ uint32_t window4(uint32_t hi, uint32_t lo, int sh) {
 // and multiplied on its own.
 // All index arithmetic is 32-bit (the host checks the ranges). Same arithmetic as
 // dwconv_i8_kernel: exact int32 tap sums, then the shared dequant epilogue.
-template <int KS, int S, int CPT, int OWB>
+template <int KS, int S, int CPT, int OWB, bool PRE>
 __global__ __launch_bounds__(256) void dwconv_blk_kernel(const int8_t* __restrict__ x, int H, int Wd, int C,
                                                          const int8_t* __restrict__ w, int pad, int OH, int OW,
                                                          int rows, const float* __restrict__ sA,
@@ -1212,54 +1212,105 @@ __global__ __launch_bounds__(256) void dwconv_blk_kernel(const int8_t* __restric
     for (int o = 0; o < OWB; ++o)
 #pragma unroll
       for (int j = 0; j < CPT; ++j) a[o][j] = 0;
-#pragma unroll 1
-    for (int kh = 0; kh < KS; ++kh) {
-      const int ih = oh * S - pad + kh;
-      if ((unsigned)ih >= (unsigned)H) continue;
-      const int8_t* xrow = x + ((size_t)(n * H + ih) * Wd) * C + c;
-      // The filter row's taps per channel: wa[ch] = taps 0..3 of channel ch (tap 3 zero for a
-      // 3-wide filter), wb[ch] = tap 4 in byte 0 (5-wide filters).
-      uint32_t wt[4], wa[CPT], wb[CPT];
-#pragma unroll
-      for (int kw = 0; kw < 4; ++kw)
-        wt[kw] = kw < KS ? *reinterpret_cast<const uint32_t*>(w + (size_t)(kh * KS + kw) * C + c) : 0u;
-      transpose4x4(wt[0], wt[1], wt[2], wt[3], wa);
-      if constexpr (KS == 5) {
-        const uint32_t w4 = *reinterpret_cast<const uint32_t*>(w + (size_t)(kh * KS + 4) * C + c);
-#pragma unroll
-        for (int ch = 0; ch < CPT; ++ch) wb[ch] = (w4 >> (8 * ch)) & 0xffu;
-      }
-      // The NCOL input columns (zero outside the row), regrouped four at a time into
-      // per-channel words: xs[t][ch] byte b = column 4 t + b of channel ch.
+    if constexpr (PRE) {
+      // PRE: every filter row's columns and taps are loaded before any is used (rows outside
+      // the input read as zeros instead of being skipped), so the KS rows' loads are in
+      // flight together rather than one row's round trip after another; more registers
+      // (up to 193 VGPRs), which the 5x5 filters on larger maps pay for in occupancy.
       constexpr int NWT = (NCOL + 3) / 4;
-      uint32_t xs[NWT + 1][CPT];
-#pragma unroll
-      for (int t = 0; t < NWT; ++t) {
-        uint32_t col[4];
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          const int jj = 4 * t + b;
+      uint32_t colv[KS][NWT * 4], wtv[KS][KS];
+  #pragma unroll
+      for (int kh = 0; kh < KS; ++kh) {
+        const int ih = oh * S - pad + kh;
+        const bool rin = (unsigned)ih < (unsigned)H;
+        const int8_t* xrow = x + ((size_t)(n * H + (rin ? ih : 0)) * Wd) * C + c;
+  #pragma unroll
+        for (int kw = 0; kw < KS; ++kw) wtv[kh][kw] = *reinterpret_cast<const uint32_t*>(w + (size_t)(kh * KS + kw) * C + c);
+  #pragma unroll
+        for (int jj = 0; jj < NWT * 4; ++jj) {
           const int iw = iw0 + jj;
-          col[b] = (jj < NCOL && (unsigned)iw < (unsigned)Wd) ? *reinterpret_cast<const uint32_t*>(xrow + (size_t)iw * C)
-                                                              : 0u;
+          colv[kh][jj] = (rin && jj < NCOL && (unsigned)iw < (unsigned)Wd)
+                             ? *reinterpret_cast<const uint32_t*>(xrow + (size_t)iw * C) : 0u;
         }
-        transpose4x4(col[0], col[1], col[2], col[3], xs[t]);
       }
-#pragma unroll
-      for (int ch = 0; ch < CPT; ++ch) xs[NWT][ch] = 0u;
-      // Output o's taps start at column o S: four taps are one byte-aligned word of the
-      // channel's column sequence, multiplied and summed by one v_dot4 (exact int32).
-#pragma unroll
-      for (int o = 0; o < OWB; ++o) {
-        const int p0 = o * S;
-#pragma unroll
-        for (int ch = 0; ch < CPT; ++ch) {
-          const uint32_t win = window4(xs[p0 / 4 + 1][ch], xs[p0 / 4][ch], p0 % 4);
-          a[o][ch] = __builtin_amdgcn_sdot4((int)win, (int)wa[ch], a[o][ch], false);
-          if constexpr (KS == 5) {
-            const int p1 = p0 + 4;
-            const uint32_t win2 = window4(xs[p1 / 4 + 1][ch], xs[p1 / 4][ch], p1 % 4);
-            a[o][ch] = __builtin_amdgcn_sdot4((int)win2, (int)wb[ch], a[o][ch], false);
+  #pragma unroll
+      for (int kh = 0; kh < KS; ++kh) {
+        uint32_t wa[CPT], wb[CPT];
+        transpose4x4(wtv[kh][0], wtv[kh][1], wtv[kh][2], KS > 3 ? wtv[kh][3 % KS] : 0u, wa);
+        if constexpr (KS == 5) {
+  #pragma unroll
+          for (int ch = 0; ch < CPT; ++ch) wb[ch] = (wtv[kh][4 % KS] >> (8 * ch)) & 0xffu;
+        }
+        uint32_t xs[NWT + 1][CPT];
+  #pragma unroll
+        for (int t = 0; t < NWT; ++t) transpose4x4(colv[kh][4 * t], colv[kh][4 * t + 1], colv[kh][4 * t + 2], colv[kh][4 * t + 3], xs[t]);
+  #pragma unroll
+        for (int ch = 0; ch < CPT; ++ch) xs[NWT][ch] = 0u;
+  #pragma unroll
+        for (int o = 0; o < OWB; ++o) {
+          const int p0 = o * S;
+  #pragma unroll
+          for (int ch = 0; ch < CPT; ++ch) {
+            const uint32_t win = window4(xs[p0 / 4 + 1][ch], xs[p0 / 4][ch], p0 % 4);
+            a[o][ch] = __builtin_amdgcn_sdot4((int)win, (int)wa[ch], a[o][ch], false);
+            if constexpr (KS == 5) {
+              const int p1 = p0 + 4;
+              const uint32_t win2 = window4(xs[p1 / 4 + 1][ch], xs[p1 / 4][ch], p1 % 4);
+              a[o][ch] = __builtin_amdgcn_sdot4((int)win2, (int)wb[ch], a[o][ch], false);
+            }
+          }
+        }
+      }
+    } else {
+  #pragma unroll 1
+      for (int kh = 0; kh < KS; ++kh) {
+        const int ih = oh * S - pad + kh;
+        if ((unsigned)ih >= (unsigned)H) continue;
+        const int8_t* xrow = x + ((size_t)(n * H + ih) * Wd) * C + c;
+        // The filter row's taps per channel: wa[ch] = taps 0..3 of channel ch (tap 3 zero for a
+        // 3-wide filter), wb[ch] = tap 4 in byte 0 (5-wide filters).
+        uint32_t wt[4], wa[CPT], wb[CPT];
+  #pragma unroll
+        for (int kw = 0; kw < 4; ++kw)
+          wt[kw] = kw < KS ? *reinterpret_cast<const uint32_t*>(w + (size_t)(kh * KS + kw) * C + c) : 0u;
+        transpose4x4(wt[0], wt[1], wt[2], wt[3], wa);
+        if constexpr (KS == 5) {
+          const uint32_t w4 = *reinterpret_cast<const uint32_t*>(w + (size_t)(kh * KS + 4) * C + c);
+  #pragma unroll
+          for (int ch = 0; ch < CPT; ++ch) wb[ch] = (w4 >> (8 * ch)) & 0xffu;
+        }
+        // The NCOL input columns (zero outside the row), regrouped four at a time into
+        // per-channel words: xs[t][ch] byte b = column 4 t + b of channel ch.
+        constexpr int NWT = (NCOL + 3) / 4;
+        uint32_t xs[NWT + 1][CPT];
+  #pragma unroll
+        for (int t = 0; t < NWT; ++t) {
+          uint32_t col[4];
+  #pragma unroll
+          for (int b = 0; b < 4; ++b) {
+            const int jj = 4 * t + b;
+            const int iw = iw0 + jj;
+            col[b] = (jj < NCOL && (unsigned)iw < (unsigned)Wd) ? *reinterpret_cast<const uint32_t*>(xrow + (size_t)iw * C)
+                                                                : 0u;
+          }
+          transpose4x4(col[0], col[1], col[2], col[3], xs[t]);
+        }
+  #pragma unroll
+        for (int ch = 0; ch < CPT; ++ch) xs[NWT][ch] = 0u;
+        // Output o's taps start at column o S: four taps are one byte-aligned word of the
+        // channel's column sequence, multiplied and summed by one v_dot4 (exact int32).
+  #pragma unroll
+        for (int o = 0; o < OWB; ++o) {
+          const int p0 = o * S;
+  #pragma unroll
+          for (int ch = 0; ch < CPT; ++ch) {
+            const uint32_t win = window4(xs[p0 / 4 + 1][ch], xs[p0 / 4][ch], p0 % 4);
+            a[o][ch] = __builtin_amdgcn_sdot4((int)win, (int)wa[ch], a[o][ch], false);
+            if constexpr (KS == 5) {
+              const int p1 = p0 + 4;
+              const uint32_t win2 = window4(xs[p1 / 4 + 1][ch], xs[p1 / 4][ch], p1 % 4);
+              a[o][ch] = __builtin_amdgcn_sdot4((int)win2, (int)wb[ch], a[o][ch], false);
+            }
           }
         }
       }
@@ -1814,16 +1865,23 @@ int bq_dwconv_i8_nhwc(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t 
     // Output rows of 7, 14 or 28 pixels: 7 pixels a thread (no idle slot, and each loaded
     // column serves more outputs), except a 5x5 stride-2 filter onto 7 pixels, whose 17-column
     // window costs more than the idle slot (B0 b64's 16 layers 282.8 -> 267.8 us).
+    // All filter rows' loads issued first (PRE) for 3x3 filters and for output rows of at
+    // most 7 pixels; the 5x5 filters on larger maps keep the row-by-row loop, whose fewer
+    // registers they need for occupancy (B0 b64: 267.6 -> ~254 us over the 16 layers).
     const bool seven = OW % 7 == 0 && OW <= 28 && !(KH == 5 && stride == 2 && OW < 14);
-    switch ((int)KH * 10 + (int)stride + (seven ? 100 : 0)) {
-      case 31: launch(dwconv_blk_kernel<3, 1, 4, 4>, 4); break;
-      case 32: launch(dwconv_blk_kernel<3, 2, 4, 4>, 4); break;
-      case 51: launch(dwconv_blk_kernel<5, 1, 4, 4>, 4); break;
-      case 52: launch(dwconv_blk_kernel<5, 2, 4, 4>, 4); break;
-      case 131: launch(dwconv_blk_kernel<3, 1, 4, 7>, 7); break;
-      case 132: launch(dwconv_blk_kernel<3, 2, 4, 7>, 7); break;
-      case 151: launch(dwconv_blk_kernel<5, 1, 4, 7>, 7); break;
-      default: launch(dwconv_blk_kernel<5, 2, 4, 7>, 7); break;
+    const bool pre = KH == 3 || OW <= 7;
+    switch ((int)KH * 10 + (int)stride + (seven ? 100 : 0) + (pre ? 1000 : 0)) {
+      case 51: launch(dwconv_blk_kernel<5, 1, 4, 4, false>, 4); break;
+      case 52: launch(dwconv_blk_kernel<5, 2, 4, 4, false>, 4); break;
+      case 151: launch(dwconv_blk_kernel<5, 1, 4, 7, false>, 7); break;
+      case 152: launch(dwconv_blk_kernel<5, 2, 4, 7, false>, 7); break;
+      case 1031: launch(dwconv_blk_kernel<3, 1, 4, 4, true>, 4); break;
+      case 1032: launch(dwconv_blk_kernel<3, 2, 4, 4, true>, 4); break;
+      case 1051: launch(dwconv_blk_kernel<5, 1, 4, 4, true>, 4); break;
+      case 1052: launch(dwconv_blk_kernel<5, 2, 4, 4, true>, 4); break;
+      case 1131: launch(dwconv_blk_kernel<3, 1, 4, 7, true>, 7); break;
+      case 1132: launch(dwconv_blk_kernel<3, 2, 4, 7, true>, 7); break;
+      default: launch(dwconv_blk_kernel<5, 1, 4, 7, true>, 7); break;  // 1151
     }
     return check_launch(what);
   }

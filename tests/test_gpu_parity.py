@@ -483,7 +483,7 @@ DW_CASES = [(2, 32, 16, 3, 1, 1), (2, 96, 15, 3, 2, 1), (2, 144, 14, 5, 1, 2), (
             (3, 40, 10, 3, 1, 0), (1, 16, 10, 7, 1, 3), (1, 24, 9, 5, 2, 1),
             # output rows of 14, 28 and 21 pixels: the 7-pixels-a-thread form, each filter and stride
             (2, 48, 28, 3, 2, 1), (2, 64, 28, 5, 2, 2), (1, 32, 56, 5, 2, 2), (2, 24, 28, 3, 1, 1),
-            (1, 16, 21, 3, 1, 1)]
+            (1, 16, 21, 3, 1, 1), (2, 40, 5, 5, 1, 2)]
 
 
 @pytest.mark.parametrize("N,C,H,k,stride,pad", DW_CASES)
