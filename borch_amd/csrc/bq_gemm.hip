@@ -529,28 +529,40 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
   const bool has_r = p.res != nullptr;
   float amax = 0.f;  // max |y| of the values this lane stores (fmaxf: a NaN is skipped)
 
-  // Fast path: f32 output only (no int32 or int8 twin), float4-aligned, and a tile's rows
-  // within 2 GB. Its stores are buffer stores through a resource that ends at row M of the
-  // tile: a lane's offset within the tile is one 32-bit VGPR, and rows past M fall out of
-  // range and are dropped by the hardware (no per-row test, no 64-bit address arithmetic
-  // per store). About 5 VALU instructions per output against 12 on the general path, whose
-  // per-row branches on every optional output stay for the other cases (the int8 twin's
-  // packing inlined here pushed the 256-row tiles' kernel arguments out of SGPRs). The
-  // stores write through to memory (sc1): the output does not sit dirty in the XCD's L2 to
-  // be written back at the kernel's end, which measured 4-16% faster per launch back to
-  // back (ViT qkv 23.2 -> 21.2 us, half-batch qkv 16.0 -> 13.5).
-  const bool fast = p.vec_ok && p.out && !p.acc && !p.q_out && (long long)BM * p.N * 4 < (1ll << 31);
-  const uint32_t tile_bytes = fast ? (uint32_t)((long long)min(BM, p.M - m0) * p.N * 4) : 0u;
-  const __amdgpu_buffer_rsrc_t r_out = make_rsrc(p.out + (size_t)m0 * p.N, tile_bytes);
+  // Fast path: no int32 output, float4-aligned, and a tile's rows within 2 GB. Its stores
+  // are buffer stores through resources that end at row M of the tile: a lane's offset
+  // within the tile is one 32-bit VGPR, and rows past M fall out of range and are dropped by
+  // the hardware (no per-row test, no 64-bit address arithmetic per store). About 5 VALU
+  // instructions per output against 12 on the general path, whose per-row branches on every
+  // optional output stay for the other cases. The stores write through to memory (sc1): the
+  // output does not sit dirty in the XCD's L2 to be written back at the kernel's end, which
+  // measured 4-16% faster per launch back to back (ViT qkv 23.2 -> 21.2 us, half-batch qkv
+  // 16.0 -> 13.5). The int8 twin of a calibrated layer (no per-tile maxima) takes this path
+  // on tiles of up to 128x128, beside the f32 output or alone: four packed bytes a lane and
+  // row (ResNet-18 b16's 64x64 convs: 7.3 -> 6.4 us with both outputs, 6.7 -> 6.4 us with
+  // the twin alone). The larger tiles keep the general path for the twin: inlined there, its
+  // packing pushed their kernel arguments out of SGPRs.
+  constexpr bool FASTQ = BM * BN <= 128 * 128;
+  const bool has_out = p.out != nullptr;
+  const bool fast = p.vec_ok && !p.acc && (p.q_out ? FASTQ && !p.amax : has_out) &&
+                    (long long)BM * p.N * 4 < (1ll << 31);
+  const int tile_rows = min(BM, p.M - m0);
+  const uint32_t tile_bytes = fast ? (uint32_t)((long long)tile_rows * p.N * 4) : 0u;
+  const __amdgpu_buffer_rsrc_t r_out = make_rsrc(has_out ? p.out + (size_t)m0 * p.N : p.out, has_out ? tile_bytes : 0u);
   const __amdgpu_buffer_rsrc_t r_res = make_rsrc(has_r ? p.res + (size_t)m0 * p.N : p.res, has_r ? tile_bytes : 0u);
+  const __amdgpu_buffer_rsrc_t r_q = make_rsrc(p.q_out ? p.q_out + (size_t)m0 * p.N : p.q_out,
+                                               fast && p.q_out ? (uint32_t)(tile_rows * p.N) : 0u);
   const uint32_t row_step = (uint32_t)(ROWS_PER_STORE * p.N) * 4u;  // bytes between a lane's rows
   // Rows rl, rl + ROWS_PER_STORE, ... of the tile (rl: this lane's first row of the slice).
   // (always inlined: a call would take the kernel argument block's address and move its
   // fields from SGPRs to VGPRs)
-  auto fast_rows = [&]<bool RES, bool AMAX>(int rl, int col4, int ncol) __attribute__((always_inline)) {
+  // Q: the int8 twin through r_q (byte offsets a quarter of the f32 ones), and the f32 row
+  // only when there is an f32 output.
+  auto fast_rows = [&]<bool RES, bool AMAX, bool Q>(int rl, int col4, int ncol) __attribute__((always_inline)) {
     const float4 sw4 = *reinterpret_cast<const float4*>(&s_sw[ncol]);
     const float4 b4 = *reinterpret_cast<const float4*>(&s_b[ncol]);
-    const uint32_t voff = ((uint32_t)rl * (uint32_t)p.N + (uint32_t)(n0 + ncol)) * 4u;
+    const uint32_t voffq = (uint32_t)rl * (uint32_t)p.N + (uint32_t)(n0 + ncol);
+    const uint32_t voff = voffq * 4u;
     float4 rv[NST];
     if constexpr (RES) {  // every residual row first: a load after a store waits for it
 #pragma unroll
@@ -582,7 +594,8 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
       // The row step goes into the VGPR offset: with it in the SGPR offset these stores
       // wrote wrong values to about 1% of the rows (each store followed by an LDS read
       // into its data registers); with it in the VGPR offset, none.
-      store_wt16(r_out, voff + k * row_step, o);
+      if (!Q || has_out) store_wt16(r_out, voff + k * row_step, o);
+      if constexpr (Q) store_wt4(r_q, voffq + k * (row_step / 4u), qz_out.pack(o));
       if constexpr (AMAX) {  // rows past M are computed (and dropped) but must not count
         if (m0 + rl + k * ROWS_PER_STORE < p.M)
           amax = fmaxf(amax, fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w))));
@@ -620,12 +633,17 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
     if (fast) {
       if (n < p.N) {
         const int rl = wm * WTM + i * 32 + lane / C4;
-        if (has_r) {
-          if (p.amax) fast_rows.template operator()<true, true>(rl, col4, ncol);
-          else fast_rows.template operator()<true, false>(rl, col4, ncol);
+        if (FASTQ && p.q_out) {
+          if constexpr (FASTQ) {
+            if (has_r) fast_rows.template operator()<true, false, true>(rl, col4, ncol);
+            else fast_rows.template operator()<false, false, true>(rl, col4, ncol);
+          }
+        } else if (has_r) {
+          if (p.amax) fast_rows.template operator()<true, true, false>(rl, col4, ncol);
+          else fast_rows.template operator()<true, false, false>(rl, col4, ncol);
         } else {
-          if (p.amax) fast_rows.template operator()<false, true>(rl, col4, ncol);
-          else fast_rows.template operator()<false, false>(rl, col4, ncol);
+          if (p.amax) fast_rows.template operator()<false, true, false>(rl, col4, ncol);
+          else fast_rows.template operator()<false, false, false>(rl, col4, ncol);
         }
       }
     } else if (p.vec_ok && n < p.N) {
