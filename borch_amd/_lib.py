@@ -31,6 +31,15 @@ _c_p = ctypes.c_void_p
 _c_int = ctypes.c_int
 _c_size = ctypes.c_size_t
 
+
+
+class ConvDesc(ctypes.Structure):
+    """``bq_conv_desc`` (include/bq.h): one convolution of ``bq_conv2d_i8_nhwc_pair``."""
+    _fields_ = [("w", _c_p), ("O", _c_i64), ("KH", _c_i64), ("KW", _c_i64), ("stride", _c_i64), ("pad", _c_i64),
+                ("sW", _c_p), ("bias", _c_p), ("residual", _c_p), ("act", _c_int), ("out", _c_p),
+                ("s_out", _c_p), ("q_out", _c_p), ("amax", _c_p)]
+
+
 # name -> (restype, argtypes); mirrors include/bq.h one for one.
 SIGNATURES = {
     "bq_version": (_c_int, []),
@@ -64,6 +73,8 @@ SIGNATURES = {
     "bq_conv2d_i8_nhwc": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i64,
                                    _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_int, _c_p, _c_p, _c_p, _c_p,
                                    _c_size, _c_p]),
+    "bq_conv2d_i8_nhwc_pair": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, ctypes.POINTER(ConvDesc),
+                                        ctypes.POINTER(ConvDesc), _c_p, _c_size, _c_p]),
     "bq_quantize_nhwc_parts": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_p]),
     "bq_quantize_nhwc_chscale": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_p,
                                           _c_i64, _c_p, _c_size, _c_p]),

@@ -32,7 +32,7 @@ from __future__ import annotations
 import torch
 
 from . import int8 as _i8
-from .nn import Conv2d, _int8_layers, quantize_for_int8
+from .nn import Conv2d, _int8_layers, pairing, quantize_for_int8
 from .tune import PlanCache
 from .tune import tune as _tune
 
@@ -70,7 +70,12 @@ class Compiled:
         return True
 
     def _run(self, x):
-        """The model on ``x``: whole, or as ``split`` chunks on parallel streams."""
+        """The model on ``x``: whole, or as ``split`` chunks on parallel streams; two int8 convs
+        of one input run as one launch (``pairing``)."""
+        with pairing():
+            return self._run_chunks(x)
+
+    def _run_chunks(self, x):
         if not self._split_ok(x):
             return self.model(x)
         streams = self._streams.get(x.device)
@@ -96,7 +101,7 @@ class Compiled:
             self.tuned.append(_tune(self.model, x.chunk(self.split)[0] if self._split_ok(x) else x,
                                     cache=self.plan_cache))
         if not self.graph or x.device.type != "cuda":
-            return self.model(x)
+            return self._run(x)
         entry = self._graphs.get(key)
         if entry is None:
             static_in = x.clone()

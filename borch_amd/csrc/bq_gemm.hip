@@ -389,23 +389,36 @@ __device__ __forceinline__ void mainloop_dma(const GemmP& p, int m0, int n0, int
   __syncthreads();
 }
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, bool CONV, int NBUF, int FD, bool MF16 = false>
-__global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const GemmP p) {
+// The tiled kernel's LDS: the ring of stage buffers (reused by the epilogue's patches), and
+// the tile's scales and bias, staged once so the epilogue reads no global memory (on gfx9
+// stores and loads share one counter, and a load between stores waits for them).
+template <int BM, int BN, int WAVES, int NBUF>
+struct TileLds {
+  __attribute__((aligned(16))) int8_t ring[NBUF * (BM + BN) * BK];
+  __attribute__((aligned(16))) float sa[BM];
+  __attribute__((aligned(16))) float sw[BN];
+  __attribute__((aligned(16))) float b[BN];
+  int last;            // split-K: this workgroup is the last of its tile
+  float wmax[WAVES];   // per-wave max |y| (p.amax)
+};
+
+// One workgroup of the tiled GEMM / implicit-GEMM conv: workgroup `bid` of the `nbid` that
+// cover problem p (its tiles times its K split).
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool CONV, int NBUF, int FD, bool MF16>
+__device__ __forceinline__ void gemm_tile(const GemmP& p, int bid, int nbid,
+                                          TileLds<BM, BN, WAVES_M * WAVES_N, NBUF>& sh) {
   constexpr int T = WAVES_M * WAVES_N * 64;
   constexpr int WTM = BM / WAVES_M;  // wave tile rows
   constexpr int WTN = BN / WAVES_N;
   constexpr int TM = WTM / 32;
   constexpr int TN = WTN / 32;
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile");
-
-  __shared__ __attribute__((aligned(16))) int8_t lds[NBUF * (BM + BN) * BK];
-  // Per-tile scales and bias, staged once so the epilogue reads no global memory: on
-  // gfx9 stores and loads share one counter, and a load between stores waits for them.
-  __shared__ __attribute__((aligned(16))) float s_sa[BM];
-  __shared__ __attribute__((aligned(16))) float s_sw[BN];
-  __shared__ __attribute__((aligned(16))) float s_b[BN];
-  __shared__ int s_last;  // split-K: this workgroup is the last of its tile
-  __shared__ float s_wmax[WAVES_M * WAVES_N];  // per-wave max |y| (p.amax)
+  int8_t* const lds = sh.ring;
+  float* const s_sa = sh.sa;
+  float* const s_sw = sh.sw;
+  float* const s_b = sh.b;
+  int& s_last = sh.last;
+  float* const s_wmax = sh.wmax;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -418,7 +431,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
   const int KT = (p.K + BK - 1) / BK;
   constexpr bool CAN_SPLIT = BM * BN <= SPLIT_MAX_TILE;
   const int S = CAN_SPLIT ? p.ksplit : 1;
-  const int L = xcd_order(blockIdx.x, gridDim.x);
+  const int L = xcd_order(bid, nbid);
   const int split = L % S;
   int bm, bn;
   tile_of(L / S, tiles_m, tiles_n, bm, bn);
@@ -742,6 +755,26 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const Ge
       p.amax[bm * tiles_n + bn] = m;
     }
   }
+}
+
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool CONV, int NBUF, int FD, bool MF16 = false>
+__global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const GemmP p) {
+  __shared__ TileLds<BM, BN, WAVES_M * WAVES_N, NBUF> sh;
+  gemm_tile<BM, BN, WAVES_M, WAVES_N, CONV, NBUF, FD, MF16>(p, blockIdx.x, gridDim.x, sh);
+}
+
+// Two problems of one tile configuration in one launch: workgroups [0, g0) run p0, the
+// rest p1 (a residual block's first conv and its downsampling shortcut, which read the same
+// input: two launches' fixed cost paid once, and the smaller grids share the chip). Only p0
+// may split K.
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool CONV, int NBUF, int FD>
+__global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_pair_kernel(const GemmP p0, const GemmP p1,
+                                                                           int g0) {
+  __shared__ TileLds<BM, BN, WAVES_M * WAVES_N, NBUF> sh;
+  if ((int)blockIdx.x < g0)
+    gemm_tile<BM, BN, WAVES_M, WAVES_N, CONV, NBUF, FD, false>(p0, blockIdx.x, g0, sh);
+  else
+    gemm_tile<BM, BN, WAVES_M, WAVES_N, CONV, NBUF, FD, false>(p1, blockIdx.x - g0, gridDim.x - g0, sh);
 }
 
 // ----------------------------------------------------------------------------- skinny
@@ -1391,8 +1424,10 @@ static int pick_split(long long tiles, int KT, bool conv, int planned = 0) {
   return (KT + per - 1) / per;
 }
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, bool CONV, int NBUF, int FD, bool MF16 = false>
-static void launch_tiled(GemmP p, hipStream_t st, const Ws& ws) {
+// The K split of p on BM x BN tiles (the plan's, else the rule's; 1 when the workspace cannot
+// hold it), recorded in p with the workspace's counters and partials; returns the workgroups.
+template <int BM, int BN, bool CONV>
+static long long setup_split(GemmP& p, const Ws& ws) {
   const long long tiles = (long long)((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
   int S = BM * BN <= SPLIT_MAX_TILE ? pick_split(tiles, (p.K + BK - 1) / BK, CONV, p.plan_split) : 1;
   if (S > 1) {
@@ -1405,7 +1440,26 @@ static void launch_tiled(GemmP p, hipStream_t st, const Ws& ws) {
     }
   }
   p.ksplit = S;
-  gemm_i8_kernel<BM, BN, WAVES_M, WAVES_N, CONV, NBUF, FD, MF16><<<(unsigned)(tiles * S), WAVES_M * WAVES_N * 64, 0, st>>>(p);
+  return tiles * S;
+}
+
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool CONV, int NBUF, int FD, bool MF16 = false>
+static void launch_tiled(GemmP p, hipStream_t st, const Ws& ws) {
+  const long long groups = setup_split<BM, BN, CONV>(p, ws);
+  gemm_i8_kernel<BM, BN, WAVES_M, WAVES_N, CONV, NBUF, FD, MF16><<<(unsigned)groups, WAVES_M * WAVES_N * 64, 0, st>>>(p);
+}
+
+// p0 and p1 in one launch on p0's configuration; p1 runs unsplit. False (nothing launched)
+// when the grid would not fit one launch.
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool CONV, int NBUF, int FD>
+static bool launch_pair_tiled(GemmP p0, GemmP p1, hipStream_t st, const Ws& ws) {
+  const long long g0 = setup_split<BM, BN, CONV>(p0, ws);
+  p1.ksplit = 1;
+  const long long g1 = (long long)((p1.M + BM - 1) / BM) * ((p1.N + BN - 1) / BN);
+  if (g0 + g1 > 0x7fffffffll) return false;
+  gemm_i8_pair_kernel<BM, BN, WAVES_M, WAVES_N, CONV, NBUF, FD>
+      <<<(unsigned)(g0 + g1), WAVES_M * WAVES_N * 64, 0, st>>>(p0, p1, (int)g0);
+  return true;
 }
 
 // Tiled-kernel configurations, by id: <BM, BN, waves M x N, ring depth, fragment distance>.
@@ -1488,6 +1542,20 @@ static void launch_gemm(const GemmP& p, hipStream_t st, const Ws& ws) {
       if constexpr (!CONV) return launch_tiled<320, 256, 2, 4, CONV, 2, 1>(p, st, ws);
       [[fallthrough]];
     default: return launch_tiled<64, 64, 2, 2, CONV, 4, 2>(p, st, ws);
+  }
+}
+
+// Two implicit-GEMM convs in one launch on the configuration the first would run (the
+// small-tile configurations only: the deep K of a residual block's first conv is split, and
+// its shortcut's grid fills the rest of the chip). False: not offered for that configuration.
+static bool launch_conv_pair(const GemmP& p0, const GemmP& p1, hipStream_t st, const Ws& ws) {
+  switch (choose_cfg(p0, true)) {
+    case 7: return launch_pair_tiled<64, 64, 2, 2, true, 4, 2>(p0, p1, st, ws);
+    case 10: return launch_pair_tiled<64, 64, 2, 2, true, 2, 2>(p0, p1, st, ws);
+    case 11: return launch_pair_tiled<128, 64, 4, 1, true, 2, 1>(p0, p1, st, ws);
+    case 12: return launch_pair_tiled<128, 32, 4, 1, true, 2, 1>(p0, p1, st, ws);
+    case 14: return launch_pair_tiled<128, 64, 4, 1, true, 3, 1>(p0, p1, st, ws);
+    default: return false;
   }
 }
 
@@ -1709,11 +1777,15 @@ int bq_linear_i8(const float* x, const int8_t* W, int64_t M, int64_t N, int64_t 
   return gemm_impl(what, qx, W, M, N, K, sx, sW, bias, residual, act, out, nullptr, ws, ws_bytes, false, stream);
 }
 
-static int conv_impl(const char* what, const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t C,
-                     const int8_t* w, int64_t O, int64_t KH, int64_t KW, int64_t stride, int64_t pad,
-                     const float* sA, const float* sW, const float* bias, const float* residual, int act,
-                     float* out, int32_t* acc, const float* s_out, int8_t* q_out, float* amax, void* ws,
-                     size_t ws_bytes, bq_stream_t stream) {
+// Checks one convolution's arguments and fills its kernel parameters (the tuned plan of its
+// geometry applied). `dense`: a 1x1 stride-1 unpadded conv, which runs the dense loader on
+// [N*H*W, C]. `empty`: no output rows (nothing to launch).
+static int conv_setup(const char* what, const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t C,
+                      const int8_t* w, int64_t O, int64_t KH, int64_t KW, int64_t stride, int64_t pad,
+                      const float* sA, const float* sW, const float* bias, const float* residual, int act,
+                      float* out, int32_t* acc, const float* s_out, int8_t* q_out, float* amax, GemmP& p,
+                      bool& dense, bool& empty) {
+  empty = false;
   if (N < 0 || H < 1 || W < 1 || C < 1 || O < 1 || KH < 1 || KW < 1 || stride < 1 || pad < 0)
     return set_error(BQ_ERR_ARG, "%s: bad geometry", what);
   if (C % 16) return set_error(BQ_ERR_UNSUPPORTED, "%s: C=%lld is not a multiple of 16 (pad it)", what, (long long)C);
@@ -1727,11 +1799,14 @@ static int conv_impl(const char* what, const int8_t* x, int64_t N, int64_t H, in
   if (K > KMAX_EXACT)
     return set_error(BQ_ERR_UNSUPPORTED, "%s: KH*KW*C=%lld > %d: int32 accumulators could overflow", what,
                      (long long)K, KMAX_EXACT);
-  if (M == 0) return BQ_OK;
+  if (M == 0) {
+    empty = true;
+    return BQ_OK;
+  }
   if (!x || !w || !sA || !sW || (!out && !q_out)) return set_error(BQ_ERR_ARG, "%s: null pointer", what);
   if (!aligned16(x) || !aligned16(w)) return set_error(BQ_ERR_ARG, "%s: x and w must be 16-byte aligned", what);
   if (act < BQ_ACT_NONE || act > BQ_ACT_GELU) return set_error(BQ_ERR_ARG, "%s: bad activation %d", what, act);
-  GemmP p{};
+  p = GemmP{};
   p.A = x; p.W = w; p.M = (int)M; p.N = (int)O; p.K = (int)K;
   p.sA = sA; p.sa_per_row = 0; p.sW = sW; p.bias = bias; p.res = residual; p.act = act;
   p.out = out; p.acc = acc;
@@ -1745,8 +1820,23 @@ static int conv_impl(const char* what, const int8_t* x, int64_t N, int64_t H, in
   p.q_out = q_out;
   p.amax = amax;
   apply_plan(p, conv_key(N, H, W, C, O, KH, KW, stride, pad));
+  dense = KH == 1 && KW == 1 && stride == 1 && pad == 0;
+  return BQ_OK;
+}
+
+static int conv_impl(const char* what, const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t C,
+                     const int8_t* w, int64_t O, int64_t KH, int64_t KW, int64_t stride, int64_t pad,
+                     const float* sA, const float* sW, const float* bias, const float* residual, int act,
+                     float* out, int32_t* acc, const float* s_out, int8_t* q_out, float* amax, void* ws,
+                     size_t ws_bytes, bq_stream_t stream) {
+  GemmP p;
+  bool dense, empty;
+  if (int r = conv_setup(what, x, N, H, W, C, w, O, KH, KW, stride, pad, sA, sW, bias, residual, act, out, acc,
+                         s_out, q_out, amax, p, dense, empty))
+    return r;
+  if (empty) return BQ_OK;
   hipStream_t st = (hipStream_t)stream;
-  if (KH == 1 && KW == 1 && stride == 1 && pad == 0)
+  if (dense)
     launch_gemm<false>(p, st, Ws{ws, ws_bytes});  // a 1x1 conv is the dense GEMM on [N*H*W, C]
   else
     launch_gemm<true>(p, st, Ws{ws, ws_bytes});
@@ -1843,6 +1933,36 @@ int bq_conv2d_i8_nhwc_q(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_
   if (O % 16) return set_error(BQ_ERR_UNSUPPORTED, "bq_conv2d_i8_nhwc_q: O=%lld is not a multiple of 16", (long long)O);
   return conv_impl("bq_conv2d_i8_nhwc_q", x, N, H, W, C, w, O, KH, KW, stride, pad, sA, sW, bias, residual, act,
                    out, acc, s_out, q_out, absmax_parts, ws, ws_bytes, stream);
+}
+
+int bq_conv2d_i8_nhwc_pair(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t C, const float* sA,
+                           const bq_conv_desc* a, const bq_conv_desc* b, void* ws, size_t ws_bytes,
+                           bq_stream_t stream) {
+  const char* what = "bq_conv2d_i8_nhwc_pair";
+  if (!a || !b) return set_error(BQ_ERR_ARG, "%s: null descriptor", what);
+  if (b->amax) return set_error(BQ_ERR_UNSUPPORTED, "%s: the second conv takes no absmax_parts", what);
+  for (const bq_conv_desc* d : {a, b})
+    if ((d->s_out != nullptr) != (d->q_out != nullptr) || (d->q_out && d->O % 16))
+      return set_error(BQ_ERR_ARG, "%s: an int8 twin needs s_out, q_out and O %% 16 == 0", what);
+  GemmP p[2];
+  bool dense[2], empty[2];
+  for (int i = 0; i < 2; ++i) {
+    const bq_conv_desc& d = i ? *b : *a;
+    if (int r = conv_setup(what, x, N, H, W, C, d.w, d.O, d.KH, d.KW, d.stride, d.pad, sA, d.sW, d.bias, d.residual,
+                           d.act, d.out, nullptr, d.s_out, d.q_out, d.amax, p[i], dense[i], empty[i]))
+      return r;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  const Ws w{ws, ws_bytes};
+  if (!empty[0] && !empty[1] && !dense[0] && !dense[1] && launch_conv_pair(p[0], p[1], st, w))
+    return check_launch(what);
+  for (int i = 0; i < 2; ++i) {  // separate launches, one after the other on the stream
+    if (empty[i]) continue;
+    if (dense[i]) launch_gemm<false>(p[i], st, w);
+    else launch_gemm<true>(p[i], st, w);
+    if (int r = check_launch(what)) return r;
+  }
+  return BQ_OK;
 }
 
 int bq_dwconv_i8_nhwc(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t C, const int8_t* w, int64_t KH,

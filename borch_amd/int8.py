@@ -18,7 +18,8 @@ from ._lib import ACT_GELU, ACT_NONE, ACT_RELU, ACT_SILU, SCALE_A_PER_TENSOR, ch
 __all__ = [
     "ACT_NONE", "ACT_RELU", "ACT_SILU", "ACT_GELU", "Int8Weight", "Int8ConvWeight", "Int8DwWeight",
     "quantize_rows", "quantize_weight_per_channel", "quantize_tensor", "quantize_nhwc",
-    "gemm_i8", "conv2d_i8_nhwc", "conv2d_i8_nhwc_q", "dwconv_i8_nhwc", "pack_linear_weight", "pack_conv_weight",
+    "gemm_i8", "conv2d_i8_nhwc", "conv2d_i8_nhwc_q", "conv2d_pair_i8_nhwc", "PairConv", "dwconv_i8_nhwc",
+    "pack_linear_weight", "pack_conv_weight",
     "quantize_nhwc_scaled", "quantize_nhwc_chscale", "se_gate_nhwc", "linear_w8a32", "dequant_weight",
     "pack_dw_weight", "linear", "linear_rows", "conv2d", "depthwise_conv2d", "round_up", "split_workspace",
 ]
@@ -490,6 +491,55 @@ def conv2d_i8_nhwc_q(qx, sa, wq: Int8ConvWeight, s_out, stride=1, pad=0, bias=No
                                     _ptr(out), None, s_out.data_ptr(), q.data_ptr(), None,
                                     *_ws_args(qx.device), _stream(qx)))
     return out, q
+
+
+@dataclass
+class PairConv:
+    """One convolution of ``conv2d_pair_i8_nhwc``: its packed filter and epilogue. ``s_out`` (a
+    calibrated output scale [1]) adds the int8 twin; ``amax``: the f32 output's per-tile
+    maxima are written too (the first conv of a pair only)."""
+    wq: Int8ConvWeight
+    stride: int = 1
+    pad: int = 0
+    bias: torch.Tensor | None = None
+    act: int = ACT_NONE
+    s_out: torch.Tensor | None = None
+    amax: bool = False
+
+
+def conv2d_pair_i8_nhwc(qx, sa, first: PairConv, second: PairConv):
+    """Two convs of one NHWC int8 input ``qx`` (scale ``sa``) in one launch
+    (bq_conv2d_i8_nhwc_pair): a residual block's first conv and its shortcut. Returns
+    ``[(out, q), (out, q)]``: each f32 output NCHW-shaped in channels-last memory and its int8
+    twin (None without ``s_out``), bit-identical to ``conv2d_i8_nhwc`` / ``conv2d_i8_nhwc_q``;
+    the first output carries its per-tile maxima when ``first.amax``."""
+    _need(qx, "x", torch.int8)
+    N, H, W, C = qx.shape
+    descs, results, keep = [], [], []
+    for i, c in enumerate((first, second)):
+        if C != c.wq.cpad:
+            raise RuntimeError(f"channels do not match: input {C}, filter {c.wq.cpad}")
+        OH = (H + 2 * c.pad - c.wq.KH) // c.stride + 1
+        OW = (W + 2 * c.pad - c.wq.KW) // c.stride + 1
+        if OH < 1 or OW < 1:
+            raise RuntimeError("the filter is larger than the input.")
+        out = torch.empty((N, c.wq.O, OH, OW), dtype=torch.float32, device=qx.device,
+                          memory_format=torch.channels_last)
+        q = torch.empty((N, OH, OW, c.wq.O), dtype=torch.int8, device=qx.device) if c.s_out is not None else None
+        parts = None
+        if c.amax:
+            if i:
+                raise ValueError("only the first conv of a pair writes per-tile maxima")
+            parts, nparts = _absmax_parts(N, H, W, C, c.wq, c.stride, c.pad, qx.device)
+            out._bq_absmax = (parts, nparts, out._version)
+        b = _vec(c.bias, c.wq.O, "bias")
+        keep.append((b, c.s_out))
+        descs.append(_lib.ConvDesc(c.wq.q.data_ptr(), c.wq.O, c.wq.KH, c.wq.KW, c.stride, c.pad, c.wq.s.data_ptr(),
+                                   _ptr(b), None, c.act, out.data_ptr(), _ptr(c.s_out), _ptr(q), _ptr(parts)))
+        results.append((out, q))
+    check(lib().bq_conv2d_i8_nhwc_pair(qx.contiguous().data_ptr(), N, H, W, C, sa.data_ptr(), descs[0], descs[1],
+                                       *_ws_args(qx.device), _stream(qx)))
+    return results
 
 
 def dwconv_i8_nhwc(qx, sa, wq: Int8DwWeight, stride=1, pad=0, bias=None, act=ACT_NONE, want_acc=False):

@@ -89,8 +89,10 @@ class Block(tnn.Module):
 
     def forward(self, x):
         if self.c1 is not None:
-            side = self.down(x) if self.down is not None else x
-            return self.c2(self.c1(x), side)
+            if self.down is None:
+                return self.c2(self.c1(x), x)
+            h, side = nn.pair_forward(self.c1.conv, self.down, x)  # one launch for both when int8
+            return self.c2(h, side)
         out = torch.relu(self.bn1(self.conv1(x)))
         out = self.bn2(self.conv2(out))
         side = self.downBn(self.downConv(x)) if self.downConv is not None else x

@@ -35,6 +35,7 @@ Parameter = _tnn.Parameter
 # Set by calibrate_int8: int8 convs run their f32 path and record max|input| / max|output|
 # (the reference's setInt8Calibrating, tensor.ts:11896-11901).
 _CALIBRATING = False
+_PAIRING = False  # set by `pairing` (compiled forwards): see pair_forward
 
 
 def _scale_value(peak: float) -> float:
@@ -304,6 +305,55 @@ class Conv2d(_tnn.Module):
         if self.groups != 1:
             s += f", groups={self.groups}"
         return s + (", int8" if self.int8 is not None else "")
+
+
+class pairing:
+    """Within this context ``pair_forward`` runs two int8 convs of one input in one launch
+    (``compiled`` runs its model inside it). Outside it, each conv runs through its own module
+    call, so forward hooks see every layer (the per-layer checks and the tuner use them)."""
+
+    def __enter__(self):
+        global _PAIRING
+        self._prev, _PAIRING = _PAIRING, True
+        return self
+
+    def __exit__(self, *exc):
+        global _PAIRING
+        _PAIRING = self._prev
+        return False
+
+
+def pair_forward(first: Conv2d, second: Conv2d, x):
+    """``(first(x), second(x))`` with no residual: a residual block's first conv and its
+    downsampling shortcut, which read the same input. When both are int8 convs (not depthwise,
+    neither a 1x1 stride-1 unpadded conv) on the same input scale, the input is quantized once
+    and both run in one launch (``conv2d_pair_i8_nhwc``), with the results the two calls give.
+    The first output keeps what its own call leaves for its consumer (the int8 twin, or the
+    per-tile maxima); the shortcut's f32 output is written alone, and a consumer quantizing it
+    gets the bytes its twin would have held."""
+    ok = (_PAIRING and not _CALIBRATING and x.dim() == 4 and isinstance(first, Conv2d) and isinstance(second, Conv2d)
+          and isinstance(first.int8, _i8.Int8ConvWeight) and isinstance(second.int8, _i8.Int8ConvWeight)
+          and x.shape[1] == first.in_channels == second.in_channels and first.int8.cpad == second.int8.cpad
+          and first.in_scale_v == second.in_scale_v
+          and not _dense_1x1(first) and not _dense_1x1(second))
+    if not ok:
+        return first(x), second(x)
+    qx, sa = first._int8_input(x)
+    s1, p1 = first._geometry()
+    s2, p2 = second._geometry()
+    twin = first.out_scale is not None and first.int8.O % 16 == 0
+    (h, q), (side, _) = _i8.conv2d_pair_i8_nhwc(
+        qx, sa,
+        _i8.PairConv(first.int8, s1, p1, first.bias, first.act, first.out_scale if twin else None, amax=not twin),
+        _i8.PairConv(second.int8, s2, p2, second.bias, second.act))
+    if twin:
+        h._int8_twin = (q, first.out_scale, first.out_scale_v, h._version)
+    return h, side
+
+
+def _dense_1x1(m: Conv2d) -> bool:
+    """A 1x1 stride-1 unpadded conv (the dense GEMM loader, which a pair does not take)."""
+    return m.int8.KH == 1 and m.int8.KW == 1 and m._geometry() == (1, 0)
 
 
 def _int8_layers(model):

@@ -256,6 +256,32 @@ int bq_conv2d_i8_nhwc_q(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_
                         int32_t* acc, const float* s_out, int8_t* q_out, float* absmax_parts, void* ws,
                         size_t ws_bytes, bq_stream_t stream);
 
+/* One convolution of bq_conv2d_i8_nhwc_pair: its filter and epilogue, as the arguments of
+ * the same name of bq_conv2d_i8_nhwc_q (s_out and q_out both NULL: no int8 twin, and then
+ * `out` is required; `amax` as bq_conv2d_i8_nhwc's absmax_parts, first conv only). */
+typedef struct bq_conv_desc {
+  const int8_t* w;
+  int64_t O, KH, KW, stride, pad;
+  const float* sW;
+  const float* bias;
+  const float* residual;
+  int act;
+  float* out;
+  const float* s_out;
+  int8_t* q_out;
+  float* amax;
+} bq_conv_desc;
+
+/* Two convolutions of one int8 input x [N, H, W, C] (scale sA) in one launch: a residual
+ * block's first conv and its downsampling shortcut, which the reference dispatches as two
+ * convForwardInt8 passes over the same input (borch-ts/src/kernels.ts:2084-2302; the block
+ * of tests/browser/export_resnet18.py:34-43). Each result is bit-identical to that conv's
+ * own bq_conv2d_i8_nhwc(_q) call; the second runs on the first's tile configuration and
+ * never splits K. Configurations without a paired kernel run as two launches. */
+int bq_conv2d_i8_nhwc_pair(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t C, const float* sA,
+                           const bq_conv_desc* a, const bq_conv_desc* b, void* ws, size_t ws_bytes,
+                           bq_stream_t stream);
+
 /* Depthwise int8 convolution, NHWC (groups = C, channel multiplier 1):
  *   x int8 [N, H, W, C] (C % 4 == 0, per-tensor sA f32 [1]), w int8 [KH*KW, C]
  *   (per-channel sW f32 [C]), out f32 [N, OH, OW, C] with the same epilogue.

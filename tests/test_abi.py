@@ -69,6 +69,16 @@ def test_argument_checks_run_on_host():
     assert lib.bq_conv2d_i8_nhwc(None, 1, 9, 9, 16656, None, 8, 3, 3, 1, 1, None, None, None, None, 0, None, None,
                                  None, None, 0, None) == _lib.BQ_ERR_UNSUPPORTED
     assert "overflow" in _lib.last_error()
+    # the paired convs: descriptors required, per-tile maxima from the first conv only, and
+    # each conv's own geometry checks
+    d = _lib.ConvDesc(None, 32, 3, 3, 2, 1, None, None, None, 0, None, None, None, None)
+    d_amax = _lib.ConvDesc(None, 32, 1, 1, 2, 0, None, None, None, 0, None, None, None, 16)
+    assert lib.bq_conv2d_i8_nhwc_pair(None, 1, 8, 8, 16, None, None, d, None, 0, None) == _lib.BQ_ERR_ARG
+    assert lib.bq_conv2d_i8_nhwc_pair(None, 1, 8, 8, 16, None, d, d_amax, None, 0, None) == _lib.BQ_ERR_UNSUPPORTED
+    assert "first conv" not in _lib.last_error() and "absmax" in _lib.last_error()
+    big = _lib.ConvDesc(None, 32, 9, 9, 1, 0, None, None, None, 0, None, None, None, None)
+    assert lib.bq_conv2d_i8_nhwc_pair(None, 1, 8, 8, 16, None, big, d, None, 0, None) == _lib.BQ_ERR_ARG
+    assert "larger than the input" in _lib.last_error()
     # zero-size work is a no-op success
     assert lib.bq_gemm_i8(None, None, 0, 4, 16, None, None, None, None, 0, None, None, None, 0, None) == 0
 

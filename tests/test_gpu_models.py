@@ -231,7 +231,8 @@ def test_c5_vit_b16(dev):
 
 def test_graph_replay_matches_eager(dev):
     """The compiled (HIP graph) int8 forward equals the eager int8 forward bit for bit, on
-    every replay, with eager work and synchronizations between replays."""
+    every replay, with eager work and synchronizations between replays (the compiled ResNet
+    runs each block's first conv and its shortcut as one launch, the eager one as two)."""
     say("graph replay vs eager (ResNet-18 b4, EfficientNet-B0 b2)")
     for name, x in (("resnet18", WL.c3_input(4, 1)), ("efficientnet_b0", WL.c4_input(2, 1))):
         model = nets.build(name, seed=1, device=dev)
@@ -304,6 +305,22 @@ def test_c3_resnet18_static_calibrated(dev):
     gap = np.abs(logits - f32_logits).max() / np.abs(f32_logits).max()
     say(f"  static int8 vs f32 logits: max |diff| / max |logit| = {gap:.3g}")
     assert gap < 0.05
+    # compiled: each block's first conv and its shortcut in one launch, the same logits
+    pairs = {"n": 0}
+    orig_pair = I.conv2d_pair_i8_nhwc
+
+    def counting_pair(*a, **k):
+        pairs["n"] += 1
+        return orig_pair(*a, **k)
+    I.conv2d_pair_i8_nhwc = counting_pair
+    try:
+        c = bt.compiled(model, int8=False, graph=True, fuse=False, plan_cache=False)
+        with torch.no_grad():
+            for _ in range(3):
+                assert np.array_equal(n(c(xt)), logits), "paired graph != eager"
+    finally:
+        I.conv2d_pair_i8_nhwc = orig_pair
+    assert pairs["n"] >= 3, pairs
     bt.clear_int8(model)
     assert model.stem_f.conv.in_scale is None
 

@@ -753,6 +753,61 @@ def test_every_conv_plan_gives_the_same_result(dev, no_plans, N, C, H, O_, k, st
         assert torch.equal(q, want_q), (cfg, split)
 
 
+@pytest.mark.parametrize("N,C,H,O_,stride", [(16, 64, 32, 128, 2), (16, 128, 16, 256, 2), (16, 256, 8, 512, 2),
+                                             (3, 32, 9, 48, 2), (2, 16, 7, 16, 1)])
+@pytest.mark.parametrize("twin", [False, True])
+def test_conv_pair_matches_two_calls(dev, no_plans, N, C, H, O_, stride, twin):
+    """A residual block's first conv (3x3) and its shortcut (1x1) in one launch
+    (bq_conv2d_i8_nhwc_pair) give each conv's own call bit for bit: f32 outputs, the first's
+    int8 twin (calibrated) or per-tile maxima (dynamic), under every plan of the first conv
+    (paired kernels, the split first conv, and the configurations that run two launches).
+    The last case's shortcut is a 1x1 stride-1 conv (the dense loader): two launches."""
+    T = no_plans
+    say(f"pair N={N} C={C} H={H} O={O_} s={stride} twin={twin}")
+    rng = np.random.default_rng(N * C + H + O_ + stride)
+    x = rng.normal(size=(N, C, H, H)).astype(np.float32)
+    w1 = (rng.normal(size=(O_, C, 3, 3)) * np.sqrt(2.0 / (C * 9))).astype(np.float32)
+    w2 = (rng.normal(size=(O_, C, 1, 1)) * np.sqrt(2.0 / C)).astype(np.float32)
+    b1 = t((rng.normal(size=O_) * 0.1).astype(np.float32), dev)
+    b2 = t((rng.normal(size=O_) * 0.1).astype(np.float32), dev)
+    p1, p2 = I.pack_conv_weight(t(w1, dev)), I.pack_conv_weight(t(w2, dev))
+    qx, sa = I.quantize_nhwc(t(x, dev), p1.cpad)
+    s_out = torch.tensor([0.05], dtype=torch.float32, device=dev) if twin else None
+    I.split_workspace(dev)
+    problem = (N, H, H, p1.cpad, O_, 3, 3, stride, 1)
+    for cfg, split in T.candidates(problem):
+        T.set_plan(problem, cfg, split)
+        if twin:
+            want1, want_q = I.conv2d_i8_nhwc_q(qx, sa, p1, s_out, stride, 1, b1, None, I.ACT_RELU)
+        else:
+            want1, want_q = I.conv2d_i8_nhwc(qx, sa, p1, stride, 1, b1, None, I.ACT_RELU), None
+        want2 = I.conv2d_i8_nhwc(qx, sa, p2, stride, 0, b2)
+        (got1, q), (got2, q2) = I.conv2d_pair_i8_nhwc(
+            qx, sa, I.PairConv(p1, stride, 1, b1, I.ACT_RELU, s_out, amax=not twin), I.PairConv(p2, stride, 0, b2))
+        assert q2 is None
+        assert torch.equal(got1, want1), (cfg, split)
+        assert torch.equal(got2, want2), (cfg, split)
+        if twin:
+            assert torch.equal(q, want_q), (cfg, split)
+        else:
+            parts, nparts, _ = got1._bq_absmax
+            wparts, wn, _ = want1._bq_absmax
+            assert nparts == wn and torch.equal(parts[:nparts], wparts[:wn]), (cfg, split)
+
+
+def test_conv_pair_rejects(dev):
+    """Only the first conv of a pair writes per-tile maxima; a twin needs O % 16 == 0."""
+    rng = np.random.default_rng(5)
+    p1 = I.pack_conv_weight(t(rng.normal(size=(24, 16, 3, 3)).astype(np.float32), dev))
+    p2 = I.pack_conv_weight(t(rng.normal(size=(24, 16, 1, 1)).astype(np.float32), dev))
+    qx, sa = I.quantize_nhwc(t(rng.normal(size=(2, 16, 8, 8)).astype(np.float32), dev), 16)
+    with pytest.raises(ValueError, match="first conv"):
+        I.conv2d_pair_i8_nhwc(qx, sa, I.PairConv(p1, 2, 1), I.PairConv(p2, 2, 0, amax=True))
+    s_out = torch.tensor([0.05], dtype=torch.float32, device=dev)
+    with pytest.raises(ValueError, match="O % 16"):
+        I.conv2d_pair_i8_nhwc(qx, sa, I.PairConv(p1, 2, 1, s_out=s_out), I.PairConv(p2, 2, 0))
+
+
 # ------------------------------------------------- per-tensor activation scale (matmulInt8)
 
 @pytest.mark.parametrize("M,N,K", [(1, 96, 512), (3, 300, 1040), (16, 512, 512), (40, 200, 768), (256, 512, 4608),
