@@ -136,7 +136,7 @@ def layer_summary(rows):
 
 
 def probes(dev, stream, qa, qw, wcopies):
-    """The day's ceilings on this GPU (libbqprobe, include/bq_probe.h), measured in the same
+    """The day's ceilings on this GPU (bench_probe/libbqprobe.so, bench_probe/bq_probe.h), measured in the same
     run as the kernels they bound:
     * the int8 MFMA rate with no memory traffic, on fragments of the 4096^3 GEMM's own
       quantized operands (the MFMA clock falls with the power the operand bits draw), in the
@@ -146,7 +146,7 @@ def probes(dev, stream, qa, qw, wcopies):
       load depths per lane; the floor of any kernel that reads those bytes once."""
     import ctypes
     import torch
-    lib = ctypes.CDLL(str(ROOT / "borch_amd" / "lib" / "libbqprobe.so"))
+    lib = ctypes.CDLL(str(ROOT / "bench_probe" / "libbqprobe.so"))
     lib.bqp_mfma_rate.restype = ctypes.c_int
     lib.bqp_mfma_rate.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int,
                                   ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
@@ -785,6 +785,9 @@ def main():
                                "+ fused dequant/bias epilogue, f32 out", "M": M, "N": N, "K": K},
         "roofline": {"bound": "mfma", "achieved": round(gemm_tops, 2), "peak": PEAK_INT8_TOPS, "unit": "TOPS",
                      "frac": round(gemm_tops / PEAK_INT8_TOPS, 4), "traffic": traffic,
+                     "traffic_source": ("not measured in this run: HBM bytes per launch from the committed "
+                                        "rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of this kernel "
+                                        "(profiles/gemm_4096_traffic.json)") if traffic is not None else None,
                      "kernel": "gemm_i8_kernel 256x256 (bq_gemm_i8)", "kernel_ms": round(gemm_ms, 5),
                      "timing": "HIP events around HIP-graph replays on the launch stream",
                      "measured_ceiling_TOPS": ceilings["mfma_int8_TOPS_no_memory"],

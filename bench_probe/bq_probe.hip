@@ -1,4 +1,4 @@
-// Measurement probes for bench.py (declared in include/bq_probe.h): the int8 MFMA rate the
+// Measurement probes for bench.py (declared in bq_probe.h beside this file): the int8 MFMA rate the
 // GPU sustains on given operand bytes, and the duration of a plain streaming read. They
 // give the day's ceilings beside the nominal peaks; nothing in the int8 path calls them.
 #include <hip/hip_runtime.h>
@@ -6,8 +6,8 @@
 #include <stdint.h>
 #include <stdio.h>
 
-#include "../../../include/bq.h"
-#include "../../../include/bq_probe.h"
+#include "../include/bq.h"
+#include "bq_probe.h"
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));

@@ -20,7 +20,6 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIBDIR = PKG / "lib"
 LIB = LIBDIR / "libbq.so"
-PROBE_LIB = LIBDIR / "libbqprobe.so"  # bench.py's measurement probes (include/bq_probe.h)
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -61,26 +60,31 @@ def _link(objs, out: Path) -> None:
 
 
 def build(verbose: bool = True) -> Path:
-    """Compile every ``csrc/*.hip`` and link ``lib/libbq.so`` (returned), and the probes of
-    ``csrc/probe/*.hip`` into ``lib/libbqprobe.so``."""
+    """Compile every ``csrc/*.hip`` and link ``lib/libbq.so`` (returned)."""
     srcs = sorted(CSRC.glob("*.hip"))
-    probe_srcs = sorted((CSRC / "probe").glob("*.hip"))
     if not srcs:
         raise RuntimeError(f"no HIP sources under {CSRC}")
     objdir = PKG / "_build"
     objdir.mkdir(exist_ok=True)
     LIBDIR.mkdir(exist_ok=True)
     objs = [objdir / (s.stem + ".o") for s in srcs]
-    probe_objs = [objdir / ("probe_" + s.stem + ".o") for s in probe_srcs]
-    with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs) + len(probe_srcs))) as ex:
-        list(ex.map(_compile, srcs + probe_srcs, objs + probe_objs))
+    with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
+        list(ex.map(_compile, srcs, objs))
     _link(objs, LIB)
-    if probe_objs:
-        _link(probe_objs, PROBE_LIB)
     if verbose:
-        print(f"built {LIB.relative_to(ROOT)} from {len(srcs)} sources"
-              + (f", {PROBE_LIB.relative_to(ROOT)} from {len(probe_srcs)}" if probe_objs else ""))
+        print(f"built {LIB.relative_to(ROOT)} from {len(srcs)} sources")
     return LIB
+
+
+def build_objects(srcs, objdir: Path, out: Path) -> Path:
+    """Compile ``srcs`` with the library's flags into ``objdir`` and link the shared library
+    ``out`` (bench.py's measurement probes use it)."""
+    objdir.mkdir(parents=True, exist_ok=True)
+    objs = [objdir / (Path(s).stem + ".o") for s in srcs]
+    with cf.ThreadPoolExecutor(max_workers=max(1, min(8, len(srcs)))) as ex:
+        list(ex.map(_compile, [Path(s) for s in srcs], objs))
+    _link(objs, out)
+    return out
 
 
 if __name__ == "__main__":

@@ -102,11 +102,11 @@ def test_quantize_for_int8_refuses_without_device():
         bt.quantize_for_int8(m)
 
 
-PROBE_HEADER = ROOT / "include" / "bq_probe.h"
+PROBE_HEADER = ROOT / "bench_probe" / "bq_probe.h"
 
 
 def probe_lib():
-    lib = ctypes.CDLL(str(ROOT / "borch_amd" / "lib" / "libbqprobe.so"))
+    lib = ctypes.CDLL(str(ROOT / "bench_probe" / "libbqprobe.so"))
     lib.bqp_last_error.restype = ctypes.c_char_p
     return lib
 

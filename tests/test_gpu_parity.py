@@ -664,7 +664,7 @@ def test_probe_stream_read_folds_every_byte(dev):
     """The read-floor probe bench.py times reads every 16-byte chunk once: its per-workgroup
     XOR fold equals the host's fold of the same bytes, for each load depth."""
     import ctypes
-    lib = ctypes.CDLL(str(ROOT / "borch_amd" / "lib" / "libbqprobe.so"))
+    lib = ctypes.CDLL(str(ROOT / "bench_probe" / "libbqprobe.so"))
     lib.bqp_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
     g = torch.Generator().manual_seed(5)
     n16 = 3 * 2048 + 37  # a ragged last workgroup for every depth
