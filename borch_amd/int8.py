@@ -19,7 +19,7 @@ __all__ = [
     "ACT_NONE", "ACT_RELU", "ACT_SILU", "ACT_GELU", "Int8Weight", "Int8ConvWeight", "Int8DwWeight",
     "quantize_rows", "quantize_weight_per_channel", "quantize_tensor", "quantize_nhwc",
     "gemm_i8", "conv2d_i8_nhwc", "conv2d_i8_nhwc_q", "conv2d_pair_i8_nhwc", "PairConv", "dwconv_i8_nhwc",
-    "pack_linear_weight", "pack_conv_weight",
+    "pack_linear_weight", "pack_conv_weight", "attention_f32",
     "quantize_nhwc_scaled", "quantize_nhwc_chscale", "se_gate_nhwc", "linear_w8a32", "dequant_weight",
     "pack_dw_weight", "linear", "linear_rows", "conv2d", "depthwise_conv2d", "round_up", "split_workspace",
 ]
@@ -540,6 +540,24 @@ def conv2d_pair_i8_nhwc(qx, sa, first: PairConv, second: PairConv):
     check(lib().bq_conv2d_i8_nhwc_pair(qx.contiguous().data_ptr(), N, H, W, C, sa.data_ptr(), descs[0], descs[1],
                                        *_ws_args(qx.device), _stream(qx)))
     return results
+
+
+def attention_f32(qkv: torch.Tensor, heads: int) -> torch.Tensor:
+    """Softmax attention of every head in f32, from a qkv projection's output ``[B, T, 3 D]``
+    (per token q, k, v side by side, each ``[heads, 64]``) to ``[B, T, D]``, the heads side by
+    side (bq_attention_f32: ``softmax((q k^T) / 8) v``, head width 64, T <= 256; the int8
+    layers on either side stay as they are: this is f32 beside the path)."""
+    if qkv.dtype != torch.float32:
+        raise TypeError(f"attention_f32 takes float32, got {qkv.dtype}")
+    require_device(qkv.device)
+    B, T, D3 = qkv.shape
+    D = D3 // 3
+    if D3 != 3 * D or D % heads:
+        raise RuntimeError(f"qkv of width {D3} does not hold {heads} heads of q, k and v")
+    x = qkv.contiguous()
+    out = torch.empty((B, T, D), dtype=torch.float32, device=qkv.device)
+    check(lib().bq_attention_f32(x.data_ptr(), B, T, heads, D // heads, out.data_ptr(), _stream(x)))
+    return out
 
 
 def dwconv_i8_nhwc(qx, sa, wq: Int8DwWeight, stride=1, pad=0, bias=None, act=ACT_NONE, want_acc=False):

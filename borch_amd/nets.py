@@ -277,13 +277,15 @@ class EncoderLayer(tnn.Module):
         return self.attend(self.qkv(h))
 
     def attend(self, qkv):
-        """The attention core on the qkv projection's output [B, T, 3 D], f32: torch's fused
-        scaled-dot-product attention (its memory-efficient kernel here: within 1e-6 of
-        float64, as the separate products and softmax, and 1.5 ms faster a B/16 b32
-        forward), reading q, k and v as strided views of the one projection output."""
+        """The attention core on the qkv projection's output [B, T, 3 D], f32. On a gfx950
+        device with heads of 64 and at most 256 tokens: ``I8.attention_f32`` (one HIP kernel,
+        f32 MFMAs; q, k, v read in place and the heads written side by side). Otherwise torch's
+        fused scaled-dot-product attention on strided views of the projection output."""
         B, T, D3 = qkv.shape
         D = D3 // 3
         H, dh = self.heads, D // self.heads
+        if qkv.is_cuda and dh == 64 and T <= 256 and qkv.dtype == torch.float32:
+            return I8.attention_f32(qkv, H)
         qkv = qkv.reshape(B, T, 3, H, dh).permute(2, 0, 3, 1, 4)
         o = torch.nn.functional.scaled_dot_product_attention(qkv[0], qkv[1], qkv[2])
         return o.transpose(1, 2).reshape(B, T, D)

@@ -292,6 +292,19 @@ int bq_dwconv_i8_nhwc(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t 
                       const float* sA, const float* sW, const float* bias, int act,
                       float* out, int32_t* acc, bq_stream_t stream);
 
+/* Softmax attention in f32, beside the int8 path (a transformer's heads between its int8
+ * qkv and output projections): for every image b and head h,
+ *   out[b, t, h*64 + d] = sum_u softmax_u((q_t . k_u) * (1/sqrt(64))) v[u, d]
+ * with q, k, v read from the qkv projection's output qkv f32 [B, T, 3, H, 64] (q, k, v of a
+ * token side by side, each [H, 64]) and out f32 [B, T, H * 64]. f32 throughout: the
+ * exponentials exp(s - max) are summed against v and the result divided by their sum (the
+ * reference divides each probability first; the f32 sums run in another order too): within
+ * 1e-5 of the output's scale of the float64 result. dh == 64, T <= 256; qkv and out 16-byte
+ * aligned.
+ * Replaces scaled_dot_product_attention (borch/_nn.py:2143-2170; its softmax is softmaxRows,
+ * borch-ts/src/kernels.ts:2483-2532) on that layout. */
+int bq_attention_f32(const float* qkv, int64_t B, int64_t T, int64_t H, int64_t dh, float* out, bq_stream_t stream);
+
 /* Workspace bytes of bq_se_gate_nhwc for this size (per-chunk partial sums and maxima). */
 size_t bq_se_gate_ws_bytes(int64_t N, int64_t HW, int64_t C);
 

@@ -79,6 +79,10 @@ def test_argument_checks_run_on_host():
     big = _lib.ConvDesc(None, 32, 9, 9, 1, 0, None, None, None, 0, None, None, None, None)
     assert lib.bq_conv2d_i8_nhwc_pair(None, 1, 8, 8, 16, None, big, d, None, 0, None) == _lib.BQ_ERR_ARG
     assert "larger than the input" in _lib.last_error()
+    # f32 attention: head width 64 and at most 256 tokens
+    assert lib.bq_attention_f32(None, 1, 10, 2, 32, None, None) == _lib.BQ_ERR_UNSUPPORTED
+    assert lib.bq_attention_f32(None, 1, 257, 2, 64, None, None) == _lib.BQ_ERR_UNSUPPORTED
+    assert lib.bq_attention_f32(None, 1, 10, 2, 64, None, None) == _lib.BQ_ERR_ARG
     # zero-size work is a no-op success
     assert lib.bq_gemm_i8(None, None, 0, 4, 16, None, None, None, None, 0, None, None, None, 0, None) == 0
 

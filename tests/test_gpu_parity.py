@@ -808,6 +808,37 @@ def test_conv_pair_rejects(dev):
         I.conv2d_pair_i8_nhwc(qx, sa, I.PairConv(p1, 2, 1, s_out=s_out), I.PairConv(p2, 2, 0))
 
 
+# ------------------------------------------------- f32 attention beside the path (ViT)
+
+@pytest.mark.parametrize("B,T,H,scale", [(2, 197, 12, 1.0), (1, 1, 1, 1.0), (3, 16, 2, 1.0), (2, 17, 3, 1.0),
+                                         (1, 64, 4, 1.0), (1, 100, 2, 1.0), (2, 128, 1, 1.0), (1, 129, 2, 1.0),
+                                         (1, 256, 2, 1.0), (2, 197, 2, 6.0)])
+def test_attention_f32(dev, B, T, H, scale):
+    """bq_attention_f32 against the float64 restatement of scaled_dot_product_attention
+    (borch/_nn.py:2143-2170: scores = (q @ k^T) / sqrt(64), softmax exp(s - max) / sum,
+    then @ v), on q, k, v read from a packed [B, T, 3, H, 64] projection output: within the
+    f32 bound (1e-5 relative / 2e-6 absolute of the output's scale), across ragged T (the
+    masked key padding, the partial query blocks) and with scores of +-50 (scale 6)."""
+    say(f"attention B={B} T={T} H={H} scale={scale}")
+    rng = np.random.default_rng(B * 1000 + T * 10 + H)
+    qkv = (rng.normal(size=(B, T, 3, H, 64)) * scale).astype(np.float32)
+    got = n(I.attention_f32(t(qkv.reshape(B, T, 3 * H * 64), dev), H))
+    q, k, v = (qkv[:, :, i].astype(np.float64).transpose(0, 2, 1, 3) for i in range(3))  # [B, H, T, 64]
+    s = (q @ k.transpose(0, 1, 3, 2)) / 8.0
+    p = np.exp(s - s.max(axis=-1, keepdims=True))
+    p /= p.sum(axis=-1, keepdims=True)
+    want = (p @ v).transpose(0, 2, 1, 3).reshape(B, T, H * 64)
+    err = np.abs(got - want).max()
+    say(f"  max |err| {err:.3g} (output scale {np.abs(want).max():.3g})")
+    assert err <= 1e-5 * np.abs(want).max() + 2e-6
+    # torch's own f32 attention on the same operands: within the same bound of float64, so
+    # the two f32 results agree to twice it
+    qt, kt, vt = (t(np.ascontiguousarray(qkv[:, :, i].transpose(0, 2, 1, 3)), dev) for i in range(3))
+    ref = n(torch.nn.functional.scaled_dot_product_attention(qt, kt, vt).transpose(1, 2).reshape(B, T, H * 64))
+    say(f"  torch f32: max |err| {np.abs(ref - want).max():.3g}")
+    assert np.abs(got - ref).max() <= 2e-5 * np.abs(want).max() + 4e-6
+
+
 # ------------------------------------------------- per-tensor activation scale (matmulInt8)
 
 @pytest.mark.parametrize("M,N,K", [(1, 96, 512), (3, 300, 1040), (16, 512, 512), (40, 200, 768), (256, 512, 4608),
