@@ -43,33 +43,49 @@ __global__ __launch_bounds__(ATT_WAVES * 64) void attention_f32_kernel(const flo
   const size_t tok = (size_t)3 * D;  // floats from one token's q to the next's
   const float* base = qkv + (size_t)b * T * tok + (size_t)h * ATT_DH;
 
-  // k and v of the head into LDS, keys past T as zeros (their scores are masked below)
-  for (int idx = threadIdx.x; idx < TK * (ATT_DH / 4); idx += ATT_WAVES * 64) {
-    const int key = idx >> 4, c4 = (idx & 15) * 4;
-    float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
-    if (key < T) {
-      kv = *reinterpret_cast<const float4*>(base + key * tok + D + c4);
-      vv = *reinterpret_cast<const float4*>(base + key * tok + 2 * D + c4);
-    }
-    *reinterpret_cast<float4*>(&ks[key * ATT_PITCH + c4]) = kv;
-    *reinterpret_cast<float4*>(&vs[key * ATT_PITCH + c4]) = vv;
-  }
-  __syncthreads();
-
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int n = lane & 15;  // this lane's query within the wave's 16
   const int g = lane >> 4;  // its group: head dims 16 g .. 16 g + 15 of q and k
   const int q0 = qb * (ATT_WAVES * 16) + wave * 16;
-  if (q0 >= T) return;  // a wave past the last query (no barrier follows)
   const int q = q0 + n;
 
-  float qv[16];  // q[q][16 g .. 16 g + 15] (zeros past T)
+  // Every load of the workgroup issued before the first is waited for: this lane's q
+  // (q[q][16 g .. 16 g + 15], zeros past T), then its share of the head's k and v (keys past
+  // T as zeros: their scores are masked below), then k and v go to LDS. (A load-then-store
+  // loop waited for each round trip in turn.)
+  float4 q4[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    q4[e] = q < T ? *reinterpret_cast<const float4*>(base + q * tok + 16 * g + 4 * e) : make_float4(0.f, 0.f, 0.f, 0.f);
+  constexpr int THREADS = ATT_WAVES * 64;
+  constexpr int PER = (TK * (ATT_DH / 4) + THREADS - 1) / THREADS;  // float4 of k (and of v) a thread
+  float4 kr[PER], vr[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int idx = threadIdx.x + i * THREADS;
+    const int key = idx >> 4, c4 = (idx & 15) * 4;
+    kr[i] = vr[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (key < T) {
+      kr[i] = *reinterpret_cast<const float4*>(base + key * tok + D + c4);
+      vr[i] = *reinterpret_cast<const float4*>(base + key * tok + 2 * D + c4);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int idx = threadIdx.x + i * THREADS;
+    const int key = idx >> 4, c4 = (idx & 15) * 4;
+    if (key < TK) {
+      *reinterpret_cast<float4*>(&ks[key * ATT_PITCH + c4]) = kr[i];
+      *reinterpret_cast<float4*>(&vs[key * ATT_PITCH + c4]) = vr[i];
+    }
+  }
+  __syncthreads();
+  if (q0 >= T) return;  // a wave past the last query (no barrier follows)
+  float qv[16];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    const float4 v4 = q < T ? *reinterpret_cast<const float4*>(base + q * tok + 16 * g + 4 * e)
-                            : make_float4(0.f, 0.f, 0.f, 0.f);
-    qv[4 * e] = v4.x; qv[4 * e + 1] = v4.y; qv[4 * e + 2] = v4.z; qv[4 * e + 3] = v4.w;
+    qv[4 * e] = q4[e].x; qv[4 * e + 1] = q4[e].y; qv[4 * e + 2] = q4[e].z; qv[4 * e + 3] = q4[e].w;
   }
 
   // S^T = k q^T: key block j, lane (n, g), register i -> key 16 j + 4 g + i, query q
