@@ -84,6 +84,7 @@ SIGNATURES = {
     "bq_linear_w8a32": (_c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_int, _c_p, _c_p]),
     "bq_dequant_i8": (_c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_p]),
     "bq_attention_f32": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p]),
+    "bq_avgpool_linear_f32": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_p]),
     "bq_se_gate_ws_bytes": (_c_size, [_c_i64, _c_i64, _c_i64]),
     "bq_se_gate_absmax_parts": (_c_i64, [_c_i64, _c_i64]),
     "bq_se_gate_nhwc": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_p,

@@ -213,6 +213,55 @@ static int se_chunks(int64_t HW, int64_t C) {
   return (int)std::max<int64_t>(k, 1);
 }
 
+// A classifier head in f32, beside the int8 path: the global average pool of a channels-last
+// activation x [N, HW, C] and the Linear after it, out[n, o] = b[o] + sum_c pooled[n, c] *
+// w[o, c] with pooled[n, c] = (sum over the HW pixels of x[n, p, c], in pixel order) / HW.
+// One workgroup per image: the pooled vector in LDS, then a wave per output, its lanes over
+// c in order and a fixed-order wave sum. For the small heads (O * C <= 65536: CIFAR
+// ResNet-18's 512 -> 10) where the pool and the GEMM would be two launches of a few
+// microseconds each.
+constexpr int HEAD_THREADS = 256;
+
+__global__ __launch_bounds__(HEAD_THREADS) void avgpool_linear_kernel(const float* __restrict__ x, int HW, int C,
+                                                                      const float* __restrict__ w,
+                                                                      const float* __restrict__ b, int O,
+                                                                      float* __restrict__ out) {
+  extern __shared__ float pooled[];
+  const int n = blockIdx.x;
+  const float* xn = x + (size_t)n * HW * C;
+  // eight loads in flight before their adds / FMAs (in order): a loop of dependent round trips
+  // would cost one each
+  constexpr int U = 8;
+  for (int c = threadIdx.x; c < C; c += HEAD_THREADS) {
+    float s = 0.f;
+    for (int p0 = 0; p0 < HW; p0 += U) {
+      float v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) v[u] = p0 + u < HW ? xn[(size_t)(p0 + u) * C + c] : 0.f;
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (p0 + u < HW) s = __fadd_rn(s, v[u]);
+    }
+    pooled[c] = __fdiv_rn(s, (float)HW);
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int o = wave; o < O; o += HEAD_THREADS / 64) {
+    const float* wo = w + (size_t)o * C;
+    float acc = 0.f;
+    for (int c0 = lane; c0 < C; c0 += 64 * U) {
+      float v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) v[u] = c0 + 64 * u < C ? wo[c0 + 64 * u] : 0.f;
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (c0 + 64 * u < C) acc = __fmaf_rn(pooled[c0 + 64 * u], v[u], acc);
+    }
+    const float v = wave_sum_fixed(acc);  // the whole wave is here (the loop is per wave)
+    if (lane == 0) out[(size_t)n * O + o] = b ? __fadd_rn(v, b[o]) : v;
+  }
+}
+
 }  // namespace bq
 
 using namespace bq;
@@ -255,6 +304,20 @@ int bq_se_gate_nhwc(const float* x, int64_t N, int64_t HW, int64_t C, const floa
   const size_t lds = (size_t)(C + S + (absmax_parts ? C : 0)) * sizeof(float);
   se_gate_kernel<<<(unsigned)N, GATE_THREADS, lds, st>>>(partial, pmax, chunks, (int)HW, (int)C, (int)S, w1, b1, w2t,
                                                          b2, gate, absmax_parts);
+  return check_launch(what);
+}
+
+int bq_avgpool_linear_f32(const float* x, int64_t N, int64_t HW, int64_t C, const float* w, const float* b,
+                          int64_t O, float* out, bq_stream_t stream) {
+  const char* what = "bq_avgpool_linear_f32";
+  if (N < 0 || HW < 1 || C < 1 || O < 1) return set_error(BQ_ERR_ARG, "%s: bad sizes", what);
+  if (O * C > 65536 || C > 16384) return set_error(BQ_ERR_UNSUPPORTED, "%s: O * C = %lld (at most 65536)", what,
+                                                   (long long)(O * C));
+  if (N * HW * C >= ((int64_t)1 << 31) || N > 0x7fffffff) return set_error(BQ_ERR_ARG, "%s: size too large", what);
+  if (N == 0) return BQ_OK;
+  if (!x || !w || !out) return set_error(BQ_ERR_ARG, "%s: null pointer", what);
+  avgpool_linear_kernel<<<(unsigned)N, HEAD_THREADS, (size_t)C * sizeof(float), (hipStream_t)stream>>>(
+      x, (int)HW, (int)C, w, b, (int)O, out);
   return check_launch(what);
 }
 

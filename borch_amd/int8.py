@@ -19,7 +19,7 @@ __all__ = [
     "ACT_NONE", "ACT_RELU", "ACT_SILU", "ACT_GELU", "Int8Weight", "Int8ConvWeight", "Int8DwWeight",
     "quantize_rows", "quantize_weight_per_channel", "quantize_tensor", "quantize_nhwc",
     "gemm_i8", "conv2d_i8_nhwc", "conv2d_i8_nhwc_q", "conv2d_pair_i8_nhwc", "PairConv", "dwconv_i8_nhwc",
-    "pack_linear_weight", "pack_conv_weight", "attention_f32",
+    "pack_linear_weight", "pack_conv_weight", "attention_f32", "avgpool_linear",
     "quantize_nhwc_scaled", "quantize_nhwc_chscale", "se_gate_nhwc", "linear_w8a32", "dequant_weight",
     "pack_dw_weight", "linear", "linear_rows", "conv2d", "depthwise_conv2d", "round_up", "split_workspace",
 ]
@@ -557,6 +557,25 @@ def attention_f32(qkv: torch.Tensor, heads: int) -> torch.Tensor:
     x = qkv.contiguous()
     out = torch.empty((B, T, D), dtype=torch.float32, device=qkv.device)
     check(lib().bq_attention_f32(x.data_ptr(), B, T, heads, D // heads, out.data_ptr(), _stream(x)))
+    return out
+
+
+def avgpool_linear(x: torch.Tensor, weight: torch.Tensor, bias=None) -> torch.Tensor:
+    """``linear(x.mean((2, 3)), weight, bias)`` in f32 for a channels-last ``x [N, C, H, W]`` and a
+    small head (``O * C <= 65536``) in one launch (bq_avgpool_linear_f32) → ``[N, O]``."""
+    if x.dtype != torch.float32:
+        raise TypeError(f"avgpool_linear takes float32, got {x.dtype}")
+    require_device(x.device)
+    N, C, H, W = x.shape
+    O = weight.shape[0]
+    if weight.shape[1] != C:
+        raise RuntimeError(f"mat1 and mat2 shapes cannot be multiplied ({N}x{C} and {weight.shape[1]}x{O})")
+    xl = x.contiguous(memory_format=torch.channels_last)
+    w = weight.detach().float().contiguous()
+    b = _vec(bias, O, "bias")
+    out = torch.empty((N, O), dtype=torch.float32, device=x.device)
+    check(lib().bq_avgpool_linear_f32(xl.data_ptr(), N, H * W, C, w.data_ptr(), _ptr(b), O, out.data_ptr(),
+                                      _stream(xl)))
     return out
 
 

@@ -130,7 +130,12 @@ class ResNet18(tnn.Module):
         return self.body(h)
 
     def forward(self, x):
-        return self.fc(self.features(x).mean(dim=(2, 3)))
+        h = self.features(x)
+        fc = self.fc
+        if (h.is_cuda and h.dtype == torch.float32 and getattr(fc, "int8", None) is None
+                and fc.weight.shape[0] * fc.weight.shape[1] <= 65536):
+            return I8.avgpool_linear(h, fc.weight, fc.bias)  # the f32 head in one launch
+        return fc(h.mean(dim=(2, 3)))
 
     def fuse(self):
         self.eval()

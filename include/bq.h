@@ -305,6 +305,15 @@ int bq_dwconv_i8_nhwc(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t 
  * borch-ts/src/kernels.ts:2483-2532) on that layout. */
 int bq_attention_f32(const float* qkv, int64_t B, int64_t T, int64_t H, int64_t dh, float* out, bq_stream_t stream);
 
+/* A classifier head in f32, beside the int8 path: the global average pool of a channels-last
+ * activation x f32 [N, HW, C] and the Linear w f32 [O, C], b f32 [O] (nullable) after it:
+ *   out f32 [N, O] = b + (sum over the HW pixels of x[n, :, c], pixel order) / HW . w[o, :]
+ * one f32 rounding per operation. O * C <= 65536 (a small head: the pool and the product in
+ * one launch). Replaces the mean over H, W and the f32 Linear of the configuration's head
+ * (tests/browser/export_resnet18.py:56-59; borch/_nn.py:397-415). */
+int bq_avgpool_linear_f32(const float* x, int64_t N, int64_t HW, int64_t C, const float* w, const float* b,
+                          int64_t O, float* out, bq_stream_t stream);
+
 /* Workspace bytes of bq_se_gate_nhwc for this size (per-chunk partial sums and maxima). */
 size_t bq_se_gate_ws_bytes(int64_t N, int64_t HW, int64_t C);
 

@@ -83,6 +83,9 @@ def test_argument_checks_run_on_host():
     assert lib.bq_attention_f32(None, 1, 10, 2, 32, None, None) == _lib.BQ_ERR_UNSUPPORTED
     assert lib.bq_attention_f32(None, 1, 257, 2, 64, None, None) == _lib.BQ_ERR_UNSUPPORTED
     assert lib.bq_attention_f32(None, 1, 10, 2, 64, None, None) == _lib.BQ_ERR_ARG
+    # the f32 head: small heads only
+    assert lib.bq_avgpool_linear_f32(None, 2, 16, 1000, None, None, 1000, None, None) == _lib.BQ_ERR_UNSUPPORTED
+    assert lib.bq_avgpool_linear_f32(None, 2, 16, 512, None, None, 10, None, None) == _lib.BQ_ERR_ARG
     # zero-size work is a no-op success
     assert lib.bq_gemm_i8(None, None, 0, 4, 16, None, None, None, None, 0, None, None, None, 0, None) == 0
 

@@ -839,6 +839,24 @@ def test_attention_f32(dev, B, T, H, scale):
     assert np.abs(got - ref).max() <= 2e-5 * np.abs(want).max() + 4e-6
 
 
+@pytest.mark.parametrize("N,C,H,O_,bias", [(16, 512, 4, 10, True), (3, 64, 7, 100, False), (1, 16384, 1, 4, True),
+                                          (5, 1000, 3, 65, True)])
+def test_avgpool_linear(dev, N, C, H, O_, bias):
+    """bq_avgpool_linear_f32 (the CIFAR ResNet-18 head: mean over H, W, then the f32 Linear)
+    against float64, within the f32 bound of its two sums (1e-5 of sum |pooled * w| + 1e-6)."""
+    say(f"avgpool+linear N={N} C={C} H={H} O={O_}")
+    rng = np.random.default_rng(N + C + O_)
+    x = rng.normal(size=(N, C, H, H)).astype(np.float32)
+    w = (rng.normal(size=(O_, C)) / np.sqrt(C)).astype(np.float32)
+    b = rng.normal(size=O_).astype(np.float32) if bias else None
+    xt = t(x, dev).contiguous(memory_format=torch.channels_last)
+    got = n(I.avgpool_linear(xt, t(w, dev), None if b is None else t(b, dev)))
+    pooled = x.astype(np.float64).mean(axis=(2, 3))
+    want = pooled @ w.astype(np.float64).T + (0.0 if b is None else b.astype(np.float64))
+    scale = np.abs(pooled) @ np.abs(w.astype(np.float64)).T
+    assert np.all(np.abs(got - want) <= 1e-5 * scale + 1e-6)
+
+
 # ------------------------------------------------- per-tensor activation scale (matmulInt8)
 
 @pytest.mark.parametrize("M,N,K", [(1, 96, 512), (3, 300, 1040), (16, 512, 512), (40, 200, 768), (256, 512, 4608),
