@@ -11,7 +11,10 @@ under test after the BN fold) and applies oracle.quant's arithmetic:
 * ``dwconv_layer`` — the same for a depthwise conv (lib.rs:598-641's tap sum, integers);
 * ``linear_layer`` — per-row activations, per-channel weights (quant.ts:23-53);
 * ``resnet18_features`` — the CIFAR ResNet-18 conv stack of export_resnet18.py:27-60
-  chained layer by layer (pinned by the per-layer checks and the brute-force conv tests).
+  chained layer by layer (pinned by the per-layer checks and the brute-force conv tests);
+* ``se_gate``, ``attention_qkv``, ``avgpool_linear`` — the f32 pieces beside the path in
+  float64 (the GPU tests also hold the attention to torch's own f32 attention, an
+  independent implementation, and tests/test_oracle.py pins these two against torch).
 """
 from __future__ import annotations
 
@@ -154,3 +157,29 @@ def se_gate(x_nchw, w1, b1, w2, b2):
     z = z / (1.0 + np.exp(-z))
     g = z @ np.asarray(w2, np.float64).T + (0.0 if b2 is None else np.asarray(b2, np.float64))
     return (1.0 / (1.0 + np.exp(-g))).astype(np.float32)
+
+
+def attention_qkv(qkv, heads):
+    """Softmax attention of every head in float64 from a packed qkv projection output
+    [B, T, 3 * heads * dh] (per token q, k, v side by side, each [heads, dh]) to [B, T, heads *
+    dh]: scores = (q @ k^T) / sqrt(dh), softmax exp(s - max) / sum, then @ v
+    (borch/_nn.py:2143-2170 scaled_dot_product_attention; its softmax borch-ts/src/kernels.ts:
+    2483-2532 softmaxRows)."""
+    x = np.asarray(qkv, np.float64)
+    B, T, D3 = x.shape
+    dh = D3 // (3 * heads)
+    q, k, v = (x.reshape(B, T, 3, heads, dh)[:, :, i].transpose(0, 2, 1, 3) for i in range(3))
+    s = (q @ k.transpose(0, 1, 3, 2)) / np.sqrt(dh)
+    p = np.exp(s - s.max(axis=-1, keepdims=True))
+    p /= p.sum(axis=-1, keepdims=True)
+    return (p @ v).transpose(0, 2, 1, 3).reshape(B, T, heads * dh)
+
+
+def avgpool_linear(x_nchw, w, b=None):
+    """The configuration's f32 head in float64: the mean over H, W, then the Linear
+    (tests/browser/export_resnet18.py:56-59; borch/_nn.py:397-415). Returns (out [N, O], the
+    scale sum |pooled| . |w| the f32 error bound is proportional to)."""
+    pooled = np.asarray(x_nchw, np.float64).mean(axis=(2, 3))
+    wd = np.asarray(w, np.float64)
+    out = pooled @ wd.T + (0.0 if b is None else np.asarray(b, np.float64))
+    return out, np.abs(pooled) @ np.abs(wd).T

@@ -822,12 +822,9 @@ def test_attention_f32(dev, B, T, H, scale):
     say(f"attention B={B} T={T} H={H} scale={scale}")
     rng = np.random.default_rng(B * 1000 + T * 10 + H)
     qkv = (rng.normal(size=(B, T, 3, H, 64)) * scale).astype(np.float32)
+    from oracle import models as OM
     got = n(I.attention_f32(t(qkv.reshape(B, T, 3 * H * 64), dev), H))
-    q, k, v = (qkv[:, :, i].astype(np.float64).transpose(0, 2, 1, 3) for i in range(3))  # [B, H, T, 64]
-    s = (q @ k.transpose(0, 1, 3, 2)) / 8.0
-    p = np.exp(s - s.max(axis=-1, keepdims=True))
-    p /= p.sum(axis=-1, keepdims=True)
-    want = (p @ v).transpose(0, 2, 1, 3).reshape(B, T, H * 64)
+    want = OM.attention_qkv(qkv.reshape(B, T, 3 * H * 64), H)
     err = np.abs(got - want).max()
     say(f"  max |err| {err:.3g} (output scale {np.abs(want).max():.3g})")
     assert err <= 1e-5 * np.abs(want).max() + 2e-6
@@ -850,10 +847,9 @@ def test_avgpool_linear(dev, N, C, H, O_, bias):
     w = (rng.normal(size=(O_, C)) / np.sqrt(C)).astype(np.float32)
     b = rng.normal(size=O_).astype(np.float32) if bias else None
     xt = t(x, dev).contiguous(memory_format=torch.channels_last)
+    from oracle import models as OM
     got = n(I.avgpool_linear(xt, t(w, dev), None if b is None else t(b, dev)))
-    pooled = x.astype(np.float64).mean(axis=(2, 3))
-    want = pooled @ w.astype(np.float64).T + (0.0 if b is None else b.astype(np.float64))
-    scale = np.abs(pooled) @ np.abs(w.astype(np.float64)).T
+    want, scale = OM.avgpool_linear(x, w, b)
     assert np.all(np.abs(got - want) <= 1e-5 * scale + 1e-6)
 
 

@@ -450,3 +450,41 @@ def test_mmi8_operands_layout():
     assert np.array_equal(W, B.T)
     ref = A.astype(np.int64) @ B.astype(np.int64)
     assert np.array_equal(O.gemm_i8_i32(A, W), ref.astype(np.int32))
+
+
+def test_attention_oracle_against_torch_and_closed_forms():
+    """oracle.models.attention_qkv against torch's scaled_dot_product_attention in float64 on
+    the CPU (an independent implementation), and two closed forms: identical keys give every
+    query the mean of v; one dominant key per query selects that key's value row."""
+    import torch
+
+    from oracle import models as OM
+    rng = np.random.default_rng(3)
+    B, T, H, dh = 2, 9, 3, 64
+    qkv = rng.normal(size=(B, T, 3, H, dh))
+    got = OM.attention_qkv(qkv.reshape(B, T, -1), H)
+    x = torch.from_numpy(qkv).permute(2, 0, 3, 1, 4)
+    ref = torch.nn.functional.scaled_dot_product_attention(x[0], x[1], x[2]).transpose(1, 2).reshape(B, T, -1)
+    np.testing.assert_allclose(got, ref.numpy(), rtol=1e-12, atol=1e-12)
+    same = qkv.copy()
+    same[:, :, 1] = same[:, :1, 1]  # every key equal to token 0's
+    np.testing.assert_allclose(OM.attention_qkv(same.reshape(B, T, -1), H).reshape(B, T, H, dh),
+                               np.broadcast_to(same[:, :, 2].mean(axis=1, keepdims=True), (B, T, H, dh)), atol=1e-12)
+    sel = np.zeros((1, 4, 3, 1, dh))
+    sel[0, :, 0, 0, :] = np.eye(4, dh) * 400.0  # query t matches key t only (scores 0 or 400^2 / 8)
+    sel[0, :, 1, 0, :] = np.eye(4, dh) * 400.0
+    sel[0, :, 2, 0, :] = rng.normal(size=(4, dh))
+    np.testing.assert_allclose(OM.attention_qkv(sel.reshape(1, 4, -1), 1).reshape(4, dh), sel[0, :, 2, 0], atol=1e-9)
+
+
+def test_avgpool_linear_oracle_against_torch():
+    """oracle.models.avgpool_linear against torch's mean over H, W and linear in float64."""
+    import torch
+
+    from oracle import models as OM
+    rng = np.random.default_rng(4)
+    x, w, b = rng.normal(size=(3, 8, 4, 4)), rng.normal(size=(5, 8)), rng.normal(size=5)
+    got, scale = OM.avgpool_linear(x, w, b)
+    ref = torch.nn.functional.linear(torch.from_numpy(x).mean(dim=(2, 3)), torch.from_numpy(w), torch.from_numpy(b))
+    np.testing.assert_allclose(got, ref.numpy(), rtol=1e-12, atol=1e-12)
+    assert np.all(scale >= np.abs(got - b) - 1e-12)
