@@ -187,6 +187,139 @@ def probes(dev, stream, qa, qw, wcopies):
                           f"{ch} x 16 B loads a lane (best of 1/2/4/8)"}
 
 
+def _fit_line(xs, ys):
+    """Least-squares t = t0 + x / bw over (bytes, us) points: (t0 us, bw GB/s)."""
+    A = np.vstack([np.ones(len(xs)), np.asarray(xs, np.float64)]).T
+    (t0, slope), *_ = np.linalg.lstsq(A, np.asarray(ys, np.float64), rcond=None)
+    return float(t0), float(1.0 / slope / 1e3)  # bytes / us -> GB/s: 1e-3
+
+
+def gemv_sweep(dev, stream):
+    """The M = 1 int8 GEMV (bq_gemm_i8, gemv_i8_kernel) and a plain streaming read of the
+    same bytes (bqp_stream_read, the best of 1/2/4/8 loads a lane) over weights of 16 to
+    256 MiB (K = 4096, N = 4096 ... 65536), each timed over rotated copies that together
+    exceed the 256 MB Infinity Cache (cache-cold). A line t = t0 + bytes / BW fitted to each
+    separates the fixed cost of a launch (ramp-up, drain) from the steady streaming rate."""
+    import ctypes
+    import torch
+    from borch_amd import int8 as I
+    lib = ctypes.CDLL(str(ROOT / "bench_probe" / "libbqprobe.so"))
+    lib.bqp_stream_read.restype = ctypes.c_int
+    lib.bqp_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    K = 4096
+    rows = []
+    rng = np.random.default_rng(1)
+    x = torch.from_numpy(rng.normal(size=(1, K)).astype(np.float32)).to(dev)
+    qa, sa = I.quantize_rows(x)
+    for N in (4096, 8192, 16384, 32768, 65536):
+        nbytes = N * K
+        copies = max(3, -(-(768 << 20) // nbytes))
+        base = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev)
+        ws = [base.clone() for _ in range(copies)]
+        del base
+        sw = torch.rand(N, device=dev) * 1e-3
+        b = torch.zeros(N, device=dev)
+        g = capture(lambda i: I.gemm_i8(qa, ws[i], sa, sw, b), copies)
+        t_g = time_graph(g, copies, 6, stream) * 1e3
+        del g
+        rsink = torch.empty(nbytes // 4096 + 1, dtype=torch.int32, device=dev)
+        t_r = float("inf")
+        for ch in (1, 2, 4, 8):
+            g = capture(lambda i: lib.bqp_stream_read(ws[i].data_ptr(), nbytes, ch, rsink.data_ptr(),
+                                                      torch.cuda.current_stream().cuda_stream), copies)
+            t_r = min(t_r, time_graph(g, copies, 6, stream) * 1e3)
+            del g
+        gbytes = WL_gemm_bytes(1, N, K)
+        rows.append({"N": N, "weight_MiB": nbytes >> 20, "gemv_us": round(t_g, 3), "read_us": round(t_r, 3),
+                     "gemv_GBps": round(gbytes / (t_g * 1e-6) / 1e9, 1),
+                     "read_GBps": round(nbytes / (t_r * 1e-6) / 1e9, 1)})
+        log(f"GEMV sweep: {rows[-1]}")
+        del ws, rsink
+        torch.cuda.empty_cache()
+    g0, gbw = _fit_line([WL_gemm_bytes(1, r["N"], K) for r in rows], [r["gemv_us"] for r in rows])
+    r0, rbw = _fit_line([r["N"] * K for r in rows], [r["read_us"] for r in rows])
+    return {"rows": rows,
+            "gemv_fit": {"t0_us": round(g0, 3), "steady_GBps": round(gbw, 1),
+                         "steady_hbm_frac": round(gbw / PEAK_HBM_GBS, 4)},
+            "read_fit": {"t0_us": round(r0, 3), "steady_GBps": round(rbw, 1),
+                         "steady_hbm_frac": round(rbw / PEAK_HBM_GBS, 4)},
+            "method": "t = t0 + bytes / BW, least squares over 16-256 MiB weights (K = 4096), cache-cold rotations"}
+
+
+def WL_gemm_bytes(M, N, K):
+    from borch_amd import workloads as WL
+    return WL.gemm_bytes(M, N, K)
+
+
+def stream_rows(dev, stream, D=4096, NB=12, slots=3):
+    """stream_sequential(int8=True) (borch_amd.streaming; stream.ts:36-68): NB blocks of a
+    D x D Linear + ReLU (16 MiB of int8 each at D = 4096, C2's weight), packed once on the
+    host into pinned memory, streamed through a window of ``slots`` blocks with block k+1's
+    copy on the window's copy stream under block k's kernel; M = 1 and 16 rows. Beside it:
+    the same pass with no prefetch (copy, then compute), the plain pinned host-to-device
+    copy of one block's bytes (the link's rate on the day), the W8A32 kernel alone on a
+    resident block, and the host packing of one block."""
+    import torch
+    from borch_amd import int8 as I
+    from borch_amd import streaming as S
+    from borch_amd.nn import functional as F
+    rng = np.random.default_rng(9)
+    Ws = [(rng.normal(size=(D, D)) / np.sqrt(D)).astype(np.float32) for _ in range(NB)]
+    t0 = time.perf_counter()
+    packed = [S.pack_int8_host(w) for w in Ws]
+    pack_ms = (time.perf_counter() - t0) * 1e3 / NB
+    bias = [torch.from_numpy((rng.normal(size=D) * 0.1).astype(np.float32)).to(dev) for _ in range(NB)]
+
+    def make(b):
+        return lambda h, ws: torch.relu(F.linear(h, ws[0], b))
+    blocks = [S.StreamBlock([p], [(D, D)], make(b)) for p, b in zip(packed, bias)]
+    win = S.window(slots * D * D, dev)
+    out = {"blocks": NB, "block_MiB": D * D >> 20, "window_blocks": slots, "host_pack_ms_per_block": round(pack_ms, 2)}
+    # the link: one block's pinned bytes to the device on a side stream
+    dst = torch.empty(D * D, dtype=torch.uint8, device=dev)
+    side = torch.cuda.Stream(device=dev)
+    src = packed[0].q.reshape(-1).view(torch.uint8)
+    with torch.cuda.stream(side):
+        dst.copy_(src, non_blocking=True)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(side)
+        for _ in range(8):
+            dst.copy_(src, non_blocking=True)
+        e1.record(side)
+    torch.cuda.synchronize()
+    copy_ms = e0.elapsed_time(e1) / 8
+    out["h2d_copy_GBps"] = round(D * D / (copy_ms * 1e-3) / 1e9, 2)
+    for M in (1, 16):
+        x0 = torch.from_numpy(rng.normal(size=(M, D)).astype(np.float32)).to(dev)
+        w8 = I.Int8Weight(torch.empty((D, D), dtype=torch.int8, device=dev).copy_(packed[0].q), packed[0].s.to(dev),
+                          D, D, True)
+        g = capture(lambda i: I.linear_w8a32(x0, w8, bias[0]), 10)
+        gemv_us = time_graph(g, 10, 6, stream) * 1e3
+        del g
+        res = {}
+        for prefetch in (True, False):
+            S.stream_sequential(win, x0, blocks, int8=True, prefetch=prefetch)
+            best = float("inf")
+            for _ in range(3):
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                S.stream_sequential(win, x0, blocks, int8=True, prefetch=prefetch)
+                torch.cuda.synchronize()
+                best = min(best, time.perf_counter() - t0)
+            res[prefetch] = best * 1e3
+        out[f"M{M}"] = {"pass_ms": round(res[True], 3), "pass_ms_no_prefetch": round(res[False], 3),
+                        "ms_per_block": round(res[True] / NB, 4),
+                        "h2d_GBps": round(NB * D * D / (res[True] * 1e-3) / 1e9, 2),
+                        "frac_of_copy_rate": round(NB * D * D / (res[True] * 1e-3) / 1e9 / out["h2d_copy_GBps"], 4),
+                        "w8a32_kernel_us_resident": round(gemv_us, 3)}
+        log(f"stream_sequential int8 M={M}: {out[f'M{M}']}")
+    out["window_used_MiB"] = round(win.used / 2**20, 2)
+    out["method"] = ("host wall clock around one stream_sequential call between synchronizations, best of 3; "
+                     "h2d_GBps = the blocks' int8 bytes / that time")
+    win.free()
+    return out
+
+
 # EfficientNet-B0 b64 depthwise layers (channels, input size, kernel, stride) timed alone
 B0_DW = [(96, 112, 3, 2), (144, 56, 3, 1), (144, 56, 5, 2), (240, 28, 5, 1), (672, 14, 5, 1), (1152, 7, 5, 1)]
 
@@ -247,16 +380,37 @@ def hbm_kernels(dev):
     print(json.dumps({"hbm_kernels": ran, "copy_launches": 5, "copy_bytes": 64 << 20}))
 
 
+def _resnet18_params():
+    """The folded C3 ResNet-18's f32 parameters by name, for the CPU legs."""
+    from borch_amd import nets
+    model = nets.build("resnet18", seed=0, device="cpu")
+
+    def cp(conv):
+        s, p = conv._geometry()
+        return (conv.weight.detach().numpy(), conv.bias.detach().numpy(), s, p)
+    params = {"stem": cp(model.stem_f.conv), "fc": (model.fc.weight.detach().numpy(), model.fc.bias.detach().numpy())}
+    for i, blk in enumerate(model.body):
+        params[f"body.{i}.c1"] = cp(blk.c1.conv)
+        params[f"body.{i}.c2"] = cp(blk.c2.conv)
+        if blk.down is not None:
+            params[f"body.{i}.down"] = cp(blk.down)
+    return params
+
+
 def cpu_baseline(M_sample=512):
-    """The reference's CPU path on the host cores, on a bounded sample of the same workload.
+    """The reference's CPU paths on the host cores, on a bounded sample of the same workload.
 
     ``value``: borch_cpu's f32 ``gemm_bias_act`` (4x16 register-blocked, row-sliced over
     threads; restated in C from borch-ts/wasm/src/lib.rs:508-584 in oracle/cpu_ref.c) on
     M_sample rows of the 4096^3 Linear, min of 3 — "kind": "port" (the Rust/wasm original
-    cannot be built or run here). Beside it: the numpy int8 oracle on 256 rows, and one
-    ResNet-18 CIFAR b16 f32 forward through the same C kernels (im2col_rows +
-    gemm_bias_act per conv, as the reference CPU runner does)."""
+    cannot be built or run here). Beside it: the numpy core's own f32 arithmetic on the same
+    sample (``x @ W.T + b`` through numpy's BLAS, borch/_nn.py:413-415, with the BLAS library
+    and its thread count from threadpoolctl) and its im2col + GEMM ResNet-18 b16 forward
+    (borch/_ops.py:671-791; oracle/numpy_core.py); the numpy int8 oracle on 256 rows; one
+    ResNet-18 CIFAR b16 f32 forward through the C kernels (im2col_rows + gemm_bias_act per
+    conv, as the reference CPU runner does)."""
     from oracle import cpu_ref as R
+    from oracle import numpy_core as NC
     from oracle import quant as O
     from borch_amd import workloads as WL
     nthreads = R.threads()
@@ -272,7 +426,25 @@ def cpu_baseline(M_sample=512):
     out = {"value": round(2 * M_sample * 4096 * 4096 / t / 1e12, 5), "unit": "TOPS", "cores": int(nthreads),
            "kind": "port",
            "sample": f"borch_cpu gemm_bias_act (f32, C restatement of lib.rs:508-584, {nthreads} threads) on "
-                     f"{M_sample}x4096x4096 rows of the 4096^3 workload, min of 3: {t * 1e3:.1f} ms"}
+                     f"{M_sample}x4096x4096 rows of the 4096^3 workload, min of 3: {t * 1e3:.1f} ms",
+           "host_cpu_count": os.cpu_count()}
+    # the numpy core: x @ W.T + b through numpy's BLAS, on the same rows
+    try:
+        from threadpoolctl import threadpool_info
+        blas = [{"api": i.get("internal_api"), "threads": i.get("num_threads"), "version": i.get("version")}
+                for i in threadpool_info() if i.get("user_api") == "blas"]
+    except Exception as e:  # pragma: no cover - reported, not fatal
+        blas = f"threadpoolctl failed: {e}"
+    NC.linear(a[:16], w, b)
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        NC.linear(a, w, b)
+        times.append(time.perf_counter() - t0)
+    tn = min(times)
+    out["numpy_core"] = {"linear_TOPS": round(2 * M_sample * 4096 * 4096 / tn / 1e12, 5),
+                         "linear_ms": round(tn * 1e3, 2), "blas": blas,
+                         "sample": f"x @ W.T + b (borch/_nn.py:413-415) in f32 numpy on {M_sample}x4096x4096, min of 3"}
     # int8 oracle (numpy: per-row quantize + float64-BLAS exact GEMM + f32 epilogue)
     a2, w2, b2 = WL.c2_gemm(256, 0)
     qw, sw = O.quantize_weight_per_channel(w2)
@@ -280,27 +452,18 @@ def cpu_baseline(M_sample=512):
     qa, sa = O.quantize_rows(a2)
     O.dequant(O.gemm_i8_i32(qa, qw), sa, sw, b2)
     out["int8_oracle_TOPS"] = round(2 * 256 * 4096 * 4096 / (time.perf_counter() - t0) / 1e12, 5)
-    # ResNet-18 CIFAR b16 f32 through the C kernels
+    # ResNet-18 CIFAR b16 f32: through the C kernels, and through the numpy core's im2col conv
     try:
-        import torch
-        from borch_amd import nets
-        model = nets.build("resnet18", seed=0, device="cpu")
-
-        def cp(conv):
-            s, p = conv._geometry()
-            return (conv.weight.detach().numpy(), conv.bias.detach().numpy(), s, p)
-        params = {"stem": cp(model.stem_f.conv),
-                  "fc": (model.fc.weight.detach().numpy(), model.fc.bias.detach().numpy())}
-        for i, blk in enumerate(model.body):
-            params[f"body.{i}.c1"] = cp(blk.c1.conv)
-            params[f"body.{i}.c2"] = cp(blk.c2.conv)
-            if blk.down is not None:
-                params[f"body.{i}.down"] = cp(blk.down)
+        params = _resnet18_params()
         x = WL.c3_input(16, 0)
         R.resnet18_forward(params, x[:2], nthreads)
         t0 = time.perf_counter()
         R.resnet18_forward(params, x, nthreads)
         out["resnet18_b16_f32_ms"] = round((time.perf_counter() - t0) * 1e3, 2)
+        NC.resnet18_forward(params, x[:2])
+        t0 = time.perf_counter()
+        NC.resnet18_forward(params, x)
+        out["numpy_core"]["resnet18_b16_f32_ms"] = round((time.perf_counter() - t0) * 1e3, 2)
     except Exception as e:  # pragma: no cover - reported, not fatal
         out["resnet18_b16_f32_ms"] = f"failed: {e}"
     return out
@@ -730,6 +893,8 @@ def main():
     log(f"W8A32 M=1: {sweep['W8A32_M1']}")
     del g_w, qws, w8v, w8s
     sweep["W8A32"] = w8a32_rows(dev, stream)
+    sweep["stream_int8"] = stream_rows(dev, stream)
+    sweep["gemv_size_sweep"] = gemv_sweep(dev, stream)
     # C1: the Linear 16x512x512 through nn.Linear (per-row quantize + GEMM), latency
     from borch_amd import nn as bnn
     x_c1, w_c1, b_c1 = WL.c1_linear(0)

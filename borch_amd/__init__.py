@@ -13,7 +13,7 @@ import types as _types
 
 import torch as _torch
 
-from . import int8, nn  # noqa: F401
+from . import int8, nn, streaming  # noqa: F401
 from .compiled import Compiled, compiled  # noqa: F401
 from .nn import calibrate_int8, clear_int8, int8_report, quantize_for_int8  # noqa: F401
 from .serialize import load_int8, save_int8  # noqa: F401

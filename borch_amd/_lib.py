@@ -25,6 +25,7 @@ BQ_ERR_UNSUPPORTED = -4
 
 ACT_NONE, ACT_RELU, ACT_SILU, ACT_GELU = 0, 1, 2, 3
 SCALE_A_PER_TENSOR = 0x100  # OR-ed into bq_gemm_i8's act: one activation scale for the whole A
+ROUND_EXACT, ROUND_REFERENCE, ROUND_REFERENCE_CONV = 0, 1, 2  # bq_quantize_weight_host's rules
 
 _c_i64 = ctypes.c_int64
 _c_p = ctypes.c_void_p
@@ -50,6 +51,7 @@ SIGNATURES = {
     "bq_layernorm_quantize_rows": (_c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_p, ctypes.c_float, _c_p, _c_p, _c_p,
                                             _c_p]),
     "bq_quantize_weight_per_channel": (_c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_p]),
+    "bq_quantize_weight_host": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_p, _c_int]),
     "bq_quantize_tensor_ws_bytes": (_c_size, [_c_i64]),
     "bq_quantize_tensor": (_c_int, [_c_p, _c_i64, _c_p, _c_p, _c_p, _c_size, _c_p]),
     "bq_quantize_nhwc": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_size, _c_p]),

@@ -402,10 +402,11 @@ struct TileLds {
   float wmax[WAVES];   // per-wave max |y| (p.amax)
 };
 
-// One workgroup of the tiled GEMM / implicit-GEMM conv: workgroup `bid` of the `nbid` that
-// cover problem p (its tiles times its K split).
+// One workgroup of the tiled GEMM / implicit-GEMM conv: the workgroup of XCD-regrouped id
+// L (xcd_order over the whole launch) among those that cover problem p (its tiles times its
+// K split).
 template <int BM, int BN, int WAVES_M, int WAVES_N, bool CONV, int NBUF, int FD, bool MF16>
-__device__ __forceinline__ void gemm_tile(const GemmP& p, int bid, int nbid,
+__device__ __forceinline__ void gemm_tile(const GemmP& p, const int L,
                                           TileLds<BM, BN, WAVES_M * WAVES_N, NBUF>& sh) {
   constexpr int T = WAVES_M * WAVES_N * 64;
   constexpr int WTM = BM / WAVES_M;  // wave tile rows
@@ -431,7 +432,6 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, int bid, int nbid,
   const int KT = (p.K + BK - 1) / BK;
   constexpr bool CAN_SPLIT = BM * BN <= SPLIT_MAX_TILE;
   const int S = CAN_SPLIT ? p.ksplit : 1;
-  const int L = xcd_order(bid, nbid);
   const int split = L % S;
   int bm, bn;
   tile_of(L / S, tiles_m, tiles_n, bm, bn);
@@ -760,7 +760,7 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, int bid, int nbid,
 template <int BM, int BN, int WAVES_M, int WAVES_N, bool CONV, int NBUF, int FD, bool MF16 = false>
 __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_kernel(const GemmP p) {
   __shared__ TileLds<BM, BN, WAVES_M * WAVES_N, NBUF> sh;
-  gemm_tile<BM, BN, WAVES_M, WAVES_N, CONV, NBUF, FD, MF16>(p, blockIdx.x, gridDim.x, sh);
+  gemm_tile<BM, BN, WAVES_M, WAVES_N, CONV, NBUF, FD, MF16>(p, xcd_order(blockIdx.x, gridDim.x), sh);
 }
 
 // Two problems of one tile configuration in one launch: workgroups [0, g0) run p0, the
@@ -771,10 +771,13 @@ template <int BM, int BN, int WAVES_M, int WAVES_N, bool CONV, int NBUF, int FD>
 __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_i8_pair_kernel(const GemmP p0, const GemmP p1,
                                                                            int g0) {
   __shared__ TileLds<BM, BN, WAVES_M * WAVES_N, NBUF> sh;
-  if ((int)blockIdx.x < g0)
-    gemm_tile<BM, BN, WAVES_M, WAVES_N, CONV, NBUF, FD, false>(p0, blockIdx.x, g0, sh);
+  // regrouped once over the whole grid (the hardware puts workgroup i on XCD i % 8), so
+  // both convs' consecutive ids stay on one XCD whatever g0 is
+  const int L = xcd_order(blockIdx.x, gridDim.x);
+  if (L < g0)
+    gemm_tile<BM, BN, WAVES_M, WAVES_N, CONV, NBUF, FD, false>(p0, L, sh);
   else
-    gemm_tile<BM, BN, WAVES_M, WAVES_N, CONV, NBUF, FD, false>(p1, blockIdx.x - g0, gridDim.x - g0, sh);
+    gemm_tile<BM, BN, WAVES_M, WAVES_N, CONV, NBUF, FD, false>(p1, L - g0, sh);
 }
 
 // ----------------------------------------------------------------------------- skinny
@@ -1643,29 +1646,30 @@ constexpr int SCRATCH_MAX_DEVICES = 64;
 static std::mutex g_scratch_mu;
 static void* g_scratch_ptr[SCRATCH_MAX_DEVICES];  // per device ordinal; null until set up
 
-__global__ void zero_words_kernel(uint32_t* __restrict__ p, int n) {
-  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
-}
-
-// The current device's scratch address, set up on its first call: the symbol's address
-// looked up once, with that device current, and the tile counters (the part that must
-// start at zero; every launch leaves them zero again) cleared by a kernel on `st`.
+// The scratch address of the device `st` belongs to (not the calling thread's current
+// device), set up on that device's first call: the symbol's address looked up once, with
+// that device current. A static __device__ array is zero when the code object is loaded,
+// so the tile counters (the part that must start at zero) need no clearing launch, and
+// every split launch leaves them zero again.
 static int noalloc_scratch(const char* what, hipStream_t st, void** out) {
   int dev = -1;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return set_error(BQ_ERR_DEVICE, "%s: hipGetDevice: %s", what, hipGetErrorString(e));
+  hipError_t e = hipStreamGetDevice(st, &dev);
+  if (e != hipSuccess) return set_error(BQ_ERR_DEVICE, "%s: hipStreamGetDevice: %s", what, hipGetErrorString(e));
   if (dev < 0 || dev >= SCRATCH_MAX_DEVICES)
     return set_error(BQ_ERR_DEVICE, "%s: device %d beyond the %d this library keeps scratch for", what, dev,
                      SCRATCH_MAX_DEVICES);
   std::lock_guard<std::mutex> lk(g_scratch_mu);
   if (!g_scratch_ptr[dev]) {
+    int cur = -1;
+    e = hipGetDevice(&cur);
+    if (e != hipSuccess) return set_error(BQ_ERR_DEVICE, "%s: hipGetDevice: %s", what, hipGetErrorString(e));
+    if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess)
+      return set_error(BQ_ERR_DEVICE, "%s: hipSetDevice(%d): %s", what, dev, hipGetErrorString(e));
     void* ptr = nullptr;
     e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (cur != dev) (void)hipSetDevice(cur);  // restoring what was current a moment ago
     if (e != hipSuccess || !ptr)
       return set_error(BQ_ERR_DEVICE, "%s: hipGetSymbolAddress(scratch): %s", what, hipGetErrorString(e));
-    zero_words_kernel<<<1, 256, 0, st>>>(static_cast<uint32_t*>(ptr), (int)(SPLIT_CNT_BYTES / 4));
-    const int rc = check_launch(what);
-    if (rc != BQ_OK) return rc;
     g_scratch_ptr[dev] = ptr;
   }
   *out = g_scratch_ptr[dev];

@@ -28,9 +28,25 @@ import torch
 import torch.nn as tnn
 
 from . import int8 as I8
+from ._lib import Int8Unavailable, require_device
 from . import nn
 from .nn import intrinsic as I
 from .nn.utils.fusion import fuse_conv_bn_eval
+
+
+def _hip_f32_ok(t: torch.Tensor, *params) -> bool:
+    """Whether the f32 side kernels (attention, the pooled head) take ``t``: float32 on a
+    gfx950 device with the library built, and nothing for autograd to record (the raw-pointer
+    kernels keep no graph, so a forward that needs gradients stays on torch's ops)."""
+    if not (t.is_cuda and t.dtype == torch.float32):
+        return False
+    if torch.is_grad_enabled() and (t.requires_grad or any(p is not None and p.requires_grad for p in params)):
+        return False
+    try:
+        require_device(t.device)
+    except Int8Unavailable:
+        return False
+    return True
 
 
 def _bn_stats(bn: tnn.BatchNorm2d, g: torch.Generator) -> None:
@@ -91,7 +107,7 @@ class Block(tnn.Module):
         if self.c1 is not None:
             if self.down is None:
                 return self.c2(self.c1(x), x)
-            h, side = nn.pair_forward(self.c1.conv, self.down, x)  # one launch for both when int8
+            h, side = nn.pair_forward(self.c1, self.down, x)  # one launch for both when int8
             return self.c2(h, side)
         out = torch.relu(self.bn1(self.conv1(x)))
         out = self.bn2(self.conv2(out))
@@ -132,8 +148,8 @@ class ResNet18(tnn.Module):
     def forward(self, x):
         h = self.features(x)
         fc = self.fc
-        if (h.is_cuda and h.dtype == torch.float32 and getattr(fc, "int8", None) is None
-                and fc.weight.shape[0] * fc.weight.shape[1] <= 65536):
+        if (getattr(fc, "int8", None) is None and fc.weight.shape[0] * fc.weight.shape[1] <= 65536
+                and _hip_f32_ok(h, fc.weight, fc.bias)):
             return I8.avgpool_linear(h, fc.weight, fc.bias)  # the f32 head in one launch
         return fc(h.mean(dim=(2, 3)))
 
@@ -289,7 +305,7 @@ class EncoderLayer(tnn.Module):
         B, T, D3 = qkv.shape
         D = D3 // 3
         H, dh = self.heads, D // self.heads
-        if qkv.is_cuda and dh == 64 and T <= 256 and qkv.dtype == torch.float32:
+        if dh == 64 and T <= 256 and _hip_f32_ok(qkv):
             return I8.attention_f32(qkv, H)
         qkv = qkv.reshape(B, T, 3, H, dh).permute(2, 0, 3, 1, 4)
         o = torch.nn.functional.scaled_dot_product_attention(qkv[0], qkv[1], qkv[2])

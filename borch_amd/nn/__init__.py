@@ -323,21 +323,25 @@ class pairing:
         return False
 
 
-def pair_forward(first: Conv2d, second: Conv2d, x):
-    """``(first(x), second(x))`` with no residual: a residual block's first conv and its
-    downsampling shortcut, which read the same input. When both are int8 convs (not depthwise,
-    neither a 1x1 stride-1 unpadded conv) on the same input scale, the input is quantized once
-    and both run in one launch (``conv2d_pair_i8_nhwc``), with the results the two calls give.
-    The first output keeps what its own call leaves for its consumer (the int8 twin, or the
-    per-tile maxima); the shortcut's f32 output is written alone, and a consumer quantizing it
-    gets the bytes its twin would have held."""
+def pair_forward(first_mod, second_mod, x):
+    """``(first_mod(x), second_mod(x))`` with no residual: a residual block's first conv and
+    its downsampling shortcut, which read the same input (each a ``Conv2d`` or a fused module
+    wrapping one, such as ``ConvReLU2d``). Inside ``pairing``, when both are int8 convs (not
+    depthwise, neither a 1x1 stride-1 unpadded conv) on the same input scale, the input is
+    quantized once and both run in one launch (``conv2d_pair_i8_nhwc``), with the results the
+    two calls give. The first output keeps what its own call leaves for its consumer (the int8
+    twin, or the per-tile maxima); the shortcut's f32 output is written alone, and a consumer
+    quantizing it gets the bytes its twin would have held. Otherwise the two modules are
+    called, so hooks on them (and on the convs they wrap) see both layers."""
+    first = getattr(first_mod, "conv", first_mod)
+    second = getattr(second_mod, "conv", second_mod)
     ok = (_PAIRING and not _CALIBRATING and x.dim() == 4 and isinstance(first, Conv2d) and isinstance(second, Conv2d)
           and isinstance(first.int8, _i8.Int8ConvWeight) and isinstance(second.int8, _i8.Int8ConvWeight)
           and x.shape[1] == first.in_channels == second.in_channels and first.int8.cpad == second.int8.cpad
           and first.in_scale_v == second.in_scale_v
           and not _dense_1x1(first) and not _dense_1x1(second))
     if not ok:
-        return first(x), second(x)
+        return first_mod(x), second_mod(x)
     qx, sa = first._int8_input(x)
     s1, p1 = first._geometry()
     s2, p2 = second._geometry()

@@ -12,6 +12,7 @@ import torch
 import torch.nn.functional as _tF
 
 from .. import int8 as _i8
+from .. import streaming as _stream
 
 
 def _f32_linear(x, w, b=None):
@@ -32,9 +33,13 @@ def _f32_conv2d(x, w, b=None, stride=1, padding=0, dilation=1, groups=1, padding
 
 
 def linear(input, weight, bias=None):  # noqa: A002
-    """``input @ weight.T + bias``; an ``Int8Weight`` runs the W8A8 kernels."""
+    """``input @ weight.T + bias``; an ``Int8Weight`` runs the W8A8 kernels (or the W8A32
+    one when packed weight-only), a windowed int8 weight (``streaming.in_window_int8``) the
+    W8A32 kernel on its window slot."""
     if isinstance(weight, _i8.Int8Weight):
         return _i8.linear(input, weight, bias)
+    if isinstance(weight, _stream.WindowedWeight):
+        return _stream._linear(input, weight, bias)
     return _f32_linear(input, weight, bias)
 
 

@@ -95,6 +95,26 @@ int bq_layernorm_quantize_rows(const float* x, int64_t M, int64_t K, const float
 int bq_quantize_weight_per_channel(const float* w, int64_t N, int64_t K, int8_t* q,
                                    float* s, bq_stream_t stream);
 
+/* Rounding rules of bq_quantize_weight_host. */
+#define BQ_ROUND_EXACT 0          /* this library's rule: the bytes of bq_quantize_weight_per_channel */
+#define BQ_ROUND_REFERENCE 1      /* quant.ts:35-41 (Linear): double scale, w * (1/scale), Math.round */
+#define BQ_ROUND_REFERENCE_CONV 2 /* quant.ts:88-96 (conv): f32 scale, w / scale in double, Math.round */
+
+/* Per-output-channel weight quantization on the HOST (every pointer is host memory):
+ * w f32 [N, K] row-major -> q int8 [N, Kpad] (columns K..Kpad-1 zero), s f32 [N], with
+ * `rule` one of BQ_ROUND_*. BQ_ROUND_EXACT gives the bytes and scales of
+ * bq_quantize_weight_per_channel; BQ_ROUND_REFERENCE the bytes of borch-ts's Linear packer
+ * (scale = peak / 127 in double, stored as f32; q = Math.round(w * (1 / scale)), a tie
+ * toward +inf; it differs from the exact rule on some near-ties as well as ties);
+ * BQ_ROUND_REFERENCE_CONV those of its conv packer (f32 scale, Math.round(w / scale): it
+ * differs from the exact rule on exact ties only). Rows are split over `nthreads` host
+ * threads (<= 0: all hardware threads). Replaces quantizeInt8PerChannel
+ * (borch-ts/src/quant.ts:23-53), which Tensor.inWindowInt8 runs on the host before the
+ * upload (tensor.ts:1681-1705), and the scale and rounding of
+ * quantizeConvWeightInt8TapMajor (quant.ts:80-96). */
+int bq_quantize_weight_host(const float* w, int64_t N, int64_t K, int64_t Kpad, int rule, int8_t* q, float* s,
+                            int nthreads);
+
 /* Bytes of `ws` that bq_quantize_tensor / bq_quantize_nhwc need for n elements. */
 size_t bq_quantize_tensor_ws_bytes(int64_t n);
 
@@ -193,10 +213,12 @@ int bq_linear_i8(const float* x, const int8_t* W, int64_t M, int64_t N, int64_t 
  * the library's own static device array of bq_gemm_ws_bytes() bytes (about 6.5 MiB), one
  * copy per GPU, held until the process ends. That size covers the K split the rule picks
  * for every shape, so no shape is refused for its size; every other limit is
- * bq_gemm_i8's. The first call on a device looks up that device's copy and enqueues one
- * small kernel on `stream` that zeroes its tile counters (every launch leaves them zero
- * again). All calls on one GPU share that GPU's copy: calls that overlap on one GPU (two
- * streams, or two threads) race and give wrong results. */
+ * bq_gemm_i8's. The copy used is that of the GPU `stream` belongs to; the first call on a
+ * GPU looks up its address (no launch: the array is zero when the library is loaded, and
+ * every launch leaves its tile counters zero again), so a caller that captures a graph
+ * makes one call on each GPU before the capture. All calls on one GPU share that GPU's
+ * copy: calls that overlap on one GPU (two streams, or two threads) race and give wrong
+ * results. */
 int bq_gemm_i8_noalloc(const int8_t* A, const int8_t* W, int64_t M, int64_t N, int64_t K, const float* sA,
                        const float* sW, const float* bias, const float* residual, int act, float* out,
                        int32_t* acc, bq_stream_t stream);

@@ -17,8 +17,18 @@ Rounding rule (one rule for weights and activations, fixed by the task contract)
   (borch/_ops.py:4559-4568, ``np.round`` of a float64 quotient);
 * ``s == 0`` (an all-zero row or tensor) gives ``q = 0`` (borch-ts/src/quant.ts:36).
 
-The reference's weight packer uses JS ``Math.round`` (half toward +inf,
-borch-ts/src/quant.ts:40,96); that differs from this rule only on exact ties.
+The reference's two weight packers are restated bit for bit below
+(``quantize_weight_reference_linear``, ``quantize_conv_weight_reference``), and they relate
+to this rule differently:
+
+* the conv packer (borch-ts/src/quant.ts:88-96) divides by the *stored* float32 scale and
+  rounds with JS ``Math.round`` (half toward +inf): it differs from this rule only on exact
+  ties;
+* the Linear packer (quant.ts:35-40) multiplies by ``1/scale`` with the *unrounded* float64
+  scale ``peak/127``. Its quotient ``w·(127/peak)`` differs from ``w/f32(peak/127)`` by up to
+  a few 1e-6, so near-ties (not only exact ties) can round to the other side: on C2's
+  4096×4096 weight 12 bytes differ and none is an exact tie; on C1's 512×512 none differ.
+  ``tests/test_oracle.py`` pins both counts and positions.
 
 Pinning (what checks each function; see tests/test_oracle.py):
 
@@ -92,6 +102,59 @@ def quantize_weight_per_channel(w):
     zeros (:36), byte order = W's own row-major order (:42-51). Returns
     ``(q int8 [N,K], s float32 [N])``."""
     return quantize_rows(w)
+
+
+def js_math_round(x):
+    """JavaScript ``Math.round`` on float64: the nearest integer, a tie going toward +inf
+    (ECMA-262 §21.3.2.28). ``x - floor(x)`` is exact for every double, so the comparison
+    with 0.5 decides ties exactly (``floor(x + 0.5)`` would not: 0.49999999999999994 + 0.5
+    rounds up to 1)."""
+    x = np.asarray(x, dtype=np.float64)
+    f = np.floor(x)
+    return f + ((x - f) >= 0.5)
+
+
+def quantize_weight_reference_linear(w):
+    """borch-ts/src/quant.ts:23-41 as JavaScript evaluates it, bit for bit.
+
+    Per row ``o`` of ``w [N, K]``: ``peak`` = the largest ``|w|`` (a float32 value, held as
+    a double); ``scale = peak / 127`` in float64 (:35), stored as float32 in the returned
+    scales (``Float32Array``, :36); a zero scale leaves the row zero (:37); otherwise
+    ``inv = 1 / scale`` in float64 (:38) and ``q = clamp(Math.round(w · inv), ±127)`` with the
+    product in float64 (:39-41). Returns ``(q int8 [N, K], s float32 [N])``."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    N = w.shape[0]
+    w2 = w.reshape(N, -1)
+    peak = (np.abs(w2).max(axis=1) if w2.shape[1] else np.zeros(N, np.float32)).astype(np.float64)
+    scale = peak / 127.0
+    with np.errstate(divide="ignore"):
+        inv = np.where(scale != 0, 1.0 / np.where(scale != 0, scale, 1.0), 0.0)
+    r = js_math_round(w2.astype(np.float64) * inv[:, None])
+    r = np.clip(r, -I8_MAX, I8_MAX)
+    r[scale == 0] = 0
+    return r.astype(np.int8).reshape(w.shape), scale.astype(np.float32)
+
+
+def quantize_conv_weight_reference(w):
+    """borch-ts/src/quant.ts:80-96's arithmetic, bit for bit, on a weight ``[O, ...]`` with
+    one scale per leading index (the layout change of :97-99 aside).
+
+    ``scales[o] = f32(peak / 127)`` (the float64 quotient stored in a ``Float32Array``,
+    :88, which equals the correctly rounded float32 quotient); each element
+    ``q = clamp(Math.round(w / scales[o]), ±127)`` with the division in float64 by the
+    stored float32 scale (:93-95); a zero scale gives 0 (:92). Returns
+    ``(q int8 [O, ...], s float32 [O])`` in the input's own order."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    O = w.shape[0]
+    w2 = w.reshape(O, -1)
+    peak = np.abs(w2).max(axis=1) if w2.shape[1] else np.zeros(O, np.float32)
+    s = (peak.astype(np.float64) / 127.0).astype(np.float32)
+    s64 = s.astype(np.float64)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        r = js_math_round(w2.astype(np.float64) / np.where(s64 != 0, s64, 1.0)[:, None])
+    r = np.clip(r, -I8_MAX, I8_MAX)
+    r[s == 0] = 0
+    return r.astype(np.int8).reshape(w.shape), s
 
 
 def pack_words(q):

@@ -81,3 +81,64 @@ def test_resnet18_forward_matches_torch_f32():
             params[f"body.{i}.down"] = cp(blk.down)
     got = R.resnet18_forward(params, x, nthreads=4)
     np.testing.assert_allclose(got, ref, rtol=1e-3, atol=1e-3)
+
+
+# --------------------------------------------- the numpy core's f32 forward (oracle/numpy_core.py)
+
+def test_numpy_core_im2col_brute_force():
+    """borch/_ops.py:671-689's row layout: row (n, oh, ow), column (c, kh, kw)."""
+    from oracle import numpy_core as NC
+    rng = np.random.default_rng(4)
+    x = rng.normal(size=(2, 3, 7, 6)).astype(np.float32)
+    for k, s in ((3, 1), (3, 2), (1, 2), (2, 3)):
+        cols, OH, OW = NC.im2col(x, k, k, s)
+        want = np.zeros((2 * OH * OW, 3 * k * k), np.float32)
+        for n_ in range(2):
+            for oh in range(OH):
+                for ow in range(OW):
+                    r = (n_ * OH + oh) * OW + ow
+                    for c in range(3):
+                        for i in range(k):
+                            for j in range(k):
+                                want[r, (c * k + i) * k + j] = x[n_, c, oh * s + i, ow * s + j]
+        assert np.array_equal(cols, want)
+
+
+def test_numpy_core_conv_and_linear_match_torch():
+    torch = pytest.importorskip("torch")
+    from oracle import numpy_core as NC
+    rng = np.random.default_rng(5)
+    for (C, O, k, s, p) in ((3, 8, 3, 1, 1), (16, 32, 3, 2, 1), (16, 8, 1, 2, 0), (4, 4, 5, 1, 2)):
+        x = rng.normal(size=(2, C, 9, 9)).astype(np.float32)
+        w = rng.normal(size=(O, C, k, k)).astype(np.float32)
+        b = rng.normal(size=O).astype(np.float32)
+        ref = torch.nn.functional.conv2d(torch.from_numpy(x), torch.from_numpy(w), torch.from_numpy(b), s, p).numpy()
+        np.testing.assert_allclose(NC.conv2d(x, w, b, s, p), ref, rtol=1e-4, atol=1e-4)
+    with pytest.raises(RuntimeError, match="channels do not match: input 3, filter 4"):
+        NC.conv2d(np.zeros((1, 3, 5, 5), np.float32), np.zeros((2, 4, 3, 3), np.float32))
+    x = rng.normal(size=(5, 33)).astype(np.float32)
+    w = rng.normal(size=(7, 33)).astype(np.float32)
+    b = rng.normal(size=7).astype(np.float32)
+    np.testing.assert_allclose(NC.linear(x, w, b), x.astype(np.float64) @ w.T.astype(np.float64) + b, rtol=1e-5,
+                               atol=1e-5)
+
+
+def test_numpy_core_resnet18_matches_torch_f32():
+    torch = pytest.importorskip("torch")
+    from borch_amd import nets, workloads as WL
+    from oracle import numpy_core as NC
+    model = nets.build("resnet18", seed=3, device="cpu")
+    x = WL.c3_input(2, 3)
+    with torch.no_grad():
+        ref = model(torch.from_numpy(x)).numpy()
+
+    def cp(conv):
+        s, p = conv._geometry()
+        return (conv.weight.detach().numpy(), conv.bias.detach().numpy(), s, p)
+    params = {"stem": cp(model.stem_f.conv), "fc": (model.fc.weight.detach().numpy(), model.fc.bias.detach().numpy())}
+    for i, blk in enumerate(model.body):
+        params[f"body.{i}.c1"] = cp(blk.c1.conv)
+        params[f"body.{i}.c2"] = cp(blk.c2.conv)
+        if blk.down is not None:
+            params[f"body.{i}.down"] = cp(blk.down)
+    np.testing.assert_allclose(NC.resnet18_forward(params, x), ref, rtol=1e-3, atol=1e-3)

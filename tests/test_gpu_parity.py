@@ -753,6 +753,46 @@ def test_every_conv_plan_gives_the_same_result(dev, no_plans, N, C, H, O_, k, st
         assert torch.equal(q, want_q), (cfg, split)
 
 
+@pytest.mark.parametrize("M,N,K", [(6304, 768, 768), (1000, 520, 784), (300, 200, 4112), (257, 2304, 768),
+                                   (4096, 4096, 512)])
+def test_regression_fast_path_stores_equal_general_path(dev, no_plans, M, N, K):
+    """Regression test for the 16-byte buffer-store hazard: on every tile configuration the
+    epilogue's fast path (no int32 output: buffer stores with the whole row offset in the
+    VGPR, written through) equals the general path (int32 output requested) bit for bit,
+    with bias and residual, dense and conv. With part of the row offset in the SGPR offset
+    those stores once wrote wrong values to about 1% of the rows, so a toolchain that
+    folds a uniform offset back into the SGPR fails here."""
+    T = no_plans
+    say(f"fast path vs general path M={M} N={N} K={K}")
+    rng = np.random.default_rng(M * 3 + N + K)
+    qa = t(rng.integers(-127, 128, size=(M, K)).astype(np.int8), dev)
+    qw = t(rng.integers(-127, 128, size=(N, K)).astype(np.int8), dev)
+    sa = t(rng.uniform(1e-4, 1e-3, M).astype(np.float32), dev)
+    sw = t(rng.uniform(1e-4, 1e-3, N).astype(np.float32), dev)
+    b = t(rng.normal(size=N).astype(np.float32), dev)
+    r = t(rng.normal(size=(M, N)).astype(np.float32), dev)
+    I.split_workspace(dev)
+    cands = T.candidates((M, N, K))
+    for cfg, split in cands:
+        T.set_plan((M, N, K), cfg, split)
+        fast = I.gemm_i8(qa, qw, sa, sw, b, I.ACT_RELU, residual=r)
+        general, _ = I.gemm_i8(qa, qw, sa, sw, b, I.ACT_RELU, want_acc=True, residual=r)
+        assert torch.equal(fast, general), (cfg, split, int((fast != general).any(1).sum()))
+    # and a conv: the implicit-GEMM loader's configurations, a ragged last row tile
+    T.clear_plans()
+    Nn, C, H, O_ = 3, 64, 19, 128
+    x = rng.normal(size=(Nn, C, H, H)).astype(np.float32)
+    w8 = I.pack_conv_weight(t((rng.normal(size=(O_, C, 3, 3)) * 0.05).astype(np.float32), dev))
+    qx, sx = I.quantize_nhwc(t(x, dev), w8.cpad)
+    rr = t(rng.normal(size=(Nn, O_, H, H)).astype(np.float32), dev)
+    problem = (Nn, H, H, w8.cpad, O_, 3, 3, 1, 1)
+    for cfg, split in T.candidates(problem):
+        T.set_plan(problem, cfg, split)
+        fast = I.conv2d_i8_nhwc(qx, sx, w8, 1, 1, b[:O_].contiguous(), rr, I.ACT_RELU)
+        general, _ = I.conv2d_i8_nhwc(qx, sx, w8, 1, 1, b[:O_].contiguous(), rr, I.ACT_RELU, want_acc=True)
+        assert torch.equal(fast, general), (cfg, split)
+
+
 @pytest.mark.parametrize("N,C,H,O_,stride", [(16, 64, 32, 128, 2), (16, 128, 16, 256, 2), (16, 256, 8, 512, 2),
                                              (3, 32, 9, 48, 2), (2, 16, 7, 16, 1)])
 @pytest.mark.parametrize("twin", [False, True])

@@ -488,3 +488,144 @@ def test_avgpool_linear_oracle_against_torch():
     ref = torch.nn.functional.linear(torch.from_numpy(x).mean(dim=(2, 3)), torch.from_numpy(w), torch.from_numpy(b))
     np.testing.assert_allclose(got, ref.numpy(), rtol=1e-12, atol=1e-12)
     assert np.all(scale >= np.abs(got - b) - 1e-12)
+
+
+# ------------------------------------------- the reference's two weight packers, restated
+
+def _js_round_scalar(x: float) -> float:
+    """ECMA-262 Math.round from its definition: the integer nearest x, a tie toward +inf
+    (decided in exact rationals, so independent of the oracle's floor-based form)."""
+    fx = Fraction(x)
+    lo = fx.numerator // fx.denominator  # floor
+    return float(lo + 1) if fx - lo >= Fraction(1, 2) else float(lo)
+
+
+def _ref_linear_row(row):
+    """quant.ts:31-41 element by element in Python floats (IEEE doubles, as JavaScript)."""
+    peak = 0.0
+    for v in row:
+        if abs(v) > peak:
+            peak = abs(v)
+    scale = peak / 127
+    if scale == 0:
+        return [0] * len(row), f32(scale)
+    inv = 1 / scale
+    return [int(max(-127.0, min(127.0, _js_round_scalar(v * inv)))) for v in row], f32(scale)
+
+
+def _ref_conv_row(row):
+    """quant.ts:86-96 element by element: the f32-stored scale, then Math.round(w / scale)."""
+    peak = 0.0
+    for v in row:
+        if abs(v) > peak:
+            peak = abs(v)
+    scale = f32(peak / 127)
+    if scale == 0:
+        return [0] * len(row), scale
+    return [int(max(-127.0, min(127.0, _js_round_scalar(v / scale)))) for v in row], scale
+
+
+def test_js_math_round_known_answers():
+    xs = [2.5, -2.5, 0.5, -0.5, 1.5, -1.5, 0.49999999999999994, -0.49999999999999994, 126.5, -126.5,
+          1.4999999999999998, 3.0, -3.0]
+    want = [3, -2, 1, 0, 2, -1, 0, 0, 127, -126, 1, 3, -3]
+    assert O.js_math_round(np.array(xs)).tolist() == want
+    assert [_js_round_scalar(x) for x in xs] == want
+
+
+def _planted_rows(rng):
+    rows = [rng.normal(size=64).astype(np.float32) * np.float32(0.05) for _ in range(6)]
+    # exact ties of the stored f32 scale: peak 127 * 2^-6 gives s = 2^-6 exactly
+    s = 2.0 ** -6
+    tie = np.array([127 * s] + [(k + 0.5) * s for k in range(-126, 126, 7)], np.float32)
+    rows.append(tie)
+    rows.append(-tie)
+    rows.append(np.zeros(40, np.float32))
+    return rows
+
+
+def test_reference_linear_packer_restates_quant_ts_35_41():
+    rng = np.random.default_rng(11)
+    for row in _planted_rows(rng):
+        q, s = O.quantize_weight_reference_linear(row[None, :])
+        q_s, s_s = _ref_linear_row([float(v) for v in row])
+        assert q[0].tolist() == q_s and f32(float(s[0])) == s_s
+
+
+def test_reference_conv_packer_restates_quant_ts_86_96():
+    rng = np.random.default_rng(12)
+    for row in _planted_rows(rng):
+        q, s = O.quantize_conv_weight_reference(row[None, :])
+        q_s, s_s = _ref_conv_row([float(v) for v in row])
+        assert q[0].tolist() == q_s and float(s[0]) == s_s
+    # the conv packer's scale is the build rule's (the f64 quotient stored in f32 equals
+    # the correctly rounded f32 quotient)
+    w = rng.normal(size=(300, 50)).astype(np.float32)
+    assert np.array_equal(O.quantize_conv_weight_reference(w)[1], O.quantize_weight_per_channel(w)[1])
+
+
+def _diff_positions(w):
+    q0, s0 = O.quantize_weight_per_channel(w)
+    q1, s1 = O.quantize_weight_reference_linear(w)
+    q2, s2 = O.quantize_conv_weight_reference(w)
+    assert np.array_equal(s0, s1) and np.array_equal(s0, s2)
+    lin = [tuple(int(i) for i in p) for p in np.argwhere(q0 != q1)]
+    conv = [tuple(int(i) for i in p) for p in np.argwhere(q0 != q2)]
+
+    def tie(p):
+        return (Fraction(float(w[p])) / Fraction(float(s0[p[0]]))).denominator == 2
+    # the conv packer differs from the build rule exactly on ties of the exact quotient
+    assert all(tie(p) for p in conv)
+    return lin, [tie(p) for p in lin], conv, q0, q1
+
+
+# C2's 4096 x 4096 weight (seed 0): the 12 bytes where quant.ts:35-41 and the build rule
+# disagree, with the build's and the reference's byte. None is an exact tie: each exact
+# quotient is within 1.1e-6 of k + 1/2, and the reference's double scale puts w·(1/scale)
+# on the other side.
+C2_LINEAR_DIFFS = [((147, 1391), -21, -22), ((490, 674), 21, 22), ((725, 1224), 57, 56), ((742, 1293), 47, 46),
+                   ((805, 3780), 11, 10), ((1842, 3269), 55, 54), ((2067, 2755), 29, 28), ((2319, 1316), -16, -17),
+                   ((2495, 3654), 45, 46), ((2515, 693), -15, -14), ((3207, 3640), -24, -23),
+                   ((3682, 3921), -14, -15)]
+
+
+def test_reference_linear_packer_against_build_rule_c1_c2():
+    from borch_amd import workloads as WL
+    _, w1, _ = WL.c1_linear(0)
+    lin, ties, conv, _, _ = _diff_positions(w1)
+    assert lin == [] and conv == []
+    _, w2, _ = WL.c2_gemm(1, 0)
+    lin, ties, conv, q0, q1 = _diff_positions(w2)
+    assert conv == []
+    assert [(p, int(q0[p]), int(q1[p])) for p in lin] == C2_LINEAR_DIFFS
+    assert not any(ties)
+    for p, _, _ in C2_LINEAR_DIFFS:  # near-ties: the exact quotient is within 1.1e-6 of k + 1/2
+        qq = Fraction(float(w2[p])) / Fraction(float(O.scale_of(np.abs(w2[p[0]]).max())))
+        frac = qq - (qq.numerator // qq.denominator)  # qq - floor(qq), in [0, 1)
+        assert 0 < abs(frac - Fraction(1, 2)) < Fraction(11, 10**7)
+    # the rows holding them, element by element in Python floats (JavaScript's arithmetic)
+    for r in sorted({p[0] for p, _, _ in C2_LINEAR_DIFFS}):
+        assert q1[r].tolist() == _ref_linear_row([float(v) for v in w2[r]])[0]
+
+
+C5_DIFF_DIGEST = "83d7fa44705a776e"  # sha256 of the repr of the 150 (layer, name, n, k) positions
+
+
+def test_reference_linear_packer_against_build_rule_c5():
+    """C5's 48 Linear weights (ViT-B/16, seed 0): 150 bytes differ, one of them on an exact
+    tie of the build rule's quotient; the conv packer's rule differs on exact ties only."""
+    import hashlib
+    from borch_amd import nets
+    model = nets.build("vit_b16", seed=0, device="cpu")
+    allpos, nties, per_kind = [], 0, {}
+    for li, layer in enumerate(model.layers):
+        for name in ("qkv", "proj", "fc1", "fc2"):
+            w = getattr(layer, name).weight.detach().numpy()
+            lin, ties, _, _, _ = _diff_positions(w)
+            nties += sum(ties)
+            per_kind[name] = per_kind.get(name, 0) + len(lin)
+            allpos += [(li, name, *p) for p in lin]
+    assert len(allpos) == 150 and nties == 1
+    assert per_kind == {"qkv": 40, "proj": 15, "fc1": 45, "fc2": 50}
+    digest = hashlib.sha256(repr(allpos).encode()).hexdigest()[:16]
+    assert digest == C5_DIFF_DIGEST

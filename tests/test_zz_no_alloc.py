@@ -3,7 +3,10 @@ device memory, for callers that cannot allocate — against bq_gemm_i8 with a ca
 workspace, through the C ABI: outputs and int32 accumulators bit for bit, and the
 accumulators against the oracle's exact integer GEMM. Two split-K calls in a row (the
 second smaller, so it reuses the scratch the first left behind), then a GEMV-sized one
-that needs no scratch, then the first shape again."""
+that needs no scratch, then the first shape again. Every K split the library offers for a
+split-K shape is forced in turn (bq_plan_set), so the static scratch is what the split
+workgroups exchange their partials through; and the calls replayed from a captured HIP
+graph give the same bits on every replay."""
 import sys
 
 import numpy as np
@@ -62,6 +65,79 @@ def test_noalloc_matches_workspace_entry(dev, M, N, K, act):
                                act, out3.data_ptr(), None, ws.data_ptr(), ws.numel(), stream))
     torch.cuda.synchronize()
     assert torch.equal(out2, out3)
+
+
+@pytest.fixture
+def no_plans():
+    from borch_amd import tune as T
+    T.clear_plans()
+    yield T
+    T.clear_plans()
+
+
+def _both(dev, qa, qw, sa, sw, b, r, M, N, K, act, stream):
+    out0 = torch.empty((M, N), dtype=torch.float32, device=dev)
+    acc0 = torch.empty((M, N), dtype=torch.int32, device=dev)
+    ws = I.split_workspace(dev)
+    L.check(L.lib().bq_gemm_i8(qa.data_ptr(), qw.data_ptr(), M, N, K, sa.data_ptr(), sw.data_ptr(), b.data_ptr(),
+                               r.data_ptr(), act, out0.data_ptr(), acc0.data_ptr(), ws.data_ptr(), ws.numel(),
+                               stream))
+    out1 = torch.full((M, N), float("nan"), dtype=torch.float32, device=dev)
+    acc1 = torch.full((M, N), -1, dtype=torch.int32, device=dev)
+    L.check(_fn()(qa.data_ptr(), qw.data_ptr(), M, N, K, sa.data_ptr(), sw.data_ptr(), b.data_ptr(), r.data_ptr(),
+                  act, out1.data_ptr(), acc1.data_ptr(), stream))
+    return out0, acc0, out1, acc1
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 512, 4608), (128, 256, 8192)])
+def test_noalloc_forced_splits(dev, no_plans, M, N, K):
+    """Each (configuration, K split) candidate with a split, forced through the plan API:
+    bq_gemm_i8_noalloc then splits K through its static scratch, bit for bit as bq_gemm_i8
+    with a caller workspace and the oracle."""
+    T = no_plans
+    qa, sa, qw, sw, b, r = _case(dev, M, N, K, I.ACT_RELU, seed=M + K)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    want = O.gemm_i8_i32(qa.cpu().numpy(), qw.cpu().numpy())
+    splits = [(cfg, sp) for cfg, sp in T.candidates((M, N, K)) if sp > 1]
+    assert splits, "the shape offers no K split"
+    for cfg, sp in splits:
+        print(f"bq_gemm_i8_noalloc M={M} N={N} K={K} cfg={cfg} split={sp}", flush=True)
+        T.set_plan((M, N, K), cfg, sp)
+        out0, acc0, out1, acc1 = _both(dev, qa, qw, sa, sw, b, r, M, N, K, I.ACT_RELU, stream)
+        torch.cuda.synchronize()
+        assert torch.equal(acc1, acc0) and torch.equal(out1, out0), (cfg, sp)
+        assert np.array_equal(acc1.cpu().numpy(), want), (cfg, sp)
+
+
+def test_noalloc_in_a_captured_graph(dev, no_plans):
+    """Warmed up outside the capture (the scratch address looked up), then captured: the
+    graph's replays, with eager work between them, equal bq_gemm_i8's output every time."""
+    T = no_plans
+    M, N, K = 256, 512, 4608
+    qa, sa, qw, sw, b, r = _case(dev, M, N, K, I.ACT_NONE, seed=7)
+    cands = [(cfg, sp) for cfg, sp in T.candidates((M, N, K)) if sp > 1]
+    T.set_plan((M, N, K), *cands[0])
+    side = torch.cuda.Stream(device=dev)
+    out0, _, _, _ = _both(dev, qa, qw, sa, sw, b, r, M, N, K, I.ACT_NONE, torch.cuda.current_stream(dev).cuda_stream)
+    outg = torch.empty((M, N), dtype=torch.float32, device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        L.check(_fn()(qa.data_ptr(), qw.data_ptr(), M, N, K, sa.data_ptr(), sw.data_ptr(), b.data_ptr(),
+                      r.data_ptr(), I.ACT_NONE, outg.data_ptr(), None, side.cuda_stream))
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        L.check(_fn()(qa.data_ptr(), qw.data_ptr(), M, N, K, sa.data_ptr(), sw.data_ptr(), b.data_ptr(),
+                      r.data_ptr(), I.ACT_NONE, outg.data_ptr(), None, side.cuda_stream))
+    for i in range(4):
+        print(f"noalloc graph replay {i}", flush=True)
+        outg.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(outg, out0), f"replay {i}"
+        _both(dev, qa, qw, sa, sw, b, r, 64, N, K, I.ACT_NONE, torch.cuda.current_stream(dev).cuda_stream)
+        torch.cuda.synchronize()
+    del g
 
 
 def test_noalloc_refuses_what_bq_gemm_i8_refuses(dev):
