@@ -246,6 +246,37 @@ def gemv_sweep(dev, stream):
             "method": "t = t0 + bytes / BW, least squares over 16-256 MiB weights (K = 4096), cache-cold rotations"}
 
 
+def decode_rows(dev, stream, copies=24):
+    """The two decode kernels at M = 1..8 on C2's 4096 x 4096 weight (cache-cold: 24 rotated
+    copies), each forced through the plan API: the v_dot4 wave-reduction GEMV (gemv_i8_kernel)
+    and the weight-streaming MFMA kernel (skinny_i8_kernel). The rule's pick is reported."""
+    import torch
+    from borch_amd import int8 as I
+    from borch_amd import tune as T
+    rows = {}
+    rng = np.random.default_rng(3)
+    qw = torch.randint(-127, 128, (4096, 4096), dtype=torch.int8, device=dev)
+    qws = [qw.clone() for _ in range(copies)]
+    sw = torch.rand(4096, device=dev) * 1e-3
+    b = torch.zeros(4096, device=dev)
+    for M in range(1, 9):
+        qa = torch.from_numpy(rng.integers(-127, 128, size=(M, 4096)).astype(np.int8)).to(dev)
+        sa = torch.rand(M, device=dev) * 1e-3
+        row = {}
+        for cfg, name in ((I.CFG_GEMV, "gemv_us"), (I.CFG_SKINNY, "skinny_us")):
+            T.set_plan((M, 4096, 4096), cfg, 1)
+            g = capture(lambda i: I.gemm_i8(qa, qws[i], sa, sw, b), copies)
+            row[name] = round(time_graph(g, copies, 8, stream) * 1e3, 3)
+            del g
+        T.set_plan((M, 4096, 4096), 0, 1)
+        row["rule"] = "gemv" if T.candidates((M, 4096, 4096))[0][0] == I.CFG_GEMV else "skinny"
+        rows[f"M{M}"] = row
+        log(f"decode M={M}: {row}")
+    del qws
+    torch.cuda.empty_cache()
+    return rows
+
+
 def WL_gemm_bytes(M, N, K):
     from borch_amd import workloads as WL
     return WL.gemm_bytes(M, N, K)
@@ -895,6 +926,7 @@ def main():
     sweep["W8A32"] = w8a32_rows(dev, stream)
     sweep["stream_int8"] = stream_rows(dev, stream)
     sweep["gemv_size_sweep"] = gemv_sweep(dev, stream)
+    sweep["decode_kernels"] = decode_rows(dev, stream)
     # C1: the Linear 16x512x512 through nn.Linear (per-row quantize + GEMM), latency
     from borch_amd import nn as bnn
     x_c1, w_c1, b_c1 = WL.c1_linear(0)

@@ -825,7 +825,7 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_i8_kernel(const GemmP p) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int k = (s0 + u) * 256 + j * 64 + kg * 16;
-        w[u][j] = buf_load16(rw, k < p.K ? (uint32_t)(col * p.K + k) : OOB);
+        w[u][j] = load_nt16(rw, k < p.K ? (uint32_t)(col * p.K + k) : OOB);
       }
     __builtin_amdgcn_sched_barrier(0);  // keep every load of the share ahead of the MFMAs
 #pragma unroll
@@ -866,7 +866,7 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_i8_kernel(const GemmP p) {
   }
 }
 
-// GEMV for M <= 4 (the HBM-bound decode shape): no MFMA. A weight row is read as
+// GEMV for M <= 8 (the HBM-bound decode shapes): no MFMA. A weight row is read as
 // contiguous 1 KB wave-loads (64 lanes x 16 bytes); each lane dots its 16 weight bytes
 // (v_dot4_i32_i8) against the same 16 bytes of every activation row, which sit in
 // registers for the whole kernel (K <= KC * 1024); one wave reduction per (row, m).
@@ -925,7 +925,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_i8_kernel(const GemmP p) {
 #pragma unroll
     for (int c = 0; c < KC; ++c) {
       const int k = c * 1024 + lane * 16;
-      w[j][c] = buf_load16(rw, k < p.K ? (uint32_t)(j * p.K + k) : OOB);
+      w[j][c] = load_nt16(rw, k < p.K ? (uint32_t)(j * p.K + k) : OOB);
     }
   __builtin_amdgcn_sched_barrier(0);  // every load of the wave in flight before anything waits
 #pragma unroll
@@ -1010,7 +1010,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_i8_fq_kernel(const GemmP p) {
 #pragma unroll
     for (int c = 0; c < KC; ++c) {
       const int k = c * 1024 + lane * 16;
-      w[j][c] = buf_load16(rw, k < p.K ? (uint32_t)(j * p.K + k) : OOB);
+      w[j][c] = load_nt16(rw, k < p.K ? (uint32_t)(j * p.K + k) : OOB);
     }
   __builtin_amdgcn_sched_barrier(0);  // every load in flight before anything waits
   // row maxima (the padding and rows past M read as zeros)
@@ -1136,11 +1136,30 @@ static bool launch_gemv_cfg(const GemmP& p, hipStream_t st) {
 }
 
 // One weight row per wave (the most rows in flight per byte of activation); four waves a
-// workgroup for one or two activation rows, eight for three or four (measured).
+// workgroup for one or two activation rows, eight for three or more (measured). From five
+// rows the activations held in registers (MR * KC * 4 VGPRs) limit K to 4096.
 template <int MR>
 static bool launch_gemv(const GemmP& p, hipStream_t st) {
+  if constexpr (MR > 4) {
+    if (p.K > 4096) return false;
+  }
   if constexpr (MR <= 2) return launch_gemv_cfg<MR, 1, 4>(p, st);
   else return launch_gemv_cfg<MR, 1, 8>(p, st);
+}
+
+// The wave-reduction GEMV for 1..8 activation rows; false where it does not apply.
+static bool launch_gemv_rows(const GemmP& p, hipStream_t st) {
+  switch (p.M) {
+    case 1: return launch_gemv<1>(p, st);
+    case 2: return launch_gemv<2>(p, st);
+    case 3: return launch_gemv<3>(p, st);
+    case 4: return launch_gemv<4>(p, st);
+    case 5: return launch_gemv<5>(p, st);
+    case 6: return launch_gemv<6>(p, st);
+    case 7: return launch_gemv<7>(p, st);
+    case 8: return launch_gemv<8>(p, st);
+    default: return false;
+  }
 }
 
 // -------------------------------------------------------------------------- depthwise
@@ -1595,6 +1614,14 @@ static void apply_plan(GemmP& p, const PlanKey& k) {
   }
 }
 
+// Dense problems of at most DECODE_MAX_M rows choose between the two decode kernels
+// (BQ_CFG_GEMV, BQ_CFG_SKINNY); the rule takes the GEMV up to GEMV_RULE_M rows where it
+// takes K. Measured on the 4096 x 4096 weight, cache-cold, both with non-temporal weight
+// loads: GEMV / skinny 4.88 / 6.28 us at M = 1, 5.38 / 6.66 at 4, 5.81 / 6.55 at 5, 6.10 /
+// 6.63 at 6, 6.40 / 6.71 at 7, 6.12 / 6.76 at 8.
+constexpr int DECODE_MAX_M = 8;
+constexpr int GEMV_RULE_M = 8;
+
 // The GEMM view of a problem given as (M, N, K) or (N, H, W, C, O, KH, KW, stride, pad);
 // false for a bad geometry. `tiled`: whether the tiled kernel runs it (a dense GEMM of at
 // most 64 rows takes the GEMV / skinny kernels: nothing to choose).
@@ -1699,13 +1726,14 @@ static int gemm_impl(const char* what, const int8_t* A, const int8_t* W, int64_t
   p.vec_ok = (N % 4 == 0) && aligned16(out) && aligned16(acc) && aligned16(residual);
   hipStream_t st = (hipStream_t)stream;
   bool done = false;
-  if (M <= 4) {
-    switch (M) {
-      case 1: done = launch_gemv<1>(p, st); break;
-      case 2: done = launch_gemv<2>(p, st); break;
-      case 3: done = launch_gemv<3>(p, st); break;
-      default: done = launch_gemv<4>(p, st); break;
-    }
+  if (M <= DECODE_MAX_M) {
+    // the decode shapes: the wave-reduction GEMV up to GEMV_RULE_M rows, the weight-streaming
+    // MFMA kernel above; a plan may pick either for up to DECODE_MAX_M rows
+    apply_plan(p, dense_key(M, N, K));
+    bool gemv = M <= GEMV_RULE_M;
+    if (p.plan_cfg == BQ_CFG_GEMV) gemv = true;
+    else if (p.plan_cfg == BQ_CFG_SKINNY) gemv = false;
+    if (gemv) done = launch_gemv_rows(p, st);
   }
   if (done) {
   } else if (M <= 64) {
@@ -1868,7 +1896,21 @@ int bq_plan_candidates(const int64_t* problem, int n, int32_t* cfgs, int32_t* sp
   bool conv, tiled;
   if (!problem_view(problem, n, key, p, conv, tiled))
     return set_error(BQ_ERR_ARG, "bq_plan_candidates: bad problem (3 dense or 9 conv dimensions)");
-  if (!tiled) return 0;
+  if (!tiled) {
+    if (conv || p.M > DECODE_MAX_M) return 0;
+    // the decode kernels: the rule's first, the GEMV only where it takes the shape
+    const bool gemv_ok = p.K <= (p.M <= 4 ? 8192 : 4096);
+    const bool rule_gemv = p.M <= GEMV_RULE_M && gemv_ok;
+    int cnt = 0;
+    int32_t c[2];
+    c[cnt++] = rule_gemv ? BQ_CFG_GEMV : BQ_CFG_SKINNY;
+    if (gemv_ok) c[cnt++] = rule_gemv ? BQ_CFG_SKINNY : BQ_CFG_GEMV;
+    for (int i = 0; i < cnt && i < cap; ++i) {
+      if (cfgs) cfgs[i] = c[i];
+      if (splits) splits[i] = 1;
+    }
+    return cnt;
+  }
   std::pair<int, int> out[64];
   int cnt = 0;
   const int rule = choose_cfg(p, conv);
@@ -1907,9 +1949,17 @@ int bq_plan_set(const int64_t* problem, int n, int32_t cfg, int32_t split) {
     g_plans.erase(key);
     return BQ_OK;
   }
+  if (!tiled) {
+    if (p.M > DECODE_MAX_M || (cfg != BQ_CFG_GEMV && cfg != BQ_CFG_SKINNY) || split != 1)
+      return set_error(BQ_ERR_ARG, "bq_plan_set: a GEMM of at most 64 rows has no tiled kernel to plan (up to %d "
+                       "rows: BQ_CFG_GEMV or BQ_CFG_SKINNY, split 1)", DECODE_MAX_M);
+    if (cfg == BQ_CFG_GEMV && p.K > (p.M <= 4 ? 8192 : 4096))
+      return set_error(BQ_ERR_ARG, "bq_plan_set: the GEMV takes K <= %d at M = %d", p.M <= 4 ? 8192 : 4096, p.M);
+    g_plans[key] = Plan{cfg, split};
+    return BQ_OK;
+  }
   if (cfg < 1 || cfg >= NCFG || cfg == 3 || cfg == 9 || (cfg == 16 && conv) || split < 1 || split > 64)
     return set_error(BQ_ERR_ARG, "bq_plan_set: bad configuration %d / split %d", cfg, split);
-  if (!tiled) return set_error(BQ_ERR_ARG, "bq_plan_set: a GEMM of at most 64 rows has no tiled kernel to plan");
   g_plans[key] = Plan{cfg, split};
   return BQ_OK;
 }

@@ -75,7 +75,7 @@ __global__ __launch_bounds__(WA_WAVES * 64) void gemv_w8a32_kernel(const float* 
 #pragma unroll
     for (int j = 0; j < RPW; ++j) {
       const int k = c * 1024 + lane * 16;
-      w[j][c] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rw, k < K ? (uint32_t)(j * K + k) : W_OOB, 0, 0));
+      w[j][c] = load_nt16(rw, k < K ? (uint32_t)(j * K + k) : W_OOB);
     }
   __builtin_amdgcn_sched_barrier(0);
   if constexpr (XL) {
@@ -241,7 +241,7 @@ __global__ __launch_bounds__(WA_WAVES * 64) void gemv_w8a32_mfma_kernel(const fl
 #pragma unroll
   for (int c = 0; c < CPW; ++c) {
     const int k = (wave + WA_WAVES * c) * 64 + kq;
-    w[c] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rw, k < K ? (uint32_t)(r * K + k) : W_OOB, 0, 0));
+    w[c] = load_nt16(rw, k < K ? (uint32_t)(r * K + k) : W_OOB);
   }
   __builtin_amdgcn_sched_barrier(0);  // every load above is issued before the first MFMA
   v4f acc = {0.f, 0.f, 0.f, 0.f};

@@ -13,7 +13,8 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from ._lib import ACT_GELU, ACT_NONE, ACT_RELU, ACT_SILU, SCALE_A_PER_TENSOR, check, lib, require_device
+from ._lib import ACT_GELU, ACT_NONE, ACT_RELU, ACT_SILU, CFG_GEMV, CFG_SKINNY, SCALE_A_PER_TENSOR, check, lib, \
+    require_device
 
 __all__ = [
     "ACT_NONE", "ACT_RELU", "ACT_SILU", "ACT_GELU", "Int8Weight", "Int8ConvWeight", "Int8DwWeight",

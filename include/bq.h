@@ -253,14 +253,18 @@ int64_t bq_conv2d_absmax_parts(int64_t N, int64_t H, int64_t W, int64_t C, int64
  *   n == 3: a dense bq_gemm_i8 (M, N, K), or
  *   n == 9: a bq_conv2d_i8_nhwc(_q) (N, H, W, C, O, KH, KW, stride, pad), C the padded count.
  * bq_plan_candidates writes up to `cap` (configuration id, K split) pairs, the rules' pick
- * first, and returns how many there are (0: nothing to choose, as for a dense GEMM of at
- * most 64 rows; negative: a bad problem). bq_plan_set records one (cfg == 0 removes the
+ * first, and returns how many there are (0: nothing to choose, as for a dense GEMM of 9 to
+ * 64 rows; negative: a bad problem). A dense GEMM of at most 8 rows chooses between the two
+ * decode kernels, BQ_CFG_GEMV and BQ_CFG_SKINNY (split 1). bq_plan_set records one (cfg == 0 removes the
  * problem's plan); bq_plan_clear removes all. A plan in force when bq_conv2d_absmax_parts
  * sizes a buffer must stay in force for the conv that fills it. Plans are process-wide;
  * set them before a graph capture (a captured launch keeps the choice it was made with).
  * Replaces Device.choose / runTuning (borch-ts/src/device.ts:2686-2700, 2834-2846), the
  * rule's pick first and the fastest cached per key, that compiled(..., {tune}) drives
  * (borch-ts/src/compile.ts:55-62). */
+#define BQ_CFG_GEMV 32   /* dense, M <= 8: the v_dot4 wave-reduction GEMV (K <= 8192; 4096 above 4 rows;
+                          * the rule's pick where it takes K) */
+#define BQ_CFG_SKINNY 33 /* dense, M <= 8: the weight-streaming MFMA kernel */
 int bq_plan_candidates(const int64_t* problem, int n, int32_t* cfgs, int32_t* splits, int cap);
 int bq_plan_set(const int64_t* problem, int n, int32_t cfg, int32_t split);
 int bq_plan_clear(void);

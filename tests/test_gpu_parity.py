@@ -753,6 +753,34 @@ def test_every_conv_plan_gives_the_same_result(dev, no_plans, N, C, H, O_, k, st
         assert torch.equal(q, want_q), (cfg, split)
 
 
+@pytest.mark.parametrize("M", [1, 3, 4, 5, 6, 7, 8])
+@pytest.mark.parametrize("N,K", [(4096, 4096), (300, 1040), (70, 8192)])
+def test_decode_kernels_give_the_same_result(dev, no_plans, M, N, K):
+    """Both decode kernels (the v_dot4 wave-reduction GEMV and the weight-streaming MFMA
+    kernel), each forced through the plan API, give the oracle's int32 sums and f32 outputs
+    bit for bit; the GEMV is offered only where it takes K."""
+    T = no_plans
+    say(f"decode kernels M={M} N={N} K={K}")
+    rng = np.random.default_rng(M * 11 + N + K)
+    qa_o = rng.integers(-127, 128, size=(M, K)).astype(np.int8)
+    qw_o = rng.integers(-127, 128, size=(N, K)).astype(np.int8)
+    sa_o = rng.uniform(1e-4, 1e-3, M).astype(np.float32)
+    sw_o = rng.uniform(1e-4, 1e-3, N).astype(np.float32)
+    b_o = rng.normal(size=N).astype(np.float32)
+    acc_o = O.gemm_i8_i32(qa_o, qw_o)
+    y_o = O.dequant(acc_o, sa_o, sw_o, b_o, relu=True)
+    cands = T.candidates((M, N, K))
+    want = {I.CFG_GEMV, I.CFG_SKINNY} if K <= (8192 if M <= 4 else 4096) else {I.CFG_SKINNY}
+    assert {c for c, _ in cands} == want and all(sp == 1 for _, sp in cands)
+    assert cands[0][0] == (I.CFG_GEMV if I.CFG_GEMV in want else I.CFG_SKINNY)  # the rule: the GEMV where it fits
+    for cfg, sp in cands:
+        T.set_plan((M, N, K), cfg, sp)
+        y, acc = I.gemm_i8(t(qa_o, dev), t(qw_o, dev), t(sa_o, dev), t(sw_o, dev), t(b_o, dev), I.ACT_RELU,
+                           want_acc=True)
+        assert np.array_equal(n(acc), acc_o), cfg
+        assert_f32(n(y), y_o)
+
+
 @pytest.mark.parametrize("M,N,K", [(6304, 768, 768), (1000, 520, 784), (300, 200, 4112), (257, 2304, 768),
                                    (4096, 4096, 512)])
 def test_regression_fast_path_stores_equal_general_path(dev, no_plans, M, N, K):
