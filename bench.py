@@ -277,6 +277,80 @@ def decode_rows(dev, stream, copies=24):
     return rows
 
 
+def gemm_phases(dev, stream, M=4096, N=4096, K=4096, launches=6):
+    """Where one launch of the tiled GEMM spends its time: ``bq_gemm_i8_phases`` stamps each
+    workgroup's entry, the end of its main loop and the completion of its last store with the
+    steady wall clock (hipDeviceAttributeWallClockRate), and its XCC. Per launch, relative to
+    the first workgroup's entry: each XCC's first entry (the staggered start), the main loop
+    (prologue + K loop) and the epilogue (the f32 stores) per workgroup, and the span from the
+    first entry to the last store. Printed as one JSON line."""
+    import ctypes
+    import torch
+    from borch_amd import _lib as L
+    from borch_amd import int8 as I
+    from borch_amd import workloads as WL
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    rate = ctypes.c_int(0)
+    hip.hipDeviceGetAttribute(ctypes.byref(rate), 10017, dev.index or 0)  # hipDeviceAttributeWallClockRate, kHz
+    khz = rate.value or 100000
+    a, w, b = WL.c2_gemm(M, 0, K, N)
+    qa, sa = I.quantize_rows(torch.from_numpy(a).to(dev))
+    qw, sw = I.quantize_weight_per_channel(torch.from_numpy(w).to(dev))
+    B = torch.from_numpy(b).to(dev)
+    out = torch.empty((M, N), dtype=torch.float32, device=dev)
+    cap = 4 * 4096
+    nwg = [0]
+
+    def launch(buf):
+        n = L.lib().bq_gemm_i8_phases(qa.data_ptr(), qw.data_ptr(), M, N, K, sa.data_ptr(), sw.data_ptr(),
+                                      B.data_ptr(), out.data_ptr(), buf.data_ptr(), cap,
+                                      torch.cuda.current_stream().cuda_stream)
+        if n < 0:
+            L.check(int(n))
+        nwg[0] = int(n)
+    # eager launches back to back (the first two warm up), then the same from a HIP graph
+    st_e = [torch.zeros(cap, dtype=torch.int64, device=dev) for _ in range(launches)]
+    for i in range(launches + 2):
+        launch(st_e[max(0, i - 2)])
+    torch.cuda.synchronize()
+    ref = I.gemm_i8(qa, qw, sa, sw, B)
+    same = bool(torch.equal(out, ref))
+    st_g = [torch.zeros(cap, dtype=torch.int64, device=dev) for _ in range(launches)]
+    g = capture(lambda i: launch(st_g[i]), launches)
+    g.replay()
+    torch.cuda.synchronize()
+    del g
+    n = nwg[0]
+    us = 1e3 / khz
+
+    def summary(t):
+        v = t[: 4 * n].view(n, 4).cpu().numpy().astype(np.int64)
+        t0 = v[:, 0].min()
+        entry, loop, end = (v[:, 0] - t0) * us, (v[:, 1] - v[:, 0]) * us, (v[:, 2] - v[:, 1]) * us
+        xcc = (v[:, 3] >> 6) & 15
+        per = {}
+        for x in sorted(set(xcc.tolist())):
+            m = xcc == x
+            per[int(x)] = {"first_entry_us": round(float(entry[m].min()), 2), "last_entry_us": round(float(entry[m].max()), 2),
+                           "main_loop_us_median": round(float(np.median(loop[m])), 2),
+                           "epilogue_us_median": round(float(np.median(end[m])), 2),
+                           "last_store_us": round(float((entry[m] + loop[m] + end[m]).max()), 2)}
+        return {"span_us": round(float((entry + loop + end).max()), 2), "start_us": int(t0),
+                "main_loop_us": [round(float(q), 2) for q in np.percentile(loop, [0, 50, 100])],
+                "epilogue_us": [round(float(q), 2) for q in np.percentile(end, [0, 50, 100])],
+                "xcc": per}
+    eager = [summary(t) for t in st_e]
+    graph = [summary(t) for t in st_g]
+    gaps = [round((graph[i + 1]["start_us"] - graph[i]["start_us"]) * us, 2) for i in range(len(graph) - 1)]
+    for r in eager + graph:
+        del r["start_us"]
+    g = capture(lambda i: I.gemm_i8(qa, qw, sa, sw, B), 10)
+    t_graph = time_graph(g, 10, 5, stream) * 1e3
+    print(json.dumps({"phases": f"{M}x{N}x{K}", "workgroups": n, "wall_clock_kHz": khz,
+                      "output_equals_bq_gemm_i8": same, "graph_us_per_launch_bq_gemm_i8": round(t_graph, 2),
+                      "graph_entry_to_entry_us": gaps, "graph_launches": graph, "eager_launches": eager}), flush=True)
+
+
 def WL_gemm_bytes(M, N, K):
     from borch_amd import workloads as WL
     return WL.gemm_bytes(M, N, K)
@@ -760,6 +834,8 @@ def main():
                     help="for kernel traces: the model's int8 forward as a HIP graph, replayed --steps times with "
                          "dynamic scales, then (ResNet-18, EfficientNet-B0) --steps times calibrated; prints the "
                          "replay times")
+    ap.add_argument("--phases", action="store_true",
+                    help="per-workgroup phase stamps of the 4096^3 GEMM (bq_gemm_i8_phases), one JSON line")
     ap.add_argument("--layers", action="store_true",
                     help="the model configurations only, then every int8 layer's table as markdown "
                          "(GEMM shape, ops, bytes, us alone, TOPS, MFMA fraction, GB/s)")
@@ -791,6 +867,9 @@ def main():
         model_trace(dev, stream, args.model_trace, args.steps)
         return
 
+    if args.phases:
+        gemm_phases(dev, stream)
+        return
     if args.layers:
         tables = {}
         models = bench_models(dev, stream, steps=max(args.steps // 2, 10), layers_out=tables)

@@ -64,6 +64,7 @@ SIGNATURES = {
                             _c_size, _c_p]),
     "bq_linear_i8": (_c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_int, _c_p, _c_p, _c_p, _c_p,
                               _c_size, _c_p]),
+    "bq_gemm_i8_phases": (_c_i64, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_p]),
     "bq_gemm_i8_noalloc": (_c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_int, _c_p, _c_p,
                                     _c_p]),
     "bq_conv2d_i8_nhwc_q": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i64,

@@ -71,6 +71,10 @@ struct GemmP {
   const float* X;
   int8_t* qx;
   float* sx;
+  // Diagnostics (tiled kernel, nullable): four words a workgroup at 4 * (its regrouped id):
+  // the steady wall clock (100 MHz) at entry, after the main loop and after its last store
+  // completed, then its hardware id (__smid: XCC, SE, CU). bq_gemm_i8_phases sets it.
+  uint64_t* stamps;
 };
 
 constexpr int BK = 128;  // bytes of K per LDS stage: one cache line per row
@@ -440,6 +444,7 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, const int L,
   const int per = (KT + S - 1) / S;  // stages of each split (the host picks S with no empty split)
   const int kt0 = split * per;
 
+  const uint64_t t_entry = p.stamps ? (uint64_t)wall_clock64() : 0;
   const Quantizer qz_out(p.q_out ? p.s_out[0] : 0.f);
   // the accumulators: TM x TN blocks of 32 x 32 (16 registers each), or with MF16
   // (2 TM) x (2 TN) blocks of 16 x 16 (4 registers each): the same registers either way
@@ -457,6 +462,7 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, const int L,
   }
   mainloop_dma<BM, BN, WAVES_M, WAVES_N, CONV, NBUF, FD, MF16>(p, m0, n0, kt0, min(per, KT - kt0), lds, s_sa, s_sw,
                                                          s_b, c);
+  const uint64_t t_loop = p.stamps ? (uint64_t)wall_clock64() : 0;
   if (CAN_SPLIT && S > 1) {
     // Exact split-K reduction in the same launch. Partials are int32, so the sum is exact
     // whatever the order. Each lane stores its accumulator registers as 8-byte chunks at
@@ -753,6 +759,17 @@ __device__ __forceinline__ void gemm_tile(const GemmP& p, const int L,
 #pragma unroll
       for (int w = 1; w < WAVES_M * WAVES_N; ++w) m = fmaxf(m, s_wmax[w]);
       p.amax[bm * tiles_n + bn] = m;
+    }
+  }
+  if (p.stamps) {  // uniform
+    wait_dma_all();  // this lane's stores have completed
+    __syncthreads();
+    if (tid == 0) {
+      uint64_t* st = p.stamps + 4 * (size_t)L;
+      st[0] = t_entry;
+      st[1] = t_loop;
+      st[2] = (uint64_t)wall_clock64();
+      st[3] = __smid();
     }
   }
 }
@@ -1705,7 +1722,8 @@ static int noalloc_scratch(const char* what, hipStream_t st, void** out) {
 
 static int gemm_impl(const char* what, const int8_t* A, const int8_t* W, int64_t M, int64_t N, int64_t K,
                      const float* sA, const float* sW, const float* bias, const float* residual, int act,
-                     float* out, int32_t* acc, void* ws, size_t ws_bytes, bool noalloc, bq_stream_t stream) {
+                     float* out, int32_t* acc, void* ws, size_t ws_bytes, bool noalloc, bq_stream_t stream,
+                     uint64_t* stamps = nullptr, int64_t stamps_cap = 0, int64_t* stamped = nullptr) {
   if (M < 0 || N < 0 || K < 0) return set_error(BQ_ERR_ARG, "%s: negative size", what);
   if (M > 0x7fffffff || N > 0x7fffffff || M * N > ((int64_t)1 << 40))
     return set_error(BQ_ERR_ARG, "%s: size too large", what);
@@ -1725,6 +1743,18 @@ static int gemm_impl(const char* what, const int8_t* A, const int8_t* W, int64_t
   p.out = out; p.acc = acc;
   p.vec_ok = (N % 4 == 0) && aligned16(out) && aligned16(acc) && aligned16(residual);
   hipStream_t st = (hipStream_t)stream;
+  if (stamps) {  // diagnostics: the tiled kernel, unsplit, one stamped workgroup a tile
+    if (M <= 64) return set_error(BQ_ERR_UNSUPPORTED, "%s: phase stamps cover the tiled kernel (M > 64)", what);
+    apply_plan(p, dense_key(M, N, K));
+    const long long tiles = out_tiles(p, false);
+    if (4 * tiles > stamps_cap)
+      return set_error(BQ_ERR_ARG, "%s: %lld workgroups need %lld stamp words, %lld given", what, tiles, 4 * tiles,
+                       (long long)stamps_cap);
+    p.stamps = stamps;
+    *stamped = tiles;
+    launch_gemm<false>(p, st, Ws{nullptr, 0});
+    return check_launch(what);
+  }
   bool done = false;
   if (M <= DECODE_MAX_M) {
     // the decode shapes: the wave-reduction GEMV up to GEMV_RULE_M rows, the weight-streaming
@@ -1769,6 +1799,16 @@ int bq_gemm_i8(const int8_t* A, const int8_t* W, int64_t M, int64_t N, int64_t K
                void* ws, size_t ws_bytes, bq_stream_t stream) {
   return gemm_impl("bq_gemm_i8", A, W, M, N, K, sA, sW, bias, residual, act, out, acc, ws, ws_bytes, false,
                    stream);
+}
+
+int64_t bq_gemm_i8_phases(const int8_t* A, const int8_t* W, int64_t M, int64_t N, int64_t K, const float* sA,
+                          const float* sW, const float* bias, float* out, uint64_t* stamps, int64_t stamps_cap,
+                          bq_stream_t stream) {
+  if (!stamps) return set_error(BQ_ERR_ARG, "bq_gemm_i8_phases: null stamps");
+  int64_t n = 0;
+  const int rc = gemm_impl("bq_gemm_i8_phases", A, W, M, N, K, sA, sW, bias, nullptr, BQ_ACT_NONE, out, nullptr,
+                           nullptr, 0, false, stream, stamps, stamps_cap, &n);
+  return rc != BQ_OK ? rc : n;
 }
 
 int bq_gemm_i8_noalloc(const int8_t* A, const int8_t* W, int64_t M, int64_t N, int64_t K, const float* sA,

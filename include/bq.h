@@ -223,6 +223,18 @@ int bq_gemm_i8_noalloc(const int8_t* A, const int8_t* W, int64_t M, int64_t N, i
                        const float* sW, const float* bias, const float* residual, int act, float* out,
                        int32_t* acc, bq_stream_t stream);
 
+/* Diagnostics, no counterpart in the reference: bq_gemm_i8 (no residual, no activation, no
+ * int32 output, no K split) on the tiled kernel (M > 64) that also records, for each
+ * workgroup, four words at stamps[4 * i .. 4 * i + 3] (i: the workgroup's tile order): the
+ * steady wall clock (100 MHz, hipDeviceAttributeWallClockRate) at entry, after its main loop
+ * and after its last output store completed, then its hardware id (bits 3:0 CU, 5:4 SE,
+ * 9:6 XCC, as HIP's __smid). Returns the number of workgroups stamped, or a negative
+ * BQ_ERR_* (stamps_cap, in words, too small: BQ_ERR_ARG). For measuring where a launch's
+ * time goes (the start of each XCD, prologue and main loop, the output stores). */
+int64_t bq_gemm_i8_phases(const int8_t* A, const int8_t* W, int64_t M, int64_t N, int64_t K, const float* sA,
+                          const float* sW, const float* bias, float* out, uint64_t* stamps, int64_t stamps_cap,
+                          bq_stream_t stream);
+
 /* Implicit-GEMM int8 convolution, NHWC, groups 1, dilation 1:
  *   x int8 [N, H, W, C] (C % 16 == 0, per-tensor scale sA f32 [1]),
  *   w int8 [O, KH, KW, C] (per-channel scale sW f32 [O]),

@@ -76,6 +76,9 @@ def test_argument_checks_run_on_host():
     assert lib.bq_conv2d_i8_nhwc_pair(None, 1, 8, 8, 16, None, None, d, None, 0, None) == _lib.BQ_ERR_ARG
     assert lib.bq_conv2d_i8_nhwc_pair(None, 1, 8, 8, 16, None, d, d_amax, None, 0, None) == _lib.BQ_ERR_UNSUPPORTED
     assert "first conv" not in _lib.last_error() and "absmax" in _lib.last_error()
+    # the phase-stamped GEMM: stamps required, the tiled kernel only
+    assert lib.bq_gemm_i8_phases(None, None, 256, 256, 256, None, None, None, None, None, 0, None) == _lib.BQ_ERR_ARG
+    assert lib.bq_gemm_i8_phases(None, None, 16, 256, 256, None, None, None, None, 1, 64, None) == _lib.BQ_ERR_ARG
     big = _lib.ConvDesc(None, 32, 9, 9, 1, 0, None, None, None, 0, None, None, None, None)
     assert lib.bq_conv2d_i8_nhwc_pair(None, 1, 8, 8, 16, None, big, d, None, 0, None) == _lib.BQ_ERR_ARG
     assert "larger than the input" in _lib.last_error()

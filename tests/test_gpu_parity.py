@@ -753,6 +753,32 @@ def test_every_conv_plan_gives_the_same_result(dev, no_plans, N, C, H, O_, k, st
         assert torch.equal(q, want_q), (cfg, split)
 
 
+def test_phase_stamps_are_ordered_and_output_unchanged(dev):
+    """bq_gemm_i8_phases: the output is bq_gemm_i8's bit for bit, one stamp record per
+    workgroup, entry <= end of main loop <= last store, an XCC id below 8."""
+    from borch_amd import _lib as L
+    M, N, K = 1024, 768, 1040
+    rng = np.random.default_rng(17)
+    qa = t(rng.integers(-127, 128, size=(M, K)).astype(np.int8), dev)
+    qw = t(rng.integers(-127, 128, size=(N, K)).astype(np.int8), dev)
+    sa = t(rng.uniform(1e-4, 1e-3, M).astype(np.float32), dev)
+    sw = t(rng.uniform(1e-4, 1e-3, N).astype(np.float32), dev)
+    b = t(rng.normal(size=N).astype(np.float32), dev)
+    out = torch.empty((M, N), dtype=torch.float32, device=dev)
+    st = torch.zeros(4 * 4096, dtype=torch.int64, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+    assert L.lib().bq_gemm_i8_phases(qa.data_ptr(), qw.data_ptr(), M, N, K, sa.data_ptr(), sw.data_ptr(),
+                                     b.data_ptr(), out.data_ptr(), st.data_ptr(), 4, stream) == L.BQ_ERR_ARG
+    nwg = L.lib().bq_gemm_i8_phases(qa.data_ptr(), qw.data_ptr(), M, N, K, sa.data_ptr(), sw.data_ptr(),
+                                    b.data_ptr(), out.data_ptr(), st.data_ptr(), st.numel(), stream)
+    assert nwg > 0
+    assert torch.equal(out, I.gemm_i8(qa, qw, sa, sw, b))
+    v = st[: 4 * nwg].view(nwg, 4).cpu().numpy()
+    assert np.all(v[:, 0] > 0) and np.all(v[:, 0] <= v[:, 1]) and np.all(v[:, 1] <= v[:, 2])
+    assert np.all(((v[:, 3] >> 6) & 15) < 8)
+    assert not st[4 * nwg:].any()
+
+
 @pytest.mark.parametrize("M", [1, 3, 4, 5, 6, 7, 8])
 @pytest.mark.parametrize("N,K", [(4096, 4096), (300, 1040), (70, 8192)])
 def test_decode_kernels_give_the_same_result(dev, no_plans, M, N, K):
