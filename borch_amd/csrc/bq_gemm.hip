@@ -807,7 +807,8 @@ constexpr int SK_COLS = 16;  // output channels a workgroup
 // contiguous bytes of each of the 16 rows (16-byte pieces 64 bytes apart: 7.4 -> 6.9 us at
 // M = 16, the same sums in another order of k), and every weight load of a wave's share
 // (U steps) is issued before the first MFMA, so a whole 16-row slab is in flight at once.
-// The activation rows (tiny, L2-resident) are loaded first. v_mfma_i32_16x16x64_i8
+// The activation rows (tiny, L2-resident) are loaded first, after the epilogue's scales,
+// bias and residual, so that no memory round trip is left after the sums. v_mfma_i32_16x16x64_i8
 // multiplies the weight bytes against up to four 16-row activation tiles; the waves'
 // partial sums meet in LDS.
 template <int MT, int WAVES, int U>
@@ -820,6 +821,25 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_i8_kernel(const GemmP p) {
   const int kg = lane >> 4;   // which 64-byte group of a 256-byte step
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.W + (size_t)n0 * p.K, (uint32_t)(min(SK_COLS, p.N - n0) * p.K));
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, (uint32_t)(p.M * p.K));
+
+  // Thread e < 256 writes output (t * 16 + e / 16, n0 + e % 16) of each 16-row tile t: its
+  // epilogue operands are fetched now, ahead of the operand stream.
+  const int e = threadIdx.x;
+  const int ml = (e >> 4) & 15, nl = e & 15;
+  const int nn = n0 + nl;
+  const bool writer = e < 256 && nn < p.N;
+  float e_sw = 0.f, e_b = 0.f, e_sa[MT], e_r[MT];
+  if (writer) {
+    e_sw = p.sW[nn];
+    e_b = p.bias ? p.bias[nn] : 0.f;
+  }
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    const int m = t * 16 + ml;
+    const bool mine = writer && m < p.M;
+    e_sa[t] = mine ? (p.sa_per_row ? p.sA[m] : p.sA[0]) : 0.f;
+    e_r[t] = mine && p.res ? p.res[(size_t)m * p.N + nn] : 0.f;
+  }
 
   v4i c[MT];
 #pragma unroll
@@ -858,27 +878,18 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_i8_kernel(const GemmP p) {
     for (int r = 0; r < 4; ++r) red[wave][t][lane][r] = c[t][r];
   __syncthreads();
   // 16x16 result layout: lane l, register r holds row 4*(l/16) + r, column l%16.
-  const int e = threadIdx.x;  // one output of a 16x16 tile per thread
-  if (e >= 256) return;
-  const int ml = e >> 4, nl = e & 15;
+  if (!writer) return;
   const int src_lane = (ml >> 2) * 16 + nl, src_r = ml & 3;
-  const int nn = n0 + nl;
-  if (nn < p.N) {
-    const float sw = p.sW[nn];
-    const float b = p.bias ? p.bias[nn] : 0.f;
 #pragma unroll
-    for (int t = 0; t < MT; ++t) {
-      const int m = t * 16 + ml;
-      if (m < p.M) {
-        int acc = 0;
+  for (int t = 0; t < MT; ++t) {
+    const int m = t * 16 + ml;
+    if (m < p.M) {
+      int acc = 0;
 #pragma unroll
-        for (int w = 0; w < WAVES; ++w) acc += red[w][t][src_lane][src_r];
-        const size_t idx = (size_t)m * p.N + nn;
-        const float sa = p.sa_per_row ? p.sA[m] : p.sA[0];
-        const float rv = p.res ? p.res[idx] : 0.f;
-        p.out[idx] = dequant_one(acc, sa, sw, b, p.bias != nullptr, rv, p.res != nullptr, p.act);
-        if (p.acc) p.acc[idx] = acc;
-      }
+      for (int w = 0; w < WAVES; ++w) acc += red[w][t][src_lane][src_r];
+      const size_t idx = (size_t)m * p.N + nn;
+      p.out[idx] = dequant_one(acc, e_sa[t], e_sw, e_b, p.bias != nullptr, e_r[t], p.res != nullptr, p.act);
+      if (p.acc) p.acc[idx] = acc;
     }
   }
 }
