@@ -894,6 +894,176 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_i8_kernel(const GemmP p) {
   }
 }
 
+// ----------------------------------------------------------------------------- small K
+
+// Dense GEMM for a narrow output (N <= 64, N % 4 == 0) and a short K (<= 256) over many
+// rows: a 1x1 conv's projection to a few channels (EfficientNet-B0 b64's blocks.0.project,
+// 802816 x 16 x 32). The tiled kernel's tiles spend most of their time outside their MFMAs
+// there (a 128 x 32 tile for 16 output columns, one K stage). Here the weight fragments stay
+// in registers for the whole launch; each wave takes 16 rows a step (v_mfma_i32_16x16x64_i8
+// against NB 16-column blocks and KS 64-byte K steps; lane l holds row l % 16 and K chunk
+// l / 16 of an operand, and result register r is row 4 (l / 16) + r, column l % 16),
+// loads its next step's activation rows before this step's MFMAs, and writes its 16 x N
+// results, contiguous in memory, as 16-byte pieces through a per-wave LDS patch (the
+// epilogue arithmetic of the tiled kernel's, in the same order). Workgroups stride over
+// the 64-row steps; each writes one max |y| (p.amax). Unaligned outputs take four-byte
+// stores instead.
+constexpr int SMALLK_ROWS = 64;  // rows a workgroup step: 4 waves x 16
+template <int NB, int KS>
+__global__ __launch_bounds__(256) void smallk_i8_kernel(const GemmP p) {
+  constexpr int NP = NB * 16 + 4;  // patch pitch (ints): 4 NP % 64 == 16, conflict-free writes
+  __shared__ __attribute__((aligned(16))) int patch[4][16 * NP];
+  __shared__ __attribute__((aligned(16))) float s_sw[NB * 16], s_b[NB * 16];
+  __shared__ float s_wmax[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c16 = lane & 15, kq = lane >> 4;
+  const int M = p.M, N = p.N, K = p.K;
+  const int steps = (M + SMALLK_ROWS - 1) / SMALLK_ROWS;
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.W, (uint32_t)(N * K));
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, (uint32_t)(M * K));
+  v4i b[NB][KS];
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    const int n = j * 16 + c16;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int k = ks * 64 + kq * 16;
+      b[j][ks] = buf_load16(rw, (n < N && k < K) ? (uint32_t)(n * K + k) : OOB);
+    }
+  }
+  if (tid < NB * 16) {
+    s_sw[tid] = tid < N ? p.sW[tid] : 0.f;
+    s_b[tid] = (tid < N && p.bias) ? p.bias[tid] : 0.f;  // 0 without bias: y + 0.0f == y here
+  }
+  const float sa0 = p.sa_per_row ? 0.f : p.sA[0];
+  const Quantizer qz_out(p.q_out ? p.s_out[0] : 0.f);
+  // This lane's first (row, column) in a wave's 16 x N block, read as 16-byte pieces 256
+  // values apart, and the step between its pieces.
+  const int row0 = (lane * 4) / N, col0 = lane * 4 - row0 * N;
+  const int drow = 256 / N, dcol = 256 - drow * N;
+  const bool has_r = p.res != nullptr, vec = p.vec_ok;
+  float amax = 0.f;
+  auto load_a = [&](v4i (&a)[KS], int t) {
+    const int row = t * SMALLK_ROWS + wave * 16 + c16;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int k = ks * 64 + kq * 16;
+      a[ks] = buf_load16(ra, (t < steps && row < M && k < K) ? (uint32_t)(row * K + k) : OOB);
+    }
+  };
+  v4i a[KS];
+  int t = blockIdx.x;
+  load_a(a, t);
+  __syncthreads();  // the scales and bias are staged
+  int* const pw = patch[wave];
+  for (; t < steps; t += gridDim.x) {
+    v4i an[KS];
+    load_a(an, t + gridDim.x);
+    v4i c[NB];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      c[j] = v4i{};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) c[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[ks], b[j][ks], c[j], 0, 0, 0);
+    }
+    const int m0w = t * SMALLK_ROWS + wave * 16;
+    const int rows = min(16, M - m0w);  // <= 0 past M (the last step's later waves): all dropped
+    const size_t base = (size_t)m0w * N;
+    const uint32_t bytes = rows > 0 ? (uint32_t)(rows * N) * 4u : 0u;
+    const __amdgpu_buffer_rsrc_t r_out = make_rsrc(p.out ? p.out + base : p.out, p.out ? bytes : 0u);
+    const __amdgpu_buffer_rsrc_t r_res = make_rsrc(has_r ? p.res + base : p.res, has_r ? bytes : 0u);
+    const __amdgpu_buffer_rsrc_t r_acc = make_rsrc(p.acc ? p.acc + base : p.acc, p.acc ? bytes : 0u);
+    const __amdgpu_buffer_rsrc_t r_q = make_rsrc(p.q_out ? p.q_out + base : p.q_out, p.q_out ? bytes / 4u : 0u);
+    // Per-row scales of this wave's rows (lane r holds row r's), and every residual piece,
+    // before any store: on gfx9 a load issued after stores waits for them.
+    const float sa_l = p.sa_per_row && lane < rows ? p.sA[m0w + lane] : sa0;
+    float4 rv[NB];
+    if (has_r) {
+#pragma unroll
+      for (int it = 0; it < NB; ++it) {
+        const uint32_t off = (uint32_t)(lane * 4 + it * 256) * 4u;
+        if (vec) {
+          rv[it] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r_res, off, 0, 0));
+        } else {
+          rv[it] = make_float4(__builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r_res, off, 0, 0)),
+                               __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r_res, off + 4, 0, 0)),
+                               __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r_res, off + 8, 0, 0)),
+                               __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r_res, off + 12, 0, 0)));
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) pw[(4 * kq + r) * NP + j * 16 + c16] = c[j][r];
+    // The patch is written before any lane reads another lane's values (an asm wait with a
+    // memory clobber: the compiler sees one lane and could move a read above a write).
+    wait_lds();
+    __builtin_amdgcn_wave_barrier();
+    int row = row0, col = col0;
+#pragma unroll
+    for (int it = 0; it < NB; ++it) {
+      if (lane * 4 + it * 256 < 16 * N) {
+        const int4 v = *reinterpret_cast<const int4*>(pw + row * NP + col);
+        const float sa = p.sa_per_row ? __int_as_float(__builtin_amdgcn_ds_bpermute(row * 4, __float_as_int(sa_l)))
+                                      : sa0;
+        const float4 sw4 = *reinterpret_cast<const float4*>(s_sw + col);
+        const float4 b4 = *reinterpret_cast<const float4*>(s_b + col);
+        float4 o;
+        o.x = __fadd_rn(__fmul_rn(__fmul_rn((float)v.x, sa), sw4.x), b4.x);
+        o.y = __fadd_rn(__fmul_rn(__fmul_rn((float)v.y, sa), sw4.y), b4.y);
+        o.z = __fadd_rn(__fmul_rn(__fmul_rn((float)v.z, sa), sw4.z), b4.z);
+        o.w = __fadd_rn(__fmul_rn(__fmul_rn((float)v.w, sa), sw4.w), b4.w);
+        if (has_r) {
+          o.x = __fadd_rn(o.x, rv[it].x); o.y = __fadd_rn(o.y, rv[it].y);
+          o.z = __fadd_rn(o.z, rv[it].z); o.w = __fadd_rn(o.w, rv[it].w);
+        }
+        if (p.act == BQ_ACT_RELU) {
+          o.x = o.x > 0.f ? o.x : 0.f; o.y = o.y > 0.f ? o.y : 0.f;
+          o.z = o.z > 0.f ? o.z : 0.f; o.w = o.w > 0.f ? o.w : 0.f;
+        } else if (p.act == BQ_ACT_SILU) {
+          o.x = silu(o.x); o.y = silu(o.y); o.z = silu(o.z); o.w = silu(o.w);
+        } else if (p.act == BQ_ACT_GELU) {
+          o = gelu4(o);
+        }
+        const uint32_t off = (uint32_t)(lane * 4 + it * 256) * 4u;  // past the block: dropped
+        if (vec) {
+          if (p.out) store_wt16(r_out, off, o);
+          if (p.acc) __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, v), r_acc, off, 0, CPOL_WT);
+          if (p.q_out) store_wt4(r_q, off / 4u, qz_out.pack(o));
+        } else {
+          const float of[4] = {o.x, o.y, o.z, o.w};
+          const int vf[4] = {v.x, v.y, v.z, v.w};
+          const uint32_t qw = p.q_out ? qz_out.pack(o) : 0u;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if (p.out) __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, of[e]), r_out, off + 4 * e, 0, CPOL_WT);
+            if (p.acc) __builtin_amdgcn_raw_buffer_store_b32((uint32_t)vf[e], r_acc, off + 4 * e, 0, CPOL_WT);
+            if (p.q_out) __builtin_amdgcn_raw_buffer_store_b8((uint8_t)(qw >> (8 * e)), r_q, off / 4u + e, 0, CPOL_WT);
+          }
+        }
+        if (row < rows) amax = fmaxf(amax, fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w))));
+      }
+      row += drow;
+      col += dcol;
+      if (col >= N) {
+        col -= N;
+        ++row;
+      }
+    }
+    wait_lds();  // this block's patch reads are done before the next block's writes
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) a[ks] = an[ks];
+  }
+  if (p.amax) {
+    amax = wave_max(amax);
+    if (lane == 0) s_wmax[wave] = amax;
+    __syncthreads();
+    if (tid == 0) p.amax[blockIdx.x] = fmaxf(fmaxf(s_wmax[0], s_wmax[1]), fmaxf(s_wmax[2], s_wmax[3]));
+  }
+}
+
 // GEMV for M <= 8 (the HBM-bound decode shapes): no MFMA. A weight row is read as
 // contiguous 1 KB wave-loads (64 lanes x 16 bytes); each lane dots its 16 weight bytes
 // (v_dot4_i32_i8) against the same 16 bytes of every activation row, which sit in
@@ -1528,7 +1698,9 @@ static bool launch_pair_tiled(GemmP p0, GemmP p1, hipStream_t st, const Ws& ws) 
 struct TileDims {
   int bm, bn;
 };
-constexpr int NCFG = 18;  // ids 1 .. NCFG - 1
+constexpr int NCFG = 18;  // tiled ids 1 .. NCFG - 1
+constexpr int CFG_SMALLK = BQ_CFG_SMALLK;  // smallk_i8_kernel (dense)
+static_assert(CFG_SMALLK == NCFG, "the small-K kernel's id follows the tiled ids");
 constexpr TileDims CFG_TILES[NCFG] = {{0, 0},    {256, 256}, {256, 256}, {256, 256}, {128, 128}, {128, 128},
                                       {256, 128}, {64, 64},   {256, 64},  {64, 64},   {64, 64},   {128, 64},
                                       {128, 32},  {256, 64},  {128, 64},  {256, 256}, {320, 256}, {128, 256}};
@@ -1549,8 +1721,28 @@ constexpr TileDims CFG_TILES[NCFG] = {{0, 0},    {256, 256}, {256, 256}, {256, 2
 // sustain a higher rate than 32x32x32 at the power limit (4096^3: 67-69 against 73-75 us);
 // its convolution form keeps 32x32x32, which needs fewer fragment registers next to the
 // implicit-GEMM addressing (the 16x16 form spills there).
+// Whether the small-K kernel takes a problem (its shape only: an unaligned output takes
+// its four-byte stores), and its grid.
+static bool smallk_ok(const GemmP& p, bool conv) {
+  return !conv && !p.stamps && p.M >= 1 && p.N >= 4 && p.N <= 64 && p.N % 4 == 0 && p.K <= 256 &&
+         (long long)p.M * p.K < (1ll << 31);
+}
+static int smallk_grid(const GemmP& p) {
+  const long long steps = (p.M + SMALLK_ROWS - 1) / SMALLK_ROWS;
+  return (int)std::min<long long>(steps, steps >= 8192 ? 2048 : 1024);
+}
+
 static int choose_cfg(const GemmP& p, bool conv) {
-  if (p.plan_cfg >= 1 && p.plan_cfg < NCFG) return p.plan_cfg;
+  if (p.plan_cfg == CFG_SMALLK) {
+    if (smallk_ok(p, conv)) return CFG_SMALLK;
+  } else if (p.plan_cfg >= 1 && p.plan_cfg < NCFG) {
+    return p.plan_cfg;
+  }
+  // A narrow output over many rows (a 1x1 projection to a few channels): the small-K
+  // kernel (EfficientNet-B0 b64: 802816 x 16 x 32 34.3 -> 10.7 us, 200704 x 24 x 96 11.9 ->
+  // 8.1 us, 200704 x 24 x 144 17.1 -> 12.8 us; from 40 columns, or at 50176 rows, the tiled
+  // kernel was faster).
+  if (smallk_ok(p, conv) && p.N <= 32 && p.M >= 131072) return CFG_SMALLK;
   const long long t256 = (long long)((p.M + 255) / 256) * ((p.N + 255) / 256);
   const long long t128 = (long long)((p.M + 127) / 128) * ((p.N + 127) / 128);
   const long long t128x32 = (long long)((p.M + 127) / 128) * ((p.N + 31) / 32);
@@ -1568,8 +1760,24 @@ static int choose_cfg(const GemmP& p, bool conv) {
 
 // Output tiles of the tiled kernel for this problem (the length of its absmax output).
 static long long out_tiles(const GemmP& p, bool conv) {
-  const TileDims d = CFG_TILES[choose_cfg(p, conv)];
+  const int cfg = choose_cfg(p, conv);
+  if (cfg == CFG_SMALLK) return smallk_grid(p);  // one maximum a workgroup
+  const TileDims d = CFG_TILES[cfg];
   return (long long)((p.M + d.bm - 1) / d.bm) * ((p.N + d.bn - 1) / d.bn);
+}
+
+static void launch_smallk(const GemmP& p, hipStream_t st) {
+  const dim3 grid((unsigned)smallk_grid(p));
+  const int NB = (p.N + 15) / 16, KS = (p.K + 63) / 64;
+  switch ((NB - 1) * 4 + (KS - 1)) {
+#define BQ_SMALLK(nb, ks) \
+  case (nb - 1) * 4 + (ks - 1): smallk_i8_kernel<nb, ks><<<grid, 256, 0, st>>>(p); break;
+    BQ_SMALLK(1, 1) BQ_SMALLK(1, 2) BQ_SMALLK(1, 3) BQ_SMALLK(1, 4)
+    BQ_SMALLK(2, 1) BQ_SMALLK(2, 2) BQ_SMALLK(2, 3) BQ_SMALLK(2, 4)
+    BQ_SMALLK(3, 1) BQ_SMALLK(3, 2) BQ_SMALLK(3, 3) BQ_SMALLK(3, 4)
+    BQ_SMALLK(4, 1) BQ_SMALLK(4, 2) BQ_SMALLK(4, 3) BQ_SMALLK(4, 4)
+#undef BQ_SMALLK
+  }
 }
 
 template <bool CONV>
@@ -1590,6 +1798,9 @@ static void launch_gemm(const GemmP& p, hipStream_t st, const Ws& ws) {
     case 17: return launch_tiled<128, 256, 2, 4, CONV, 2, 2>(p, st, ws);
     case 16:  // dense only (the implicit-GEMM loader does not fit beside its 160 accumulators)
       if constexpr (!CONV) return launch_tiled<320, 256, 2, 4, CONV, 2, 1>(p, st, ws);
+      [[fallthrough]];
+    case CFG_SMALLK:  // dense only (choose_cfg offers it for no conv)
+      if constexpr (!CONV) return launch_smallk(p, st);
       [[fallthrough]];
     default: return launch_tiled<64, 64, 2, 2, CONV, 4, 2>(p, st, ws);
   }
@@ -1965,7 +2176,8 @@ int bq_plan_candidates(const int64_t* problem, int n, int32_t* cfgs, int32_t* sp
   std::pair<int, int> out[64];
   int cnt = 0;
   const int rule = choose_cfg(p, conv);
-  out[cnt++] = {rule, split_of(p, rule, conv, 0)};
+  out[cnt++] = {rule, rule == CFG_SMALLK ? 1 : split_of(p, rule, conv, 0)};
+  if (rule != CFG_SMALLK && smallk_ok(p, conv)) out[cnt++] = {CFG_SMALLK, 1};
   // 3 (four waves on 256x256) and 9 (64x64 with an 8-deep ring) never won a measurement
   static const int ids[] = {1, 2, 4, 5, 6, 7, 8, 10, 11, 12, 13, 14, 15, 16, 17};
   for (int cfg : ids) {
@@ -2006,6 +2218,13 @@ int bq_plan_set(const int64_t* problem, int n, int32_t cfg, int32_t split) {
                        "rows: BQ_CFG_GEMV or BQ_CFG_SKINNY, split 1)", DECODE_MAX_M);
     if (cfg == BQ_CFG_GEMV && p.K > (p.M <= 4 ? 8192 : 4096))
       return set_error(BQ_ERR_ARG, "bq_plan_set: the GEMV takes K <= %d at M = %d", p.M <= 4 ? 8192 : 4096, p.M);
+    g_plans[key] = Plan{cfg, split};
+    return BQ_OK;
+  }
+  if (cfg == CFG_SMALLK) {
+    if (!smallk_ok(p, conv) || split != 1)
+      return set_error(BQ_ERR_ARG, "bq_plan_set: BQ_CFG_SMALLK takes a dense problem (or a 1x1 stride-1 unpadded "
+                       "conv) of N <= 64 (N %% 4 == 0) and K <= 256, split 1");
     g_plans[key] = Plan{cfg, split};
     return BQ_OK;
   }
