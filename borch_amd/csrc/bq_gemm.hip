@@ -44,9 +44,10 @@ struct GemmP {
   int32_t* acc;  // [M, N] or null
   // conv geometry (CONV only)
   int H, Wd, C, OH, OW, KWd, stride, pad;
-  // k / C and tap / KW of the implicit im2col as multiply-high and shift (FastDiv)
-  uint32_t c_mul, kw_mul;
-  int c_shift, kw_shift;
+  // k / C and tap / KW of the implicit im2col as multiply-high and shift (FastDiv), and
+  // m / (OH OW) and r / OW (the small-K kernel's per-row decomposition)
+  uint32_t c_mul, kw_mul, plane_mul, ow_mul;
+  int c_shift, kw_shift, plane_shift, ow_shift;
   int64_t Nimg_HWC;  // conv: bytes of the NHWC activation
   int vec_ok;        // N % 4 == 0 and out/res/acc 16-byte aligned: float4 epilogue
   const float* s_out;  // static output scale [1] (nullable): the int8 twin of the output
@@ -896,9 +897,11 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_i8_kernel(const GemmP p) {
 
 // ----------------------------------------------------------------------------- small K
 
-// Dense GEMM for a narrow output (N <= 64, N % 4 == 0) and a short K (<= 256) over many
-// rows: a 1x1 conv's projection to a few channels (EfficientNet-B0 b64's blocks.0.project,
-// 802816 x 16 x 32). The tiled kernel's tiles spend most of their time outside their MFMAs
+// GEMM for a narrow output (N <= 64, N % 4 == 0) and a short K (<= 256) over many rows: a
+// 1x1 conv's projection to a few channels (EfficientNet-B0 b64's blocks.0.project,
+// 802816 x 16 x 32), or with CONV an implicit-GEMM conv of that shape (its stem: 3x3 / 2
+// over 16 padded channels into 32, 802816 rows, each lane's 16-byte chunk of a row at the
+// tap its K offset names). The tiled kernel's tiles spend most of their time outside their MFMAs
 // there (a 128 x 32 tile for 16 output columns, one K stage). Here the weight fragments stay
 // in registers for the whole launch; each wave takes 16 rows a step (v_mfma_i32_16x16x64_i8
 // against NB 16-column blocks and KS 64-byte K steps; lane l holds row l % 16 and K chunk
@@ -909,7 +912,7 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_i8_kernel(const GemmP p) {
 // the 64-row steps; each writes one max |y| (p.amax). Unaligned outputs take four-byte
 // stores instead.
 constexpr int SMALLK_ROWS = 64;  // rows a workgroup step: 4 waves x 16
-template <int NB, int KS>
+template <int NB, int KS, bool CONV>
 __global__ __launch_bounds__(256) void smallk_i8_kernel(const GemmP p) {
   constexpr int NP = NB * 16 + 4;  // patch pitch (ints): 4 NP % 64 == 16, conflict-free writes
   __shared__ __attribute__((aligned(16))) int patch[4][16 * NP];
@@ -920,7 +923,21 @@ __global__ __launch_bounds__(256) void smallk_i8_kernel(const GemmP p) {
   const int M = p.M, N = p.N, K = p.K;
   const int steps = (M + SMALLK_ROWS - 1) / SMALLK_ROWS;
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.W, (uint32_t)(N * K));
-  const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, (uint32_t)(M * K));
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, CONV ? (uint32_t)p.Nimg_HWC : (uint32_t)(M * K));
+  // CONV: this lane's K chunks as (filter row, filter column, channel offset); a chunk past K
+  // gets a row offset no input row passes
+  int t_kh[KS], t_kw[KS], t_c0[KS];
+  if constexpr (CONV) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int k = ks * 64 + kq * 16;
+      const int tap = fdiv(k, p.c_mul, p.c_shift);
+      t_c0[ks] = k - tap * p.C;
+      t_kh[ks] = fdiv(tap, p.kw_mul, p.kw_shift);
+      t_kw[ks] = tap - t_kh[ks] * p.KWd;
+      if (k >= K) t_kh[ks] = -(1 << 20);
+    }
+  }
   v4i b[NB][KS];
 #pragma unroll
   for (int j = 0; j < NB; ++j) {
@@ -945,10 +962,25 @@ __global__ __launch_bounds__(256) void smallk_i8_kernel(const GemmP p) {
   float amax = 0.f;
   auto load_a = [&](v4i (&a)[KS], int t) {
     const int row = t * SMALLK_ROWS + wave * 16 + c16;
+    const bool live = t < steps && row < M;
+    if constexpr (CONV) {
+      const int n = fdiv(row, p.plane_mul, p.plane_shift);
+      const int r = row - n * p.OH * p.OW;
+      const int oh = fdiv(r, p.ow_mul, p.ow_shift);
+      const int ih0 = oh * p.stride - p.pad, iw0 = (r - oh * p.OW) * p.stride - p.pad;
+      const uint32_t img = (uint32_t)(n * p.H * p.Wd * p.C);
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const int k = ks * 64 + kq * 16;
-      a[ks] = buf_load16(ra, (t < steps && row < M && k < K) ? (uint32_t)(row * K + k) : OOB);
+      for (int ks = 0; ks < KS; ++ks) {
+        const int ih = ih0 + t_kh[ks], iw = iw0 + t_kw[ks];
+        const bool ok = live && (unsigned)ih < (unsigned)p.H && (unsigned)iw < (unsigned)p.Wd;
+        a[ks] = buf_load16(ra, ok ? img + (uint32_t)((ih * p.Wd + iw) * p.C + t_c0[ks]) : OOB);
+      }
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int k = ks * 64 + kq * 16;
+        a[ks] = buf_load16(ra, (live && k < K) ? (uint32_t)(row * K + k) : OOB);
+      }
     }
   };
   v4i a[KS];
@@ -1724,8 +1756,8 @@ constexpr TileDims CFG_TILES[NCFG] = {{0, 0},    {256, 256}, {256, 256}, {256, 2
 // Whether the small-K kernel takes a problem (its shape only: an unaligned output takes
 // its four-byte stores), and its grid.
 static bool smallk_ok(const GemmP& p, bool conv) {
-  return !conv && !p.stamps && p.M >= 1 && p.N >= 4 && p.N <= 64 && p.N % 4 == 0 && p.K <= 256 &&
-         (long long)p.M * p.K < (1ll << 31);
+  return !p.stamps && p.M >= 1 && p.N >= 4 && p.N <= 64 && p.N % 4 == 0 && p.K <= 256 &&
+         (conv || (long long)p.M * p.K < (1ll << 31));
 }
 static int smallk_grid(const GemmP& p) {
   const long long steps = (p.M + SMALLK_ROWS - 1) / SMALLK_ROWS;
@@ -1738,10 +1770,10 @@ static int choose_cfg(const GemmP& p, bool conv) {
   } else if (p.plan_cfg >= 1 && p.plan_cfg < NCFG) {
     return p.plan_cfg;
   }
-  // A narrow output over many rows (a 1x1 projection to a few channels): the small-K
-  // kernel (EfficientNet-B0 b64: 802816 x 16 x 32 34.3 -> 10.7 us, 200704 x 24 x 96 11.9 ->
-  // 8.1 us, 200704 x 24 x 144 17.1 -> 12.8 us; from 40 columns, or at 50176 rows, the tiled
-  // kernel was faster).
+  // A narrow output over many rows (a 1x1 projection to a few channels, a stem conv): the
+  // small-K kernel (EfficientNet-B0 b64: 802816 x 16 x 32 34.3 -> 10.7 us, 200704 x 24 x 96
+  // 11.9 -> 8.1 us, 200704 x 24 x 144 17.1 -> 12.8 us; from 40 columns, or at 50176 rows,
+  // the tiled kernel was faster).
   if (smallk_ok(p, conv) && p.N <= 32 && p.M >= 131072) return CFG_SMALLK;
   const long long t256 = (long long)((p.M + 255) / 256) * ((p.N + 255) / 256);
   const long long t128 = (long long)((p.M + 127) / 128) * ((p.N + 127) / 128);
@@ -1766,12 +1798,13 @@ static long long out_tiles(const GemmP& p, bool conv) {
   return (long long)((p.M + d.bm - 1) / d.bm) * ((p.N + d.bn - 1) / d.bn);
 }
 
+template <bool CONV>
 static void launch_smallk(const GemmP& p, hipStream_t st) {
   const dim3 grid((unsigned)smallk_grid(p));
   const int NB = (p.N + 15) / 16, KS = (p.K + 63) / 64;
   switch ((NB - 1) * 4 + (KS - 1)) {
 #define BQ_SMALLK(nb, ks) \
-  case (nb - 1) * 4 + (ks - 1): smallk_i8_kernel<nb, ks><<<grid, 256, 0, st>>>(p); break;
+  case (nb - 1) * 4 + (ks - 1): smallk_i8_kernel<nb, ks, CONV><<<grid, 256, 0, st>>>(p); break;
     BQ_SMALLK(1, 1) BQ_SMALLK(1, 2) BQ_SMALLK(1, 3) BQ_SMALLK(1, 4)
     BQ_SMALLK(2, 1) BQ_SMALLK(2, 2) BQ_SMALLK(2, 3) BQ_SMALLK(2, 4)
     BQ_SMALLK(3, 1) BQ_SMALLK(3, 2) BQ_SMALLK(3, 3) BQ_SMALLK(3, 4)
@@ -1799,9 +1832,7 @@ static void launch_gemm(const GemmP& p, hipStream_t st, const Ws& ws) {
     case 16:  // dense only (the implicit-GEMM loader does not fit beside its 160 accumulators)
       if constexpr (!CONV) return launch_tiled<320, 256, 2, 4, CONV, 2, 1>(p, st, ws);
       [[fallthrough]];
-    case CFG_SMALLK:  // dense only (choose_cfg offers it for no conv)
-      if constexpr (!CONV) return launch_smallk(p, st);
-      [[fallthrough]];
+    case CFG_SMALLK: return launch_smallk<CONV>(p, st);
     default: return launch_tiled<64, 64, 2, 2, CONV, 4, 2>(p, st, ws);
   }
 }
@@ -2108,6 +2139,8 @@ static int conv_setup(const char* what, const int8_t* x, int64_t N, int64_t H, i
   p.stride = (int)stride; p.pad = (int)pad;
   const FastDiv dc = fast_div((uint32_t)C), dkw = fast_div((uint32_t)KW);
   p.c_mul = dc.mul; p.c_shift = dc.shift; p.kw_mul = dkw.mul; p.kw_shift = dkw.shift;
+  const FastDiv dpl = fast_div((uint32_t)(OH * OW)), dow = fast_div((uint32_t)OW);
+  p.plane_mul = dpl.mul; p.plane_shift = dpl.shift; p.ow_mul = dow.mul; p.ow_shift = dow.shift;
   p.Nimg_HWC = N * H * W * C;
   p.vec_ok = (O % 4 == 0) && aligned16(out) && aligned16(acc) && aligned16(residual) && ((uintptr_t)q_out & 3) == 0;
   p.s_out = s_out;
@@ -2223,8 +2256,8 @@ int bq_plan_set(const int64_t* problem, int n, int32_t cfg, int32_t split) {
   }
   if (cfg == CFG_SMALLK) {
     if (!smallk_ok(p, conv) || split != 1)
-      return set_error(BQ_ERR_ARG, "bq_plan_set: BQ_CFG_SMALLK takes a dense problem (or a 1x1 stride-1 unpadded "
-                       "conv) of N <= 64 (N %% 4 == 0) and K <= 256, split 1");
+      return set_error(BQ_ERR_ARG, "bq_plan_set: BQ_CFG_SMALLK takes a problem of N <= 64 (N %% 4 == 0) and "
+                       "K <= 256, split 1");
     g_plans[key] = Plan{cfg, split};
     return BQ_OK;
   }

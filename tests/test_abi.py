@@ -171,16 +171,22 @@ def _candidates(lib, problem):
                                      (64, 112, 112, 32, 96, 1, 1, 1, 0), (2, 13, 13, 16, 24, 3, 3, 2, 1)])
 def test_plan_candidates(problem):
     """The kernel-choice candidates (host code, no GPU): the rules' pick first, no pair twice,
-    configuration ids of the tiled kernel only (3 and 9 are never offered, 16 only for a dense
-    GEMM), K splits only on tiles of at most 4096 outputs, and never more splits than K
-    stages."""
+    configuration ids of the tiled kernel (3 and 9 are never offered, 16 only for a dense
+    GEMM) and the small-K kernel (only where N <= 64, N % 4 == 0 and K <= 256, unsplit), K
+    splits only on tiles of at most 4096 outputs, and never more splits than K stages."""
     from borch_amd import _lib
     lib = _lib.lib()
     cands = _candidates(lib, problem)
     assert isinstance(cands, list) and len(cands) >= 2
     assert len(set(cands)) == len(cands)
     small = {7, 9, 10, 12}  # tiles of 64 x 64 and 128 x 32 outputs
+    N, K = (problem[1], problem[2]) if len(problem) == 3 else (problem[4], problem[3] * problem[5] * problem[6])
+    smallk_ok = N <= 64 and N % 4 == 0 and K <= 256
+    assert ((_lib.CFG_SMALLK, 1) in cands) == smallk_ok
     for cfg, split in cands:
+        if cfg == _lib.CFG_SMALLK:
+            assert split == 1
+            continue
         assert 1 <= cfg <= 17 and split >= 1
         assert cfg not in (3, 9) or (cfg, split) == cands[0]
         # 16 only where the dense loader runs: a GEMM or a 1x1 stride-1 unpadded conv

@@ -128,6 +128,44 @@ def test_conv_twin_and_maxima(dev, no_plans, Nimg, H, C, O_):
         assert torch.equal(outs[0][3], outs[0][0]) and torch.equal(outs[0][4], outs[0][5])
 
 
+# (N, H, W, C, O, k, stride, pad): EfficientNet-B0 b64's stem (the rule's pick), then
+# strides, paddings, ragged images and K steps, 2x2 and 4x4 filters (K <= 256)
+CONV_CASES = [(64, 224, 224, 16, 32, 3, 2, 1), (2, 40, 40, 16, 32, 3, 2, 1), (3, 17, 13, 16, 20, 3, 1, 1),
+              (2, 15, 15, 32, 64, 2, 2, 0), (1, 23, 19, 16, 48, 4, 1, 2), (2, 12, 12, 16, 8, 2, 3, 1),
+              (4, 9, 9, 96, 12, 1, 2, 0), (2, 11, 11, 16, 4, 4, 4, 0)]
+
+
+@pytest.mark.parametrize("Nimg,H,W,C,O_,k,stride,pad", CONV_CASES)
+def test_implicit_gemm_conv(dev, no_plans, Nimg, H, W, C, O_, k, stride, pad):
+    """Implicit-GEMM convs under the small-K plan against the tiled kernel (f32 output,
+    accumulators, maxima, residual and SiLU), and the small ones against the oracle."""
+    T = no_plans
+    say(f"small-K conv N={Nimg} H={H} W={W} C={C} O={O_} k={k} s={stride} p={pad}")
+    rng = np.random.default_rng(Nimg + H + W + C + O_ + k)
+    x = rng.integers(-127, 128, size=(Nimg, H, W, C)).astype(np.int8)
+    qx = t(x, dev)
+    sa = t(np.array([0.011], np.float32), dev)
+    wf = (rng.normal(size=(O_, C, k, k)) * 0.1).astype(np.float32)
+    w8 = I.pack_conv_weight(t(wf, dev))
+    b = t(rng.normal(size=O_).astype(np.float32), dev)
+    OH, OW = (H + 2 * pad - k) // stride + 1, (W + 2 * pad - k) // stride + 1
+    r = t(rng.normal(size=(Nimg, O_, OH, OW)).astype(np.float32), dev).contiguous(memory_format=torch.channels_last)
+    problem = (Nimg, H, W, C, O_, k, k, stride, pad)
+    if Nimg * OH * OW >= 131072 and O_ <= 32:
+        assert T.candidates(problem)[0] == (SMALLK, 1)
+    outs = []
+    for cfg in (SMALLK, 12):
+        T.set_plan(problem, cfg, 1)
+        y, acc = I.conv2d_i8_nhwc(qx, sa, w8, stride, pad, b, r, I.ACT_SILU, want_acc=True)
+        parts, nparts, _ = y._bq_absmax
+        outs.append((y, acc, parts[:nparts].max()))
+    for a_, b_ in zip(outs[0], outs[1]):
+        assert torch.equal(a_, b_)
+    if Nimg * OH * OW <= 4096:
+        acc_o, _, _ = O.conv2d_i8_nhwc(x, n(w8.q), k, k, stride, pad)
+        assert np.array_equal(n(outs[0][1]), acc_o)
+
+
 def test_unaligned_outputs(dev, no_plans):
     """Output, accumulator and residual pointers 4 bytes off 16-byte alignment (the C ABI
     takes any float pointer): the small-K kernel's four-byte stores give the tiled kernel's
@@ -164,7 +202,8 @@ def test_plan_set_refuses_what_it_does_not_take(dev, no_plans):
     with pytest.raises(ValueError):
         T.set_plan((1000, 32, 272), SMALLK, 1)  # K > 256
     with pytest.raises(ValueError):
-        T.set_plan((2, 32, 32, 16, 32, 3, 3, 1, 1), SMALLK, 1)  # an implicit-GEMM conv
+        T.set_plan((2, 32, 32, 32, 32, 3, 3, 1, 1), SMALLK, 1)  # a conv of K = 288
     with pytest.raises(ValueError):
         T.set_plan((1000, 32, 64), SMALLK, 2)   # split
     T.set_plan((2, 32, 32, 16, 32, 1, 1, 1, 0), SMALLK, 1)  # a 1x1 stride-1 unpadded conv
+    T.set_plan((2, 32, 32, 16, 32, 3, 3, 2, 1), SMALLK, 1)  # an implicit-GEMM conv of K = 144
