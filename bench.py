@@ -477,6 +477,18 @@ def hbm_kernels(dev):
     for _ in range(3):
         I.quantize_nhwc(x, 144)
     ran["quantize_nhwc 64x144x56x56 two-pass (3x)"] = 64 * 144 * 56 * 56 * 9
+    del x
+    # the small-K kernel (the rule's pick): EfficientNet-B0 b64's blocks.0.project (1x1, 32 -> 16
+    # channels at 112^2) and its stem (3x3 / 2, 16 padded channels -> 32 at 224^2), f32 out
+    sa1 = torch.tensor([0.02], device=dev)
+    for (H, C, O_, k, st, pad) in ((112, 32, 16, 1, 1, 0), (224, 16, 32, 3, 2, 1)):
+        qx = torch.randint(-127, 128, (64, H, H, C), generator=g, dtype=torch.int8).to(dev)
+        w8 = I.pack_conv_weight(torch.randn(O_, C, k, k, generator=g).to(dev))
+        OH = (H + 2 * pad - k) // st + 1
+        for _ in range(3):
+            I.conv2d_i8_nhwc(qx, sa1, w8, st, pad, None, None, I.ACT_NONE)
+        ran[f"conv {k}x{k}/{st} {C}->{O_} at {H}^2 b64 (3x)"] = 64 * H * H * C + 64 * OH * OH * O_ * 4 + O_ * k * k * C
+        del qx
     src = torch.randn(16 << 20, device=dev)
     dst = torch.empty_like(src)
     for _ in range(5):
