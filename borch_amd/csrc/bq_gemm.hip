@@ -897,26 +897,23 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_i8_kernel(const GemmP p) {
 
 // ----------------------------------------------------------------------------- small K
 
-// GEMM for a narrow output (N <= 64, N % 4 == 0) and a short K (<= 256) over many rows: a
-// 1x1 conv's projection to a few channels (EfficientNet-B0 b64's blocks.0.project,
-// 802816 x 16 x 32), or with CONV an implicit-GEMM conv of that shape (its stem: 3x3 / 2
-// over 16 padded channels into 32, 802816 rows, each lane's 16-byte chunk of a row at the
-// tap its K offset names). The tiled kernel's tiles spend most of their time outside their MFMAs
-// there (a 128 x 32 tile for 16 output columns, one K stage). Here the weight fragments stay
-// in registers for the whole launch; each wave takes 16 rows a step (v_mfma_i32_16x16x64_i8
-// against NB 16-column blocks and KS 64-byte K steps; lane l holds row l % 16 and K chunk
-// l / 16 of an operand, and result register r is row 4 (l / 16) + r, column l % 16),
-// loads its next step's activation rows before this step's MFMAs, and writes its 16 x N
-// results, contiguous in memory, as 16-byte pieces through a per-wave LDS patch (the
-// epilogue arithmetic of the tiled kernel's, in the same order). Workgroups stride over
-// the 64-row steps; each writes one max |y| (p.amax). Unaligned outputs take four-byte
-// stores instead.
+// GEMM for a narrow output (N <= 160, N % 4 == 0) and a short K (<= 256) over many rows: a
+// 1x1 conv's projection or expansion over a large image (EfficientNet-B0 b64's
+// blocks.1.expand, 802816 x 96 x 16), or with CONV an implicit-GEMM conv of that shape (its
+// stem: 3x3 / 2 over 16 padded channels into 32, each lane's 16-byte chunk of a row at the
+// tap its K offset names). The tiled kernel spends most of its time outside its MFMAs there
+// (one K stage, a 128 x 128 tile for 96 columns). Here the weight fragments stay in
+// registers for the whole launch, and each wave takes 16 rows a step: the weight is the
+// MFMA's first operand and the activation rows its second (v_mfma_i32_16x16x64_i8; lane l
+// holds row l % 16 and K chunk l / 16 of each), so lane l's four results of 16-column block
+// j are columns 16 j + 4 (l / 16) .. + 3 of row l % 16, four consecutive outputs it stores
+// as one 16-byte piece straight from the accumulators (the epilogue arithmetic of the
+// tiled kernel's, in the same order). The next step's activation rows load before this
+// step's MFMAs, its residual pieces before its stores. Workgroups stride over the 64-row
+// steps; each writes one max |y| (p.amax). Unaligned outputs take four-byte stores.
 constexpr int SMALLK_ROWS = 64;  // rows a workgroup step: 4 waves x 16
 template <int NB, int KS, bool CONV>
 __global__ __launch_bounds__(256) void smallk_i8_kernel(const GemmP p) {
-  constexpr int NP = NB * 16 + 4;  // patch pitch (ints): 4 NP % 64 == 16, conflict-free writes
-  __shared__ __attribute__((aligned(16))) int patch[4][16 * NP];
-  __shared__ __attribute__((aligned(16))) float s_sw[NB * 16], s_b[NB * 16];
   __shared__ float s_wmax[4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c16 = lane & 15, kq = lane >> 4;
@@ -924,6 +921,22 @@ __global__ __launch_bounds__(256) void smallk_i8_kernel(const GemmP p) {
   const int steps = (M + SMALLK_ROWS - 1) / SMALLK_ROWS;
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.W, (uint32_t)(N * K));
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, CONV ? (uint32_t)p.Nimg_HWC : (uint32_t)(M * K));
+  v4i b[NB][KS];
+  float4 e_sw[NB], e_b[NB];  // the scales and bias of this lane's four columns of block j
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    const int n = j * 16 + c16;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int k = ks * 64 + kq * 16;
+      b[j][ks] = buf_load16(rw, (n < N && k < K) ? (uint32_t)(n * K + k) : OOB);
+    }
+    const int n0 = j * 16 + 4 * kq;
+    e_sw[j] = n0 < N ? make_float4(p.sW[n0], p.sW[n0 + 1], p.sW[n0 + 2], p.sW[n0 + 3]) : make_float4(0.f, 0.f, 0.f, 0.f);
+    // 0 without bias: y + 0.0f == y for every y this produces
+    e_b[j] = (n0 < N && p.bias) ? make_float4(p.bias[n0], p.bias[n0 + 1], p.bias[n0 + 2], p.bias[n0 + 3])
+                                : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
   // CONV: this lane's K chunks as (filter row, filter column, channel offset); a chunk past K
   // gets a row offset no input row passes
   int t_kh[KS], t_kw[KS], t_c0[KS];
@@ -938,27 +951,17 @@ __global__ __launch_bounds__(256) void smallk_i8_kernel(const GemmP p) {
       if (k >= K) t_kh[ks] = -(1 << 20);
     }
   }
-  v4i b[NB][KS];
-#pragma unroll
-  for (int j = 0; j < NB; ++j) {
-    const int n = j * 16 + c16;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const int k = ks * 64 + kq * 16;
-      b[j][ks] = buf_load16(rw, (n < N && k < K) ? (uint32_t)(n * K + k) : OOB);
-    }
-  }
-  if (tid < NB * 16) {
-    s_sw[tid] = tid < N ? p.sW[tid] : 0.f;
-    s_b[tid] = (tid < N && p.bias) ? p.bias[tid] : 0.f;  // 0 without bias: y + 0.0f == y here
-  }
   const float sa0 = p.sa_per_row ? 0.f : p.sA[0];
   const Quantizer qz_out(p.q_out ? p.s_out[0] : 0.f);
-  // This lane's first (row, column) in a wave's 16 x N block, read as 16-byte pieces 256
-  // values apart, and the step between its pieces.
-  const int row0 = (lane * 4) / N, col0 = lane * 4 - row0 * N;
-  const int drow = 256 / N, dcol = 256 - drow * N;
   const bool has_r = p.res != nullptr, vec = p.vec_ok;
+  // Write-through stores measured faster up to 96 columns, plain ones above (802816 x 96:
+  // 65.8 against 107.1 us; 200704 x 144: 30.2 against 27.0 us).
+  const bool wt = N <= 96;
+  const uint32_t out_bytes = (uint32_t)std::min<long long>((long long)M * N * 4, 0x7fffffff);
+  const __amdgpu_buffer_rsrc_t r_out = make_rsrc(p.out, p.out ? out_bytes : 0u);
+  const __amdgpu_buffer_rsrc_t r_acc = make_rsrc(p.acc, p.acc ? out_bytes : 0u);
+  const __amdgpu_buffer_rsrc_t r_res = make_rsrc(p.res, has_r ? out_bytes : 0u);
+  const __amdgpu_buffer_rsrc_t r_q = make_rsrc(p.q_out, p.q_out ? out_bytes / 4u : 0u);
   float amax = 0.f;
   auto load_a = [&](v4i (&a)[KS], int t) {
     const int row = t * SMALLK_ROWS + wave * 16 + c16;
@@ -986,105 +989,74 @@ __global__ __launch_bounds__(256) void smallk_i8_kernel(const GemmP p) {
   v4i a[KS];
   int t = blockIdx.x;
   load_a(a, t);
-  __syncthreads();  // the scales and bias are staged
-  int* const pw = patch[wave];
   for (; t < steps; t += gridDim.x) {
     v4i an[KS];
     load_a(an, t + gridDim.x);
-    v4i c[NB];
-#pragma unroll
-    for (int j = 0; j < NB; ++j) {
-      c[j] = v4i{};
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) c[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[ks], b[j][ks], c[j], 0, 0, 0);
-    }
-    const int m0w = t * SMALLK_ROWS + wave * 16;
-    const int rows = min(16, M - m0w);  // <= 0 past M (the last step's later waves): all dropped
-    const size_t base = (size_t)m0w * N;
-    const uint32_t bytes = rows > 0 ? (uint32_t)(rows * N) * 4u : 0u;
-    const __amdgpu_buffer_rsrc_t r_out = make_rsrc(p.out ? p.out + base : p.out, p.out ? bytes : 0u);
-    const __amdgpu_buffer_rsrc_t r_res = make_rsrc(has_r ? p.res + base : p.res, has_r ? bytes : 0u);
-    const __amdgpu_buffer_rsrc_t r_acc = make_rsrc(p.acc ? p.acc + base : p.acc, p.acc ? bytes : 0u);
-    const __amdgpu_buffer_rsrc_t r_q = make_rsrc(p.q_out ? p.q_out + base : p.q_out, p.q_out ? bytes / 4u : 0u);
-    // Per-row scales of this wave's rows (lane r holds row r's), and every residual piece,
-    // before any store: on gfx9 a load issued after stores waits for them.
-    const float sa_l = p.sa_per_row && lane < rows ? p.sA[m0w + lane] : sa0;
-    float4 rv[NB];
+    const int m = t * SMALLK_ROWS + wave * 16 + c16;  // this lane's row
+    const bool live = m < M;
+    const float sa = p.sa_per_row ? (live ? p.sA[m] : 0.f) : sa0;
+    // the row's residual pieces, all before any store (on gfx9 a load issued after stores
+    // waits for them); past M or N the range check gives zeros
+    float4 rv[NB] = {};
     if (has_r) {
 #pragma unroll
-      for (int it = 0; it < NB; ++it) {
-        const uint32_t off = (uint32_t)(lane * 4 + it * 256) * 4u;
+      for (int j = 0; j < NB; ++j) {
+        const int n0 = j * 16 + 4 * kq;
+        const uint32_t off = live && n0 < N ? (uint32_t)((size_t)m * N + n0) * 4u : OOB;
         if (vec) {
-          rv[it] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r_res, off, 0, 0));
+          rv[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r_res, off, 0, 0));
         } else {
-          rv[it] = make_float4(__builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r_res, off, 0, 0)),
-                               __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r_res, off + 4, 0, 0)),
-                               __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r_res, off + 8, 0, 0)),
-                               __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r_res, off + 12, 0, 0)));
+          rv[j] = make_float4(__builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r_res, off, 0, 0)),
+                              __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r_res, off + 4, 0, 0)),
+                              __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r_res, off + 8, 0, 0)),
+                              __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r_res, off + 12, 0, 0)));
         }
       }
     }
 #pragma unroll
-    for (int j = 0; j < NB; ++j)
+    for (int j = 0; j < NB; ++j) {
+      v4i c = v4i{};
 #pragma unroll
-      for (int r = 0; r < 4; ++r) pw[(4 * kq + r) * NP + j * 16 + c16] = c[j][r];
-    // The patch is written before any lane reads another lane's values (an asm wait with a
-    // memory clobber: the compiler sees one lane and could move a read above a write).
-    wait_lds();
-    __builtin_amdgcn_wave_barrier();
-    int row = row0, col = col0;
-#pragma unroll
-    for (int it = 0; it < NB; ++it) {
-      if (lane * 4 + it * 256 < 16 * N) {
-        const int4 v = *reinterpret_cast<const int4*>(pw + row * NP + col);
-        const float sa = p.sa_per_row ? __int_as_float(__builtin_amdgcn_ds_bpermute(row * 4, __float_as_int(sa_l)))
-                                      : sa0;
-        const float4 sw4 = *reinterpret_cast<const float4*>(s_sw + col);
-        const float4 b4 = *reinterpret_cast<const float4*>(s_b + col);
-        float4 o;
-        o.x = __fadd_rn(__fmul_rn(__fmul_rn((float)v.x, sa), sw4.x), b4.x);
-        o.y = __fadd_rn(__fmul_rn(__fmul_rn((float)v.y, sa), sw4.y), b4.y);
-        o.z = __fadd_rn(__fmul_rn(__fmul_rn((float)v.z, sa), sw4.z), b4.z);
-        o.w = __fadd_rn(__fmul_rn(__fmul_rn((float)v.w, sa), sw4.w), b4.w);
-        if (has_r) {
-          o.x = __fadd_rn(o.x, rv[it].x); o.y = __fadd_rn(o.y, rv[it].y);
-          o.z = __fadd_rn(o.z, rv[it].z); o.w = __fadd_rn(o.w, rv[it].w);
-        }
-        if (p.act == BQ_ACT_RELU) {
-          o.x = o.x > 0.f ? o.x : 0.f; o.y = o.y > 0.f ? o.y : 0.f;
-          o.z = o.z > 0.f ? o.z : 0.f; o.w = o.w > 0.f ? o.w : 0.f;
-        } else if (p.act == BQ_ACT_SILU) {
-          o.x = silu(o.x); o.y = silu(o.y); o.z = silu(o.z); o.w = silu(o.w);
-        } else if (p.act == BQ_ACT_GELU) {
-          o = gelu4(o);
-        }
-        const uint32_t off = (uint32_t)(lane * 4 + it * 256) * 4u;  // past the block: dropped
-        if (vec) {
-          if (p.out) store_wt16(r_out, off, o);
-          if (p.acc) __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, v), r_acc, off, 0, CPOL_WT);
-          if (p.q_out) store_wt4(r_q, off / 4u, qz_out.pack(o));
-        } else {
-          const float of[4] = {o.x, o.y, o.z, o.w};
-          const int vf[4] = {v.x, v.y, v.z, v.w};
-          const uint32_t qw = p.q_out ? qz_out.pack(o) : 0u;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            if (p.out) __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, of[e]), r_out, off + 4 * e, 0, CPOL_WT);
-            if (p.acc) __builtin_amdgcn_raw_buffer_store_b32((uint32_t)vf[e], r_acc, off + 4 * e, 0, CPOL_WT);
-            if (p.q_out) __builtin_amdgcn_raw_buffer_store_b8((uint8_t)(qw >> (8 * e)), r_q, off / 4u + e, 0, CPOL_WT);
-          }
-        }
-        if (row < rows) amax = fmaxf(amax, fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w))));
+      for (int ks = 0; ks < KS; ++ks) c = __builtin_amdgcn_mfma_i32_16x16x64_i8(b[j][ks], a[ks], c, 0, 0, 0);
+      const int n0 = j * 16 + 4 * kq;
+      if (!live || n0 >= N) continue;
+      float4 o;
+      o.x = __fadd_rn(__fmul_rn(__fmul_rn((float)c[0], sa), e_sw[j].x), e_b[j].x);
+      o.y = __fadd_rn(__fmul_rn(__fmul_rn((float)c[1], sa), e_sw[j].y), e_b[j].y);
+      o.z = __fadd_rn(__fmul_rn(__fmul_rn((float)c[2], sa), e_sw[j].z), e_b[j].z);
+      o.w = __fadd_rn(__fmul_rn(__fmul_rn((float)c[3], sa), e_sw[j].w), e_b[j].w);
+      if (has_r) {
+        o.x = __fadd_rn(o.x, rv[j].x); o.y = __fadd_rn(o.y, rv[j].y);
+        o.z = __fadd_rn(o.z, rv[j].z); o.w = __fadd_rn(o.w, rv[j].w);
       }
-      row += drow;
-      col += dcol;
-      if (col >= N) {
-        col -= N;
-        ++row;
+      if (p.act == BQ_ACT_RELU) {
+        o.x = o.x > 0.f ? o.x : 0.f; o.y = o.y > 0.f ? o.y : 0.f;
+        o.z = o.z > 0.f ? o.z : 0.f; o.w = o.w > 0.f ? o.w : 0.f;
+      } else if (p.act == BQ_ACT_SILU) {
+        o.x = silu(o.x); o.y = silu(o.y); o.z = silu(o.z); o.w = silu(o.w);
+      } else if (p.act == BQ_ACT_GELU) {
+        o = gelu4(o);
       }
+      const uint32_t off = (uint32_t)((size_t)m * N + n0) * 4u;
+      if (vec) {
+        if (p.out) {
+          if (wt) store_wt16(r_out, off, o);
+          else __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, o), r_out, off, 0, 0);
+        }
+        if (p.acc) __builtin_amdgcn_raw_buffer_store_b128(c, r_acc, off, 0, CPOL_WT);
+        if (p.q_out) store_wt4(r_q, off / 4u, qz_out.pack(o));
+      } else {
+        const float of[4] = {o.x, o.y, o.z, o.w};
+        const uint32_t qw = p.q_out ? qz_out.pack(o) : 0u;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (p.out) __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, of[e]), r_out, off + 4 * e, 0, CPOL_WT);
+          if (p.acc) __builtin_amdgcn_raw_buffer_store_b32((uint32_t)c[e], r_acc, off + 4 * e, 0, CPOL_WT);
+          if (p.q_out) __builtin_amdgcn_raw_buffer_store_b8((uint8_t)(qw >> (8 * e)), r_q, off / 4u + e, 0, CPOL_WT);
+        }
+      }
+      amax = fmaxf(amax, fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w))));
     }
-    wait_lds();  // this block's patch reads are done before the next block's writes
-    __builtin_amdgcn_wave_barrier();
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) a[ks] = an[ks];
   }
@@ -1756,8 +1728,9 @@ constexpr TileDims CFG_TILES[NCFG] = {{0, 0},    {256, 256}, {256, 256}, {256, 2
 // Whether the small-K kernel takes a problem (its shape only: an unaligned output takes
 // its four-byte stores), and its grid.
 static bool smallk_ok(const GemmP& p, bool conv) {
-  return !p.stamps && p.M >= 1 && p.N >= 4 && p.N <= 64 && p.N % 4 == 0 && p.K <= 256 &&
-         (conv || (long long)p.M * p.K < (1ll << 31));
+  const int NB = (p.N + 15) / 16, KS = (p.K + 63) / 64;
+  return !p.stamps && p.M >= 1 && p.N >= 4 && p.N <= 160 && p.N % 4 == 0 && p.K <= 256 && NB * KS <= 16 &&
+         (long long)p.M * p.N * 4 < (1ll << 31) && (conv || (long long)p.M * p.K < (1ll << 31));
 }
 static int smallk_grid(const GemmP& p) {
   const long long steps = (p.M + SMALLK_ROWS - 1) / SMALLK_ROWS;
@@ -1770,11 +1743,13 @@ static int choose_cfg(const GemmP& p, bool conv) {
   } else if (p.plan_cfg >= 1 && p.plan_cfg < NCFG) {
     return p.plan_cfg;
   }
-  // A narrow output over many rows (a 1x1 projection to a few channels, a stem conv): the
-  // small-K kernel (EfficientNet-B0 b64: 802816 x 16 x 32 34.3 -> 10.7 us, 200704 x 24 x 96
-  // 11.9 -> 8.1 us, 200704 x 24 x 144 17.1 -> 12.8 us; from 40 columns, or at 50176 rows,
-  // the tiled kernel was faster).
-  if (smallk_ok(p, conv) && p.N <= 32 && p.M >= 131072) return CFG_SMALLK;
+  // A narrow output over many rows (a 1x1 projection or expansion, a stem conv): the small-K
+  // kernel (EfficientNet-B0 b64 against the best tiled configuration: 802816 x 16 x 32
+  // 34.1 -> 10.0 us, 802816 x 96 x 16 93.1 -> 65.8 us, 200704 x 144 x 32 37.3 -> 27.0 us,
+  // 200704 x 24 x 96 11.6 -> 8.4 us; at 240 columns, or at 50176 rows, the tiled kernel was
+  // faster). Not for a calibrated layer's int8 twin alone, which the tiled kernel writes as
+  // whole rows (such a call writes no per-tile maxima, whose count would follow the choice).
+  if (smallk_ok(p, conv) && p.M >= 131072 && !(p.q_out && !p.out && !p.amax)) return CFG_SMALLK;
   const long long t256 = (long long)((p.M + 255) / 256) * ((p.N + 255) / 256);
   const long long t128 = (long long)((p.M + 127) / 128) * ((p.N + 127) / 128);
   const long long t128x32 = (long long)((p.M + 127) / 128) * ((p.N + 31) / 32);
@@ -1802,13 +1777,18 @@ template <bool CONV>
 static void launch_smallk(const GemmP& p, hipStream_t st) {
   const dim3 grid((unsigned)smallk_grid(p));
   const int NB = (p.N + 15) / 16, KS = (p.K + 63) / 64;
-  switch ((NB - 1) * 4 + (KS - 1)) {
+  switch ((NB - 1) * 4 + (KS - 1)) {  // NB * KS <= 16 (smallk_ok)
 #define BQ_SMALLK(nb, ks) \
   case (nb - 1) * 4 + (ks - 1): smallk_i8_kernel<nb, ks, CONV><<<grid, 256, 0, st>>>(p); break;
     BQ_SMALLK(1, 1) BQ_SMALLK(1, 2) BQ_SMALLK(1, 3) BQ_SMALLK(1, 4)
     BQ_SMALLK(2, 1) BQ_SMALLK(2, 2) BQ_SMALLK(2, 3) BQ_SMALLK(2, 4)
     BQ_SMALLK(3, 1) BQ_SMALLK(3, 2) BQ_SMALLK(3, 3) BQ_SMALLK(3, 4)
     BQ_SMALLK(4, 1) BQ_SMALLK(4, 2) BQ_SMALLK(4, 3) BQ_SMALLK(4, 4)
+    BQ_SMALLK(5, 1) BQ_SMALLK(5, 2) BQ_SMALLK(5, 3)
+    BQ_SMALLK(6, 1) BQ_SMALLK(6, 2)
+    BQ_SMALLK(7, 1) BQ_SMALLK(7, 2)
+    BQ_SMALLK(8, 1) BQ_SMALLK(8, 2)
+    BQ_SMALLK(9, 1) BQ_SMALLK(10, 1)
 #undef BQ_SMALLK
   }
 }
