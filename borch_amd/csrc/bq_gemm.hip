@@ -897,7 +897,7 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_i8_kernel(const GemmP p) {
 
 // ----------------------------------------------------------------------------- small K
 
-// GEMM for a narrow output (N <= 160, N % 4 == 0) and a short K (<= 256) over many rows: a
+// GEMM for a narrow output (N <= 256, N % 4 == 0) and a short K (<= 256) over many rows: a
 // 1x1 conv's projection or expansion over a large image (EfficientNet-B0 b64's
 // blocks.1.expand, 802816 x 96 x 16), or with CONV an implicit-GEMM conv of that shape (its
 // stem: 3x3 / 2 over 16 padded channels into 32, each lane's 16-byte chunk of a row at the
@@ -909,12 +909,17 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_i8_kernel(const GemmP p) {
 // j are columns 16 j + 4 (l / 16) .. + 3 of row l % 16, four consecutive outputs it stores
 // as one 16-byte piece straight from the accumulators (the epilogue arithmetic of the
 // tiled kernel's, in the same order). The next step's activation rows load before this
-// step's MFMAs, its residual pieces before its stores. Workgroups stride over the 64-row
-// steps; each writes one max |y| (p.amax). Unaligned outputs take four-byte stores.
+// step's MFMAs, its residual pieces before its stores. The column scales and bias sit in
+// registers up to 8 column blocks and in LDS beyond (the registers they would take cost more
+// occupancy than the reads: 50176 x 240 x 48 19.9 -> 13.0 us). Stores write through (sc1):
+// 802816 x 96 75.7 against 96.1 us plain. Workgroups stride over the 64-row steps; each
+// writes one max |y| (p.amax). Unaligned outputs take four-byte stores.
 constexpr int SMALLK_ROWS = 64;  // rows a workgroup step: 4 waves x 16
 template <int NB, int KS, bool CONV>
 __global__ __launch_bounds__(256) void smallk_i8_kernel(const GemmP p) {
+  constexpr bool LDSS = NB > 8;  // column scales and bias in LDS
   __shared__ float s_wmax[4];
+  __shared__ __attribute__((aligned(16))) float s_sw[LDSS ? NB * 16 : 4], s_b[LDSS ? NB * 16 : 4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c16 = lane & 15, kq = lane >> 4;
   const int M = p.M, N = p.N, K = p.K;
@@ -922,7 +927,8 @@ __global__ __launch_bounds__(256) void smallk_i8_kernel(const GemmP p) {
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.W, (uint32_t)(N * K));
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, CONV ? (uint32_t)p.Nimg_HWC : (uint32_t)(M * K));
   v4i b[NB][KS];
-  float4 e_sw[NB], e_b[NB];  // the scales and bias of this lane's four columns of block j
+  constexpr int NE = LDSS ? 1 : NB;
+  float4 e_sw[NE], e_b[NE];  // the scales and bias of this lane's four columns of block j
 #pragma unroll
   for (int j = 0; j < NB; ++j) {
     const int n = j * 16 + c16;
@@ -931,11 +937,21 @@ __global__ __launch_bounds__(256) void smallk_i8_kernel(const GemmP p) {
       const int k = ks * 64 + kq * 16;
       b[j][ks] = buf_load16(rw, (n < N && k < K) ? (uint32_t)(n * K + k) : OOB);
     }
-    const int n0 = j * 16 + 4 * kq;
-    e_sw[j] = n0 < N ? make_float4(p.sW[n0], p.sW[n0 + 1], p.sW[n0 + 2], p.sW[n0 + 3]) : make_float4(0.f, 0.f, 0.f, 0.f);
-    // 0 without bias: y + 0.0f == y for every y this produces
-    e_b[j] = (n0 < N && p.bias) ? make_float4(p.bias[n0], p.bias[n0 + 1], p.bias[n0 + 2], p.bias[n0 + 3])
-                                : make_float4(0.f, 0.f, 0.f, 0.f);
+    if constexpr (!LDSS) {
+      const int n0 = j * 16 + 4 * kq;
+      e_sw[j] = n0 < N ? make_float4(p.sW[n0], p.sW[n0 + 1], p.sW[n0 + 2], p.sW[n0 + 3])
+                       : make_float4(0.f, 0.f, 0.f, 0.f);
+      // 0 without bias: y + 0.0f == y for every y this produces
+      e_b[j] = (n0 < N && p.bias) ? make_float4(p.bias[n0], p.bias[n0 + 1], p.bias[n0 + 2], p.bias[n0 + 3])
+                                  : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+  if constexpr (LDSS) {
+    if (tid < NB * 16) {
+      s_sw[tid] = tid < N ? p.sW[tid] : 0.f;
+      s_b[tid] = (tid < N && p.bias) ? p.bias[tid] : 0.f;
+    }
+    __syncthreads();
   }
   // CONV: this lane's K chunks as (filter row, filter column, channel offset); a chunk past K
   // gets a row offset no input row passes
@@ -954,9 +970,6 @@ __global__ __launch_bounds__(256) void smallk_i8_kernel(const GemmP p) {
   const float sa0 = p.sa_per_row ? 0.f : p.sA[0];
   const Quantizer qz_out(p.q_out ? p.s_out[0] : 0.f);
   const bool has_r = p.res != nullptr, vec = p.vec_ok;
-  // Write-through stores measured faster up to 96 columns, plain ones above (802816 x 96:
-  // 65.8 against 107.1 us; 200704 x 144: 30.2 against 27.0 us).
-  const bool wt = N <= 96;
   const uint32_t out_bytes = (uint32_t)std::min<long long>((long long)M * N * 4, 0x7fffffff);
   const __amdgpu_buffer_rsrc_t r_out = make_rsrc(p.out, p.out ? out_bytes : 0u);
   const __amdgpu_buffer_rsrc_t r_acc = make_rsrc(p.acc, p.acc ? out_bytes : 0u);
@@ -1020,11 +1033,19 @@ __global__ __launch_bounds__(256) void smallk_i8_kernel(const GemmP p) {
       for (int ks = 0; ks < KS; ++ks) c = __builtin_amdgcn_mfma_i32_16x16x64_i8(b[j][ks], a[ks], c, 0, 0, 0);
       const int n0 = j * 16 + 4 * kq;
       if (!live || n0 >= N) continue;
+      float4 sw4, b4;
+      if constexpr (LDSS) {
+        sw4 = *reinterpret_cast<const float4*>(s_sw + n0);
+        b4 = *reinterpret_cast<const float4*>(s_b + n0);
+      } else {
+        sw4 = e_sw[LDSS ? 0 : j];
+        b4 = e_b[LDSS ? 0 : j];
+      }
       float4 o;
-      o.x = __fadd_rn(__fmul_rn(__fmul_rn((float)c[0], sa), e_sw[j].x), e_b[j].x);
-      o.y = __fadd_rn(__fmul_rn(__fmul_rn((float)c[1], sa), e_sw[j].y), e_b[j].y);
-      o.z = __fadd_rn(__fmul_rn(__fmul_rn((float)c[2], sa), e_sw[j].z), e_b[j].z);
-      o.w = __fadd_rn(__fmul_rn(__fmul_rn((float)c[3], sa), e_sw[j].w), e_b[j].w);
+      o.x = __fadd_rn(__fmul_rn(__fmul_rn((float)c[0], sa), sw4.x), b4.x);
+      o.y = __fadd_rn(__fmul_rn(__fmul_rn((float)c[1], sa), sw4.y), b4.y);
+      o.z = __fadd_rn(__fmul_rn(__fmul_rn((float)c[2], sa), sw4.z), b4.z);
+      o.w = __fadd_rn(__fmul_rn(__fmul_rn((float)c[3], sa), sw4.w), b4.w);
       if (has_r) {
         o.x = __fadd_rn(o.x, rv[j].x); o.y = __fadd_rn(o.y, rv[j].y);
         o.z = __fadd_rn(o.z, rv[j].z); o.w = __fadd_rn(o.w, rv[j].w);
@@ -1039,10 +1060,7 @@ __global__ __launch_bounds__(256) void smallk_i8_kernel(const GemmP p) {
       }
       const uint32_t off = (uint32_t)((size_t)m * N + n0) * 4u;
       if (vec) {
-        if (p.out) {
-          if (wt) store_wt16(r_out, off, o);
-          else __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, o), r_out, off, 0, 0);
-        }
+        if (p.out) store_wt16(r_out, off, o);
         if (p.acc) __builtin_amdgcn_raw_buffer_store_b128(c, r_acc, off, 0, CPOL_WT);
         if (p.q_out) store_wt4(r_q, off / 4u, qz_out.pack(o));
       } else {
@@ -1729,12 +1747,12 @@ constexpr TileDims CFG_TILES[NCFG] = {{0, 0},    {256, 256}, {256, 256}, {256, 2
 // its four-byte stores), and its grid.
 static bool smallk_ok(const GemmP& p, bool conv) {
   const int NB = (p.N + 15) / 16, KS = (p.K + 63) / 64;
-  return !p.stamps && p.M >= 1 && p.N >= 4 && p.N <= 160 && p.N % 4 == 0 && p.K <= 256 && NB * KS <= 16 &&
+  return !p.stamps && p.M >= 1 && p.N >= 4 && p.N <= 256 && p.N % 4 == 0 && p.K <= 256 && NB * KS <= 16 &&
          (long long)p.M * p.N * 4 < (1ll << 31) && (conv || (long long)p.M * p.K < (1ll << 31));
 }
-static int smallk_grid(const GemmP& p) {
+static int smallk_grid(const GemmP& p) {  // by measurement on EfficientNet-B0 b64's shapes
   const long long steps = (p.M + SMALLK_ROWS - 1) / SMALLK_ROWS;
-  return (int)std::min<long long>(steps, steps >= 8192 ? 2048 : 1024);
+  return (int)std::min<long long>(steps, p.N >= 64 ? 4096 : steps >= 8192 ? 2048 : 1024);
 }
 
 static int choose_cfg(const GemmP& p, bool conv) {
@@ -1744,11 +1762,11 @@ static int choose_cfg(const GemmP& p, bool conv) {
     return p.plan_cfg;
   }
   // A narrow output over many rows (a 1x1 projection or expansion, a stem conv): the small-K
-  // kernel (EfficientNet-B0 b64 against the best tiled configuration: 802816 x 16 x 32
-  // 34.1 -> 10.0 us, 802816 x 96 x 16 93.1 -> 65.8 us, 200704 x 144 x 32 37.3 -> 27.0 us,
-  // 200704 x 24 x 96 11.6 -> 8.4 us; at 240 columns, or at 50176 rows, the tiled kernel was
-  // faster). Not for a calibrated layer's int8 twin alone, which the tiled kernel writes as
-  // whole rows (such a call writes no per-tile maxima, whose count would follow the choice).
+  // kernel (EfficientNet-B0 b64 against the best tiled configuration, each layer alone with
+  // fresh outputs: 802816 x 16 x 32 34.2 -> 10.7 us, 802816 x 96 x 16 88.2 -> 75.7 us,
+  // 200704 x 144 x 32 37.9 -> 29.4 us, 200704 x 24 x 96 11.8 -> 8.5 us). Not for a
+  // calibrated layer's int8 twin alone, which the tiled kernel writes as whole rows (such a
+  // call writes no per-tile maxima, whose count would follow the choice).
   if (smallk_ok(p, conv) && p.M >= 131072 && !(p.q_out && !p.out && !p.amax)) return CFG_SMALLK;
   const long long t256 = (long long)((p.M + 255) / 256) * ((p.N + 255) / 256);
   const long long t128 = (long long)((p.M + 127) / 128) * ((p.N + 127) / 128);
@@ -1788,7 +1806,8 @@ static void launch_smallk(const GemmP& p, hipStream_t st) {
     BQ_SMALLK(6, 1) BQ_SMALLK(6, 2)
     BQ_SMALLK(7, 1) BQ_SMALLK(7, 2)
     BQ_SMALLK(8, 1) BQ_SMALLK(8, 2)
-    BQ_SMALLK(9, 1) BQ_SMALLK(10, 1)
+    BQ_SMALLK(9, 1) BQ_SMALLK(10, 1) BQ_SMALLK(11, 1) BQ_SMALLK(12, 1) BQ_SMALLK(13, 1) BQ_SMALLK(14, 1)
+    BQ_SMALLK(15, 1) BQ_SMALLK(16, 1)
 #undef BQ_SMALLK
   }
 }

@@ -277,7 +277,7 @@ int64_t bq_conv2d_absmax_parts(int64_t N, int64_t H, int64_t W, int64_t C, int64
 #define BQ_CFG_GEMV 32   /* dense, M <= 8: the v_dot4 wave-reduction GEMV (K <= 8192; 4096 above 4 rows;
                           * the rule's pick where it takes K) */
 #define BQ_CFG_SKINNY 33 /* dense, M <= 8: the weight-streaming MFMA kernel */
-#define BQ_CFG_SMALLK 18 /* dense or conv, N <= 160 with N % 4 == 0, K <= 256 (ceil(N/16) ceil(K/64) <= 16),
+#define BQ_CFG_SMALLK 18 /* dense or conv, N <= 256 with N % 4 == 0, K <= 256 (ceil(N/16) ceil(K/64) <= 16),
                           * M N < 2^29: the small-K kernel, weights in registers, 16 rows a wave-step
                           * (split 1; the rule's pick from 131072 rows). Its absmax_parts count is its
                           * workgroups. */

@@ -172,7 +172,7 @@ def _candidates(lib, problem):
 def test_plan_candidates(problem):
     """The kernel-choice candidates (host code, no GPU): the rules' pick first, no pair twice,
     configuration ids of the tiled kernel (3 and 9 are never offered, 16 only for a dense
-    GEMM) and the small-K kernel (only where N <= 160, N % 4 == 0, K <= 256 and its weight
+    GEMM) and the small-K kernel (only where N <= 256, N % 4 == 0, K <= 256 and its weight
     fragments fit, unsplit), K
     splits only on tiles of at most 4096 outputs, and never more splits than K stages."""
     from borch_amd import _lib
@@ -182,7 +182,7 @@ def test_plan_candidates(problem):
     assert len(set(cands)) == len(cands)
     small = {7, 9, 10, 12}  # tiles of 64 x 64 and 128 x 32 outputs
     N, K = (problem[1], problem[2]) if len(problem) == 3 else (problem[4], problem[3] * problem[5] * problem[6])
-    smallk_ok = N <= 160 and N % 4 == 0 and K <= 256 and ((N + 15) // 16) * ((K + 63) // 64) <= 16
+    smallk_ok = N <= 256 and N % 4 == 0 and K <= 256 and ((N + 15) // 16) * ((K + 63) // 64) <= 16
     assert ((_lib.CFG_SMALLK, 1) in cands) == smallk_ok
     for cfg, split in cands:
         if cfg == _lib.CFG_SMALLK:

@@ -1,7 +1,7 @@
 """GPU parity of the small-K dense kernel (smallk_i8_kernel, plan id BQ_CFG_SMALLK).
 
 At the shapes the rule gives it (a narrow output over many rows) it is held to the CPU
-oracle bit for bit. Everywhere it may run (N <= 160, N % 4 == 0, K <= 256), forced through
+oracle bit for bit. Everywhere it may run (N <= 256, N % 4 == 0, K <= 256), forced through
 the plan API, it must give what the tiled kernel gives on every epilogue: per-row and
 per-tensor activation scales, bias or none, the residual, ReLU / SiLU / GELU, the int32
 accumulators, the int8 twin, the maxima and outputs that are not 16-byte aligned.
@@ -72,7 +72,8 @@ def test_rule_shapes_match_the_oracle(dev, no_plans, M, N, K, act):
 
 
 SHAPES = [(1000, 40, 96), (4097, 4, 16), (777, 64, 256), (130, 12, 48), (65, 36, 144), (50176, 40, 240),
-          (70, 8, 208), (3001, 96, 16), (1000, 160, 64), (999, 112, 128), (300, 80, 192)]
+          (70, 8, 208), (3001, 96, 16), (1000, 160, 64), (999, 112, 128), (300, 80, 192), (2000, 240, 48),
+          (777, 256, 64)]
 
 
 @pytest.mark.parametrize("M,N,K", SHAPES)
@@ -95,7 +96,7 @@ def test_equals_the_tiled_kernel(dev, no_plans, M, N, K, act):
 
 
 @pytest.mark.parametrize("Nimg,H,C,O_", [(64, 112, 32, 16), (64, 56, 96, 24), (3, 15, 48, 64), (7, 9, 256, 48),
-                                         (5, 11, 16, 20), (64, 112, 16, 96), (64, 56, 32, 144)])
+                                         (5, 11, 16, 20), (64, 112, 16, 96), (64, 56, 32, 144), (64, 28, 48, 240)])
 def test_conv_twin_and_maxima(dev, no_plans, Nimg, H, C, O_):
     """A 1x1 conv (per-tensor scale) under the small-K plan and a tiled plan: the f32 output,
     the accumulators, the largest of the per-workgroup maxima (which the next quantizer
@@ -134,7 +135,7 @@ def test_conv_twin_and_maxima(dev, no_plans, Nimg, H, C, O_):
 CONV_CASES = [(64, 224, 224, 16, 32, 3, 2, 1), (2, 40, 40, 16, 32, 3, 2, 1), (3, 17, 13, 16, 20, 3, 1, 1),
               (2, 15, 15, 32, 64, 2, 2, 0), (1, 23, 19, 16, 48, 4, 1, 2), (2, 12, 12, 16, 8, 2, 3, 1),
               (4, 9, 9, 96, 12, 1, 2, 0), (2, 11, 11, 16, 4, 4, 4, 0), (2, 13, 13, 16, 160, 2, 1, 0),
-              (3, 10, 10, 32, 96, 1, 1, 0)]
+              (3, 10, 10, 32, 96, 1, 1, 0), (2, 9, 9, 48, 240, 1, 1, 0), (2, 12, 12, 16, 256, 2, 2, 0)]
 
 
 @pytest.mark.parametrize("Nimg,H,W,C,O_,k,stride,pad", CONV_CASES)
@@ -198,7 +199,7 @@ def test_unaligned_outputs(dev, no_plans):
 def test_plan_set_refuses_what_it_does_not_take(dev, no_plans):
     T = no_plans
     with pytest.raises(ValueError):
-        T.set_plan((1000, 164, 64), SMALLK, 1)  # N > 160
+        T.set_plan((1000, 260, 64), SMALLK, 1)  # N > 256
     with pytest.raises(ValueError):
         T.set_plan((1000, 80, 256), SMALLK, 1)  # 5 column blocks x 4 K steps of weight registers
     with pytest.raises(ValueError):
