@@ -18,6 +18,10 @@ int set_error(int code, const char* fmt, ...);
 // Maps the launch status (hipGetLastError) onto the return codes.
 int check_launch(const char* what);
 
+// Partial maxima of |x| over n floats into ws (bq_quantize_tensor_ws_bytes(n) bytes): one
+// launch; *np receives their count. Defined with the quantizers.
+int absmax_parts_ws(const char* what, const float* x, int64_t n, void* ws, size_t ws_bytes, hipStream_t st, int* np);
+
 // Division by a run-time invariant d >= 1 of any n < 2^31 as (umulhi(n, mul) + n) >> shift
 // with shift = ceil(log2 d) and mul = floor(2^32 (2^shift - d) / d) + 1 (Granlund and
 // Montgomery, "Division by invariant integers using multiplication", PLDI 1994, the

@@ -48,7 +48,7 @@ struct GemmP {
   // m / (OH OW) and r / OW (the small-K kernel's per-row decomposition)
   uint32_t c_mul, kw_mul, plane_mul, ow_mul;
   int c_shift, kw_shift, plane_shift, ow_shift;
-  int64_t Nimg_HWC;  // conv: bytes of the NHWC activation
+  int64_t Nimg_HWC;  // conv: bytes of the NHWC activation (the small-K f32 input: of Xf)
   int vec_ok;        // N % 4 == 0 and out/res/acc 16-byte aligned: float4 epilogue
   const float* s_out;  // static output scale [1] (nullable): the int8 twin of the output
   int8_t* q_out;       // [M, N] int8 = clip(rint(y / s_out)) (nullable)
@@ -72,6 +72,16 @@ struct GemmP {
   const float* X;
   int8_t* qx;
   float* sx;
+  // The small-K conv on an f32 NCHW input [N, Cin, H, W] (Cin <= 8 < C = 16, the padded
+  // channels of the packed weight read as zeros), its per-tensor quantization fused: Xf in
+  // place of A; the scale sx_given[0] (calibrated) or float32(max / 127) of the partial
+  // maxima xparts [nxparts]; sx_out (nullable) receives it.
+  const float* Xf;
+  int Cin;
+  const float* sx_given;
+  const float* xparts;
+  int nxparts;
+  float* sx_out;
   // Diagnostics (tiled kernel, nullable): four words a workgroup at 4 * (its regrouped id):
   // the steady wall clock (100 MHz) at entry, after the main loop and after its last store
   // completed, then its hardware id (__smid: XCC, SE, CU). bq_gemm_i8_phases sets it.
@@ -915,8 +925,10 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_i8_kernel(const GemmP p) {
 // 802816 x 96 75.7 against 96.1 us plain. Workgroups stride over the 64-row steps; each
 // writes one max |y| (p.amax). Unaligned outputs take four-byte stores.
 constexpr int SMALLK_ROWS = 64;  // rows a workgroup step: 4 waves x 16
-template <int NB, int KS, bool CONV>
+template <int NB, int KS, bool CONV, int CINM = 0>
 __global__ __launch_bounds__(256) void smallk_i8_kernel(const GemmP p) {
+  constexpr bool F32IN = CINM > 0;  // an f32 NCHW input of at most CINM channels, quantized here
+  static_assert(!F32IN || CONV, "an f32 input is a conv's");
   constexpr bool LDSS = NB > 8;  // column scales and bias in LDS
   __shared__ float s_wmax[4];
   __shared__ __attribute__((aligned(16))) float s_sw[LDSS ? NB * 16 : 4], s_b[LDSS ? NB * 16 : 4];
@@ -967,7 +979,26 @@ __global__ __launch_bounds__(256) void smallk_i8_kernel(const GemmP p) {
       if (k >= K) t_kh[ks] = -(1 << 20);
     }
   }
-  const float sa0 = p.sa_per_row ? 0.f : p.sA[0];
+  float sa0;
+  if constexpr (F32IN) {
+    // the input's scale: calibrated, or from the partial maxima (every workgroup reduces
+    // them; a maximum does not depend on the order)
+    if (p.sx_given) {
+      sa0 = p.sx_given[0];
+    } else {
+      float mx = 0.f;
+      for (int i = tid; i < p.nxparts; i += 256) mx = fmaxf(mx, p.xparts[i]);
+      mx = wave_max(mx);
+      if (lane == 0) s_wmax[wave] = mx;
+      __syncthreads();
+      sa0 = scale_of(fmaxf(fmaxf(s_wmax[0], s_wmax[1]), fmaxf(s_wmax[2], s_wmax[3])));
+      __syncthreads();  // s_wmax is reused for the output's maximum
+    }
+    if (p.sx_out && blockIdx.x == 0 && tid == 0) p.sx_out[0] = sa0;
+  } else {
+    sa0 = p.sa_per_row ? 0.f : p.sA[0];
+  }
+  const Quantizer qz_in(F32IN ? sa0 : 0.f);
   const Quantizer qz_out(p.q_out ? p.s_out[0] : 0.f);
   const bool has_r = p.res != nullptr, vec = p.vec_ok;
   const uint32_t out_bytes = (uint32_t)std::min<long long>((long long)M * N * 4, 0x7fffffff);
@@ -976,7 +1007,16 @@ __global__ __launch_bounds__(256) void smallk_i8_kernel(const GemmP p) {
   const __amdgpu_buffer_rsrc_t r_res = make_rsrc(p.res, has_r ? out_bytes : 0u);
   const __amdgpu_buffer_rsrc_t r_q = make_rsrc(p.q_out, p.q_out ? out_bytes / 4u : 0u);
   float amax = 0.f;
-  auto load_a = [&](v4i (&a)[KS], int t) {
+  // The next step's operand in flight: its int8 chunks, or with F32IN the raw f32 values of
+  // this lane's taps (quantized when the step runs, so their loads overlap this step's work)
+  constexpr int CM = F32IN ? CINM : 1;
+  struct Pending {
+    v4i q[KS];
+    float x[KS][CM];
+  };
+  const __amdgpu_buffer_rsrc_t r_x =
+      make_rsrc(p.Xf, F32IN ? (uint32_t)p.Nimg_HWC : 0u);
+  auto fetch = [&](Pending& pd, int t) {
     const int row = t * SMALLK_ROWS + wave * 16 + c16;
     const bool live = t < steps && row < M;
     if constexpr (CONV) {
@@ -984,27 +1024,60 @@ __global__ __launch_bounds__(256) void smallk_i8_kernel(const GemmP p) {
       const int r = row - n * p.OH * p.OW;
       const int oh = fdiv(r, p.ow_mul, p.ow_shift);
       const int ih0 = oh * p.stride - p.pad, iw0 = (r - oh * p.OW) * p.stride - p.pad;
-      const uint32_t img = (uint32_t)(n * p.H * p.Wd * p.C);
+      if constexpr (F32IN) {
+        // a chunk is one tap's 16 channels (C == 16): the Cin real ones from the NCHW planes,
+        // the rest zeros (an out-of-range buffer load reads 0)
+        const uint32_t plane = (uint32_t)(p.H * p.Wd);
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const int ih = ih0 + t_kh[ks], iw = iw0 + t_kw[ks];
-        const bool ok = live && (unsigned)ih < (unsigned)p.H && (unsigned)iw < (unsigned)p.Wd;
-        a[ks] = buf_load16(ra, ok ? img + (uint32_t)((ih * p.Wd + iw) * p.C + t_c0[ks]) : OOB);
+        for (int ks = 0; ks < KS; ++ks) {
+          const int ih = ih0 + t_kh[ks], iw = iw0 + t_kw[ks];
+          const bool ok = live && (unsigned)ih < (unsigned)p.H && (unsigned)iw < (unsigned)p.Wd;
+          const uint32_t o = ((uint32_t)n * (uint32_t)p.Cin * plane + (uint32_t)(ih * p.Wd + iw)) * 4u;
+#pragma unroll
+          for (int c = 0; c < CM; ++c)
+            pd.x[ks][c] = __builtin_bit_cast(
+                float, __builtin_amdgcn_raw_buffer_load_b32(r_x, ok && c < p.Cin ? o + (uint32_t)c * plane * 4u : OOB,
+                                                            0, 0));
+        }
+      } else {
+        const uint32_t img = (uint32_t)(n * p.H * p.Wd * p.C);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const int ih = ih0 + t_kh[ks], iw = iw0 + t_kw[ks];
+          const bool ok = live && (unsigned)ih < (unsigned)p.H && (unsigned)iw < (unsigned)p.Wd;
+          pd.q[ks] = buf_load16(ra, ok ? img + (uint32_t)((ih * p.Wd + iw) * p.C + t_c0[ks]) : OOB);
+        }
       }
     } else {
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         const int k = ks * 64 + kq * 16;
-        a[ks] = buf_load16(ra, (live && k < K) ? (uint32_t)(row * K + k) : OOB);
+        pd.q[ks] = buf_load16(ra, (live && k < K) ? (uint32_t)(row * K + k) : OOB);
       }
     }
   };
-  v4i a[KS];
+  auto operand = [&](v4i (&a)[KS], const Pending& pd) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      if constexpr (F32IN) {
+        uint32_t w4[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int c4 = 0; c4 < CM / 4; ++c4)
+          w4[c4] = qz_in.pack(make_float4(pd.x[ks][4 * c4], pd.x[ks][4 * c4 + 1], pd.x[ks][4 * c4 + 2],
+                                          pd.x[ks][4 * c4 + 3]));
+        a[ks] = v4i{(int)w4[0], (int)w4[1], (int)w4[2], (int)w4[3]};
+      } else {
+        a[ks] = pd.q[ks];
+      }
+    }
+  };
+  Pending pd;
   int t = blockIdx.x;
-  load_a(a, t);
+  fetch(pd, t);
   for (; t < steps; t += gridDim.x) {
-    v4i an[KS];
-    load_a(an, t + gridDim.x);
+    v4i a[KS];
+    operand(a, pd);
+    fetch(pd, t + gridDim.x);
     const int m = t * SMALLK_ROWS + wave * 16 + c16;  // this lane's row
     const bool live = m < M;
     const float sa = p.sa_per_row ? (live ? p.sA[m] : 0.f) : sa0;
@@ -1075,8 +1148,6 @@ __global__ __launch_bounds__(256) void smallk_i8_kernel(const GemmP p) {
       }
       amax = fmaxf(amax, fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w))));
     }
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) a[ks] = an[ks];
   }
   if (p.amax) {
     amax = wave_max(amax);
@@ -1812,6 +1883,22 @@ static void launch_smallk(const GemmP& p, hipStream_t st) {
   }
 }
 
+// The small-K conv on an f32 NCHW input: up to 4 column blocks, 4 or 8 input channels a tap.
+template <int CINM>
+static void launch_smallk_f32in(const GemmP& p, hipStream_t st) {
+  const dim3 grid((unsigned)smallk_grid(p));
+  const int NB = (p.N + 15) / 16, KS = (p.K + 63) / 64;
+  switch ((NB - 1) * 4 + (KS - 1)) {
+#define BQ_SMALLK(nb, ks) \
+  case (nb - 1) * 4 + (ks - 1): smallk_i8_kernel<nb, ks, true, CINM><<<grid, 256, 0, st>>>(p); break;
+    BQ_SMALLK(1, 1) BQ_SMALLK(1, 2) BQ_SMALLK(1, 3) BQ_SMALLK(1, 4)
+    BQ_SMALLK(2, 1) BQ_SMALLK(2, 2) BQ_SMALLK(2, 3) BQ_SMALLK(2, 4)
+    BQ_SMALLK(3, 1) BQ_SMALLK(3, 2) BQ_SMALLK(3, 3) BQ_SMALLK(3, 4)
+    BQ_SMALLK(4, 1) BQ_SMALLK(4, 2) BQ_SMALLK(4, 3) BQ_SMALLK(4, 4)
+#undef BQ_SMALLK
+  }
+}
+
 template <bool CONV>
 static void launch_gemm(const GemmP& p, hipStream_t st, const Ws& ws) {
   switch (choose_cfg(p, CONV)) {
@@ -2167,6 +2254,56 @@ static int conv_impl(const char* what, const int8_t* x, int64_t N, int64_t H, in
   else
     launch_gemm<true>(p, st, Ws{ws, ws_bytes});
   return check_launch(what);
+}
+
+int bq_conv2d_i8_nchw_fq(const float* x, int64_t N, int64_t Cin, int64_t H, int64_t W, const float* s_x,
+                         const int8_t* w, int64_t O, int64_t KH, int64_t KW, int64_t stride, int64_t pad,
+                         const float* sW, const float* bias, const float* residual, int act, float* out,
+                         int32_t* acc, const float* s_out, int8_t* q_out, float* absmax_parts, int64_t parts_cap,
+                         int64_t* nparts, float* sx, void* ws, size_t ws_bytes, bq_stream_t stream) {
+  const char* what = "bq_conv2d_i8_nchw_fq";
+  if (Cin < 1 || Cin > 8) return set_error(BQ_ERR_UNSUPPORTED, "%s: %lld input channels (1 to 8)", what, (long long)Cin);
+  if (N < 0 || H < 1 || W < 1 || N * Cin * H * W >= ((int64_t)1 << 31) / 4)
+    return set_error(BQ_ERR_ARG, "%s: bad or too large input (the f32 input must be < 2 GiB)", what);
+  if (!x || ((uintptr_t)x & 3)) return set_error(BQ_ERR_ARG, "%s: null or unaligned input", what);
+  GemmP p;
+  bool dense, empty;
+  // conv_setup checks the geometry (over the weight's 16 padded channels), the weight and the
+  // epilogue; the f32 input and the weight scales stand in for the int8 input and its scale
+  // in its pointer checks (neither is read through A / sA)
+  if (int r = conv_setup(what, reinterpret_cast<const int8_t*>(x), N, H, W, 16, w, O, KH, KW, stride, pad, sW, sW,
+                         bias, residual, act, out, acc, s_out, q_out, absmax_parts, p, dense, empty))
+    return r;
+  if (nparts) *nparts = 0;
+  if (empty) return BQ_OK;
+  if (O > 64 || O % 4 || !smallk_ok(p, true))
+    return set_error(BQ_ERR_UNSUPPORTED, "%s: takes O <= 64 (O %% 4 == 0) and KH*KW*16 <= 256", what);
+  if ((s_out != nullptr) != (q_out != nullptr) || (q_out && O % 16))
+    return set_error(BQ_ERR_ARG, "%s: an int8 twin needs s_out, q_out and O %% 16 == 0", what);
+  const long long grid = smallk_grid(p);
+  if (absmax_parts && parts_cap < grid)
+    return set_error(BQ_ERR_ARG, "%s: %lld partial maxima, room for %lld", what, grid, (long long)parts_cap);
+  hipStream_t st = (hipStream_t)stream;
+  p.A = nullptr;
+  p.sA = nullptr;
+  p.Nimg_HWC = N * Cin * H * W * 4;  // the f32 input's bytes (its buffer range)
+  p.Xf = x;
+  p.Cin = (int)Cin;
+  p.sx_given = s_x;
+  p.sx_out = sx;
+  if (!s_x) {  // the dynamic scale: partial maxima of |x| first
+    int np = 0;
+    if (int r = absmax_parts_ws(what, x, N * Cin * H * W, ws, ws_bytes, st, &np)) return r;
+    p.xparts = static_cast<const float*>(ws);
+    p.nxparts = np;
+  }
+  if (Cin <= 4)
+    launch_smallk_f32in<4>(p, st);
+  else
+    launch_smallk_f32in<8>(p, st);
+  if (int r = check_launch(what)) return r;
+  if (nparts && absmax_parts) *nparts = grid;
+  return BQ_OK;
 }
 
 int64_t bq_conv2d_absmax_parts(int64_t N, int64_t H, int64_t W, int64_t C, int64_t O, int64_t KH, int64_t KW,

@@ -462,6 +462,16 @@ static int nparts_for(int64_t n) {
   return (int)p;
 }
 
+int absmax_parts_ws(const char* what, const float* x, int64_t n, void* ws, size_t ws_bytes, hipStream_t st, int* np) {
+  const int parts = nparts_for(n);
+  if (!ws || ws_bytes < (size_t)parts * sizeof(float))
+    return set_error(BQ_ERR_ARG, "%s: workspace %zu bytes, need %zu", what, ws_bytes, (size_t)parts * sizeof(float));
+  const int64_t chunk = n == 0 ? 1 : (n + parts - 1) / parts;
+  absmax_parts_kernel<<<parts, QT_THREADS, 0, st>>>(x, n, ((chunk + 3) / 4) * 4, static_cast<float*>(ws));
+  *np = parts;
+  return check_launch(what);
+}
+
 static int launch_rows(const float* x, int64_t M, int64_t K, int8_t* q, float* s, hipStream_t st,
                        const char* what, int act = BQ_ACT_NONE, float* y = nullptr) {
   if (M < 0 || K < 0) return set_error(BQ_ERR_ARG, "%s: negative size (%lld x %lld)", what, (long long)M, (long long)K);

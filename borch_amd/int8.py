@@ -8,6 +8,7 @@ its conv input). There is no CPU path: a tensor that is not on a gfx950 device r
 """
 from __future__ import annotations
 
+import ctypes
 from dataclasses import dataclass
 
 import torch
@@ -454,6 +455,56 @@ def conv2d_i8_nhwc(qx, sa, wq: Int8ConvWeight, stride=1, pad=0, bias=None, resid
                                   out.data_ptr(), _ptr(acc), parts.data_ptr(), *_ws_args(qx.device), _stream(qx)))
     out._bq_absmax = (parts, nparts, out._version)
     return (out, acc) if want_acc else out
+
+
+def conv2d_nchw_fq(x, wq: Int8ConvWeight, stride=1, pad=0, bias=None, residual=None, act=ACT_NONE, s_x=None,
+                   s_out=None, f32_out=True, want_acc=False, want_scale=False):
+    """``conv2d_i8_nhwc(*quantize_nhwc(x, 16))`` (with ``s_out``: ``conv2d_i8_nhwc_q``) of an
+    NCHW-contiguous f32 input of at most 8 channels (a network's image), the quantization
+    fused into the conv (bq_conv2d_i8_nchw_fq): one launch with a calibrated scale ``s_x``
+    [1], two without (partial maxima first). The same bytes as the two-pass form. Returns
+    ``out`` (NCHW-shaped channels-last, carrying its per-workgroup maxima; None with
+    ``f32_out=False``), then the int8 twin with ``s_out``, the accumulators with
+    ``want_acc``, the input's scale with ``want_scale``. Raises NotImplementedError (nothing
+    launched) where the small-K kernel does not take the layer."""
+    if x.dtype != torch.float32:
+        raise TypeError(f"int8 path takes float32 activations, got {x.dtype}")
+    require_device(x.device)
+    if x.dim() != 4 or not x.is_contiguous():
+        raise ValueError("conv2d_nchw_fq takes an NCHW-contiguous 4-D input")
+    N, C, H, W = x.shape
+    if wq.cpad != 16 or C != wq.C or C > 8:
+        raise NotImplementedError(f"conv2d_nchw_fq: {C} input channels packed over {wq.cpad} (16 padded channels)")
+    if wq.KH * wq.KW * 16 > 256 or wq.O > 64 or wq.O % 4:  # the library's own limits, checked before allocating
+        raise NotImplementedError(f"conv2d_nchw_fq: O={wq.O}, {wq.KH}x{wq.KW} filter (O <= 64, O % 4 == 0, "
+                                  "KH*KW <= 16)")
+    OH = (H + 2 * pad - wq.KH) // stride + 1
+    OW = (W + 2 * pad - wq.KW) // stride + 1
+    if OH < 1 or OW < 1:
+        raise RuntimeError("the filter is larger than the input.")
+    dev = x.device
+    out = (torch.empty((N, wq.O, OH, OW), dtype=torch.float32, device=dev, memory_format=torch.channels_last)
+           if f32_out else None)
+    q = torch.empty((N, OH, OW, wq.O), dtype=torch.int8, device=dev) if s_out is not None else None
+    res = None
+    if residual is not None:
+        if tuple(residual.shape) != (N, wq.O, OH, OW):
+            raise RuntimeError(f"residual shape {tuple(residual.shape)} != output {(N, wq.O, OH, OW)}")
+        res = residual.float().contiguous(memory_format=torch.channels_last)
+    acc = torch.empty((N * OH * OW, wq.O), dtype=torch.int32, device=dev) if want_acc else None
+    sx = torch.empty((1,), dtype=torch.float32, device=dev) if want_scale else None
+    parts = torch.empty((4096,), dtype=torch.float32, device=dev) if f32_out else None
+    nparts = ctypes.c_int64(0)
+    ws = _ws(x.numel(), dev) if s_x is None else None
+    b = _vec(bias, wq.O, "bias")
+    check(lib().bq_conv2d_i8_nchw_fq(x.data_ptr(), N, C, H, W, _ptr(s_x), wq.q.data_ptr(), wq.O, wq.KH, wq.KW,
+                                     stride, pad, wq.s.data_ptr(), _ptr(b), _ptr(res), act, _ptr(out), _ptr(acc),
+                                     _ptr(s_out), _ptr(q), _ptr(parts), 4096, ctypes.byref(nparts), _ptr(sx),
+                                     _ptr(ws), 0 if ws is None else ws.numel(), _stream(x)))
+    if out is not None:
+        out._bq_absmax = (parts, int(nparts.value), out._version)
+    ret = (out,) + ((q,) if s_out is not None else ()) + ((acc,) if want_acc else ()) + ((sx,) if want_scale else ())
+    return ret if len(ret) > 1 else out
 
 
 def _absmax_parts(N, H, W, C, wq, stride, pad, device):

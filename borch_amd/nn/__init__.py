@@ -219,6 +219,29 @@ class Conv2d(_tnn.Module):
             return _i8.quantize_nhwc_scaled(x, self.in_scale, cpad), self.in_scale
         return _i8.quantize_nhwc(x, cpad)
 
+    def _fused_input_forward(self, x, residual, twin_only=False):
+        """A network's NCHW f32 image into a conv over 16 padded channels (the stem) with its
+        quantization fused into the conv (conv2d_nchw_fq): ``forward`` / ``twin_forward``'s
+        result, or None where that path does not take the layer (the caller quantizes first)."""
+        wq = self.int8
+        if not (isinstance(wq, _i8.Int8ConvWeight) and wq.cpad == 16 and _i8._nchw_padded(x, 16)
+                and x.dtype == torch.float32 and getattr(x, "_bq_absmax", None) is None):
+            return None
+        stride, pad = self._geometry()
+        twin = self.out_scale is not None and wq.O % 16 == 0
+        try:
+            r = _i8.conv2d_nchw_fq(x, wq, stride, pad, self.bias, residual, self.act, s_x=self.in_scale,
+                                   s_out=self.out_scale if twin else None, f32_out=not twin_only)
+        except NotImplementedError:
+            return None
+        if twin_only:
+            return r[1], self.out_scale
+        if twin:
+            out, q = r
+            out._int8_twin = (q, self.out_scale, self.out_scale_v, out._version)
+            return out
+        return r
+
     def _f32_forward(self, x, residual):
         out = functional._f32_conv2d(x, self.weight, self.bias, self.stride, self.padding, self.dilation,
                                      self.groups, self.padding_mode)
@@ -243,6 +266,10 @@ class Conv2d(_tnn.Module):
             if x.dim() != 4 or x.shape[1] != self.in_channels:
                 raise RuntimeError(f"channels do not match: input {x.shape[1] if x.dim() > 1 else x.shape}, "
                                    f"filter {self.in_channels}")
+            if channel_scale is None:
+                out = self._fused_input_forward(x, residual)
+                if out is not None:
+                    return out
             qx, sa = self._int8_input(x, channel_scale)
             return self.forward_int8(qx, sa, residual)
         out = functional._f32_conv2d(x, self.weight, self.bias, self.stride, self.padding, self.dilation,
@@ -272,6 +299,9 @@ class Conv2d(_tnn.Module):
         if x.dim() != 4 or x.shape[1] != self.in_channels:
             raise RuntimeError(f"channels do not match: input {x.shape[1] if x.dim() > 1 else x.shape}, "
                                f"filter {self.in_channels}")
+        r = self._fused_input_forward(x, residual, twin_only=True)
+        if r is not None:
+            return r
         qx, sa = self._int8_input(x)
         stride, pad = self._geometry()
         _, q = _i8.conv2d_i8_nhwc_q(qx, sa, self.int8, self.out_scale, stride, pad, self.bias, residual, self.act,

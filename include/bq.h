@@ -253,6 +253,24 @@ int bq_conv2d_i8_nhwc(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t 
                       const float* residual, int act, float* out, int32_t* acc,
                       float* absmax_parts, void* ws, size_t ws_bytes, bq_stream_t stream);
 
+/* A conv of an f32 NCHW input x [N, Cin, H, W] (a network's image, Cin <= 8) with its
+ * per-tensor quantization fused: bq_conv2d_i8_nhwc(_q) of quantize(x) into 16 padded NHWC
+ * channels, bit for bit, in one launch. The scale is s_x[0] (calibrated) or, with s_x NULL,
+ * float32(max|x| / 127) from partial maxima computed first into ws
+ * (bq_quantize_tensor_ws_bytes(N*Cin*H*W) bytes; a second launch); sx (nullable) receives
+ * it. w is packed over 16 channels ([O, KH*KW*16]); O <= 64 with O % 4 == 0 and
+ * KH*KW*16 <= 256 (the small-K kernel), else BQ_ERR_UNSUPPORTED (nothing launched).
+ * absmax_parts (nullable, room for parts_cap floats; 4096 always suffice) receives the
+ * output's partial maxima and *nparts (nullable) their count. The rest as
+ * bq_conv2d_i8_nhwc_q (s_out / q_out nullable, out nullable with q_out). Replaces the
+ * reference's input quantize pass before its first conv (tensor.ts:11909-11921;
+ * kernels.ts:2057-2081). */
+int bq_conv2d_i8_nchw_fq(const float* x, int64_t N, int64_t Cin, int64_t H, int64_t W, const float* s_x,
+                         const int8_t* w, int64_t O, int64_t KH, int64_t KW, int64_t stride, int64_t pad,
+                         const float* sW, const float* bias, const float* residual, int act, float* out,
+                         int32_t* acc, const float* s_out, int8_t* q_out, float* absmax_parts, int64_t parts_cap,
+                         int64_t* nparts, float* sx, void* ws, size_t ws_bytes, bq_stream_t stream);
+
 /* The number of floats bq_conv2d_i8_nhwc(_q) writes to a non-null `absmax_parts` for this
  * geometry (its output tile count), or a negative BQ_ERR_* for a bad geometry. */
 int64_t bq_conv2d_absmax_parts(int64_t N, int64_t H, int64_t W, int64_t C, int64_t O, int64_t KH, int64_t KW,

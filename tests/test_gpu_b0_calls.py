@@ -8,14 +8,16 @@ batch, so it is checked on the whole tensor; everything per image on the sample)
   the scale equals ``scale_of(max|v|)`` of the full tensor (v the input, or the
   squeeze-excite product ``fl(x * g)``) or the calibrated scale, and the bytes equal
   ``quantize_with_scale`` of the sampled images, bit for bit;
-* convs (``conv2d_i8_nhwc``, ``conv2d_i8_nhwc_q`` with or without its f32 output) and
-  depthwise convs: the packed weight equals the oracle packing of the layer's folded f32
+* convs (``conv2d_i8_nhwc``, ``conv2d_i8_nhwc_q`` with or without its f32 output, the
+  stem's ``conv2d_nchw_fq`` with its input quantization fused) and depthwise convs: the packed weight equals the oracle packing of the layer's folded f32
   weight, the int32 accumulators (re-read through the C ABI) equal the oracle's exact
   integer conv of the int8 input actually passed, the f32 output equals the oracle
   epilogue (bit for bit, SiLU layers within 1e-5 rel / 1e-6 abs: the device's exp and
   numpy's differ in the last bit), and an int8 twin equals ``quantize_with_scale`` of the
   device's own f32 output with the calibrated scale. A twin-only call (no f32 output) is
-  re-run with its f32 output and must give the same twin.
+  re-run with its f32 output and must give the same twin. The fused stem's scale equals
+  ``scale_of(max|x|)`` or the calibrated one, and its accumulators the oracle's conv of
+  ``quantize_with_scale`` of the sampled images.
 
 With calibrated scales this covers the bench's static path: the static network input, the
 expand convs that write their twin alone, the depthwise convs that read those twins with a
@@ -66,7 +68,7 @@ class Recorder:
 
     def __enter__(self):
         for fn in ("quantize_nhwc", "quantize_nhwc_scaled", "quantize_nhwc_chscale", "conv2d_i8_nhwc",
-                   "conv2d_i8_nhwc_q", "dwconv_i8_nhwc"):
+                   "conv2d_i8_nhwc_q", "conv2d_nchw_fq", "dwconv_i8_nhwc"):
             self.real[fn] = getattr(I, fn)
             setattr(I, fn, getattr(self, fn))
         return self
@@ -120,12 +122,15 @@ class Recorder:
         name, mod = self.by_w[id(wq)]
         return name, mod
 
-    def _oracle_conv(self, qx, sa, wq, stride, pad, bias, residual, act):
+    def _oracle_conv(self, qx, sa, wq, stride, pad, bias, residual, act, qsel=None):
+        """The oracle conv of the sampled images of ``qx`` (or of ``qsel``, their int8 NHWC
+        bytes given on the host) with scale ``sa``."""
         name, mod = self._layer(wq)
         w = n(mod.weight)
         qw_o, sw_o = Q.quantize_conv_weight(w, wq.cpad)
         assert np.array_equal(n(wq.q), qw_o) and np.array_equal(n(wq.s), sw_o), f"{name}: packing differs"
-        qsel = n(qx[self.images])
+        if qsel is None:
+            qsel = n(qx[self.images])
         acc_o, OH, OW = Q.conv2d_i8_nhwc(qsel, qw_o, wq.KH, wq.KW, stride, pad)
         res = None
         if residual is not None:
@@ -172,6 +177,33 @@ class Recorder:
         assert np.array_equal(n(q[self.images]), Q.quantize_with_scale(y_dev, n(s_out)[0])), f"{name}: twin differs"
         return out, q
 
+    def conv2d_nchw_fq(self, x, wq, stride=1, pad=0, bias=None, residual=None, act=I.ACT_NONE, s_x=None,
+                       s_out=None, f32_out=True, want_acc=False, want_scale=False):
+        r = self.real["conv2d_nchw_fq"](x, wq, stride, pad, bias, residual, act, s_x, s_out, f32_out, want_acc,
+                                        want_scale)
+        self._count("conv2d_nchw_fq" + ("_static" if s_x is not None else "") + ("_twin" if s_out is not None else ""))
+        # the same call with every output: its scale, accumulators and f32 output
+        full = self.real["conv2d_nchw_fq"](x, wq, stride, pad, bias, residual, act, s_x, s_out, True, True, True)
+        out, acc, sx = full[0], full[-2], full[-1]
+        want_s = n(s_x)[0] if s_x is not None else self._peak_scale(x)
+        assert n(sx)[0] == want_s, "fused stem: input scale differs"
+        C, H, W = x.shape[1], x.shape[2], x.shape[3]
+        qsel = np.zeros((len(self.images), H, W, wq.cpad), np.int8)
+        qsel[..., :C] = Q.quantize_with_scale(n(x[self.images]), np.float32(want_s)).transpose(0, 2, 3, 1)
+        name, acc_o, y_o = self._oracle_conv(None, sx, wq, stride, pad, bias, residual, act, qsel=qsel)
+        got_acc = n(acc.reshape(x.shape[0], -1, wq.O)[self.images]).reshape(-1, wq.O)
+        assert np.array_equal(got_acc, acc_o), f"{name}: int32 accumulators differ"
+        self._check_out(name, out, y_o, act)
+        rr = r if isinstance(r, tuple) else (r,)
+        if f32_out:
+            assert torch.equal(rr[0], out), f"{name}: f32 output differs between calls"
+        if s_out is not None:
+            assert torch.equal(rr[1], full[1]), f"{name}: twin differs between calls"
+            y_dev = n(out[self.images]).transpose(0, 2, 3, 1)
+            assert np.array_equal(n(rr[1][self.images]), Q.quantize_with_scale(y_dev, n(s_out)[0])), \
+                f"{name}: twin differs"
+        return r
+
     def dwconv_i8_nhwc(self, qx, sa, wq, stride=1, pad=0, bias=None, act=I.ACT_NONE, want_acc=False):
         r = self.real["dwconv_i8_nhwc"](qx, sa, wq, stride, pad, bias, act, want_acc)
         self._count("dwconv_i8_nhwc")
@@ -206,7 +238,8 @@ def test_c4_b64_dynamic_calls(dev):
     with Recorder(model, IMAGES) as rec, torch.no_grad():
         y = model(x)
     say(f"  calls checked: {rec.counts}")
-    assert rec.counts["conv2d_i8_nhwc"] == 33 and rec.counts["dwconv_i8_nhwc"] == 16
+    assert rec.counts["conv2d_nchw_fq"] == 1  # the stem, its input quantization fused
+    assert rec.counts["conv2d_i8_nhwc"] == 32 and rec.counts["dwconv_i8_nhwc"] == 16
     assert rec.counts["quantize_nhwc_chscale"] == 16
     assert torch.isfinite(y).all()
 
@@ -223,9 +256,11 @@ def test_c4_b64_calibrated_calls(dev):
     assert rec.counts.get("conv2d_i8_nhwc_q_twin_only") == 15  # every expand conv: its twin alone
     assert rec.counts["dwconv_i8_nhwc"] == 16
     assert rec.counts.get("quantize_nhwc_chscale_static") == 16  # each projection input, gate folded in
-    # stem, 12 projections (O % 16 == 0) and the head write a twin; the 4 projections with
-    # O = 24 or 40 cannot, so the network input and those 4 outputs take a static pass
-    assert rec.counts.get("conv2d_i8_nhwc_q") == 14 and rec.counts.get("conv2d_i8_nhwc") == 4
-    assert rec.counts.get("quantize_nhwc_scaled", 0) == 5
+    # the stem quantizes the network input itself and writes a twin; 12 projections (O % 16
+    # == 0) and the head write a twin; the 4 projections with O = 24 or 40 cannot, so those
+    # 4 outputs take a static pass
+    assert rec.counts.get("conv2d_nchw_fq_static_twin") == 1
+    assert rec.counts.get("conv2d_i8_nhwc_q") == 13 and rec.counts.get("conv2d_i8_nhwc") == 4
+    assert rec.counts.get("quantize_nhwc_scaled", 0) == 4
     assert "quantize_nhwc" not in rec.counts
     assert torch.isfinite(y).all()

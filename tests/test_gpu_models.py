@@ -269,21 +269,28 @@ def test_c3_resnet18_static_calibrated(dev):
             twins[name] = (n(out), None if getattr(out, "_int8_twin", None) is None else n(out._int8_twin[0]),
                            mod.out_scale_v)
         hooks.append(m.register_forward_hook(hook))
-    calls = {"n": 0}
-    orig = I.quantize_nhwc_scaled
+    calls = {"n": 0, "stem": 0}
+    orig, orig_fq = I.quantize_nhwc_scaled, I.conv2d_nchw_fq
 
     def counting(*a, **k):
         calls["n"] += 1
         return orig(*a, **k)
-    I.quantize_nhwc_scaled = counting
+
+    def stem(*a, **k):
+        assert k.get("s_x") is not None
+        calls["stem"] += 1
+        return orig_fq(*a, **k)
+    I.quantize_nhwc_scaled, I.conv2d_nchw_fq = counting, stem
     try:
         with torch.no_grad():
             feats = model.features(xt)
     finally:
-        I.quantize_nhwc_scaled = orig
+        I.quantize_nhwc_scaled, I.conv2d_nchw_fq = orig, orig_fq
         for h in hooks:
             h.remove()
-    assert calls["n"] == 1, f"{calls['n']} static quantize passes: only the network input should need one"
+    # the stem (3x3 over the 3-channel image) quantizes the network input inside its own
+    # conv with the calibrated scale; every other input is its producer's twin
+    assert calls["stem"] == 1 and calls["n"] == 0, f"{calls} static quantize passes / fused stems"
     for name, (y, twin, s_out) in twins.items():
         assert twin is not None, name
         assert np.array_equal(twin, O_quant().quantize_with_scale(y.transpose(0, 2, 3, 1), np.float32(s_out))), name
