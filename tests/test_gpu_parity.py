@@ -491,7 +491,10 @@ DW_CASES = [(2, 32, 16, 3, 1, 1), (2, 96, 15, 3, 2, 1), (2, 144, 14, 5, 1, 2), (
             (3, 40, 10, 3, 1, 0), (1, 16, 10, 7, 1, 3), (1, 24, 9, 5, 2, 1),
             # output rows of 14, 28 and 21 pixels: the 7-pixels-a-thread form, each filter and stride
             (2, 48, 28, 3, 2, 1), (2, 64, 28, 5, 2, 2), (1, 32, 56, 5, 2, 2), (2, 24, 28, 3, 1, 1),
-            (1, 16, 21, 3, 1, 1), (2, 40, 5, 5, 1, 2)]
+            (1, 16, 21, 3, 1, 1), (2, 40, 5, 5, 1, 2),
+            # 3x3 / 1 onto rows wider than 28: 7 pixels a thread where 7 divides the width (56,
+            # 35), else 4, both with the row-by-row loads
+            (1, 24, 56, 3, 1, 1), (1, 8, 35, 3, 1, 1), (1, 20, 33, 3, 1, 1)]
 
 
 @pytest.mark.parametrize("N,C,H,k,stride,pad", DW_CASES)
