@@ -489,6 +489,15 @@ def hbm_kernels(dev):
             I.conv2d_i8_nhwc(qx, sa1, w8, st, pad, None, None, I.ACT_NONE)
         ran[f"conv {k}x{k}/{st} {C}->{O_} at {H}^2 b64 (3x)"] = 64 * H * H * C + 64 * OH * OH * O_ * 4 + O_ * k * k * C
         del qx
+    # the same stem on the f32 NCHW image with its quantization fused (bq_conv2d_i8_nchw_fq,
+    # calibrated scale): the image read once as f32, no int8 copy of it written or read
+    xf = torch.rand(64, 3, 224, 224, generator=g).to(dev)
+    w8 = I.pack_conv_weight(torch.randn(32, 3, 3, 3, generator=g).to(dev))
+    for _ in range(3):
+        I.conv2d_nchw_fq(xf, w8, 2, 1, s_x=sa1)
+    ran["conv 3x3/2 3->32 at 224^2 b64, f32 NCHW input quantized in the conv (3x)"] = (
+        64 * 3 * 224 * 224 * 4 + 64 * 112 * 112 * 32 * 4 + 32 * 9 * 16)
+    del xf
     src = torch.randn(16 << 20, device=dev)
     dst = torch.empty_like(src)
     for _ in range(5):

@@ -932,6 +932,11 @@ __global__ __launch_bounds__(256) void smallk_i8_kernel(const GemmP p) {
   constexpr bool LDSS = NB > 8;  // column scales and bias in LDS
   __shared__ float s_wmax[4];
   __shared__ __attribute__((aligned(16))) float s_sw[LDSS ? NB * 16 : 4], s_b[LDSS ? NB * 16 : 4];
+  // The int8 twin of a wave's 16 rows, packed here before it is stored as whole rows: row r
+  // at word r * TWP (a multiple of 4 words, so a 16-byte chunk is one LDS read; for even NB
+  // the 64 lanes' word writes fall in 64 distinct banks)
+  constexpr int TWP = 4 * (NB + 1);
+  __shared__ __attribute__((aligned(16))) uint32_t s_tw[4][16 * TWP];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c16 = lane & 15, kq = lane >> 4;
   const int M = p.M, N = p.N, K = p.K;
@@ -1001,6 +1006,8 @@ __global__ __launch_bounds__(256) void smallk_i8_kernel(const GemmP p) {
   const Quantizer qz_in(F32IN ? sa0 : 0.f);
   const Quantizer qz_out(p.q_out ? p.s_out[0] : 0.f);
   const bool has_r = p.res != nullptr, vec = p.vec_ok;
+  // the twin as whole rows through LDS (O % 16 == 0 always holds for a twin; its base aligned)
+  const bool tw_rows = p.q_out && vec && (N & 15) == 0 && ((uintptr_t)p.q_out & 15) == 0;
   const uint32_t out_bytes = (uint32_t)std::min<long long>((long long)M * N * 4, 0x7fffffff);
   const __amdgpu_buffer_rsrc_t r_out = make_rsrc(p.out, p.out ? out_bytes : 0u);
   const __amdgpu_buffer_rsrc_t r_acc = make_rsrc(p.acc, p.acc ? out_bytes : 0u);
@@ -1099,13 +1106,15 @@ __global__ __launch_bounds__(256) void smallk_i8_kernel(const GemmP p) {
         }
       }
     }
-#pragma unroll
-    for (int j = 0; j < NB; ++j) {
+    // Column block j, j known at compile time (a loop the unroller left rolled at 12 or more
+    // blocks put the weight fragments in scratch memory)
+    auto block = [&](auto jc) __attribute__((always_inline)) {
+      constexpr int j = decltype(jc)::value;
       v4i c = v4i{};
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) c = __builtin_amdgcn_mfma_i32_16x16x64_i8(b[j][ks], a[ks], c, 0, 0, 0);
       const int n0 = j * 16 + 4 * kq;
-      if (!live || n0 >= N) continue;
+      if (!live || n0 >= N) return;
       float4 sw4, b4;
       if constexpr (LDSS) {
         sw4 = *reinterpret_cast<const float4*>(s_sw + n0);
@@ -1135,7 +1144,12 @@ __global__ __launch_bounds__(256) void smallk_i8_kernel(const GemmP p) {
       if (vec) {
         if (p.out) store_wt16(r_out, off, o);
         if (p.acc) __builtin_amdgcn_raw_buffer_store_b128(c, r_acc, off, 0, CPOL_WT);
-        if (p.q_out) store_wt4(r_q, off / 4u, qz_out.pack(o));
+        if (p.q_out) {
+          if (tw_rows)
+            s_tw[wave][c16 * TWP + j * 4 + kq] = qz_out.pack(o);
+          else
+            store_wt4(r_q, off / 4u, qz_out.pack(o));
+        }
       } else {
         const float of[4] = {o.x, o.y, o.z, o.w};
         const uint32_t qw = p.q_out ? qz_out.pack(o) : 0u;
@@ -1147,6 +1161,31 @@ __global__ __launch_bounds__(256) void smallk_i8_kernel(const GemmP p) {
         }
       }
       amax = fmaxf(amax, fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w))));
+    };
+    [&]<int... J>(std::integer_sequence<int, J...>) __attribute__((always_inline)) {
+      (block(std::integral_constant<int, J>{}), ...);
+    }(std::make_integer_sequence<int, NB>{});
+    if (tw_rows) {
+      // The wave's 16 twin rows are one contiguous run of 16 N bytes: 16-byte pieces of it
+      // from LDS, consecutive lanes on consecutive pieces (four-byte pieces of 16 rows a
+      // store measured 90 us for EfficientNet-B0's 802816 x 96 twin). The run's start is in
+      // the resource base, so a lane's offset is its own piece and the SGPR offset stays 0
+      // (the form the tiled kernel's LDS-fed stores need); rows past M fall out of range.
+      wait_lds();
+      __builtin_amdgcn_wave_barrier();
+      const int m_first = t * SMALLK_ROWS + wave * 16;
+      if (m_first < M) {
+        const int nch = N >> 4;  // 16-byte pieces a row
+        const __amdgpu_buffer_rsrc_t r_tw =
+            make_rsrc(p.q_out + (size_t)m_first * N, (uint32_t)(min(16, M - m_first) * N));
+        for (int e = lane; e < 16 * nch; e += 64) {
+          const int row = e / nch, cc = e - row * nch;
+          const v4i v = *reinterpret_cast<const v4i*>(&s_tw[wave][row * TWP + cc * 4]);
+          __builtin_amdgcn_raw_buffer_store_b128(v, r_tw, (uint32_t)e * 16u, 0, CPOL_WT);
+        }
+      }
+      wait_lds();  // every read of the patch is done before the next step writes it
+      __builtin_amdgcn_wave_barrier();
     }
   }
   if (p.amax) {
@@ -1584,10 +1623,17 @@ static int choose_cfg(const GemmP& p, bool conv) {
   // A narrow output over many rows (a 1x1 projection or expansion, a stem conv): the small-K
   // kernel (EfficientNet-B0 b64 against the best tiled configuration, each layer alone with
   // fresh outputs: 802816 x 16 x 32 34.2 -> 10.7 us, 802816 x 96 x 16 88.2 -> 75.7 us,
-  // 200704 x 144 x 32 37.9 -> 29.4 us, 200704 x 24 x 96 11.8 -> 8.5 us). Not for a
-  // calibrated layer's int8 twin alone, which the tiled kernel writes as whole rows (such a
-  // call writes no per-tile maxima, whose count would follow the choice).
-  if (smallk_ok(p, conv) && p.M >= 131072 && !(p.q_out && !p.out && !p.amax)) return CFG_SMALLK;
+  // 200704 x 144 x 32 37.9 -> 29.4 us, 200704 x 24 x 96 11.8 -> 8.5 us), and for a
+  // calibrated layer's int8 twin alone, whose rows it stores whole (802816 x 96 x 16: 74.8
+  // against 108 us). From 65,536 rows it also takes up to 160 columns for the twin alone, and
+  // for an f32 output at most 32 or at least 128 columns (100352 x 144 x 32: twin 21.3 / f32
+  // 23.4 against 35.7 / 29.7 us, 100352 x 24 x 96 f32 6.9 against 8.3 us; at 96 columns the
+  // tiled kernel's f32 output stays faster below 131,072 rows: 100352 x 96 x 16 16.6 against
+  // 17.3 us).
+  const bool twin_only = p.q_out && !p.out;
+  if (smallk_ok(p, conv) &&
+      (p.M >= 131072 || (p.M >= 65536 && p.N <= 160 && (twin_only || p.N <= 32 || p.N >= 128))))
+    return CFG_SMALLK;
   const long long t256 = (long long)((p.M + 255) / 256) * ((p.N + 255) / 256);
   const long long t128 = (long long)((p.M + 127) / 128) * ((p.N + 127) / 128);
   const long long t128x32 = (long long)((p.M + 127) / 128) * ((p.N + 31) / 32);

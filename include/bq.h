@@ -297,8 +297,9 @@ int64_t bq_conv2d_absmax_parts(int64_t N, int64_t H, int64_t W, int64_t C, int64
 #define BQ_CFG_SKINNY 33 /* dense, M <= 8: the weight-streaming MFMA kernel */
 #define BQ_CFG_SMALLK 18 /* dense or conv, N <= 256 with N % 4 == 0, K <= 256 (ceil(N/16) ceil(K/64) <= 16),
                           * M N < 2^29: the small-K kernel, weights in registers, 16 rows a wave-step
-                          * (split 1; the rule's pick from 131072 rows). Its absmax_parts count is its
-                          * workgroups. */
+                          * (split 1; the rule's pick from 131072 rows, and from 65536 rows for the int8
+                          * twin alone up to 160 columns and for an f32 output of at most 32 or 128 to
+                          * 160 columns). Its absmax_parts count is its workgroups. */
 int bq_plan_candidates(const int64_t* problem, int n, int32_t* cfgs, int32_t* splits, int cap);
 int bq_plan_set(const int64_t* problem, int n, int32_t cfg, int32_t split);
 int bq_plan_clear(void);

@@ -55,7 +55,8 @@ def operands(M, N, K, seed, dev):
 
 @pytest.mark.parametrize("M,N,K,act", [(131072 + 37, 16, 32, I.ACT_NONE), (200704, 24, 96, I.ACT_RELU),
                                        (140001, 32, 144, I.ACT_NONE), (131079, 96, 16, I.ACT_RELU),
-                                       (200704, 144, 32, I.ACT_NONE)])
+                                       (200704, 144, 32, I.ACT_NONE), (100352, 144, 32, I.ACT_RELU),
+                                       (100352, 24, 96, I.ACT_NONE), (65536, 32, 16, I.ACT_NONE)])
 def test_rule_shapes_match_the_oracle(dev, no_plans, M, N, K, act):
     """The rule's own pick at a narrow output over many rows, against the oracle: int32
     accumulators and the f32 epilogue bit for bit (ragged last step included)."""
@@ -212,3 +213,35 @@ def test_plan_set_refuses_what_it_does_not_take(dev, no_plans):
         T.set_plan((1000, 32, 64), SMALLK, 2)   # split
     T.set_plan((2, 32, 32, 16, 32, 1, 1, 1, 0), SMALLK, 1)  # a 1x1 stride-1 unpadded conv
     T.set_plan((2, 32, 32, 16, 32, 3, 3, 2, 1), SMALLK, 1)  # an implicit-GEMM conv of K = 144
+
+
+@pytest.mark.parametrize("Nimg,H,C,O_", [(64, 112, 16, 96), (3, 15, 48, 64)])
+def test_twin_rows_and_unaligned_twin(dev, no_plans, Nimg, H, C, O_):
+    """The int8 twin alone (the rule takes the small-K kernel for it from 65,536 rows): its
+    rows staged through LDS and stored whole equal the tiled kernel's twin, and a twin
+    pointer 4 bytes off 16-byte alignment (per-lane four-byte stores, the C ABI takes it)
+    gives the same bytes."""
+    T = no_plans
+    say(f"small-K twin rows N={Nimg} H={H} C={C} O={O_}")
+    rng = np.random.default_rng(Nimg + H + C + O_)
+    qx = t(rng.integers(-127, 128, size=(Nimg, H, H, C)).astype(np.int8), dev)
+    sa = t(np.array([0.013], np.float32), dev)
+    w8 = I.pack_conv_weight(t((rng.normal(size=(O_, C, 1, 1)) * 0.1).astype(np.float32), dev))
+    b = t(rng.normal(size=O_).astype(np.float32), dev)
+    s_out = t(np.array([0.04], np.float32), dev)
+    problem = (Nimg, H, H, C, O_, 1, 1, 1, 0)
+    twins = []
+    for cfg in (SMALLK, 12):
+        T.set_plan(problem, cfg, 1)
+        _, q = I.conv2d_i8_nhwc_q(qx, sa, w8, s_out, 1, 0, b, None, I.ACT_SILU, f32_out=False)
+        twins.append(q)
+    assert torch.equal(twins[0], twins[1])
+    T.set_plan(problem, SMALLK, 1)
+    M = Nimg * H * H
+    qbuf = torch.full((M * O_ + 16,), 7, dtype=torch.int8, device=dev)
+    I.check(L.lib().bq_conv2d_i8_nhwc_q(qx.data_ptr(), Nimg, H, H, C, w8.q.data_ptr(), O_, 1, 1, 1, 0,
+                                        sa.data_ptr(), w8.s.data_ptr(), b.data_ptr(), None, I.ACT_SILU, None, None,
+                                        s_out.data_ptr(), qbuf.data_ptr() + 4, None, *I._ws_args(dev), I._stream(qx)))
+    torch.cuda.synchronize()
+    assert torch.equal(qbuf[4:4 + M * O_].reshape(twins[0].shape), twins[0])
+    assert int(qbuf[:4].eq(7).sum()) == 4 and int(qbuf[4 + M * O_:].eq(7).sum()) == 12
