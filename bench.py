@@ -83,6 +83,14 @@ def layer_work(kind, a):
         N = a["qw"].shape[0]
         byts = M * K + N * K + 4 * M + 8 * N + 4 * M * N * (2 if a["residual"] is not None else 1)
         return (M, N, K), 2 * M * N * K, byts
+    if kind == "conv2d_nchw_fq":  # the stem on the f32 NCHW image, its quantization fused
+        n, c, h, w = a["x"].shape
+        wq, s, p = a["wq"], a["stride"], a["pad"]
+        m = n * ((h + 2 * p - wq.KH) // s + 1) * ((w + 2 * p - wq.KW) // s + 1)
+        k = wq.KH * wq.KW * wq.cpad
+        out_b = (4 * m * wq.O * bool(a.get("f32_out", True)) + 4 * m * wq.O * (a.get("residual") is not None)
+                 + m * wq.O * (a.get("s_out") is not None))
+        return (m, wq.O, k), 2 * m * wq.O * k, 4 * n * c * h * w + wq.O * k + out_b
     n, h, w, c = a["qx"].shape
     wq, s, p = a["wq"], a["stride"], a["pad"]
     oh, ow = (h + 2 * p - wq.KH) // s + 1, (w + 2 * p - wq.KW) // s + 1

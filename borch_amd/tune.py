@@ -36,7 +36,7 @@ from . import int8 as _i8
 from ._lib import check, lib
 
 # the borch_amd.int8 wrappers that launch a layer's int8 kernel on an int8 input
-LAYER_KERNELS = ("conv2d_i8_nhwc", "conv2d_i8_nhwc_q", "dwconv_i8_nhwc", "gemm_i8")
+LAYER_KERNELS = ("conv2d_i8_nhwc", "conv2d_i8_nhwc_q", "conv2d_nchw_fq", "dwconv_i8_nhwc", "gemm_i8")
 
 
 def record_launches(model, x):
