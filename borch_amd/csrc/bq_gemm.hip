@@ -2060,12 +2060,12 @@ int bq_conv2d_i8_nchw_fq(const float* x, int64_t N, int64_t Cin, int64_t H, int6
   if (Cin < 1 || Cin > 8) return set_error(BQ_ERR_UNSUPPORTED, "%s: %lld input channels (1 to 8)", what, (long long)Cin);
   if (N < 0 || H < 1 || W < 1 || N * Cin * H * W >= ((int64_t)1 << 31) / 4)
     return set_error(BQ_ERR_ARG, "%s: bad or too large input (the f32 input must be < 2 GiB)", what);
-  if (!x || ((uintptr_t)x & 3)) return set_error(BQ_ERR_ARG, "%s: null or unaligned input", what);
   GemmP p;
   bool dense, empty;
   // conv_setup checks the geometry (over the weight's 16 padded channels), the weight and the
   // epilogue; the f32 input and the weight scales stand in for the int8 input and its scale
-  // in its pointer checks (neither is read through A / sA)
+  // in its pointer checks (non-null, 16-byte aligned; neither is read through A / sA), and an
+  // empty batch returns before them
   if (int r = conv_setup(what, reinterpret_cast<const int8_t*>(x), N, H, W, 16, w, O, KH, KW, stride, pad, sW, sW,
                          bias, residual, act, out, acc, s_out, q_out, absmax_parts, p, dense, empty))
     return r;

@@ -475,6 +475,8 @@ def conv2d_nchw_fq(x, wq: Int8ConvWeight, stride=1, pad=0, bias=None, residual=N
     N, C, H, W = x.shape
     if wq.cpad != 16 or C != wq.C or C > 8:
         raise NotImplementedError(f"conv2d_nchw_fq: {C} input channels packed over {wq.cpad} (16 padded channels)")
+    if x.data_ptr() % 16:  # a view into a larger image batch: the two-pass form takes it
+        raise NotImplementedError("conv2d_nchw_fq: the image is not 16-byte aligned")
     if wq.KH * wq.KW * 16 > 256 or wq.O > 64 or wq.O % 4:  # the library's own limits, checked before allocating
         raise NotImplementedError(f"conv2d_nchw_fq: O={wq.O}, {wq.KH}x{wq.KW} filter (O <= 64, O % 4 == 0, "
                                   "KH*KW <= 16)")

@@ -253,7 +253,7 @@ int bq_conv2d_i8_nhwc(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t 
                       const float* residual, int act, float* out, int32_t* acc,
                       float* absmax_parts, void* ws, size_t ws_bytes, bq_stream_t stream);
 
-/* A conv of an f32 NCHW input x [N, Cin, H, W] (a network's image, Cin <= 8) with its
+/* A conv of an f32 NCHW input x [N, Cin, H, W] (a network's image, Cin <= 8; x 16-byte aligned) with its
  * per-tensor quantization fused: bq_conv2d_i8_nhwc(_q) of quantize(x) into 16 padded NHWC
  * channels, bit for bit, in one launch. The scale is s_x[0] (calibrated) or, with s_x NULL,
  * float32(max|x| / 127) from partial maxima computed first into ws

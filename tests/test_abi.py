@@ -82,6 +82,16 @@ def test_argument_checks_run_on_host():
     big = _lib.ConvDesc(None, 32, 9, 9, 1, 0, None, None, None, 0, None, None, None, None)
     assert lib.bq_conv2d_i8_nhwc_pair(None, 1, 8, 8, 16, None, big, d, None, 0, None) == _lib.BQ_ERR_ARG
     assert "larger than the input" in _lib.last_error()
+    # the stem on an f32 NCHW image: at most 8 input channels, the small-K kernel's limits, and
+    # an empty batch is a no-op (x may then be NULL)
+    nparts = ctypes.c_int64(-1)
+    assert lib.bq_conv2d_i8_nchw_fq(None, 2, 12, 32, 32, None, None, 32, 3, 3, 2, 1, None, None, None, 0, None,
+                                    None, None, None, None, 0, None, None, None, 0, None) == _lib.BQ_ERR_UNSUPPORTED
+    assert lib.bq_conv2d_i8_nchw_fq(None, 2, 3, 32, 32, None, None, 32, 3, 3, 2, 1, None, None, None, 0, None,
+                                    None, None, None, None, 0, None, None, None, 0, None) == _lib.BQ_ERR_ARG
+    assert lib.bq_conv2d_i8_nchw_fq(None, 0, 3, 32, 32, None, None, 32, 3, 3, 2, 1, None, None, None, 0, None,
+                                    None, None, None, None, 0, ctypes.byref(nparts), None, None, 0, None) == 0
+    assert nparts.value == 0
     # f32 attention: head width 64 and at most 256 tokens
     assert lib.bq_attention_f32(None, 1, 10, 2, 32, None, None) == _lib.BQ_ERR_UNSUPPORTED
     assert lib.bq_attention_f32(None, 1, 257, 2, 64, None, None) == _lib.BQ_ERR_UNSUPPORTED

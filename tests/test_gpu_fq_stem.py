@@ -134,3 +134,25 @@ def test_a_network_stem_takes_the_fused_path(dev):
     finally:
         I.conv2d_nchw_fq = real
     assert calls == [False, True, True]
+
+
+def test_a_misaligned_image_and_an_empty_batch(dev):
+    """An image 4 bytes off 16-byte alignment (a view into a larger buffer) is not taken by the
+    fused call (NotImplementedError) and the layer gives the two-pass result; an empty batch
+    is a no-op."""
+    import borch_amd as bt
+    torch.manual_seed(1)
+    conv = bt.nn.Conv2d(3, 32, 3, stride=2, padding=1).to(dev)
+    assert conv.quantize_int8()
+    buf = torch.randn(4 * 3 * 40 * 40 + 1, device=dev)
+    x = buf[1:].view(4, 3, 40, 40)
+    assert x.data_ptr() % 16 == 4 and x.is_contiguous()
+    with pytest.raises(NotImplementedError):
+        I.conv2d_nchw_fq(x, conv.int8, 2, 1)
+    with torch.no_grad():
+        y = conv(x)
+        qx, sa = I.quantize_nhwc(x, 16)
+        assert torch.equal(y, I.conv2d_i8_nhwc(qx, sa, conv.int8, 2, 1, conv.bias, None, conv.act))
+        s_x = t(np.array([0.02], np.float32), dev)
+        y0 = I.conv2d_nchw_fq(torch.empty((0, 3, 40, 40), device=dev), conv.int8, 2, 1, s_x=s_x)
+        assert tuple(y0.shape) == (0, 32, 20, 20)
