@@ -42,6 +42,11 @@ Pinning (what checks each function; see tests/test_oracle.py):
   (kernel_bench.html:321) on hand values.
 * conv2d_i8_nhwc / dwconv_i8_nhwc: direct 7-deep brute-force loops on tiny shapes
   (kernel_bench.html:406-413), and im2col equivalence (borch/_ops.py:671-691).
+* fma_f32 / linear_w8a32_gemv: exact-rational brute force of the single rounding, a hand
+  case where the fused product keeps a bit that a separate product rounds away, integer
+  operands whose every sum is exact (the result is the integer dot product, so a dropped
+  or misplaced term shows), and a hand case whose value depends on the lane tree's order
+  (it differs from both the exact sum and a left-to-right sum).
 """
 from __future__ import annotations
 
@@ -398,6 +403,65 @@ def dequant_weight(q, s):
     int8 window matmul (kernels.ts:2695-2708, ``f32(q) * scale[bcol]``) and of
     ``dequantInt8PerChannel`` (quant.ts:60-71). ``q [N, K]`` int8, ``s [N]``."""
     return (np.asarray(q, np.int8).astype(np.float32) * np.asarray(s, np.float32).reshape(-1, 1)).astype(np.float32)
+
+
+def fma_f32(a, b, c):
+    """Correctly rounded float32 ``a * b + c`` (one rounding), elementwise on float32
+    arrays: the product is exact in float64 (24 + 24 bits); the float64 sum ``t`` and its
+    exact error ``e`` (TwoSum) give ``a * b + c = t + e`` exactly, and rounding ``t`` to
+    float32 is then the correct rounding unless ``t`` sits exactly halfway between two
+    float32 values with ``e != 0`` (an f32 midpoint is a float64 value, so the float64
+    rounding cannot cross one): there the result goes the way ``e`` points."""
+    a64 = np.asarray(a, np.float32).astype(np.float64)
+    b64 = np.asarray(b, np.float32).astype(np.float64)
+    c64 = np.asarray(c, np.float32).astype(np.float64)
+    p = a64 * b64
+    t = p + c64
+    bb = t - p
+    e = (p - (t - bb)) + (c64 - bb)
+    r = t.astype(np.float32)
+    other = np.nextafter(r, np.where(t > r.astype(np.float64), np.float32(np.inf), np.float32(-np.inf)))
+    mid = (r.astype(np.float64) + other.astype(np.float64)) * 0.5
+    fix = (t != r.astype(np.float64)) & (t == mid) & (e != 0)
+    up = np.maximum(r, other)
+    down = np.minimum(r, other)
+    return np.where(fix, np.where(e > 0, up, down), r).astype(np.float32)
+
+
+def linear_w8a32_gemv(x, q, s, b=None, residual=None, relu=False):
+    """The W8A32 decode GEMV's own float32 arithmetic (M <= 4), restated operation for
+    operation: the effective weight ``f32(q) * s[n]`` (one rounding, kernels.ts:2695-2708),
+    then for each output 64 lane sums, lane l accumulating ``acc = fma(x[k], w[k], acc)`` over
+    k = 1024 c + 16 l + j (chunk c, then j = 0..15, in that order), then the lanes added as
+    a pairwise tree in lane order ((l0 + l1) + (l2 + l3)) + ..., then ``+ b``, ``+ residual``
+    and ReLU, one rounding each. This is the reference's own gate for its int8 window weight
+    (tests/browser/window_probe.html:219-233: the int8 op equals the f32 op on the
+    reconstructed weight, bit for bit), with the f32 op in the GPU kernel's order."""
+    x = np.asarray(x, np.float32)
+    w = dequant_weight(q, s)
+    M, K = x.shape
+    N = w.shape[0]
+    kc = -(-K // 1024)
+    acc = np.zeros((M, N, 64), np.float32)
+    lanes = np.arange(64)
+    for c in range(kc):
+        for j in range(16):
+            k = c * 1024 + 16 * lanes + j            # [64]
+            valid = k < K
+            kk = np.where(valid, k, 0)
+            xv = x[:, kk][:, None, :]                # [M, 1, 64]
+            wv = w[:, kk][None, :, :]                # [1, N, 64]
+            acc = np.where(valid[None, None, :], fma_f32(xv, wv, acc), acc)
+    while acc.shape[-1] > 1:
+        acc = (acc[..., 0::2] + acc[..., 1::2]).astype(np.float32)
+    y = acc[..., 0]
+    if b is not None:
+        y = (y + np.asarray(b, np.float32)).astype(np.float32)
+    if residual is not None:
+        y = (y + np.asarray(residual, np.float32)).astype(np.float32)
+    if relu:
+        y = np.where(y > 0, y, np.float32(0)).astype(np.float32)
+    return y
 
 
 def linear_w8a32(x, q, s, b=None):

@@ -568,6 +568,51 @@ def _check_w8a32(y, y_o, bound, x, qw_o, sw_o):
         f"max err / bound = {(err / bound).max():.3g}")
 
 
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+@pytest.mark.parametrize("N,K", [(64, 16), (130, 1040), (96, 2048), (257, 4096), (33, 8192)])
+def test_w8a32_decode_gemv_bit_exact(dev, M, N, K):
+    """The decode GEMV (M <= 4) against the restatement of its own f32 arithmetic
+    (oracle.linear_w8a32_gemv: f32(q) * s, per-lane FMA chains, the lane tree), bit for bit:
+    the reference's gate for its int8 window weight (the int8 op equals the f32 op on the
+    reconstructed weight, tests/browser/window_probe.html:219-233). With bias, then with a
+    residual and ReLU."""
+    say(f"w8a32 decode bit-exact M={M} N={N} K={K}")
+    rng = np.random.default_rng(M * 31 + N + K)
+    x = rng.normal(size=(M, K)).astype(np.float32)
+    w = rng.normal(size=(N, K)).astype(np.float32) * np.float32(0.05)
+    b = rng.normal(size=N).astype(np.float32)
+    r = rng.normal(size=(M, N)).astype(np.float32)
+    w8 = I.pack_linear_weight(t(w, dev), weight_only=True)
+    qw, sw = n(w8.q), n(w8.s)
+    y = n(I.linear_w8a32(t(x, dev), w8, t(b, dev)))
+    assert np.array_equal(y, O.linear_w8a32_gemv(x, qw, sw, b))
+    y2 = n(I.linear_w8a32(t(x, dev), w8, t(b, dev), I.ACT_RELU, residual=t(r, dev)))
+    assert np.array_equal(y2, O.linear_w8a32_gemv(x, qw, sw, b, r, relu=True))
+
+
+def test_w8a32_decode_gemv_hand_cases(dev):
+    """The restatement's hand cases on the device: the fused product that keeps the 2^-24
+    bit, and the lane tree's order (1 where the exact sum is 1 + 2^-23; 1 + 2^-23 where a
+    left-to-right sum gives 1)."""
+    K = 1024
+    s = np.float32(1 + 2.0 ** -12)
+    x = np.zeros((1, K), np.float32)
+    x[0, 0], x[0, 1] = -1, s
+    q = np.zeros((1, K), np.int8)
+    q[0, :2] = 1
+    w8 = I.Int8Weight(t(q, dev), t(np.array([s], np.float32), dev), K, 1, True)
+    y = n(I.linear_w8a32(t(x, dev), w8))
+    assert y[0, 0] == np.float32(2.0 ** -12 + 2.0 ** -24)
+    x = np.zeros((1, K), np.float32)
+    x[0, 0], x[0, 16], x[0, 32], x[0, 48] = 1, 2.0 ** -24, 2.0 ** -24, 2.0 ** -24
+    q = np.zeros((2, K), np.int8)
+    q[0, [0, 16, 32]] = 1
+    q[1, [0, 32, 48]] = 1
+    w8 = I.Int8Weight(t(q, dev), t(np.ones(2, np.float32), dev), K, 2, True)
+    y = n(I.linear_w8a32(t(x, dev), w8))
+    assert y[0, 0] == np.float32(1.0) and y[0, 1] == np.float32(1 + 2.0 ** -23)
+
+
 @pytest.mark.parametrize("M", [3, 10, 100, 700])
 def test_w8a32_residual(dev, M):
     """The residual is added after the bias and before the activation (the W8A8 epilogue's

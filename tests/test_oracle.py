@@ -629,3 +629,83 @@ def test_reference_linear_packer_against_build_rule_c5():
     assert per_kind == {"qkv": 40, "proj": 15, "fc1": 45, "fc2": 50}
     digest = hashlib.sha256(repr(allpos).encode()).hexdigest()[:16]
     assert digest == C5_DIFF_DIGEST
+
+
+# ------------------------------------------------- W8A32 decode GEMV, operation for operation
+
+def _round_f32_exact(v):
+    """Correct float32 rounding (half to even) of an exact rational, by scaling to a 24-bit
+    integer significand; normal range only."""
+    from fractions import Fraction
+    if v == 0:
+        return np.float32(0.0)
+    sign = -1 if v < 0 else 1
+    a = abs(v)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    while Fraction(2) ** e > a:
+        e -= 1
+    while Fraction(2) ** (e + 1) <= a:
+        e += 1
+    m = round(a / Fraction(2) ** (e - 23))  # round() of a Fraction: half to even
+    return np.float32(sign * float(m * Fraction(2) ** (e - 23)))
+
+
+def test_fma_f32_is_one_correct_rounding():
+    from fractions import Fraction
+    rng = np.random.default_rng(5)
+    a = rng.normal(size=3000).astype(np.float32)
+    b = rng.normal(size=3000).astype(np.float32)
+    c = np.concatenate([rng.normal(size=1000), -(a[1000:2000].astype(np.float64) * b[1000:2000]),
+                        rng.normal(size=1000) * 1e-9]).astype(np.float32)
+    got = O.fma_f32(a, b, c)
+    for i in range(len(a)):
+        want = _round_f32_exact(Fraction(float(a[i])) * Fraction(float(b[i])) + Fraction(float(c[i])))
+        assert got[i] == want, (i, a[i], b[i], c[i], got[i], want)
+    # the float64 sum lands exactly on a float32 midpoint: (1 + 2^-12)^2 = 1 + 2^-11 + 2^-24, and
+    # a 2^-80 addend decides the side (a rounding of the float64 sum alone would tie to even)
+    s = np.float32(1 + 2.0 ** -12)
+    assert O.fma_f32(s, s, np.float32(2.0 ** -80)) == np.float32(1 + 2.0 ** -11 + 2.0 ** -23)
+    assert O.fma_f32(s, s, np.float32(-(2.0 ** -80))) == np.float32(1 + 2.0 ** -11)
+
+
+def test_w8a32_gemv_restatement_fused_products():
+    """acc = fma(x, w, acc): with w = 1 + 2^-12 the product s^2 needs 25 bits; fused with
+    the previous -s it is exact (2^-12 + 2^-24), where a separately rounded product gives
+    2^-12."""
+    s = np.float32(1 + 2.0 ** -12)
+    q = np.zeros((1, 16), np.int8)
+    q[0, :2] = 1
+    x = np.zeros((1, 16), np.float32)
+    x[0, 0], x[0, 1] = -1, s
+    y = O.linear_w8a32_gemv(x, q, np.array([s], np.float32))
+    assert y[0, 0] == np.float32(2.0 ** -12 + 2.0 ** -24)
+    assert np.float32(np.float32(s * s) - s) == np.float32(2.0 ** -12)  # the unfused value differs
+
+
+def test_w8a32_gemv_restatement_covers_every_term():
+    """Small integer operands: every product and partial sum is exact, so the result is the
+    integer dot product (any dropped, repeated or misplaced term shows), over ragged chunks
+    (K = 2064: the third chunk's first lane only) and a bias, residual and ReLU."""
+    rng = np.random.default_rng(9)
+    M, N, K = 3, 37, 2064
+    x = rng.integers(-4, 5, size=(M, K)).astype(np.float32)
+    q = rng.integers(-127, 128, size=(N, K)).astype(np.int8)
+    b = rng.integers(-50, 50, size=N).astype(np.float32)
+    r = rng.integers(-50, 50, size=(M, N)).astype(np.float32)
+    want = x.astype(np.int64) @ q.astype(np.int64).T + b.astype(np.int64) + r.astype(np.int64)
+    y = O.linear_w8a32_gemv(x, q, np.ones(N, np.float32), b, r, relu=True)
+    assert np.array_equal(y, np.maximum(want, 0).astype(np.float32))
+
+
+def test_w8a32_gemv_restatement_lane_tree_order():
+    """Lane sums of 1 and 2^-24 at chosen lanes: with lanes 0, 1, 2 the tree gives 1 (the
+    exact sum is 1 + 2^-23); with lanes 0, 2, 3 it gives 1 + 2^-23 (a left-to-right sum
+    gives 1)."""
+    K = 1024
+    x = np.zeros((1, K), np.float32)
+    x[0, 0], x[0, 16], x[0, 32], x[0, 48] = 1, 2.0 ** -24, 2.0 ** -24, 2.0 ** -24
+    q = np.zeros((2, K), np.int8)
+    q[0, [0, 16, 32]] = 1  # lanes 0, 1, 2
+    q[1, [0, 32, 48]] = 1  # lanes 0, 2, 3
+    y = O.linear_w8a32_gemv(x, q, np.ones(2, np.float32))
+    assert y[0, 0] == np.float32(1.0) and y[0, 1] == np.float32(1 + 2.0 ** -23)
