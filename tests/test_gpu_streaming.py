@@ -95,6 +95,8 @@ def _int8_window_case(dev, M, K, N, xs, ws, rounding="exact"):
     y_o, bound = O.linear_w8a32(x, q_want, s_want)
     err = np.abs(got.astype(np.float64) - y_o)
     assert np.all(err <= bound + 1e-30)
+    if M <= 4:  # the decode GEMV: bit for bit the f32 op on the reconstructed weight, in its order
+        assert np.array_equal(got, O.linear_w8a32_gemv(x, q_want, s_want))
     # a quarter of an f32 slot
     gw = S.window(4 * N * K + (1 << 16), dev)
     S.in_window(gw, w, (N, K))
