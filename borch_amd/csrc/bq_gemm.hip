@@ -922,8 +922,12 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_i8_kernel(const GemmP p) {
 // step's MFMAs, its residual pieces before its stores. The column scales and bias sit in
 // registers up to 8 column blocks and in LDS beyond (the registers they would take cost more
 // occupancy than the reads: 50176 x 240 x 48 19.9 -> 13.0 us). Stores write through (sc1):
-// 802816 x 96 75.7 against 96.1 us plain. Workgroups stride over the 64-row steps; each
-// writes one max |y| (p.amax). Unaligned outputs take four-byte stores.
+// 802816 x 96 75.7 against 96.1 us plain. The int8 twin goes through a per-wave LDS patch
+// and leaves as whole rows (below). With CINM > 0 the input is the network's f32 NCHW image
+// (at most CINM real channels a tap, the rest of the 16 zero): each lane loads its taps' raw
+// floats a step ahead and quantizes them when the step runs (the scale calibrated, or taken
+// from partial maxima at the start). Workgroups stride over the 64-row steps; each writes
+// one max |y| (p.amax). Unaligned outputs take four-byte stores.
 constexpr int SMALLK_ROWS = 64;  // rows a workgroup step: 4 waves x 16
 template <int NB, int KS, bool CONV, int CINM = 0>
 __global__ __launch_bounds__(256) void smallk_i8_kernel(const GemmP p) {
