@@ -397,6 +397,27 @@ def test_c4_efficientnet_b0_static_twin_only(dev):
         assert np.array_equal(n(c(x)), y_twin)
 
 
+def test_c4_static_graph_at_full_resolution(dev):
+    """EfficientNet-B0 b16 at 224^2 with calibrated scales, where the stem quantizes the
+    image inside its conv, the 112^2 expand conv (200,704 rows) writes its int8 twin alone
+    through the small-K kernel's LDS-staged rows and the 56^2 ones (50,176 rows) through the
+    tiled kernel: the HIP-graph replays equal the eager forward bit for bit, with eager
+    work between replays."""
+    say("C4 EfficientNet-B0 b16 at 224^2, calibrated: graph replays vs eager")
+    model = nets.build("efficientnet_b0", seed=3, device=dev)
+    bt.compiled(model, int8=True, graph=False, fuse=False, tune=False)
+    bt.calibrate_int8(model, [torch.from_numpy(WL.c4_input(16, 31)).to(dev)])
+    x = torch.from_numpy(WL.c4_input(16, 32)).to(dev)
+    with torch.no_grad():
+        eager = n(model(x))
+        c = bt.compiled(model, int8=False, graph=True, fuse=False, tune=False)
+        for i in range(3):
+            assert np.array_equal(n(c(x)), eager), f"replay {i}"
+            model(torch.randn_like(x))
+            torch.cuda.synchronize()
+    assert np.isfinite(eager).all()
+
+
 def test_split_batch_graph_matches_whole(dev):
     """compiled(split=2): the batch runs as two chunks on parallel streams inside the graph
     (each with its own split-K workspace). Where every quantization is per row or uses a
