@@ -497,6 +497,15 @@ def hbm_kernels(dev):
             I.conv2d_i8_nhwc(qx, sa1, w8, st, pad, None, None, I.ACT_NONE)
         ran[f"conv {k}x{k}/{st} {C}->{O_} at {H}^2 b64 (3x)"] = 64 * H * H * C + 64 * OH * OH * O_ * 4 + O_ * k * k * C
         del qx
+    # EfficientNet-B0 b64's blocks.1.expand with a calibrated scale: 1x1, 16 -> 96 channels at
+    # 112^2, SiLU, its int8 twin alone (the small-K kernel's LDS-staged rows)
+    qx = torch.randint(-127, 128, (64, 112, 112, 16), generator=g, dtype=torch.int8).to(dev)
+    w8 = I.pack_conv_weight(torch.randn(96, 16, 1, 1, generator=g).to(dev))
+    s_tw = torch.tensor([0.05], device=dev)
+    for _ in range(3):
+        I.conv2d_i8_nhwc_q(qx, sa1, w8, s_tw, 1, 0, None, None, I.ACT_SILU, f32_out=False)
+    ran["conv 1x1/1 16->96 at 112^2 b64, SiLU, int8 twin alone (3x)"] = 64 * 112 * 112 * (16 + 96) + 96 * 16
+    del qx
     # the same stem on the f32 NCHW image with its quantization fused (bq_conv2d_i8_nchw_fq,
     # calibrated scale): the image read once as f32, no int8 copy of it written or read
     xf = torch.rand(64, 3, 224, 224, generator=g).to(dev)
