@@ -936,11 +936,9 @@ __global__ __launch_bounds__(256) void smallk_i8_kernel(const GemmP p) {
   constexpr bool LDSS = NB > 8;  // column scales and bias in LDS
   __shared__ float s_wmax[4];
   __shared__ __attribute__((aligned(16))) float s_sw[LDSS ? NB * 16 : 4], s_b[LDSS ? NB * 16 : 4];
-  // The int8 twin of a wave's 16 rows, packed here before it is stored as whole rows: row r
-  // at word r * TWP (a multiple of 4 words, so a 16-byte chunk is one LDS read; for even NB
-  // the 64 lanes' word writes fall in 64 distinct banks)
-  constexpr int TWP = 4 * (NB + 1);
-  __shared__ __attribute__((aligned(16))) uint32_t s_tw[4][16 * TWP];
+  // The int8 twin of a wave's 16 rows, packed here before it is stored as whole rows, in
+  // the rows' own layout (row r at byte r * N): the 16-byte piece e of the run is LDS word 4 e
+  __shared__ __attribute__((aligned(16))) uint32_t s_tw[4][16 * 4 * NB];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c16 = lane & 15, kq = lane >> 4;
   const int M = p.M, N = p.N, K = p.K;
@@ -1150,7 +1148,7 @@ __global__ __launch_bounds__(256) void smallk_i8_kernel(const GemmP p) {
         if (p.acc) __builtin_amdgcn_raw_buffer_store_b128(c, r_acc, off, 0, CPOL_WT);
         if (p.q_out) {
           if (tw_rows)
-            s_tw[wave][c16 * TWP + j * 4 + kq] = qz_out.pack(o);
+            s_tw[wave][c16 * (N >> 2) + j * 4 + kq] = qz_out.pack(o);
           else
             store_wt4(r_q, off / 4u, qz_out.pack(o));
         }
@@ -1164,7 +1162,7 @@ __global__ __launch_bounds__(256) void smallk_i8_kernel(const GemmP p) {
           if (p.q_out) __builtin_amdgcn_raw_buffer_store_b8((uint8_t)(qw >> (8 * e)), r_q, off / 4u + e, 0, CPOL_WT);
         }
       }
-      amax = fmaxf(amax, fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w))));
+      if (p.amax) amax = fmaxf(amax, fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w))));
     };
     [&]<int... J>(std::integer_sequence<int, J...>) __attribute__((always_inline)) {
       (block(std::integral_constant<int, J>{}), ...);
@@ -1179,12 +1177,10 @@ __global__ __launch_bounds__(256) void smallk_i8_kernel(const GemmP p) {
       __builtin_amdgcn_wave_barrier();
       const int m_first = t * SMALLK_ROWS + wave * 16;
       if (m_first < M) {
-        const int nch = N >> 4;  // 16-byte pieces a row
         const __amdgpu_buffer_rsrc_t r_tw =
             make_rsrc(p.q_out + (size_t)m_first * N, (uint32_t)(min(16, M - m_first) * N));
-        for (int e = lane; e < 16 * nch; e += 64) {
-          const int row = e / nch, cc = e - row * nch;
-          const v4i v = *reinterpret_cast<const v4i*>(&s_tw[wave][row * TWP + cc * 4]);
+        for (int e = lane; e < N; e += 64) {  // 16 rows of N bytes: N pieces of 16
+          const v4i v = *reinterpret_cast<const v4i*>(&s_tw[wave][4 * e]);
           __builtin_amdgcn_raw_buffer_store_b128(v, r_tw, (uint32_t)e * 16u, 0, CPOL_WT);
         }
       }
