@@ -98,10 +98,11 @@ def layer_work(kind, a):
     if kind == "dwconv_i8_nhwc":
         return (m, c, wq.KH * wq.KW), 2 * m * c * wq.KH * wq.KW, n * h * w * c + 4 * m * c + wq.KH * wq.KW * c
     k = wq.KH * wq.KW * c
-    # the f32 output unless the launch writes the twin alone
+    # the f32 output unless the launch writes the twin alone (conv2d_i8_nhwc_dq: always; its
+    # two passes over the input count once, as the algorithm's bytes)
     f32_out = kind == "conv2d_i8_nhwc" or (kind == "conv2d_i8_nhwc_q" and a.get("f32_out", True))
     out_b = (4 * m * wq.O * f32_out + 4 * m * wq.O * (a.get("residual") is not None)
-             + (m * wq.O if kind.endswith("_q") else 0))
+             + (m * wq.O if kind.endswith(("_q", "_dq")) else 0))
     return (m, wq.O, k), 2 * m * wq.O * k, n * h * w * c + wq.O * k + out_b
 
 

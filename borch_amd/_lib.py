@@ -27,7 +27,7 @@ ACT_NONE, ACT_RELU, ACT_SILU, ACT_GELU = 0, 1, 2, 3
 SCALE_A_PER_TENSOR = 0x100  # OR-ed into bq_gemm_i8's act: one activation scale for the whole A
 ROUND_EXACT, ROUND_REFERENCE, ROUND_REFERENCE_CONV = 0, 1, 2  # bq_quantize_weight_host's rules
 CFG_GEMV, CFG_SKINNY = 32, 33  # the decode kernels' configuration ids in the plan API (M <= 8)
-CFG_SMALLK = 18  # the small-K dense kernel's configuration id in the plan API (N <= 64, K <= 256)
+CFG_SMALLK = 18  # the small-K kernel's configuration id in the plan API (N <= 256, K <= 256)
 
 _c_i64 = ctypes.c_int64
 _c_p = ctypes.c_void_p
@@ -71,6 +71,9 @@ SIGNATURES = {
     "bq_conv2d_i8_nhwc_q": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i64,
                                      _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_int, _c_p, _c_p, _c_p, _c_p,
                                      _c_p, _c_p, _c_size, _c_p]),
+    "bq_conv2d_i8_nhwc_dq": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i64,
+                                      _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_int, _c_p, _c_p, _c_p, _c_i64,
+                                      _c_p]),
     "bq_conv2d_i8_nchw_fq": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64,
                                       _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_int, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64,
                                       _c_p, _c_p, _c_p, _c_size, _c_p]),

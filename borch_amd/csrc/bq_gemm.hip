@@ -82,6 +82,13 @@ struct GemmP {
   const float* xparts;
   int nxparts;
   float* sx_out;
+  // The int8 twin at a dynamic per-tensor scale (small-K kernel only): with oparts set, the
+  // twin's scale is float32(max / 127) of the partial maxima oparts [noparts] that a pass
+  // before this one wrote for the same outputs (s_out unused), and workgroup 0 writes it to
+  // sout_write [1] (nullable).
+  const float* oparts;
+  int noparts;
+  float* sout_write;
   // Diagnostics (tiled kernel, nullable): four words a workgroup at 4 * (its regrouped id):
   // the steady wall clock (100 MHz) at entry, after the main loop and after its last store
   // completed, then its hardware id (__smid: XCC, SE, CU). bq_gemm_i8_phases sets it.
@@ -923,7 +930,10 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_i8_kernel(const GemmP p) {
 // registers up to 8 column blocks and in LDS beyond (the registers they would take cost more
 // occupancy than the reads: 50176 x 240 x 48 19.9 -> 13.0 us). Stores write through (sc1):
 // 802816 x 96 75.7 against 96.1 us plain. The int8 twin goes through a per-wave LDS patch
-// and leaves as whole rows (below). With CINM > 0 the input is the network's f32 NCHW image
+// and leaves as whole rows (below); its scale is a calibrated one, or float32(max / 127) of
+// the maxima an earlier launch over the same layer wrote with no output stored (the
+// dynamic twin: two passes of the epilogue instead of an f32 output and a quantize pass
+// over it). With CINM > 0 the input is the network's f32 NCHW image
 // (at most CINM real channels a tap, the rest of the 16 zero): each lane loads its taps' raw
 // floats a step ahead and quantizes them when the step runs (the scale calibrated, or taken
 // from partial maxima at the start). Workgroups stride over the 64-row steps; each writes
@@ -1006,7 +1016,24 @@ __global__ __launch_bounds__(256) void smallk_i8_kernel(const GemmP p) {
     sa0 = p.sa_per_row ? 0.f : p.sA[0];
   }
   const Quantizer qz_in(F32IN ? sa0 : 0.f);
-  const Quantizer qz_out(p.q_out ? p.s_out[0] : 0.f);
+  float so = 0.f;
+  if (p.q_out) {
+    if (p.oparts) {
+      // the twin's dynamic scale from the maxima of a pass before this one, reduced by every
+      // workgroup as the input's are above
+      float mx = 0.f;
+      for (int i = tid; i < p.noparts; i += 256) mx = fmaxf(mx, p.oparts[i]);
+      mx = wave_max(mx);
+      if (lane == 0) s_wmax[wave] = mx;
+      __syncthreads();
+      so = scale_of(fmaxf(fmaxf(s_wmax[0], s_wmax[1]), fmaxf(s_wmax[2], s_wmax[3])));
+      __syncthreads();  // s_wmax is reused for the output's maximum
+      if (p.sout_write && blockIdx.x == 0 && tid == 0) p.sout_write[0] = so;
+    } else {
+      so = p.s_out[0];
+    }
+  }
+  const Quantizer qz_out(so);
   const bool has_r = p.res != nullptr, vec = p.vec_ok;
   // the twin as whole rows through LDS (O % 16 == 0 always holds for a twin; its base aligned)
   const bool tw_rows = p.q_out && vec && (N & 15) == 0 && ((uintptr_t)p.q_out & 15) == 0;
@@ -2221,6 +2248,46 @@ int bq_conv2d_i8_nhwc_q(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_
   if (O % 16) return set_error(BQ_ERR_UNSUPPORTED, "bq_conv2d_i8_nhwc_q: O=%lld is not a multiple of 16", (long long)O);
   return conv_impl("bq_conv2d_i8_nhwc_q", x, N, H, W, C, w, O, KH, KW, stride, pad, sA, sW, bias, residual, act,
                    out, acc, s_out, q_out, absmax_parts, ws, ws_bytes, stream);
+}
+
+int bq_conv2d_i8_nhwc_dq(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t C, const int8_t* w, int64_t O,
+                         int64_t KH, int64_t KW, int64_t stride, int64_t pad, const float* sA, const float* sW,
+                         const float* bias, const float* residual, int act, int8_t* q_out, float* s_out, float* parts,
+                         int64_t parts_cap, bq_stream_t stream) {
+  const char* what = "bq_conv2d_i8_nhwc_dq";
+  if (O % 16) return set_error(BQ_ERR_UNSUPPORTED, "%s: O=%lld is not a multiple of 16", what, (long long)O);
+  GemmP p;
+  bool dense, empty;
+  if (int r = conv_setup(what, x, N, H, W, C, w, O, KH, KW, stride, pad, sA, sW, bias, residual, act, nullptr,
+                         nullptr, nullptr, q_out, nullptr, p, dense, empty))
+    return r;
+  if (empty) return BQ_OK;  // an empty batch: nothing launched, the pointers may be null
+  if (!s_out || !parts) return set_error(BQ_ERR_ARG, "%s: null s_out or parts", what);
+  // where the small-K kernel runs the twin alone (the rule's pick, or a plan's): its pass with
+  // no store is cheaper than an f32 output and a quantize pass over it
+  if (choose_cfg(p, !dense) != CFG_SMALLK)
+    return set_error(BQ_ERR_UNSUPPORTED, "%s: the small-K kernel does not take this layer's twin", what);
+  const long long grid = smallk_grid(p);
+  if (parts_cap < grid)
+    return set_error(BQ_ERR_ARG, "%s: %lld partial maxima, room for %lld", what, grid, (long long)parts_cap);
+  hipStream_t st = (hipStream_t)stream;
+  GemmP p1 = p;  // pass 1: every output computed, only each workgroup's max |y| stored
+  p1.q_out = nullptr;
+  p1.amax = parts;
+  GemmP p2 = p;  // pass 2: the same outputs again, stored as the twin at the scale of pass 1's maxima
+  p2.oparts = parts;
+  p2.noparts = (int)grid;
+  p2.sout_write = s_out;
+  if (dense) {
+    launch_smallk<false>(p1, st);
+    if (int r = check_launch(what)) return r;
+    launch_smallk<false>(p2, st);
+  } else {
+    launch_smallk<true>(p1, st);
+    if (int r = check_launch(what)) return r;
+    launch_smallk<true>(p2, st);
+  }
+  return check_launch(what);
 }
 
 int bq_conv2d_i8_nhwc_pair(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t C, const float* sA,

@@ -547,6 +547,37 @@ def conv2d_i8_nhwc_q(qx, sa, wq: Int8ConvWeight, s_out, stride=1, pad=0, bias=No
     return out, q
 
 
+def conv2d_i8_nhwc_dq(qx, sa, wq: Int8ConvWeight, stride=1, pad=0, bias=None, residual=None, act=ACT_NONE):
+    """``quantize_nhwc(conv2d_i8_nhwc(...), O)`` with the f32 output never stored:
+    ``(q int8 [N, OH, OW, O], s [1])`` at the output's dynamic per-tensor scale, bit for bit
+    (bq_conv2d_i8_nhwc_dq: the small-K kernel twice, its maxima, then its twin).
+    NotImplementedError (nothing launched) where the small-K kernel does not run the layer's
+    twin or O % 16 != 0: the caller takes the two-call form."""
+    _need(qx, "x", torch.int8)
+    N, H, W, C = qx.shape
+    if C != wq.cpad:
+        raise RuntimeError(f"channels do not match: input {C}, filter {wq.cpad}")
+    OH = (H + 2 * pad - wq.KH) // stride + 1
+    OW = (W + 2 * pad - wq.KW) // stride + 1
+    if OH < 1 or OW < 1:
+        raise RuntimeError("the filter is larger than the input.")
+    if wq.O % 16:
+        raise NotImplementedError(f"conv2d_i8_nhwc_dq: O={wq.O} is not a multiple of 16")
+    res = None
+    if residual is not None:
+        if tuple(residual.shape) != (N, wq.O, OH, OW):
+            raise RuntimeError(f"residual shape {tuple(residual.shape)} != output {(N, wq.O, OH, OW)}")
+        res = residual.float().contiguous(memory_format=torch.channels_last)
+    b = _vec(bias, wq.O, "bias")
+    q = torch.empty((N, OH, OW, wq.O), dtype=torch.int8, device=qx.device)
+    s = torch.empty((1,), dtype=torch.float32, device=qx.device)
+    parts = torch.empty((4096,), dtype=torch.float32, device=qx.device)
+    check(lib().bq_conv2d_i8_nhwc_dq(qx.contiguous().data_ptr(), N, H, W, C, wq.q.data_ptr(), wq.O, wq.KH, wq.KW,
+                                     stride, pad, sa.data_ptr(), wq.s.data_ptr(), _ptr(b), _ptr(res), act,
+                                     q.data_ptr(), s.data_ptr(), parts.data_ptr(), parts.numel(), _stream(qx)))
+    return q, s
+
+
 @dataclass
 class PairConv:
     """One convolution of ``conv2d_pair_i8_nhwc``: its packed filter and epilogue. ``s_out`` (a

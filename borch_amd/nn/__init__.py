@@ -308,6 +308,30 @@ class Conv2d(_tnn.Module):
                                     f32_out=False)
         return q, self.out_scale
 
+    def dynamic_twin_of(self, consumer) -> bool:
+        """Whether ``dynamic_twin_forward`` can feed ``consumer``: both int8 layers with dynamic
+        per-tensor scales (not calibrated), this one a packed conv with O % 16 == 0 whose
+        output channels are the consumer's padded input channels."""
+        return (self.int8 is not None and not _CALIBRATING and isinstance(self.int8, _i8.Int8ConvWeight)
+                and self.out_scale is None and self.int8.O % 16 == 0 and consumer.int8 is not None
+                and consumer.in_scale is None and consumer.int8.cpad == self.int8.O)
+
+    def dynamic_twin_forward(self, x, residual=None):
+        """For a consumer that reads only the int8 of this layer's output (``dynamic_twin_of``):
+        ``(q [N, OH, OW, O], s [1])``, the output quantized at its dynamic per-tensor scale with
+        the f32 output never stored (conv2d_i8_nhwc_dq), the bytes the consumer's own
+        quantization of ``self(x, residual)`` gives. Where that kernel does not take the layer:
+        ``self(x, residual)`` itself, for the consumer to quantize."""
+        if x.dim() != 4 or x.shape[1] != self.in_channels:
+            raise RuntimeError(f"channels do not match: input {x.shape[1] if x.dim() > 1 else x.shape}, "
+                               f"filter {self.in_channels}")
+        qx, sa = self._int8_input(x)
+        stride, pad = self._geometry()
+        try:
+            return _i8.conv2d_i8_nhwc_dq(qx, sa, self.int8, stride, pad, self.bias, residual, self.act)
+        except NotImplementedError:
+            return self.forward_int8(qx, sa, residual)
+
     def forward_int8(self, qx, sa, residual=None):
         """The int8 layer on an already quantized NHWC input ``qx [N, H, W, cpad]`` with its
         per-tensor scale ``sa [1]``: the conv (or depthwise) kernel and its epilogue."""

@@ -36,7 +36,8 @@ from . import int8 as _i8
 from ._lib import check, lib
 
 # the borch_amd.int8 wrappers that launch a layer's int8 kernel on an int8 input
-LAYER_KERNELS = ("conv2d_i8_nhwc", "conv2d_i8_nhwc_q", "conv2d_nchw_fq", "dwconv_i8_nhwc", "gemm_i8")
+LAYER_KERNELS = ("conv2d_i8_nhwc", "conv2d_i8_nhwc_q", "conv2d_i8_nhwc_dq", "conv2d_nchw_fq", "dwconv_i8_nhwc",
+                 "gemm_i8")
 
 
 def record_launches(model, x):
@@ -53,8 +54,9 @@ def record_launches(model, x):
         def rec(*a, _f=f, _n=n, **k):
             bound = inspect.signature(_f).bind(*a, **k)
             bound.apply_defaults()
+            r = _f(*a, **k)  # recorded once it ran: a call the kernel refused is not a launch
             calls.append((current[0], _n, _f, dict(bound.arguments)))
-            return _f(*a, **k)
+            return r
         setattr(_i8, n, rec)
     try:
         with torch.no_grad():

@@ -317,6 +317,23 @@ int bq_conv2d_i8_nhwc_q(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_
                         int32_t* acc, const float* s_out, int8_t* q_out, float* absmax_parts, void* ws,
                         size_t ws_bytes, bq_stream_t stream);
 
+/* The int8 twin of a conv's output at its dynamic per-tensor scale, the f32 output never
+ * stored: q_out int8 [N, OH, OW, O] and s_out f32 [1] are, bit for bit, what
+ * bq_conv2d_i8_nhwc (with its absmax_parts) followed by bq_quantize_nhwc_parts into O
+ * channels gives (s_out = float32(max|y| / 127), q = clip(rint(y / s_out), +-127), exact
+ * quotient, half to even). Two launches of the small-K kernel: the first computes every
+ * output and stores only its workgroups' maxima into parts (room for parts_cap floats; 4096
+ * always suffice), the second computes them again and stores the twin. O % 16 == 0. Only
+ * where the small-K kernel runs the twin alone (BQ_CFG_SMALLK: the rule's pick, or a plan's),
+ * else BQ_ERR_UNSUPPORTED with nothing launched (the caller takes the two-call form). An
+ * empty batch is a no-op. Replaces the conv output's f32 store and the dynamic quantization the next conv's input
+ * takes from it (borch-ts/src/tensor.ts:11909-11921: absMaxAtomic and quantizeActivationInt8,
+ * kernels.ts:2024-2081, over convForwardInt8's output, kernels.ts:2156-2302). */
+int bq_conv2d_i8_nhwc_dq(const int8_t* x, int64_t N, int64_t H, int64_t W, int64_t C, const int8_t* w,
+                         int64_t O, int64_t KH, int64_t KW, int64_t stride, int64_t pad, const float* sA,
+                         const float* sW, const float* bias, const float* residual, int act, int8_t* q_out,
+                         float* s_out, float* parts, int64_t parts_cap, bq_stream_t stream);
+
 /* One convolution of bq_conv2d_i8_nhwc_pair: its filter and epilogue, as the arguments of
  * the same name of bq_conv2d_i8_nhwc_q (s_out and q_out both NULL: no int8 twin, and then
  * `out` is required; `amax` as bq_conv2d_i8_nhwc's absmax_parts, first conv only). */

@@ -92,6 +92,19 @@ def test_argument_checks_run_on_host():
     assert lib.bq_conv2d_i8_nchw_fq(None, 0, 3, 32, 32, None, None, 32, 3, 3, 2, 1, None, None, None, 0, None,
                                     None, None, None, None, 0, ctypes.byref(nparts), None, None, 0, None) == 0
     assert nparts.value == 0
+    # the dynamic twin: its three outputs, O % 16, the small-K kernel's layers only, room for
+    # its maxima; an empty batch is a no-op (host checks only: the pointers are never read)
+    fake = ctypes.c_void_p(1 << 20)
+    def dq(n, h, c, o, k, q=fake, cap=4096):
+        return lib.bq_conv2d_i8_nhwc_dq(fake, n, h, h, c, fake, o, k, k, 1, k // 2, fake, fake, None, None, 0,
+                                        q, fake, fake, cap, None)
+    assert dq(64, 112, 16, 96, 1, q=None) == _lib.BQ_ERR_ARG
+    assert dq(64, 112, 16, 24, 1) == _lib.BQ_ERR_UNSUPPORTED
+    assert dq(16, 32, 64, 64, 3) == _lib.BQ_ERR_UNSUPPORTED  # K = 576: the tiled kernel's
+    assert dq(64, 112, 16, 96, 1, cap=100) == _lib.BQ_ERR_ARG  # 4096 workgroups' maxima
+    assert dq(0, 112, 16, 96, 1) == 0
+    assert lib.bq_conv2d_i8_nhwc_dq(None, 0, 112, 112, 16, None, 96, 1, 1, 1, 0, None, None, None, None, 0, None,
+                                    None, None, 0, None) == 0
     # f32 attention: head width 64 and at most 256 tokens
     assert lib.bq_attention_f32(None, 1, 10, 2, 32, None, None) == _lib.BQ_ERR_UNSUPPORTED
     assert lib.bq_attention_f32(None, 1, 257, 2, 64, None, None) == _lib.BQ_ERR_UNSUPPORTED

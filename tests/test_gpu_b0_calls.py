@@ -17,7 +17,10 @@ batch, so it is checked on the whole tensor; everything per image on the sample)
   device's own f32 output with the calibrated scale. A twin-only call (no f32 output) is
   re-run with its f32 output and must give the same twin. The fused stem's scale equals
   ``scale_of(max|x|)`` or the calibrated one, and its accumulators the oracle's conv of
-  ``quantize_with_scale`` of the sampled images.
+  ``quantize_with_scale`` of the sampled images;
+* the dynamic twin (``conv2d_i8_nhwc_dq``, an expansion that feeds its depthwise conv with no
+  f32 output): the same conv's f32 output is checked as above, and the twin and its scale
+  must equal ``quantize_nhwc`` of it, bit for bit.
 
 With calibrated scales this covers the bench's static path: the static network input, the
 expand convs that write their twin alone, the depthwise convs that read those twins with a
@@ -68,7 +71,7 @@ class Recorder:
 
     def __enter__(self):
         for fn in ("quantize_nhwc", "quantize_nhwc_scaled", "quantize_nhwc_chscale", "conv2d_i8_nhwc",
-                   "conv2d_i8_nhwc_q", "conv2d_nchw_fq", "dwconv_i8_nhwc"):
+                   "conv2d_i8_nhwc_q", "conv2d_i8_nhwc_dq", "conv2d_nchw_fq", "dwconv_i8_nhwc"):
             self.real[fn] = getattr(I, fn)
             setattr(I, fn, getattr(self, fn))
         return self
@@ -177,6 +180,23 @@ class Recorder:
         assert np.array_equal(n(q[self.images]), Q.quantize_with_scale(y_dev, n(s_out)[0])), f"{name}: twin differs"
         return out, q
 
+    def conv2d_i8_nhwc_dq(self, qx, sa, wq, stride=1, pad=0, bias=None, residual=None, act=I.ACT_NONE):
+        q, s = self.real["conv2d_i8_nhwc_dq"](qx, sa, wq, stride, pad, bias, residual, act)
+        self._count("conv2d_i8_nhwc_dq")
+        # the two-call form: the f32 output (held to the oracle as a conv2d_i8_nhwc call is)
+        # quantized at its own dynamic scale gives the same bytes and scale
+        out = self.real["conv2d_i8_nhwc"](qx, sa, wq, stride, pad, bias, residual, act)
+        name, acc_o, y_o = self._oracle_conv(qx, sa, wq, stride, pad, bias, residual, act)
+        assert np.array_equal(self._acc(qx, sa, wq, stride, pad, bias, residual, act), acc_o), \
+            f"{name}: int32 accumulators differ"
+        self._check_out(name, out, y_o, act)
+        want_s = self._peak_scale(out)
+        assert n(s)[0] == want_s, f"{name}: dynamic twin scale differs"
+        q_r, s_r = self.real["quantize_nhwc"](out, wq.O)
+        assert torch.equal(q, q_r) and torch.equal(s, s_r), f"{name}: dynamic twin differs from the two calls"
+        self._check_q(out, q, want_s, wq.O, name)
+        return q, s
+
     def conv2d_nchw_fq(self, x, wq, stride=1, pad=0, bias=None, residual=None, act=I.ACT_NONE, s_x=None,
                        s_out=None, f32_out=True, want_acc=False, want_scale=False):
         r = self.real["conv2d_nchw_fq"](x, wq, stride, pad, bias, residual, act, s_x, s_out, f32_out, want_acc,
@@ -239,7 +259,9 @@ def test_c4_b64_dynamic_calls(dev):
         y = model(x)
     say(f"  calls checked: {rec.counts}")
     assert rec.counts["conv2d_nchw_fq"] == 1  # the stem, its input quantization fused
-    assert rec.counts["conv2d_i8_nhwc"] == 32 and rec.counts["dwconv_i8_nhwc"] == 16
+    # the 112^2 and 56^2 expansions feed their depthwise convs through the dynamic twin
+    assert rec.counts["conv2d_i8_nhwc_dq"] == 3
+    assert rec.counts["conv2d_i8_nhwc"] == 29 and rec.counts["dwconv_i8_nhwc"] == 16
     assert rec.counts["quantize_nhwc_chscale"] == 16
     assert torch.isfinite(y).all()
 
