@@ -78,6 +78,7 @@ SIGNATURES = {
                                       _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_int, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64,
                                       _c_p, _c_p, _c_p, _c_size, _c_p]),
     "bq_conv2d_absmax_parts": (_c_i64, [_c_i64] * 9),
+    "bq_conv2d_i8_nhwc_dq_ok": (_c_int, [_c_i64] * 9),
     "bq_plan_candidates": (_c_int, [_c_p, _c_int, _c_p, _c_p, _c_int]),
     "bq_plan_set": (_c_int, [_c_p, _c_int, ctypes.c_int32, ctypes.c_int32]),
     "bq_plan_clear": (_c_int, []),

@@ -2135,12 +2135,28 @@ int64_t bq_conv2d_absmax_parts(int64_t N, int64_t H, int64_t W, int64_t C, int64
     return set_error(BQ_ERR_ARG, "bq_conv2d_absmax_parts: bad geometry");
   const int64_t OH = (H + 2 * pad - KH) / stride + 1;
   const int64_t OW = (W + 2 * pad - KW) / stride + 1;
-  if (N * OH * OW > 0x7fffffff || O > 0x7fffffff) return set_error(BQ_ERR_ARG, "bq_conv2d_absmax_parts: size too large");
+  if (N * OH * OW > 0x7fffffff || O > 0x7fffffff || KH * KW * C > KMAX_EXACT)
+    return set_error(BQ_ERR_ARG, "bq_conv2d_absmax_parts: size too large");
   GemmP p{};
   p.M = (int)(N * OH * OW);
   p.N = (int)O;
+  p.K = (int)(KH * KW * C);  // the small-K kernel's test reads K: the count is the launch's
   apply_plan(p, conv_key(N, H, W, C, O, KH, KW, stride, pad));
   return p.M == 0 ? 0 : out_tiles(p, !(KH == 1 && KW == 1 && stride == 1 && pad == 0));
+}
+
+int bq_conv2d_i8_nhwc_dq_ok(int64_t N, int64_t H, int64_t W, int64_t C, int64_t O, int64_t KH, int64_t KW,
+                            int64_t stride, int64_t pad) {
+  PlanKey key;
+  GemmP p;
+  bool conv, tiled;
+  const int64_t pr[9] = {N, H, W, C, O, KH, KW, stride, pad};
+  if (!problem_view(pr, 9, key, p, conv, tiled))
+    return set_error(BQ_ERR_ARG, "bq_conv2d_i8_nhwc_dq_ok: bad geometry (C %% 16 == 0, N >= 1)");
+  if (O % 16) return 0;
+  apply_plan(p, key);
+  p.q_out = reinterpret_cast<int8_t*>(&p);  // the twin alone (never dereferenced here)
+  return choose_cfg(p, conv) == CFG_SMALLK ? 1 : 0;
 }
 
 int bq_plan_candidates(const int64_t* problem, int n, int32_t* cfgs, int32_t* splits, int cap) {

@@ -547,6 +547,17 @@ def conv2d_i8_nhwc_q(qx, sa, wq: Int8ConvWeight, s_out, stride=1, pad=0, bias=No
     return out, q
 
 
+def conv2d_i8_nhwc_dq_ok(N: int, H: int, W: int, wq: Int8ConvWeight, stride=1, pad=0) -> bool:
+    """Whether ``conv2d_i8_nhwc_dq`` takes this conv of an [N, H, W, wq.cpad] input under the
+    plans in force (bq_conv2d_i8_nhwc_dq_ok; host only)."""
+    if N < 1:
+        return False
+    r = int(lib().bq_conv2d_i8_nhwc_dq_ok(N, H, W, wq.cpad, wq.O, wq.KH, wq.KW, stride, pad))
+    if r < 0:
+        check(r)
+    return r == 1
+
+
 def conv2d_i8_nhwc_dq(qx, sa, wq: Int8ConvWeight, stride=1, pad=0, bias=None, residual=None, act=ACT_NONE):
     """``quantize_nhwc(conv2d_i8_nhwc(...), O)`` with the f32 output never stored:
     ``(q int8 [N, OH, OW, O], s [1])`` at the output's dynamic per-tensor scale, bit for bit

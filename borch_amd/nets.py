@@ -219,9 +219,9 @@ class MBConv(tnn.Module):
             dw = self.dw.conv
             if self.twin_path and ex is not None and ex.twin_only() and dw.takes_twin_of(ex):
                 h = dw.forward_int8(*ex.twin_forward(x))
-            elif self.twin_path and ex is not None and ex.dynamic_twin_of(dw):
+            elif self.twin_path and ex is not None and ex.dynamic_twin_of(dw, x):
                 # dynamic scales: the expand conv's output quantized for the depthwise conv
-                # without its f32 output where the kernel takes it
+                # without its f32 output (where the kernel takes the layer)
                 r = ex.dynamic_twin_forward(x)
                 h = dw.forward_int8(*r) if isinstance(r, tuple) else self.dw(r)
             else:

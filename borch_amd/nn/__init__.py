@@ -308,20 +308,26 @@ class Conv2d(_tnn.Module):
                                     f32_out=False)
         return q, self.out_scale
 
-    def dynamic_twin_of(self, consumer) -> bool:
-        """Whether ``dynamic_twin_forward`` can feed ``consumer``: both int8 layers with dynamic
-        per-tensor scales (not calibrated), this one a packed conv with O % 16 == 0 whose
-        output channels are the consumer's padded input channels."""
-        return (self.int8 is not None and not _CALIBRATING and isinstance(self.int8, _i8.Int8ConvWeight)
+    def dynamic_twin_of(self, consumer, x) -> bool:
+        """Whether ``dynamic_twin_forward(x)`` feeds ``consumer`` through the dynamic twin: both
+        int8 layers with dynamic per-tensor scales (not calibrated), this one a packed conv
+        whose output channels are the consumer's padded input channels, and the kernel takes
+        it at ``x``'s shape (conv2d_i8_nhwc_dq_ok). Where it does not, the caller runs the
+        two layers as their own module calls."""
+        if not (self.int8 is not None and not _CALIBRATING and isinstance(self.int8, _i8.Int8ConvWeight)
                 and self.out_scale is None and self.int8.O % 16 == 0 and consumer.int8 is not None
-                and consumer.in_scale is None and consumer.int8.cpad == self.int8.O)
+                and consumer.in_scale is None and consumer.int8.cpad == self.int8.O
+                and x.dim() == 4 and x.shape[1] == self.in_channels and x.is_cuda):
+            return False
+        g = self._geometry()
+        return g is not None and _i8.conv2d_i8_nhwc_dq_ok(x.shape[0], x.shape[2], x.shape[3], self.int8, *g)
 
     def dynamic_twin_forward(self, x, residual=None):
         """For a consumer that reads only the int8 of this layer's output (``dynamic_twin_of``):
         ``(q [N, OH, OW, O], s [1])``, the output quantized at its dynamic per-tensor scale with
         the f32 output never stored (conv2d_i8_nhwc_dq), the bytes the consumer's own
-        quantization of ``self(x, residual)`` gives. Where that kernel does not take the layer:
-        ``self(x, residual)`` itself, for the consumer to quantize."""
+        quantization of ``self(x, residual)`` gives. Where that kernel does not take the layer
+        after all: ``self(x, residual)`` itself, for the consumer to quantize."""
         if x.dim() != 4 or x.shape[1] != self.in_channels:
             raise RuntimeError(f"channels do not match: input {x.shape[1] if x.dim() > 1 else x.shape}, "
                                f"filter {self.in_channels}")

@@ -44,10 +44,12 @@ def record_launches(model, x):
     """One eager forward of ``model`` with the wrappers in ``LAYER_KERNELS`` recording their
     bound arguments: ``[(layer name, wrapper name, wrapper, arguments)]`` in launch order."""
     from . import nn as bnn
-    calls, current, saved, hooks = [], [""], {}, []
+    calls, current, saved, hooks, by_w = [], [""], {}, [], {}
     for name, m in model.named_modules():
         if isinstance(m, (bnn.Conv2d, bnn.Linear)):
             hooks.append(m.register_forward_pre_hook(lambda mod, inp, _n=name: current.__setitem__(0, _n)))
+            if getattr(m, "int8", None) is not None:
+                by_w[id(m.int8)] = name  # names a launch made without the module's own call
     for n in LAYER_KERNELS:
         f = saved[n] = getattr(_i8, n)
 
@@ -55,7 +57,8 @@ def record_launches(model, x):
             bound = inspect.signature(_f).bind(*a, **k)
             bound.apply_defaults()
             r = _f(*a, **k)  # recorded once it ran: a call the kernel refused is not a launch
-            calls.append((current[0], _n, _f, dict(bound.arguments)))
+            w = bound.arguments.get("wq", bound.arguments.get("w8"))
+            calls.append((by_w.get(id(w), current[0]), _n, _f, dict(bound.arguments)))
             return r
         setattr(_i8, n, rec)
     try:

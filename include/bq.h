@@ -276,6 +276,14 @@ int bq_conv2d_i8_nchw_fq(const float* x, int64_t N, int64_t Cin, int64_t H, int6
 int64_t bq_conv2d_absmax_parts(int64_t N, int64_t H, int64_t W, int64_t C, int64_t O, int64_t KH, int64_t KW,
                                int64_t stride, int64_t pad);
 
+/* 1 if bq_conv2d_i8_nhwc_dq takes this conv under the plans in force (it launches rather than
+ * returning BQ_ERR_UNSUPPORTED), 0 if not, a negative BQ_ERR_* for a bad geometry (C % 16
+ * == 0, N >= 1). Host only: a caller decides before quantizing the conv's input which form
+ * to run. The companion of bq_conv2d_i8_nhwc_dq, as bq_conv2d_absmax_parts is of the conv
+ * (tensor.ts:11909-11921 decides there between the twin and the quantize pass). */
+int bq_conv2d_i8_nhwc_dq_ok(int64_t N, int64_t H, int64_t W, int64_t C, int64_t O, int64_t KH, int64_t KW,
+                            int64_t stride, int64_t pad);
+
 /* Kernel choice by measurement. The GEMM and conv entry points pick a tiled-kernel
  * configuration (tile, ring depth) and a K split by rule; a plan overrides both for one
  * problem. Every configuration and split computes the same exact int32 sums and the same

@@ -105,6 +105,19 @@ def test_argument_checks_run_on_host():
     assert dq(0, 112, 16, 96, 1) == 0
     assert lib.bq_conv2d_i8_nhwc_dq(None, 0, 112, 112, 16, None, 96, 1, 1, 1, 0, None, None, None, None, 0, None,
                                     None, None, 0, None) == 0
+    # which convs the dynamic twin takes (the rule's small-K twin: from 65536 rows, up to 160
+    # columns, K <= 256; O % 16), decided on the host
+    assert lib.bq_conv2d_i8_nhwc_dq_ok(64, 112, 112, 16, 96, 1, 1, 1, 0) == 1
+    assert lib.bq_conv2d_i8_nhwc_dq_ok(64, 56, 56, 32, 144, 1, 1, 1, 0) == 1
+    assert lib.bq_conv2d_i8_nhwc_dq_ok(2, 112, 112, 16, 96, 1, 1, 1, 0) == 0
+    assert lib.bq_conv2d_i8_nhwc_dq_ok(64, 112, 112, 16, 24, 1, 1, 1, 0) == 0
+    assert lib.bq_conv2d_i8_nhwc_dq_ok(64, 56, 56, 64, 64, 3, 3, 1, 1) == 0
+    assert lib.bq_conv2d_i8_nhwc_dq_ok(0, 112, 112, 16, 96, 1, 1, 1, 0) == _lib.BQ_ERR_ARG
+    # the per-tile maxima count is the launch's: a 3x3 conv over 64 channels (K = 576, the
+    # tiled kernel's 64x64 tiles) at 112^2 b64 writes 12544 maxima, not the small-K kernel's
+    # 4096 that a count blind to K would give (the buffer sized by it would be overrun)
+    assert lib.bq_conv2d_absmax_parts(64, 112, 112, 64, 64, 3, 3, 1, 1) == 12544
+    assert lib.bq_conv2d_absmax_parts(64, 112, 112, 16, 96, 1, 1, 1, 0) == 4096  # the small-K kernel's
     # f32 attention: head width 64 and at most 256 tokens
     assert lib.bq_attention_f32(None, 1, 10, 2, 32, None, None) == _lib.BQ_ERR_UNSUPPORTED
     assert lib.bq_attention_f32(None, 1, 257, 2, 64, None, None) == _lib.BQ_ERR_UNSUPPORTED

@@ -153,7 +153,7 @@ def test_a_dynamic_block_takes_it(dev):
         with torch.no_grad():
             y = blk(x)
             ex, dw = blk.expand.conv, blk.dw.conv
-            assert ex.dynamic_twin_of(dw)
+            assert ex.dynamic_twin_of(dw, x) and not ex.dynamic_twin_of(dw, x[:2])  # 25088 rows: two calls
             h = dw(ex(x))  # the two-call form of the same two layers
             q, s = ex.dynamic_twin_forward(x)
             q_r, s_r = I.quantize_nhwc(ex(x), dw.int8.cpad)
@@ -163,3 +163,42 @@ def test_a_dynamic_block_takes_it(dev):
         I.conv2d_i8_nhwc_dq = real
     assert len(calls) == 2
     assert torch.isfinite(y).all()
+
+
+def test_graph_replays_of_a_dynamic_forward(dev, no_plans):
+    """EfficientNet-B0 b16 at 224^2 with dynamic scales (its 112^2 expansion, 200704 rows, takes
+    the dynamic twin): HIP graph replays equal the eager forward, with eager work between
+    them, and the eager forward with the dynamic twin off (the two-call form) gives the same
+    logits."""
+    import borch_amd as bt
+    from borch_amd import nets, workloads as WL
+    say("EfficientNet-B0 b16 dynamic: graph replays, eager, two-call form")
+    model = nets.build("efficientnet_b0", seed=2, device=dev)
+    c = bt.compiled(model, int8=True, graph=True)
+    x = torch.from_numpy(WL.c4_input(16, 3)).to(dev)
+    calls = []
+    real = I.conv2d_i8_nhwc_dq
+
+    def spy(*a, **kw):
+        calls.append(1)
+        return real(*a, **kw)
+
+    I.conv2d_i8_nhwc_dq = spy
+    try:
+        with torch.no_grad():
+            eager = model(x).clone()
+            assert calls, "the dynamic twin was not taken"
+            for i in range(3):
+                got = c(x)
+                assert torch.equal(got, eager), f"replay {i}"
+                model(torch.randn_like(x))  # eager work in between
+                torch.cuda.synchronize()
+            for b in model.blocks:
+                b.twin_path = False
+            try:
+                assert torch.equal(model(x), eager), "the two-call form differs"
+            finally:
+                for b in model.blocks:
+                    del b.twin_path
+    finally:
+        I.conv2d_i8_nhwc_dq = real
