@@ -484,6 +484,24 @@ def test_conv_absmax_parts_feed_the_next_quantizer(dev, N, C, H, O_, k, stride, 
     assert torch.equal(s3, s2) and torch.equal(q3, q2)
 
 
+def test_conv_maxima_count_of_a_deep_k_conv_over_many_rows(dev):
+    """A 3x3 conv over 64 channels at 112^2 b64 (802816 rows, K = 576) under the rule: the
+    small-K kernel does not take K > 256, so the tiled kernel runs it and writes one maximum
+    per 64x64 tile, 12544 of them, and the buffer the wrapper sizes from
+    bq_conv2d_absmax_parts holds exactly that many (a count made without K gave the small-K
+    kernel's 4096, a buffer the launch would have overrun)."""
+    from borch_amd import tune as T
+    T.clear_plans()
+    rng = np.random.default_rng(31)
+    qx = t(rng.integers(-127, 128, size=(64, 112, 112, 64), dtype=np.int8), dev)
+    sa = t(np.array([0.01], np.float32), dev)
+    w8 = I.pack_conv_weight(t((rng.normal(size=(64, 64, 3, 3)) * 0.05).astype(np.float32), dev))
+    y = I.conv2d_i8_nhwc(qx, sa, w8, 1, 1)
+    parts, nparts, _ = y._bq_absmax
+    assert nparts == 12544 and parts.numel() == 12544
+    assert float(parts.max()) == float(y.abs().max())
+
+
 # 3x3 / 5x5 at stride 1 / 2 take the register-blocked kernel (8 or 4 channels a thread;
 # output widths that are not a multiple of its pixel block); 7x7 and the rest the generic one.
 DW_CASES = [(2, 32, 16, 3, 1, 1), (2, 96, 15, 3, 2, 1), (2, 144, 14, 5, 1, 2), (2, 240, 13, 5, 2, 2),
