@@ -113,6 +113,15 @@ def test_argument_checks_run_on_host():
     assert lib.bq_conv2d_i8_nhwc_dq_ok(64, 112, 112, 16, 24, 1, 1, 1, 0) == 0
     assert lib.bq_conv2d_i8_nhwc_dq_ok(64, 56, 56, 64, 64, 3, 3, 1, 1) == 0
     assert lib.bq_conv2d_i8_nhwc_dq_ok(0, 112, 112, 16, 96, 1, 1, 1, 0) == _lib.BQ_ERR_ARG
+    # a plan that gives the layer a tiled configuration takes it away from the dynamic twin;
+    # removing the plan gives it back (plans are host state: no device touched)
+    prob = (ctypes.c_int64 * 9)(64, 112, 112, 16, 96, 1, 1, 1, 0)
+    assert lib.bq_plan_set(prob, 9, 4, 1) == 0
+    try:
+        assert lib.bq_conv2d_i8_nhwc_dq_ok(64, 112, 112, 16, 96, 1, 1, 1, 0) == 0
+    finally:
+        assert lib.bq_plan_set(prob, 9, 0, 0) == 0
+    assert lib.bq_conv2d_i8_nhwc_dq_ok(64, 112, 112, 16, 96, 1, 1, 1, 0) == 1
     # the per-tile maxima count is the launch's: a 3x3 conv over 64 channels (K = 576, the
     # tiled kernel's 64x64 tiles) at 112^2 b64 writes 12544 maxima, not the small-K kernel's
     # 4096 that a count blind to K would give (the buffer sized by it would be overrun)
