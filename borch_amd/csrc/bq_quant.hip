@@ -323,7 +323,7 @@ __global__ __launch_bounds__(QT_THREADS) void quantize_tensor_kernel(const float
 
 // Padded-channel variant (C < Cpad, Cpad % 16 == 0): one thread per 16-byte chunk of a
 // pixel's Cpad output bytes; it reads that chunk's (up to 16) input channels and stores one
-// 16-byte word. The input is channels-last (HW == 0: a pixel's channels contiguous) or
+// 16-byte word (a channels-last input of C % 4 == 0 takes one thread a pixel instead). The input is channels-last (HW == 0: a pixel's channels contiguous) or
 // NCHW (HW = H*W: channel c of pixel n*HW + hw at (n*C + c)*HW + hw, so consecutive threads
 // read consecutive pixels of each plane) — an NCHW network input needs no permute first.
 __global__ __launch_bounds__(QT_THREADS) void quantize_pad16_kernel(const float* __restrict__ x, int64_t P,
@@ -342,6 +342,26 @@ __global__ __launch_bounds__(QT_THREADS) void quantize_pad16_kernel(const float*
   const float sc = s_given ? s_given[0] : scale_of(peak);
   if (!s_given && blockIdx.x == 0 && threadIdx.x == 0) s[0] = sc;
   const Quantizer qz(sc);
+  if (HW == 0 && (C & 3) == 0 && ((uintptr_t)x & 15) == 0) {
+    // Channels-last with C % 4 == 0 (a conv output of 24 or 40 channels into 32 or 48): one
+    // thread a pixel, its channels as 16-byte loads (consecutive threads on consecutive
+    // pixels' contiguous rows), four values a pack, its Cpad bytes as 16-byte stores; no
+    // 64-bit division or 4-byte load an element
+    for (int64_t p = (int64_t)blockIdx.x * QT_THREADS + threadIdx.x; p < P; p += (int64_t)gridDim.x * QT_THREADS) {
+      const float* xp = x + p * C;
+      int8_t* qp = q + p * Cpad;
+      for (int c0 = 0; c0 < Cpad; c0 += 16) {
+        uint32_t wv[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int c = c0 + 4 * j;
+          wv[j] = c < C ? qz.pack(*reinterpret_cast<const float4*>(xp + c)) : 0u;
+        }
+        *reinterpret_cast<uint4*>(qp + c0) = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+      }
+    }
+    return;
+  }
   const int chunks = Cpad / 16;
   const int64_t total = P * chunks;
   for (int64_t i = (int64_t)blockIdx.x * QT_THREADS + threadIdx.x; i < total; i += (int64_t)gridDim.x * QT_THREADS) {

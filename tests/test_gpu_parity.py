@@ -88,6 +88,28 @@ def test_quantize_nhwc(dev, shape, cpad, cl):
     assert np.array_equal(n(q), qo)
 
 
+def test_quantize_nhwc_padded_many_pixels(dev):
+    """A channels-last input of 24 channels into 32 over more pixels than one grid covers
+    (2.17 M, each thread takes several): the same bytes as the channel-scaled quantizer with a
+    gate of ones (fl(x * 1) = x; another kernel), with the dynamic and a static scale, and the
+    oracle's on the first and last images."""
+    rng = np.random.default_rng(77)
+    x = (rng.normal(size=(64, 24, 184, 184)) * 3).astype(np.float32)
+    xt = t(x, dev).contiguous(memory_format=torch.channels_last)
+    ones = torch.ones((64, 24), device=dev)
+    q, s = I.quantize_nhwc(xt, 32)
+    q_ch, s_ch = I.quantize_nhwc_chscale(xt, ones, 32)
+    assert torch.equal(s, s_ch) and torch.equal(q, q_ch)
+    sc = t(np.array([0.01], np.float32), dev)
+    q2 = I.quantize_nhwc_scaled(xt, sc, 32)
+    q2_ch, _ = I.quantize_nhwc_chscale(xt, ones, 32, sc)
+    assert torch.equal(q2, q2_ch)
+    for i in (0, 63):
+        want = np.zeros((184, 184, 32), np.int8)
+        want[..., :24] = O.quantize_with_scale(x[i], n(s)[0]).transpose(1, 2, 0)
+        assert np.array_equal(n(q[i]), want)
+
+
 @pytest.mark.parametrize("N,C,H,cpad", [(4, 96, 14, 96), (3, 36, 9, 48), (64, 1152, 7, 1152), (2, 8, 5, 16)])
 def test_quantize_chscale(dev, N, C, H, cpad):
     """The squeeze-excite-gated quantizer equals quantizing the stored product x * gate
